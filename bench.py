@@ -1,0 +1,269 @@
+"""Benchmark: INT8 batch-1 greedy decode of the Qwen3-0.6B shape on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload NAME]
+
+Default workload: random-init Qwen3-0.6B-architecture
+weights (seed 0, N(0, 0.02) -> bf16 -> per-row INT8), an 8-token random prompt
+prefilled one decode_step per token (untimed), then K greedy decode steps
+timed through the drop-in API (``A10Int8MegakernelDecoder.decode_step``: one
+kernel launch and one token read-back per step, as bench_int8.py:355-362).
+``value`` = K / wall time of those K steps, inputs already resident in HBM.
+
+The JSON line also carries:
+* ``roofline`` — algorithmic bytes per decode launch (all weights once + the
+  KV rows read and written) over the kernel's average duration, measured with
+  HIP events on the launch stream inside the timed region, against 8 TB/s;
+* ``cpu_baseline`` — the float32 CPU port of the same decode (oracle.ref_cpu,
+  ``(q.float() @ x) * scale``) timed on this host for the 32-token workload;
+* ``parity`` — the timed tokens against the committed oracle fixture.
+
+Other workloads (parity-case shapes, one JSON line each): ``matvec``
+``positions`` (config 3 positions, bf16 weights).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+PROMPT_LEN = 8
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-steps", type=int, default=32, help="greedy steps of the CPU baseline sample")
+    ap.add_argument("--workload", default="decode", choices=["decode", "matvec", "positions"])
+    ap.add_argument("--seed", type=int, default=0)
+    return ap.parse_args()
+
+
+def cpu_baseline(keep, cfg, prompt, steps):
+    """Time the fp32 CPU port of the reference decode on this host (bounded sample)."""
+    import torch
+    from oracle.ref_cpu import Dims, RefDecoder
+
+    embed, layers, scales, lm_q, lm_s, fnorm, cos, sin = keep
+    c = lambda t: t.cpu()
+    threads = torch.get_num_threads()
+    ref = RefDecoder(Dims(), c(embed), [c(t) for t in layers], [c(t) for t in scales], c(fnorm), c(lm_q), c(lm_s),
+                     c(cos), c(sin), cfg.num_layers, cos.shape[0], dtype=torch.float32)
+    ref.reset()
+    tok = None
+    for t in prompt:
+        tok = ref.decode_step(int(t))
+    t0 = time.perf_counter()
+    toks = []
+    for _ in range(steps):
+        tok = ref.decode_step(tok)
+        toks.append(tok)
+    dt = time.perf_counter() - t0
+    del ref
+    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} greedy decode steps after the {PROMPT_LEN}-token prefill, Qwen3-0.6B shape "
+                      f"INT8 weights, fp32 torch CPU port (oracle.ref_cpu, (q.float() @ x) * scale), "
+                      f"{threads} torch threads on {os.cpu_count()} host CPUs",
+            "seconds": round(dt, 3), "tokens": toks}
+
+
+def run_decode(args, mq, torch):
+    dev = torch.device("cuda:0")
+    cfg = mq.QWEN3_0_6B
+    state, prompt = mq.random_init_state(cfg, seed=args.seed)
+    S = PROMPT_LEN + max(args.steps, args.warmup) + 8
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    qstate = mq.quantize_state(state, cfg, dev)
+    del state
+    embed, layers, scales, lm_q, lm_s, fnorm = mq.pack_int8(qstate, cfg)
+    keep = (embed, layers, scales, lm_q, lm_s, fnorm, cos, sin)
+    dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+    prompt = prompt.tolist()
+
+    def prefill():
+        dec.reset()
+        tok = None
+        for t in prompt:
+            tok = dec.decode_step(int(t))
+        return tok
+
+    tok = prefill()
+    for _ in range(args.warmup):
+        tok = dec.decode_step(tok)
+    first = prefill()
+    torch.cuda.synchronize()
+
+    # timed region: K greedy steps through the drop-in API
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    for e in starts + ends:
+        e.record()                     # create the HIP events before the timed region
+    toks = []
+    tok = first
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        # the dispatch itself records the pair at the kernel's start and end (hipExtLaunchKernel)
+        dec.set_timing_events(starts[i], ends[i])
+        dec.launch_step(tok)
+        tok = int(dec.output_token.item())
+        toks.append(tok)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dec.set_timing_events(None, None)
+    kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    if min(toks) < 0:
+        raise RuntimeError("decode kernel reported a timeout")
+
+    # algorithmic bytes of each timed launch: positions PROMPT_LEN .. PROMPT_LEN+K-1
+    bytes_total = sum(cfg.int8_step_bytes(cache_len=PROMPT_LEN + i + 1) for i in range(args.steps))
+    kern_s = sum(kern_ms) / 1e3
+    achieved = bytes_total / kern_s / 1e9
+
+    parity = None
+    fx = ROOT / "tests" / "golden" / "tokens_qwen3_0.6b_int8.json"
+    if fx.exists() and args.seed == 0:
+        want = json.loads(fx.read_text())["tokens"]
+        n = min(len(want) - 1, args.steps)
+        parity = {"fixture": fx.name, "checked": n + 1,
+                  "match": [first] + toks[:n] == want[:n + 1]}
+
+    value = args.steps / wall
+    out = {
+        "metric": "INT8 decode tok/s, Qwen3-0.6B shape bs=1; achieved HBM GB/s vs peak",
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "config 1: INT8 greedy decode, Qwen3-0.6B architecture random-init (seed 0), "
+                               "bs=1, 8-token random prompt prefilled untimed, K greedy steps timed",
+                   "weights": "int8 per-output-channel (scale=bf16(absmax/127)); embed/norms/RoPE/KV bf16",
+                   "layers": cfg.num_layers, "hidden": cfg.hidden_size, "vocab": cfg.vocab_size,
+                   "batch": 1, "prompt_len": PROMPT_LEN, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "mq::decode_kernel<1024, 3072, Int8W>",
+                     "kernel_avg_us": round(sum(kern_ms) / len(kern_ms) * 1e3, 2),
+                     "bytes_per_launch_avg": int(bytes_total / args.steps)},
+        "device_tok_s": round(args.steps / kern_s, 1),
+        "parity": parity,
+    }
+    if not args.no_cpu:
+        cb = cpu_baseline(keep, cfg, prompt, args.cpu_steps)
+        cpu_toks = cb.pop("tokens")
+        gpu_ref = [first] + toks
+        n = min(len(cpu_toks), len(gpu_ref) - 1)
+        cb["tokens_match_gpu"] = cpu_toks[:n] == gpu_ref[1:n + 1]
+        out["cpu_baseline"] = cb
+        out["speedup_vs_cpu"] = round(value / cb["value"], 1)
+    return out
+
+
+def run_matvec(args, mq, torch):
+    """per-shape INT8 matvec GB/s, rotating weight copies past the 256 MB MALL."""
+    from oracle import quant as oquant  # noqa: F401  (not used for timing)
+    dev = torch.device("cuda:0")
+    shapes = {"qkv": (4096, 1024), "o": (1024, 2048), "gate_up": (6144, 1024), "down": (1024, 3072),
+              "lm_head": (151936, 1024)}
+    res = {}
+    g = torch.Generator().manual_seed(args.seed)
+    for name, (M, K) in shapes.items():
+        w = (torch.randn(M, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+        q, s = mq.quantize_per_channel(w)
+        del w
+        nbytes = M * K + 8 * M + 4 * K
+        copies = max(1, -(-512 * 2 ** 20 // (M * K)))
+        qs = [q.clone() for _ in range(copies)]
+        x = torch.randn(K, generator=g).to(dev)
+        y = torch.empty(M, device=dev)
+        for i in range(20):
+            mq.int8_gemv(x, qs[i % copies], s, out=y)
+        reps = 1000
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record()
+        for i in range(reps):
+            mq.int8_gemv(x, qs[i % copies], s, out=y)
+        ev1.record()
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) / reps * 1e3
+        res[name] = {"shape": [M, K], "us": round(us, 3), "GBs": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "copies": copies}
+        del qs, q, s
+        torch.cuda.empty_cache()
+    lm = res["lm_head"]
+    return {"metric": "INT8 matvec GB/s (BASELINE config 2)", "value": lm["GBs"], "unit": "GB/s", "n_gpus": 1,
+            "steps": 1000, "warmup": 20, "ms_per_step": round(lm["us"] / 1e3, 5), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+            "config": {"workload": "config 2: isolated INT8 matvec, 1000 back-to-back launches per shape, "
+                                   "weight copies rotated to exceed the 256 MB MALL", "shapes": res}}
+
+
+def run_positions(args, mq, torch):
+    """bf16 weights, tok/s at positions 1, 25, 50, 100, 200 (n / wall(reset + n steps))."""
+    dev = torch.device("cuda:0")
+    cfg = mq.QWEN3_0_6B
+    state, prompt = mq.random_init_state(cfg, seed=args.seed)
+    S = PROMPT_LEN + 208
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    embed, layers, fnorm, lm = mq.pack_bf16(state, cfg, dev)
+    del state
+    dec = mq.A10MegakernelDecoder(embed, layers, fnorm, lm, cos, sin, cfg.num_layers, S)
+    for _ in range(5):
+        dec.decode_step(0)
+    res = {}
+    for n in (1, 25, 50, 100, 200):
+        best = None
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            dec.reset()
+            for _ in range(n):
+                dec.decode_step(0)
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            best = dt if best is None else min(best, dt)
+        res[str(n)] = round(n / best, 1)
+    return {"metric": "BF16 decode tok/s at positions (BASELINE config 3)", "value": res["200"], "unit": "tok/s",
+            "n_gpus": 1, "steps": 200, "warmup": 5, "ms_per_step": round(1e3 / res["200"], 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+            "config": {"workload": "config 3: bf16 weights, n / wall(reset + n decode_step(0)) (bench_and_plot_int8.py:78-85)",
+                       "tok_s_at_position": res}}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the decode path is single-device, "
+              "see DESIGN.md for how it would shard", file=sys.stderr)
+        return 2
+    import torch
+    import __graft_entry__
+    mq = __graft_entry__.load_package()
+    if not torch.cuda.is_available():
+        print("no HIP device visible", file=sys.stderr)
+        return 1
+    fn = {"decode": run_decode, "matvec": run_matvec, "positions": run_positions}[args.workload]
+    out = fn(args, mq, torch)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

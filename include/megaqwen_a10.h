@@ -1,0 +1,198 @@
+/*
+ * megaqwen_a10.h — C ABI of the MI355X (gfx950) batch-1 decode library.
+ *
+ * Plain C: pointers, sizes and status codes; no torch or HIP C++ types.
+ * Every device pointer is a HIP device allocation on the current device.
+ * Weight matrices are row-major [out_features, in_features] (the HF layout),
+ * int8 for the quantized path and bf16 (raw uint16 bits) for the bf16 path.
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   launch_a10_int8_decode   a10_int8_decode_kernel.cu:821-842 (declared again at bench_int8.py:97-117)
+ *   launch_a10_decode        a10_decode_kernel.cu:761-780       (declared again at a10_decode.py:66-85)
+ *   LayerWeights             config.cuh:45-57, bench_int8.py:73-85
+ *   ScalePointers            config.cuh:59-67, bench_int8.py:87-95
+ *   mq_int8_gemv             int8_decoder.py:100-115 (int8_gemv: y[j] = scale[j] * sum_i x[i] * w[j,i])
+ *   mq_quantize_per_channel_bf16   bench_int8.py:19-24 (quantize_per_channel)
+ */
+#ifndef MEGAQWEN_A10_H
+#define MEGAQWEN_A10_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same opaque handle type as HIP's own hip_runtime_api.h typedef. */
+typedef struct ihipStream_t* hipStream_t;
+
+/* Status codes returned by every mq_* entry point. */
+enum {
+    MQ_OK = 0,
+    MQ_ERR_INVALID_ARGUMENT = 1, /* bad pointer, shape, token id, position ... (nothing launched) */
+    MQ_ERR_UNSUPPORTED = 2,      /* model dims / device not supported by a compiled kernel        */
+    MQ_ERR_HIP = 3,              /* a HIP runtime call failed                                      */
+    MQ_ERR_TIMEOUT = 4,          /* a kernel's bounded wait expired; the workspace must be re-initialised */
+    MQ_ERR_OUT_OF_MEMORY = 5
+};
+
+/* 11 pointers per layer, field order fixed by config.cuh:45-57 (sizeof == 88). */
+typedef struct LayerWeights {
+    const void* input_layernorm_weight;     /* bf16 [H]                         */
+    const void* q_proj_weight;              /* int8|bf16 [NQ*D, H]             */
+    const void* k_proj_weight;              /* int8|bf16 [NKV*D, H]            */
+    const void* v_proj_weight;              /* int8|bf16 [NKV*D, H]            */
+    const void* q_norm_weight;              /* bf16 [D]                         */
+    const void* k_norm_weight;              /* bf16 [D]                         */
+    const void* o_proj_weight;              /* int8|bf16 [H, NQ*D]             */
+    const void* post_attn_layernorm_weight; /* bf16 [H]                         */
+    const void* gate_proj_weight;           /* int8|bf16 [I, H]                */
+    const void* up_proj_weight;             /* int8|bf16 [I, H]                */
+    const void* down_proj_weight;           /* int8|bf16 [H, I]                */
+} LayerWeights;
+
+/* 7 per-output-channel fp32 scale vectors per layer, config.cuh:59-67 (sizeof == 56). */
+typedef struct ScalePointers {
+    float* q_scale;
+    float* k_scale;
+    float* v_scale;
+    float* o_scale;
+    float* gate_scale;
+    float* up_scale;
+    float* down_scale;
+} ScalePointers;
+
+/* Model dimensions. A NULL dims pointer means the Qwen3-0.6B shape
+ * (H=1024, I=3072, 16 Q heads, 8 KV heads, head_dim 128, vocab 151936).
+ * Compiled kernels exist for (H, I) = (1024, 3072) and (2048, 6144) with
+ * 16/8 heads of 128; vocab_size is free (>= 1). */
+typedef struct mq_model_dims {
+    int hidden_size;
+    int intermediate_size;
+    int num_q_heads;
+    int num_kv_heads;
+    int head_dim;
+    int vocab_size;
+} mq_model_dims;
+
+/* Arguments of one decode step (one token, batch 1). */
+typedef struct mq_decode_args {
+    int input_token_id;               /* 0 <= id < vocab_size                               */
+    int* output_token_id;             /* device int32[1]: greedy argmax (lowest index on ties) */
+    const void* embed_weight;         /* bf16 [V, H]                                         */
+    const LayerWeights* layer_weights;/* DEVICE array [num_layers]                           */
+    const ScalePointers* scales;      /* DEVICE array [num_layers]; NULL on the bf16 path    */
+    const void* final_norm_weight;    /* bf16 [H]                                            */
+    const void* lm_head_weight;       /* int8|bf16 [V, H]                                    */
+    const float* lm_head_scale;       /* fp32 [V]; NULL on the bf16 path                     */
+    const void* cos_table;            /* bf16 [max_seq_len, D]                               */
+    const void* sin_table;            /* bf16 [max_seq_len, D]                               */
+    void* k_cache;                    /* bf16 [num_layers, NKV, max_seq_len, D]              */
+    void* v_cache;                    /* bf16 [num_layers, NKV, max_seq_len, D]              */
+    /* Optional per-stage outputs (may be NULL). After a step they hold the
+     * last layer's values, as the reference's scratch buffers do:
+     * hidden bf16[H], activations fp32[H] (post-attn RMSNorm output),
+     * residual fp32[H] (post-attn residual), q fp32[NQ*D] and k fp32[NKV*D]
+     * after QK-norm+RoPE, v fp32[NKV*D], attn_out fp32[NQ*D],
+     * mlp_intermediate fp32[I], normalized fp32[H] (final RMSNorm output),
+     * block_max_vals fp32[>=256] / block_max_idxs int32[>=256] (per-workgroup LM-head maxima). */
+    void* hidden_buffer;
+    void* g_activations;
+    void* g_residual;
+    void* g_q;
+    void* g_k;
+    void* g_v;
+    void* g_attn_out;
+    void* g_mlp_intermediate;
+    void* g_normalized;
+    void* block_max_vals;
+    void* block_max_idxs;
+    int num_layers;
+    int position;                     /* 0 <= position < max_seq_len                         */
+    int cache_len;                    /* must equal position + 1                              */
+    int max_seq_len;
+    float attn_scale;                 /* 1/sqrt(head_dim) in the reference                    */
+    const mq_model_dims* dims;        /* NULL: Qwen3-0.6B                                     */
+    void* workspace;                  /* device memory of mq_decode_workspace_bytes(dims)     */
+    size_t workspace_bytes;
+    unsigned int spin_limit;          /* bound on each in-kernel wait (polls); 0 = default    */
+    /* Optional hipEvent_t pair. When both are set the step is dispatched with
+     * hipExtLaunchKernel, which records them at the kernel's own start and end
+     * (exact kernel time); otherwise it is a cooperative launch. Either way all
+     * 256 workgroups must be co-resident, which the library checks once per
+     * device from the kernel's occupancy. */
+    void* timing_start;
+    void* timing_stop;
+} mq_decode_args;
+
+/* ---- library information ------------------------------------------------ */
+int mq_abi_version(void);
+/* Message of the last failing mq_* call on this host thread ("" if none). */
+const char* mq_last_error(void);
+
+/* ---- decode (persistent workgroup pipeline) ----------------------------- */
+size_t mq_decode_workspace_bytes(const mq_model_dims* dims);
+/* Zero the workspace and reset its step counter. Required once after
+ * allocation and again after any MQ_ERR_TIMEOUT. */
+int mq_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* One INT8 weight-only decode step (all linears and the LM head int8 with
+ * per-row fp32 scales). Replaces launch_a10_int8_decode. Asynchronous on
+ * `stream`; the token lands in *output_token_id. */
+int mq_int8_decode_step(const mq_decode_args* args, hipStream_t stream);
+/* Same with bf16 weights (scales and lm_head_scale ignored). Replaces launch_a10_decode. */
+int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream);
+/* After a completed step: MQ_ERR_TIMEOUT if a bounded wait of that step expired, else MQ_OK.
+ * Synchronises `stream`. */
+int mq_decode_check(void* workspace, hipStream_t stream);
+
+/* ---- reference-signature entry points (drop-in for the CUDA launchers) --- */
+/* a10_int8_decode_kernel.cu:821-842. Uses a library-owned workspace per
+ * device (allocated on first use): calls that overlap on one device race.
+ * The block_max_* buffers need >= 256 entries. Errors are reported through
+ * mq_last_error() since the reference signature returns void. */
+void launch_a10_int8_decode(
+    int input_token_id, int* output_token_id,
+    const void* embed_weight, const LayerWeights* layer_weights,
+    const void* final_norm_weight, const void* lm_head_weight, const float* lm_head_scale,
+    const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache,
+    void* hidden_buffer, void* g_activations, void* g_residual,
+    void* g_q, void* g_k, void* g_v, void* g_attn_out, void* g_mlp_intermediate,
+    void* g_normalized, void* block_max_vals, void* block_max_idxs,
+    int num_layers, int position, int cache_len, int max_seq_len, float attn_scale,
+    const ScalePointers* scales, hipStream_t stream);
+
+/* a10_decode_kernel.cu:761-780 (bf16 weights, no scales). */
+void launch_a10_decode(
+    int input_token_id, int* output_token_id,
+    const void* embed_weight, const LayerWeights* layer_weights,
+    const void* final_norm_weight, const void* lm_head_weight,
+    const void* cos_table, const void* sin_table,
+    void* k_cache, void* v_cache,
+    void* hidden_buffer, void* g_activations, void* g_residual,
+    void* g_q, void* g_k, void* g_v, void* g_attn_out, void* g_mlp_intermediate,
+    void* g_normalized, void* block_max_vals, void* block_max_idxs,
+    int num_layers, int position, int cache_len, int max_seq_len, float attn_scale,
+    hipStream_t stream);
+
+/* ---- standalone kernels ------------------------------------------------- */
+/* int8_decoder.py:100-115: y[j] = scale[j] * sum_k x[k] * w[j,k].
+ * x fp32 [K], w int8 [M,K] row-major (16-byte aligned rows: K % 16 == 0),
+ * scale fp32 [M], y fp32 [M]. 1 <= K <= 16384. */
+int mq_int8_gemv(const float* x, const int8_t* w, const float* scale, float* y,
+                 int M, int K, hipStream_t stream);
+
+/* bench_int8.py:19-24: per-row symmetric int8.
+ *   amax = max_k |w[j,k]|               (bf16, exact)
+ *   s    = bf16(amax / 127)             (bf16 division), widened to fp32, clamped to >= 1e-12
+ *   q    = clamp(round_half_even(fp32(w) / s), -128, 127)
+ * w bf16 [M,K] (uint16 bits), q int8 [M,K], scale fp32 [M]. */
+int mq_quantize_per_channel_bf16(const void* w_bf16, int M, int K,
+                                 int8_t* q, float* scale, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEGAQWEN_A10_H */

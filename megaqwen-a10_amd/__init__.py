@@ -1,0 +1,27 @@
+"""MI355X (gfx950) batch-1 decode for Qwen3-shaped models — drop-in for MegaQwen-A10's decode path.
+
+Python host code on PyTorch-ROCm (device memory, streams) over a C-ABI HIP
+library (``lib/libmegaqwen_a10.so``, declared in include/megaqwen_a10.h):
+
+* ``quantize_per_channel`` — per-row symmetric INT8 (bench_int8.py:19-24), HIP kernel.
+* ``int8_gemv`` — INT8 weight-only matvec (int8_decoder.py:100-115), HIP kernel.
+* ``A10Int8MegakernelDecoder`` / ``A10MegakernelDecoder`` / ``A10Decoder`` —
+  the reference's decoder classes (bench_int8.py:119-255, a10_decode.py:35-393),
+  one persistent-kernel launch per token.
+* ``precompute_rope_freqs`` / ``make_rope`` — RoPE tables.
+* ``random_init_state`` / ``quantize_state`` / ``pack_int8`` / ``pack_bf16`` —
+  seeded weights and the reference's tensor packing.
+"""
+from .config import QWEN3_0_6B, QWEN3_1_7B, ModelConfig
+from .decoder import A10Decoder, A10Int8MegakernelDecoder, A10MegakernelDecoder
+from .gemv import int8_gemv
+from .quant import quantize_per_channel
+from .rope import make_rope, precompute_rope_freqs
+from .weights import pack_bf16, pack_int8, quantize_state, random_init_state, state_digest
+
+__all__ = [
+    "ModelConfig", "QWEN3_0_6B", "QWEN3_1_7B",
+    "A10Decoder", "A10Int8MegakernelDecoder", "A10MegakernelDecoder",
+    "int8_gemv", "quantize_per_channel", "make_rope", "precompute_rope_freqs",
+    "pack_bf16", "pack_int8", "quantize_state", "random_init_state", "state_digest",
+]

@@ -1,0 +1,275 @@
+// C-ABI entry points (include/megaqwen_a10.h): argument validation before any
+// launch, status codes, per-thread error messages, the library-owned
+// workspaces behind the reference-signature launchers, and workspace reset.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "internal.h"
+
+namespace mq {
+
+static thread_local char g_err[512] = "";
+
+// Every public entry point starts with an empty message, so after a void
+// launcher returns, an empty mq_last_error() means it was accepted.
+static void clear_error() { g_err[0] = 0; }
+
+int set_error(int status, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return status;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(e));
+    return MQ_OK;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+static int shape_of(const mq_model_dims* d, DecodeShape* s) {
+    if (d == nullptr) {
+        *s = DecodeShape{1024, 3072, 16, 8, 128, 151936};
+        return MQ_OK;
+    }
+    *s = DecodeShape{d->hidden_size, d->intermediate_size, d->num_q_heads, d->num_kv_heads, d->head_dim,
+                     d->vocab_size};
+    if (s->NQ != 16 || s->NKV != 8 || s->D != 128)
+        return set_error(MQ_ERR_UNSUPPORTED, "only 16 query heads, 8 KV heads of dim 128 are compiled (got %d/%d/%d)",
+                         s->NQ, s->NKV, s->D);
+    if (!((s->H == 1024 && s->I == 3072) || (s->H == 2048 && s->I == 6144)))
+        return set_error(MQ_ERR_UNSUPPORTED, "no kernel for hidden %d / intermediate %d", s->H, s->I);
+    if (s->V < 1) return set_error(MQ_ERR_INVALID_ARGUMENT, "vocab_size %d < 1", s->V);
+    return MQ_OK;
+}
+
+__global__ void ws_init_kernel(uint64_t* ws, size_t words) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < words; i += (size_t)gridDim.x * blockDim.x)
+        ws[i] = 0;
+    if (blockIdx.x == 0 && threadIdx.x == 0) reinterpret_cast<WsHeader*>(ws)->epoch = 1u;
+}
+
+static int validate_decode(const mq_decode_args* a, bool int8, DecodeShape* s) {
+    if (a == nullptr) return set_error(MQ_ERR_INVALID_ARGUMENT, "args is NULL");
+    int st = shape_of(a->dims, s);
+    if (st != MQ_OK) return st;
+    if (a->num_layers < 1) return set_error(MQ_ERR_INVALID_ARGUMENT, "num_layers %d < 1", a->num_layers);
+    if (a->max_seq_len < 1) return set_error(MQ_ERR_INVALID_ARGUMENT, "max_seq_len %d < 1", a->max_seq_len);
+    if (a->input_token_id < 0 || a->input_token_id >= s->V)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "input_token_id %d outside [0, %d)", a->input_token_id, s->V);
+    if (a->position < 0 || a->position >= a->max_seq_len)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "position %d outside [0, max_seq_len=%d)", a->position, a->max_seq_len);
+    if (a->cache_len != a->position + 1)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "cache_len %d != position + 1 (%d)", a->cache_len, a->position + 1);
+    if (!a->output_token_id || !a->embed_weight || !a->layer_weights || !a->final_norm_weight ||
+        !a->lm_head_weight || !a->cos_table || !a->sin_table || !a->k_cache || !a->v_cache)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+    if (int8 && (!a->scales || !a->lm_head_scale))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "int8 decode needs scales and lm_head_scale");
+    if (!aligned16(a->lm_head_weight) || !aligned16(a->k_cache) || !aligned16(a->v_cache))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "lm_head_weight and the KV caches must be 16-byte aligned");
+    if (!a->workspace || a->workspace_bytes < decode_workspace_bytes(*s))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "workspace of %zu bytes needed, %zu given",
+                         decode_workspace_bytes(*s), a->workspace ? a->workspace_bytes : (size_t)0);
+    if (!aligned16(a->workspace)) return set_error(MQ_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    return MQ_OK;
+}
+
+// Library-owned workspace per device for the reference-signature launchers.
+struct DeviceWorkspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+static std::mutex g_ws_mu;
+static DeviceWorkspace g_ws[64];
+
+static int default_workspace(hipStream_t stream, void** out, size_t* bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return set_error(MQ_ERR_HIP, "hipGetDevice failed");
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    DeviceWorkspace& w = g_ws[dev];
+    if (w.ptr == nullptr) {
+        DecodeShape s;
+        shape_of(nullptr, &s);
+        const size_t need = decode_workspace_bytes(s);
+        if (hipMalloc(&w.ptr, need) != hipSuccess) {
+            w.ptr = nullptr;
+            return set_error(MQ_ERR_OUT_OF_MEMORY, "hipMalloc(%zu) for the decode workspace failed", need);
+        }
+        w.bytes = need;
+        hipLaunchKernelGGL(ws_init_kernel, dim3(64), dim3(256), 0, stream, static_cast<uint64_t*>(w.ptr),
+                           need / 8);
+        int st = check_launch("ws_init_kernel");
+        if (st != MQ_OK) return st;
+    }
+    *out = w.ptr;
+    *bytes = w.bytes;
+    return MQ_OK;
+}
+
+}  // namespace mq
+
+using namespace mq;
+
+extern "C" {
+
+int mq_abi_version(void) { return 1; }
+
+const char* mq_last_error(void) { return g_err; }
+
+size_t mq_decode_workspace_bytes(const mq_model_dims* dims) {
+    clear_error();
+    DecodeShape s;
+    if (shape_of(dims, &s) != MQ_OK) return 0;
+    return decode_workspace_bytes(s);
+}
+
+int mq_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    if (!workspace || workspace_bytes < sizeof(WsHeader) || (workspace_bytes % 8) != 0 || !aligned16(workspace))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "workspace must be >= %zu bytes, a multiple of 8, 16-byte aligned",
+                         sizeof(WsHeader));
+    hipLaunchKernelGGL(ws_init_kernel, dim3(64), dim3(256), 0, stream, static_cast<uint64_t*>(workspace),
+                       workspace_bytes / 8);
+    return check_launch("ws_init_kernel");
+}
+
+int mq_int8_decode_step(const mq_decode_args* args, hipStream_t stream) {
+    clear_error();
+    DecodeShape s;
+    int st = validate_decode(args, true, &s);
+    if (st != MQ_OK) return st;
+    return launch_decode(*args, s, true, stream);
+}
+
+int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream) {
+    clear_error();
+    DecodeShape s;
+    int st = validate_decode(args, false, &s);
+    if (st != MQ_OK) return st;
+    return launch_decode(*args, s, false, stream);
+}
+
+int mq_decode_check(void* workspace, hipStream_t stream) {
+    clear_error();
+    if (!workspace) return set_error(MQ_ERR_INVALID_ARGUMENT, "workspace is NULL");
+    hipError_t e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+    uint32_t flag = 0;
+    e = hipMemcpy(&flag, static_cast<uint8_t*>(workspace) + offsetof(WsHeader, abort_flag), sizeof(flag),
+                  hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipMemcpy: %s", hipGetErrorString(e));
+    if (flag != 0)
+        return set_error(MQ_ERR_TIMEOUT, "a bounded wait in the decode kernel expired; re-initialise the workspace");
+    return MQ_OK;
+}
+
+void launch_a10_int8_decode(int input_token_id, int* output_token_id, const void* embed_weight,
+                            const LayerWeights* layer_weights, const void* final_norm_weight,
+                            const void* lm_head_weight, const float* lm_head_scale, const void* cos_table,
+                            const void* sin_table, void* k_cache, void* v_cache, void* hidden_buffer,
+                            void* g_activations, void* g_residual, void* g_q, void* g_k, void* g_v,
+                            void* g_attn_out, void* g_mlp_intermediate, void* g_normalized,
+                            void* block_max_vals, void* block_max_idxs, int num_layers, int position,
+                            int cache_len, int max_seq_len, float attn_scale, const ScalePointers* scales,
+                            hipStream_t stream) {
+    clear_error();
+    mq_decode_args a;
+    memset(&a, 0, sizeof(a));
+    if (default_workspace(stream, &a.workspace, &a.workspace_bytes) != MQ_OK) return;
+    a.input_token_id = input_token_id;
+    a.output_token_id = output_token_id;
+    a.embed_weight = embed_weight;
+    a.layer_weights = layer_weights;
+    a.scales = scales;
+    a.final_norm_weight = final_norm_weight;
+    a.lm_head_weight = lm_head_weight;
+    a.lm_head_scale = lm_head_scale;
+    a.cos_table = cos_table;
+    a.sin_table = sin_table;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.hidden_buffer = hidden_buffer;
+    a.g_activations = g_activations;
+    a.g_residual = g_residual;
+    a.g_q = g_q;
+    a.g_k = g_k;
+    a.g_v = g_v;
+    a.g_attn_out = g_attn_out;
+    a.g_mlp_intermediate = g_mlp_intermediate;
+    a.g_normalized = g_normalized;
+    a.block_max_vals = block_max_vals;
+    a.block_max_idxs = block_max_idxs;
+    a.num_layers = num_layers;
+    a.position = position;
+    a.cache_len = cache_len;
+    a.max_seq_len = max_seq_len;
+    a.attn_scale = attn_scale;
+    mq_int8_decode_step(&a, stream);
+}
+
+void launch_a10_decode(int input_token_id, int* output_token_id, const void* embed_weight,
+                       const LayerWeights* layer_weights, const void* final_norm_weight, const void* lm_head_weight,
+                       const void* cos_table, const void* sin_table, void* k_cache, void* v_cache,
+                       void* hidden_buffer, void* g_activations, void* g_residual, void* g_q, void* g_k, void* g_v,
+                       void* g_attn_out, void* g_mlp_intermediate, void* g_normalized, void* block_max_vals,
+                       void* block_max_idxs, int num_layers, int position, int cache_len, int max_seq_len,
+                       float attn_scale, hipStream_t stream) {
+    clear_error();
+    mq_decode_args a;
+    memset(&a, 0, sizeof(a));
+    if (default_workspace(stream, &a.workspace, &a.workspace_bytes) != MQ_OK) return;
+    a.input_token_id = input_token_id;
+    a.output_token_id = output_token_id;
+    a.embed_weight = embed_weight;
+    a.layer_weights = layer_weights;
+    a.final_norm_weight = final_norm_weight;
+    a.lm_head_weight = lm_head_weight;
+    a.cos_table = cos_table;
+    a.sin_table = sin_table;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.hidden_buffer = hidden_buffer;
+    a.g_activations = g_activations;
+    a.g_residual = g_residual;
+    a.g_q = g_q;
+    a.g_k = g_k;
+    a.g_v = g_v;
+    a.g_attn_out = g_attn_out;
+    a.g_mlp_intermediate = g_mlp_intermediate;
+    a.g_normalized = g_normalized;
+    a.block_max_vals = block_max_vals;
+    a.block_max_idxs = block_max_idxs;
+    a.num_layers = num_layers;
+    a.position = position;
+    a.cache_len = cache_len;
+    a.max_seq_len = max_seq_len;
+    a.attn_scale = attn_scale;
+    mq_bf16_decode_step(&a, stream);
+}
+
+int mq_int8_gemv(const float* x, const int8_t* w, const float* scale, float* y, int M, int K, hipStream_t stream) {
+    clear_error();
+    if (!x || !w || !scale || !y) return set_error(MQ_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (M < 1 || K < 1 || K > 16384 || (K % 16) != 0)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "need M >= 1 and 16 <= K <= 16384 with K %% 16 == 0 (M=%d K=%d)", M, K);
+    if (!aligned16(w) || !aligned16(x)) return set_error(MQ_ERR_INVALID_ARGUMENT, "x and w must be 16-byte aligned");
+    return launch_int8_gemv(x, w, scale, y, M, K, stream);
+}
+
+int mq_quantize_per_channel_bf16(const void* w_bf16, int M, int K, int8_t* q, float* scale, hipStream_t stream) {
+    clear_error();
+    if (!w_bf16 || !q || !scale) return set_error(MQ_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (M < 1 || K < 1) return set_error(MQ_ERR_INVALID_ARGUMENT, "need M >= 1 and K >= 1 (M=%d K=%d)", M, K);
+    return launch_quantize(w_bf16, M, K, q, scale, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,242 @@
+// Device helpers shared by the gfx950 kernels: bf16 conversion, wave64
+// cross-lane reductions (DPP within 16-lane rows, ds_bpermute across rows),
+// the int8/bf16 16-byte dot products and the tagged 64-bit exchange words
+// the persistent decode kernel synchronises with.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mq {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (quiet NaN preserved).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// ---- cross-lane exchange --------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Value held by this lane's partner at level M of a 64-lane butterfly. Every
+// level pairs a lane whose bit M is clear with one whose bit M is set, inside
+// the same 2M-lane group: xor for M = 32, 16, 2, 1 and the (half-)row mirrors
+// for M = 8, 4 (lane i <-> 15-i, lane i <-> 7-i).
+template <int M>
+__device__ __forceinline__ float partner(float v) {
+    if constexpr (M == 32) return __shfl_xor(v, 32);
+    else if constexpr (M == 16) return __shfl_xor(v, 16);
+    else if constexpr (M == 8) return dpp<0x140>(v);   // row_mirror
+    else if constexpr (M == 4) return dpp<0x141>(v);   // row_half_mirror
+    else if constexpr (M == 2) return dpp<0x4E>(v);    // quad_perm [2,3,0,1]
+    else return dpp<0xB1>(v);                           // quad_perm [1,0,3,2]
+}
+
+// Sum over the wave, returned uniformly (readlane of the four 16-lane row sums).
+__device__ __forceinline__ float wave_sum(float v) {
+    v += partner<1>(v);
+    v += partner<2>(v);
+    v += partner<4>(v);
+    v += partner<8>(v);
+    float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (a + b) + (c + d);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, partner<1>(v));
+    v = fmaxf(v, partner<2>(v));
+    v = fmaxf(v, partner<4>(v));
+    v = fmaxf(v, partner<8>(v));
+    float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// One transpose level: N values per lane become N/2; lanes with bit M clear
+// keep the lower half of the list, lanes with bit M set the upper half, and
+// each adds its partner's copy of the half it keeps.
+template <int M, int N>
+__device__ __forceinline__ void transpose_level(float* v, int lane) {
+    const bool hi = (lane & M) != 0;
+#pragma unroll
+    for (int r = 0; r < N / 2; ++r) {
+        float keep = hi ? v[r + N / 2] : v[r];
+        float send = hi ? v[r] : v[r + N / 2];
+        v[r] = keep + partner<M>(send);
+    }
+}
+
+// Reduce R per-lane partial sums (R a power of two <= 64) over the wave, with
+// G consecutive list entries summed together (G divides R). Afterwards every
+// lane of block b = lane / (64*G/R) holds sum over lanes and over
+// entries [b*G, b*G+G) of v.
+template <int R, int G = 1>
+__device__ __forceinline__ float transpose_reduce(float* v, int lane) {
+    constexpr int T = R / G;                         // number of distinct results
+    if constexpr (T >= 2) transpose_level<32, R>(v, lane);
+    if constexpr (T >= 4) transpose_level<16, R / 2>(v, lane);
+    if constexpr (T >= 8) transpose_level<8, R / 4>(v, lane);
+    if constexpr (T >= 16) transpose_level<4, R / 8>(v, lane);
+    if constexpr (T >= 32) transpose_level<2, R / 16>(v, lane);
+    if constexpr (T >= 64) transpose_level<1, R / 32>(v, lane);
+    float x = v[0];
+#pragma unroll
+    for (int g = 1; g < G; ++g) x += v[g];
+    if constexpr (T < 64) x += partner<1>(x);
+    if constexpr (T < 32) x += partner<2>(x);
+    if constexpr (T < 16) x += partner<4>(x);
+    if constexpr (T < 8) x += partner<8>(x);
+    if constexpr (T < 4) x += partner<16>(x);
+    if constexpr (T < 2) x += partner<32>(x);
+    return x;
+}
+
+// ---- 16-byte dot products ----------------------------------------------------------------
+// int8 x16 against 16 fp32 activations (one v_cvt_f32_i32 with a sign-extended
+// byte select plus one FMA per element).
+__device__ __forceinline__ float dot_i8x16(uint4 w, const float4* x, float acc) {
+    const int8_t* b = reinterpret_cast<const int8_t*>(&w);
+    float4 x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+    acc = fmaf((float)b[0], x0.x, acc);  acc = fmaf((float)b[1], x0.y, acc);
+    acc = fmaf((float)b[2], x0.z, acc);  acc = fmaf((float)b[3], x0.w, acc);
+    acc = fmaf((float)b[4], x1.x, acc);  acc = fmaf((float)b[5], x1.y, acc);
+    acc = fmaf((float)b[6], x1.z, acc);  acc = fmaf((float)b[7], x1.w, acc);
+    acc = fmaf((float)b[8], x2.x, acc);  acc = fmaf((float)b[9], x2.y, acc);
+    acc = fmaf((float)b[10], x2.z, acc); acc = fmaf((float)b[11], x2.w, acc);
+    acc = fmaf((float)b[12], x3.x, acc); acc = fmaf((float)b[13], x3.y, acc);
+    acc = fmaf((float)b[14], x3.z, acc); acc = fmaf((float)b[15], x3.w, acc);
+    return acc;
+}
+
+// bf16 x8 against 8 fp32 activations.
+__device__ __forceinline__ float dot_bf16x8(uint4 w, const float4* x, float acc) {
+    float4 x0 = x[0], x1 = x[1];
+    acc = fmaf(__uint_as_float(w.x << 16), x0.x, acc);
+    acc = fmaf(__uint_as_float(w.x & 0xffff0000u), x0.y, acc);
+    acc = fmaf(__uint_as_float(w.y << 16), x0.z, acc);
+    acc = fmaf(__uint_as_float(w.y & 0xffff0000u), x0.w, acc);
+    acc = fmaf(__uint_as_float(w.z << 16), x1.x, acc);
+    acc = fmaf(__uint_as_float(w.z & 0xffff0000u), x1.y, acc);
+    acc = fmaf(__uint_as_float(w.w << 16), x1.z, acc);
+    acc = fmaf(__uint_as_float(w.w & 0xffff0000u), x1.w, acc);
+    return acc;
+}
+
+// Weight element formats: bytes per element, elements per 16-byte lane load,
+// and the dot product over one lane load.
+struct Int8W {
+    static constexpr int kBytes = 1;
+    static constexpr int kPerLane = 16;
+    __device__ static float dot(uint4 w, const float4* x, float acc) { return dot_i8x16(w, x, acc); }
+};
+struct Bf16W {
+    static constexpr int kBytes = 2;
+    static constexpr int kPerLane = 8;
+    __device__ static float dot(uint4 w, const float4* x, float acc) { return dot_bf16x8(w, x, acc); }
+};
+
+// ---- activation vector in LDS, laid out per lane --------------------------------------
+// A wave-wide 16-byte-per-lane load covers one 1 KB "chunk" of a weight row
+// (64*kPerLane elements). Lane l needs elements [chunk*64*P + l*P, +P) of the
+// activation vector; they are stored as P/4 float4 values at
+// xs[(chunk*(P/4) + j)*64 + l] so that the lanes of a wave read consecutive
+// float4s (no bank conflicts).
+template <class W>
+__device__ __forceinline__ int xs_index(int k) {          // float index of element k
+    constexpr int P = W::kPerLane;
+    const int chunk = k / (64 * P);
+    const int e = k % (64 * P);
+    const int lane = e / P;
+    const int t = e % P;
+    return ((chunk * (P / 4) + (t >> 2)) * 64 + lane) * 4 + (t & 3);
+}
+template <class W>
+__device__ __forceinline__ const float4* xs_frag(const float4* xs, int chunk, int lane) {
+    constexpr int P = W::kPerLane;
+    return xs + (chunk * (P / 4)) * 64 + lane;           // stride 64 float4 between the P/4 parts
+}
+template <class W>
+__device__ __forceinline__ float dot_frag(uint4 w, const float4* frag, float acc) {
+    if constexpr (W::kPerLane == 16) {
+        float4 x[4] = {frag[0], frag[64], frag[128], frag[192]};
+        return W::dot(w, x, acc);
+    } else {
+        float4 x[2] = {frag[0], frag[64]};
+        return W::dot(w, x, acc);
+    }
+}
+
+// ---- tagged exchange words --------------------------------------------------------------
+// A 64-bit word holds a 32-bit payload and a 32-bit tag naming the step,
+// layer and stage that wrote it. Producers store it with one relaxed
+// agent-scope atomic store; consumers poll it with relaxed agent-scope atomic
+// loads until the tag matches. Payload and tag travel in one single-copy-atomic
+// access, so no fence is needed between them.
+__device__ __forceinline__ void ll_put(uint64_t* p, uint32_t payload, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
+    return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Bounded polling. After `limit` unsuccessful polls of one word, or once any
+// workgroup has raised the abort flag, every further wait returns at once, so
+// a grid whose producers stalled still drains in bounded time and the host
+// reports MQ_ERR_TIMEOUT.
+struct Waiter {
+    uint32_t* abort_flag;
+    uint32_t limit;
+    bool dead;
+
+    __device__ Waiter(uint32_t* flag, uint32_t lim) : abort_flag(flag), limit(lim), dead(false) {}
+
+    __device__ __forceinline__ uint32_t get(const uint64_t* p, uint32_t tag) {
+        uint64_t w = ll_load(p);
+        if ((uint32_t)(w >> 32) == tag || dead) return (uint32_t)w;
+        uint32_t n = 0;
+        for (;;) {
+            __builtin_amdgcn_s_sleep(1);
+            w = ll_load(p);
+            if ((uint32_t)(w >> 32) == tag) break;
+            if (++n >= limit) {
+                dead = true;
+                __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            if ((n & 127u) == 0 &&
+                __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+                dead = true;
+                break;
+            }
+        }
+        return (uint32_t)w;
+    }
+    __device__ __forceinline__ float getf(const uint64_t* p, uint32_t tag) { return __uint_as_float(get(p, tag)); }
+};
+
+// Order-preserving map fp32 -> uint32 (larger float -> larger key).
+__device__ __forceinline__ uint32_t ordered_key(float f) {
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+    uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(u);
+}
+
+}  // namespace mq

@@ -1,0 +1,692 @@
+// Persistent batch-1 decode step for Qwen3-shaped models on gfx950.
+//
+// Computes what a10_int8_decode_kernel.cu:21-815 computes (and, with bf16
+// weights and unit scales, a10_decode_kernel.cu:21-755): embedding, L layers of
+// [RMSNorm + QKV, QK-norm + RoPE + bf16 KV write, GQA attention, O + residual,
+// RMSNorm + gate/up + SwiGLU, down + residual -> bf16], final RMSNorm, LM head
+// and greedy argmax — in ONE launch of 256 workgroups x 512 threads.
+//
+// Work split (per workgroup g, 0 <= g < 256):
+//   QKV      rows [16g, 16g+16) of the concatenated q|k|v projection
+//   ATTN     workgroups 0..7: KV head g with its two query heads
+//   O, DOWN  rows [H/256*g, +H/256) of o_proj and down_proj
+//   GATE/UP  channels [I/256*g, +I/256) of gate_proj and up_proj
+//   LM HEAD  rows [V*g/256, V*(g+1)/256)
+// Every workgroup recomputes the RMSNorms it needs from the full vector, so no
+// stage waits for a single "norm" workgroup.
+//
+// Stages hand vectors to each other through 64-bit words (32-bit value +
+// 32-bit tag naming step/layer/stage) written with one relaxed agent-scope
+// atomic store and polled with relaxed agent-scope atomic loads (common.h).
+// A consumer therefore waits exactly for the words it reads; there is no
+// separate grid barrier and no cache write-back/invalidate. Each stage issues
+// its own weight loads (registers) before polling its input, so weight-fetch
+// latency overlaps the wait for the producers.
+//
+// The workspace (internal.h: WsHeader + exchange buffers) carries the step
+// counter; the last workgroup to finish the LM head publishes the token and
+// advances it.
+#include "common.h"
+#include "internal.h"
+
+#include <hip/hip_ext.h>
+
+#include <algorithm>
+
+namespace mq {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kNWG = 256;
+constexpr int kMaxAttnLen = 4096;     // positions one workgroup attends over (scores in LDS)
+constexpr float kEps = 1e-6f;
+
+enum Stage { ST_QKV = 0, ST_ATTN = 1, ST_O = 2, ST_GU = 3, ST_DOWN = 4 };
+
+struct KArgs {
+    int token;
+    int* out_token;
+    const uint16_t* embed;
+    const LayerWeights* lw;
+    const ScalePointers* sp;
+    const uint16_t* final_norm;
+    const uint8_t* lm_w;
+    const float* lm_s;
+    const uint16_t* cos_t;
+    const uint16_t* sin_t;
+    uint16_t* kc;
+    uint16_t* vc;
+    uint16_t* dbg_hidden;
+    float* dbg_act;
+    float* dbg_resid;
+    float* dbg_q;
+    float* dbg_k;
+    float* dbg_v;
+    float* dbg_attn;
+    float* dbg_mlp;
+    float* dbg_norm;
+    float* dbg_bmax;
+    int* dbg_bidx;
+    int L, pos, cache_len, S, V;
+    float attn_scale;
+    uint32_t spin_limit;
+    WsHeader* hdr;
+    uint64_t* hid_x;
+    uint64_t* qkv_x;
+    uint64_t* att_x;
+    uint64_t* act_x;
+    uint64_t* mlp_x;
+};
+
+constexpr int pow2ceil(int x) { return x <= 1 ? 1 : 2 * pow2ceil((x + 1) / 2); }
+
+// One matvec stage of a workgroup: ROWS rows of K inputs, split into (row,
+// 1 KB chunk) items handed round-robin to the 8 waves. Weights are loaded
+// into registers by load() ahead of the input poll; compute() leaves one
+// partial sum per item in `part`.
+template <class W, int ROWS, int K>
+struct Stage_ {
+    static constexpr int CHUNK = 64 * W::kPerLane;
+    static constexpr int CH = K / CHUNK;
+    static constexpr int ITEMS = ROWS * CH;
+    static constexpr int IPW = (ITEMS + kWaves - 1) / kWaves;
+    static constexpr int R = pow2ceil(IPW);
+    static_assert(K % CHUNK == 0, "row length must be a whole number of 1 KB chunks");
+    uint4 w[IPW];
+
+    template <class RowPtr>
+    __device__ __forceinline__ void load(RowPtr rowptr, int wave, int lane) {
+#pragma unroll
+        for (int j = 0; j < IPW; ++j) {
+            const int it = wave + kWaves * j;
+            if (it < ITEMS)
+                w[j] = *reinterpret_cast<const uint4*>(rowptr(it / CH) + (it % CH) * 1024 + lane * 16);
+        }
+    }
+    __device__ __forceinline__ void compute(const float4* xs, float* part, int wave, int lane) const {
+        float acc[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            acc[j] = 0.0f;
+            const int it = wave + kWaves * j;
+            if (j < IPW && it < ITEMS) acc[j] = dot_frag<W>(w[j], xs_frag<W>(xs, it % CH, lane), 0.0f);
+        }
+        const float s = transpose_reduce<R>(acc, lane);
+        constexpr int span = kWave / R;
+        const int j = lane / span;
+        if ((lane % span) == 0 && j < IPW) {
+            const int it = wave + kWaves * j;
+            if (it < ITEMS) part[it] = s;
+        }
+    }
+    __device__ __forceinline__ static float row_sum(const float* part, int row) {
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) s += part[row * CH + c];
+        return s;
+    }
+};
+
+template <int N>
+__device__ __forceinline__ float block_sum(float v, float* red, int wave, int lane) {
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; ++i) t += red[i];
+    return t;
+}
+
+template <int H, int I, class W>
+__global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
+    constexpr int NQ = 16, NKV = 8, D = 128;
+    constexpr int QD = NQ * D, KVD = NKV * D, QKV = QD + 2 * KVD;
+    constexpr int ES = W::kBytes;
+    constexpr bool kInt8 = (ES == 1);
+    constexpr int ROWS_QKV = QKV / kNWG;
+    constexpr int ROWS_H = H / kNWG;
+    constexpr int CPW = I / kNWG;
+    constexpr int XMAX = (H > QD ? (H > I ? H : I) : (QD > I ? QD : I));
+    static_assert(QKV % kNWG == 0 && H % kNWG == 0 && I % kNWG == 0, "rows must split evenly");
+    static_assert(H % kThreads == 0 && QD % kThreads == 0 && I % kThreads == 0, "vectors must split evenly");
+
+    __shared__ float4 xs[XMAX / 4];
+    __shared__ float part[256];
+    __shared__ float red[2 * kWaves];
+    __shared__ float rows_res[ROWS_H];
+    __shared__ float att_in[4 * D];
+    __shared__ float qrot[2 * D];
+    __shared__ float kv_cur[2 * D];
+    __shared__ float scores[2 * kMaxAttnLen];
+    __shared__ float pv[kWaves * 2 * D];
+    __shared__ float lm_best_v[kWaves];
+    __shared__ int lm_best_i[kWaves];
+
+    const int g = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
+    const int wave = tid / kWave;
+    float* xsf = reinterpret_cast<float*>(xs);
+
+    WsHeader* hdr = a.hdr;
+    const uint32_t E = __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (g == 0 && tid == 0) {
+        __hip_atomic_store(&hdr->done[(E + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&hdr->best[(E + 1) & 1], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const uint32_t tps = 5u * (uint32_t)a.L + 4u;
+    auto tag = [&](int l, int st) -> uint32_t { return ((E * tps + 5u * (uint32_t)l + (uint32_t)st) << 1) | 1u; };
+    Waiter wt(&hdr->abort_flag, a.spin_limit);
+
+    const int64_t kv_head_stride = (int64_t)a.S * D;
+    const int last = a.L - 1;
+
+    for (int l = 0; l < a.L; ++l) {
+        const LayerWeights& lw = a.lw[l];
+        const ScalePointers* sp = kInt8 ? &a.sp[l] : nullptr;
+
+        // ---------------- RMSNorm + QKV ----------------
+        {
+            const int row0 = g * ROWS_QKV;
+            const uint8_t* base;
+            const float* sc = nullptr;
+            int lrow0;
+            if (row0 < QD) { base = (const uint8_t*)lw.q_proj_weight; lrow0 = row0; if (kInt8) sc = sp->q_scale; }
+            else if (row0 < QD + KVD) { base = (const uint8_t*)lw.k_proj_weight; lrow0 = row0 - QD; if (kInt8) sc = sp->k_scale; }
+            else { base = (const uint8_t*)lw.v_proj_weight; lrow0 = row0 - QD - KVD; if (kInt8) sc = sp->v_scale; }
+            Stage_<W, ROWS_QKV, H> st;
+            st.load([&](int r) { return base + (int64_t)(lrow0 + r) * H * ES; }, wave, lane);
+
+            constexpr int PT = H / kThreads;
+            float hv[PT];
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                const int k = tid + i * kThreads;
+                if (l == 0) hv[i] = bf16_bits_to_f32(a.embed[(int64_t)a.token * H + k]);
+                else hv[i] = wt.getf(&a.hid_x[k], tag(l - 1, ST_DOWN));
+                ss += hv[i] * hv[i];
+            }
+            const float tot = block_sum<kWaves>(ss, red, wave, lane);
+            const float rstd = rsqrtf(tot / (float)H + kEps);
+            const uint16_t* lnw = (const uint16_t*)lw.input_layernorm_weight;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                const int k = tid + i * kThreads;
+                xsf[xs_index<W>(k)] = hv[i] * rstd * bf16_bits_to_f32(lnw[k]);
+                const int rr = k - g * ROWS_H;
+                if (rr >= 0 && rr < ROWS_H) rows_res[rr] = hv[i];
+            }
+            __syncthreads();
+            st.compute(xs, part, wave, lane);
+            __syncthreads();
+            if (tid < ROWS_QKV) {
+                float v = Stage_<W, ROWS_QKV, H>::row_sum(part, tid);
+                if (kInt8) v = v * sc[lrow0 + tid];
+                ll_put(&a.qkv_x[row0 + tid], __float_as_uint(v), tag(l, ST_QKV));
+            }
+        }
+
+        // ---------------- QK-norm + RoPE + KV write + attention (KV head g) ----------------
+        if (g < NKV) {
+            const int h = g;
+            {
+                int word;
+                if (tid < 2 * D) word = 2 * h * D + tid;
+                else if (tid < 3 * D) word = QD + h * D + (tid - 2 * D);
+                else word = QD + KVD + h * D + (tid - 3 * D);
+                att_in[tid] = wt.getf(&a.qkv_x[word], tag(l, ST_QKV));
+            }
+            __syncthreads();
+            const int64_t cache_base = ((int64_t)l * NKV + h) * kv_head_stride;
+            const int64_t cur = cache_base + (int64_t)a.pos * D;
+            if (wave < 3) {
+                const float* src = att_in + wave * D;
+                const float x0 = src[lane], x1 = src[lane + 64];
+                const float ssq = wave_sum(x0 * x0 + x1 * x1);
+                const float sc = rsqrtf(ssq / (float)D + kEps);
+                const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
+                const float y0 = x0 * sc * bf16_bits_to_f32(nw[lane]);
+                const float y1 = x1 * sc * bf16_bits_to_f32(nw[lane + 64]);
+                const uint16_t* ct = a.cos_t + (int64_t)a.pos * D;
+                const uint16_t* stt = a.sin_t + (int64_t)a.pos * D;
+                const float c0 = bf16_bits_to_f32(ct[lane]), s0 = bf16_bits_to_f32(stt[lane]);
+                const float c1 = bf16_bits_to_f32(ct[lane + 64]), s1 = bf16_bits_to_f32(stt[lane + 64]);
+                const float o0 = y0 * c0 - y1 * s0;
+                const float o1 = y0 * s1 + y1 * c1;
+                if (wave < 2) {
+                    qrot[wave * D + lane] = o0;
+                    qrot[wave * D + lane + 64] = o1;
+                    if (l == last && a.dbg_q) {
+                        a.dbg_q[(2 * h + wave) * D + lane] = o0;
+                        a.dbg_q[(2 * h + wave) * D + lane + 64] = o1;
+                    }
+                } else {
+                    const uint32_t b0 = f32_to_bf16_bits(o0), b1 = f32_to_bf16_bits(o1);
+                    kv_cur[lane] = bf16_bits_to_f32(b0);
+                    kv_cur[lane + 64] = bf16_bits_to_f32(b1);
+                    a.kc[cur + lane] = (uint16_t)b0;
+                    a.kc[cur + lane + 64] = (uint16_t)b1;
+                    if (l == last && a.dbg_k) { a.dbg_k[h * D + lane] = o0; a.dbg_k[h * D + lane + 64] = o1; }
+                }
+            } else if (wave == 3) {
+                const float v0 = att_in[3 * D + lane], v1 = att_in[3 * D + lane + 64];
+                const uint32_t b0 = f32_to_bf16_bits(v0), b1 = f32_to_bf16_bits(v1);
+                kv_cur[D + lane] = bf16_bits_to_f32(b0);
+                kv_cur[D + lane + 64] = bf16_bits_to_f32(b1);
+                a.vc[cur + lane] = (uint16_t)b0;
+                a.vc[cur + lane + 64] = (uint16_t)b1;
+                if (l == last && a.dbg_v) { a.dbg_v[h * D + lane] = v0; a.dbg_v[h * D + lane + 64] = v1; }
+            }
+            __syncthreads();
+
+            // scores: a quad of lanes per position, each lane a quarter of the head dim
+            const int n = a.cache_len;
+            {
+                const int qd = tid & 3;
+                float qa[32], qb[32];
+#pragma unroll
+                for (int i = 0; i < 32; ++i) { qa[i] = qrot[qd * 32 + i]; qb[i] = qrot[D + qd * 32 + i]; }
+                for (int j0 = 0; j0 < n; j0 += kThreads / 4) {
+                    const int j = j0 + (tid >> 2);
+                    float d0 = 0.0f, d1 = 0.0f;
+                    if (j < n) {
+                        if (j == a.pos) {
+#pragma unroll
+                            for (int i = 0; i < 32; ++i) {
+                                const float kk = kv_cur[qd * 32 + i];
+                                d0 = fmaf(qa[i], kk, d0);
+                                d1 = fmaf(qb[i], kk, d1);
+                            }
+                        } else {
+                            const uint4* kp = reinterpret_cast<const uint4*>(a.kc + cache_base + (int64_t)j * D + qd * 32);
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) {
+                                const uint4 kw = kp[u];
+                                const uint32_t wv[4] = {kw.x, kw.y, kw.z, kw.w};
+#pragma unroll
+                                for (int e = 0; e < 4; ++e) {
+                                    const float klo = __uint_as_float(wv[e] << 16);
+                                    const float khi = __uint_as_float(wv[e] & 0xffff0000u);
+                                    d0 = fmaf(qa[u * 8 + 2 * e], klo, d0);
+                                    d0 = fmaf(qa[u * 8 + 2 * e + 1], khi, d0);
+                                    d1 = fmaf(qb[u * 8 + 2 * e], klo, d1);
+                                    d1 = fmaf(qb[u * 8 + 2 * e + 1], khi, d1);
+                                }
+                            }
+                        }
+                    }
+                    d0 += partner<1>(d0); d0 += partner<2>(d0);
+                    d1 += partner<1>(d1); d1 += partner<2>(d1);
+                    if (j < n && qd == 0) {
+                        scores[j] = d0 * a.attn_scale;
+                        scores[kMaxAttnLen + j] = d1 * a.attn_scale;
+                    }
+                }
+            }
+            __syncthreads();
+            // softmax statistics over the n positions, both heads
+            float m0 = -INFINITY, m1 = -INFINITY;
+            for (int j = tid; j < n; j += kThreads) { m0 = fmaxf(m0, scores[j]); m1 = fmaxf(m1, scores[kMaxAttnLen + j]); }
+            m0 = wave_max(m0);
+            m1 = wave_max(m1);
+            if (lane == 0) { red[wave] = m0; red[kWaves + wave] = m1; }
+            __syncthreads();
+            float M0 = red[0], M1 = red[kWaves];
+#pragma unroll
+            for (int i = 1; i < kWaves; ++i) { M0 = fmaxf(M0, red[i]); M1 = fmaxf(M1, red[kWaves + i]); }
+            float l0 = 0.0f, l1 = 0.0f;
+            for (int j = tid; j < n; j += kThreads) {
+                const float p0 = expf(scores[j] - M0), p1 = expf(scores[kMaxAttnLen + j] - M1);
+                scores[j] = p0;
+                scores[kMaxAttnLen + j] = p1;
+                l0 += p0;
+                l1 += p1;
+            }
+            l0 = wave_sum(l0);
+            l1 = wave_sum(l1);
+            __syncthreads();
+            if (lane == 0) { red[wave] = l0; red[kWaves + wave] = l1; }
+            __syncthreads();
+            float L0 = 0.0f, L1 = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kWaves; ++i) { L0 += red[i]; L1 += red[kWaves + i]; }
+
+            // P @ V: lane owns a pair of dims, the 8 waves split the positions
+            {
+                const int dp = lane;
+                float a00 = 0.0f, a01 = 0.0f, a10 = 0.0f, a11 = 0.0f;
+                for (int j = wave; j < n; j += kWaves) {
+                    float v0, v1;
+                    if (j == a.pos) { v0 = kv_cur[D + 2 * dp]; v1 = kv_cur[D + 2 * dp + 1]; }
+                    else {
+                        const uint32_t vw = *reinterpret_cast<const uint32_t*>(a.vc + cache_base + (int64_t)j * D + 2 * dp);
+                        v0 = __uint_as_float(vw << 16);
+                        v1 = __uint_as_float(vw & 0xffff0000u);
+                    }
+                    const float p0 = scores[j], p1 = scores[kMaxAttnLen + j];
+                    a00 = fmaf(p0, v0, a00); a01 = fmaf(p0, v1, a01);
+                    a10 = fmaf(p1, v0, a10); a11 = fmaf(p1, v1, a11);
+                }
+                pv[wave * 2 * D + 2 * dp] = a00;
+                pv[wave * 2 * D + 2 * dp + 1] = a01;
+                pv[wave * 2 * D + D + 2 * dp] = a10;
+                pv[wave * 2 * D + D + 2 * dp + 1] = a11;
+            }
+            __syncthreads();
+            if (tid < 2 * D) {
+                float o = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) o += pv[w * 2 * D + tid];
+                o = o / (tid < D ? L0 : L1);
+                const int word = 2 * h * D + tid;
+                ll_put(&a.att_x[word], __float_as_uint(o), tag(l, ST_ATTN));
+                if (l == last && a.dbg_attn) a.dbg_attn[word] = o;
+            }
+        }
+
+        // ---------------- O projection + residual ----------------
+        {
+            const int row0 = g * ROWS_H;
+            const uint8_t* base = (const uint8_t*)lw.o_proj_weight;
+            Stage_<W, ROWS_H, QD> st;
+            st.load([&](int r) { return base + (int64_t)(row0 + r) * QD * ES; }, wave, lane);
+#pragma unroll
+            for (int i = 0; i < QD / kThreads; ++i) {
+                const int k = tid + i * kThreads;
+                xsf[xs_index<W>(k)] = wt.getf(&a.att_x[k], tag(l, ST_ATTN));
+            }
+            __syncthreads();
+            st.compute(xs, part, wave, lane);
+            __syncthreads();
+            if (tid < ROWS_H) {
+                float v = Stage_<W, ROWS_H, QD>::row_sum(part, tid);
+                if (kInt8) v = v * sp->o_scale[row0 + tid];
+                v = v + rows_res[tid];
+                ll_put(&a.act_x[row0 + tid], __float_as_uint(v), tag(l, ST_O));
+            }
+        }
+
+        // ---------------- RMSNorm + gate/up + SwiGLU ----------------
+        {
+            const int c0 = g * CPW;
+            const uint8_t* gb = (const uint8_t*)lw.gate_proj_weight;
+            const uint8_t* ub = (const uint8_t*)lw.up_proj_weight;
+            Stage_<W, 2 * CPW, H> st;
+            st.load([&](int r) {
+                return r < CPW ? gb + (int64_t)(c0 + r) * H * ES : ub + (int64_t)(c0 + r - CPW) * H * ES;
+            }, wave, lane);
+            constexpr int PT = H / kThreads;
+            float av[PT];
+            float ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                const int k = tid + i * kThreads;
+                av[i] = wt.getf(&a.act_x[k], tag(l, ST_O));
+                ss += av[i] * av[i];
+            }
+            const float tot = block_sum<kWaves>(ss, red, wave, lane);
+            const float rstd = rsqrtf(tot / (float)H + kEps);
+            const uint16_t* pnw = (const uint16_t*)lw.post_attn_layernorm_weight;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                const int k = tid + i * kThreads;
+                const float nv = av[i] * rstd * bf16_bits_to_f32(pnw[k]);
+                xsf[xs_index<W>(k)] = nv;
+                const int rr = k - g * ROWS_H;
+                if (rr >= 0 && rr < ROWS_H) rows_res[rr] = av[i];
+                if (l == last && g == 0) {
+                    if (a.dbg_act) a.dbg_act[k] = nv;
+                    if (a.dbg_resid) a.dbg_resid[k] = av[i];
+                }
+            }
+            __syncthreads();
+            st.compute(xs, part, wave, lane);
+            __syncthreads();
+            if (tid < CPW) {
+                float gs = Stage_<W, 2 * CPW, H>::row_sum(part, tid);
+                float us = Stage_<W, 2 * CPW, H>::row_sum(part, CPW + tid);
+                if (kInt8) { gs = gs * sp->gate_scale[c0 + tid]; us = us * sp->up_scale[c0 + tid]; }
+                const float m = gs / (1.0f + expf(-gs)) * us;
+                ll_put(&a.mlp_x[c0 + tid], __float_as_uint(m), tag(l, ST_GU));
+                if (l == last && a.dbg_mlp) a.dbg_mlp[c0 + tid] = m;
+            }
+        }
+
+        // ---------------- down projection + residual -> bf16 hidden ----------------
+        {
+            const int row0 = g * ROWS_H;
+            const uint8_t* base = (const uint8_t*)lw.down_proj_weight;
+            Stage_<W, ROWS_H, I> st;
+            st.load([&](int r) { return base + (int64_t)(row0 + r) * I * ES; }, wave, lane);
+#pragma unroll
+            for (int i = 0; i < I / kThreads; ++i) {
+                const int k = tid + i * kThreads;
+                xsf[xs_index<W>(k)] = wt.getf(&a.mlp_x[k], tag(l, ST_GU));
+            }
+            __syncthreads();
+            st.compute(xs, part, wave, lane);
+            __syncthreads();
+            if (tid < ROWS_H) {
+                float v = Stage_<W, ROWS_H, I>::row_sum(part, tid);
+                if (kInt8) v = v * sp->down_scale[row0 + tid];
+                v = v + rows_res[tid];
+                const uint32_t hb = f32_to_bf16_bits(v);
+                ll_put(&a.hid_x[row0 + tid], __float_as_uint(bf16_bits_to_f32(hb)), tag(l, ST_DOWN));
+                if (l == last && a.dbg_hidden) a.dbg_hidden[row0 + tid] = (uint16_t)hb;
+            }
+        }
+    }
+
+    // ---------------- final RMSNorm ----------------
+    {
+        constexpr int PT = H / kThreads;
+        float hv[PT];
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            hv[i] = wt.getf(&a.hid_x[tid + i * kThreads], tag(last, ST_DOWN));
+            ss += hv[i] * hv[i];
+        }
+        const float tot = block_sum<kWaves>(ss, red, wave, lane);
+        const float rstd = rsqrtf(tot / (float)H + kEps);
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const int k = tid + i * kThreads;
+            const float nv = hv[i] * rstd * bf16_bits_to_f32(a.final_norm[k]);
+            xsf[xs_index<W>(k)] = nv;
+            if (g == 0 && a.dbg_norm) a.dbg_norm[k] = nv;
+        }
+        __syncthreads();
+    }
+
+    // ---------------- LM head + greedy argmax ----------------
+    {
+        constexpr int CH = H / (64 * W::kPerLane);
+        constexpr int RB = CH >= 8 ? 1 : 8 / CH;          // rows per wave batch
+        constexpr int R = RB * CH;                         // 1 KB items per batch
+        constexpr int span = kWave / RB;
+        const int r0 = (int)((int64_t)a.V * g / kNWG);
+        const int r1 = (int)((int64_t)a.V * (g + 1) / kNWG);
+        const int nb = (r1 - r0 + RB - 1) / RB;
+        const int64_t rowbytes = (int64_t)H * ES;
+        float best_v = -INFINITY;
+        int best_i = 0x7fffffff;
+
+        uint4 cur[R], nxt[R];
+        float scur = 0.0f, snxt = 0.0f;
+        auto fetch = [&](int b, uint4* dst, float& s) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int row = r0 + b * RB + i / CH;
+                dst[i] = make_uint4(0, 0, 0, 0);
+                if (row < r1) dst[i] = *reinterpret_cast<const uint4*>(a.lm_w + row * rowbytes + (i % CH) * 1024 + lane * 16);
+            }
+            const int myrow = r0 + b * RB + lane / span;
+            s = 1.0f;
+            if (kInt8 && myrow < r1) s = a.lm_s[myrow];
+        };
+        int b = wave;
+        if (b < nb) fetch(b, cur, scur);
+        for (; b < nb; b += kWaves) {
+            if (b + kWaves < nb) fetch(b + kWaves, nxt, snxt);
+            float acc[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) acc[i] = dot_frag<W>(cur[i], xs_frag<W>(xs, i % CH, lane), 0.0f);
+            const float s = transpose_reduce<R, CH>(acc, lane);
+            const int row = r0 + b * RB + lane / span;
+            if ((lane % span) == 0 && row < r1) {
+                const float v = kInt8 ? s * scur : s;
+                if (v > best_v) { best_v = v; best_i = row; }
+            }
+#pragma unroll
+            for (int i = 0; i < R; ++i) cur[i] = nxt[i];
+            scur = snxt;
+        }
+        // wave argmax, ties to the lower index
+#define MQ_ARGMAX_LEVEL(M)                                                                   \
+        {                                                                                    \
+            const float ov = partner<M>(best_v);                                             \
+            const int oi = __float_as_int(partner<M>(__int_as_float(best_i)));               \
+            if (ov > best_v || (ov == best_v && oi < best_i)) { best_v = ov; best_i = oi; }  \
+        }
+        MQ_ARGMAX_LEVEL(1) MQ_ARGMAX_LEVEL(2) MQ_ARGMAX_LEVEL(4) MQ_ARGMAX_LEVEL(8)
+        MQ_ARGMAX_LEVEL(16) MQ_ARGMAX_LEVEL(32)
+#undef MQ_ARGMAX_LEVEL
+        if (lane == 0) { lm_best_v[wave] = best_v; lm_best_i[wave] = best_i; }
+        __syncthreads();
+        if (tid == 0) {
+            float bv = lm_best_v[0];
+            int bi = lm_best_i[0];
+            for (int w = 1; w < kWaves; ++w) {
+                if (lm_best_v[w] > bv || (lm_best_v[w] == bv && lm_best_i[w] < bi)) { bv = lm_best_v[w]; bi = lm_best_i[w]; }
+            }
+            if (a.dbg_bmax) a.dbg_bmax[g] = bv;
+            if (a.dbg_bidx) a.dbg_bidx[g] = bi;
+            const uint64_t key = ((uint64_t)ordered_key(bv) << 32) | (uint64_t)(~(uint32_t)bi);
+            const int slot = E & 1;
+            __hip_atomic_fetch_max(&hdr->best[slot], key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t prev = __hip_atomic_fetch_add(&hdr->done[slot], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            if (prev == gridDim.x - 1) {
+                const uint64_t k = __hip_atomic_load(&hdr->best[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const bool aborted = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+                *a.out_token = aborted ? -1 : (int)(~(uint32_t)(k & 0xffffffffu));
+                __hip_atomic_store(&hdr->epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    }
+}
+
+// ---------------- host side ----------------
+
+struct Layout {
+    size_t hid, qkv, att, act, mlp, total;
+};
+static Layout layout_of(const DecodeShape& s) {
+    Layout o;
+    size_t off = sizeof(WsHeader);
+    auto take = [&](size_t words) { size_t at = off; off += ((words * 8 + 255) / 256) * 256; return at; };
+    o.hid = take(s.H);
+    o.qkv = take((size_t)s.NQ * s.D + 2 * (size_t)s.NKV * s.D);
+    o.att = take((size_t)s.NQ * s.D);
+    o.act = take(s.H);
+    o.mlp = take(s.I);
+    o.total = off;
+    return o;
+}
+
+size_t decode_workspace_bytes(const DecodeShape& s) { return layout_of(s).total; }
+
+// All kNWG workgroups wait on each other, so they must be resident at once;
+// checked once per (kernel, device) from the occupancy calculator.
+template <int H, int I, class W>
+static int check_residency(const void* fn) {
+    static int checked[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(MQ_ERR_HIP, "hipGetDevice failed");
+    if (checked[dev]) return MQ_OK;
+    int ncu = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, 0) != hipSuccess)
+        return set_error(MQ_ERR_HIP, "occupancy query failed");
+    if ((int64_t)ncu * per_cu < kNWG)
+        return set_error(MQ_ERR_UNSUPPORTED, "device holds %d x %d resident workgroups, the decode kernel needs %d",
+                         ncu, per_cu, kNWG);
+    checked[dev] = 1;
+    return MQ_OK;
+}
+
+template <int H, int I, class W>
+static int launch_t(const KArgs& ka, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
+    auto fn = reinterpret_cast<const void*>(&decode_kernel<H, I, W>);
+    int st = check_residency<H, I, W>(fn);
+    if (st != MQ_OK) return st;
+    KArgs copy = ka;
+    void* args[] = {&copy};
+    hipError_t e;
+    if (t0 != nullptr && t1 != nullptr) {
+        e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
+        if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode): %s", hipGetErrorString(e));
+    } else {
+        e = hipLaunchCooperativeKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream);
+        if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipLaunchCooperativeKernel(decode): %s", hipGetErrorString(e));
+    }
+    return MQ_OK;
+}
+
+int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream) {
+    if (a.cache_len > kMaxAttnLen)
+        return set_error(MQ_ERR_UNSUPPORTED, "cache_len %d exceeds the single-workgroup attention limit %d",
+                         a.cache_len, kMaxAttnLen);
+    const Layout lay = layout_of(s);
+    uint8_t* ws = static_cast<uint8_t*>(a.workspace);
+    KArgs k;
+    k.token = a.input_token_id;
+    k.out_token = a.output_token_id;
+    k.embed = static_cast<const uint16_t*>(a.embed_weight);
+    k.lw = a.layer_weights;
+    k.sp = a.scales;
+    k.final_norm = static_cast<const uint16_t*>(a.final_norm_weight);
+    k.lm_w = static_cast<const uint8_t*>(a.lm_head_weight);
+    k.lm_s = a.lm_head_scale;
+    k.cos_t = static_cast<const uint16_t*>(a.cos_table);
+    k.sin_t = static_cast<const uint16_t*>(a.sin_table);
+    k.kc = static_cast<uint16_t*>(a.k_cache);
+    k.vc = static_cast<uint16_t*>(a.v_cache);
+    k.dbg_hidden = static_cast<uint16_t*>(a.hidden_buffer);
+    k.dbg_act = static_cast<float*>(a.g_activations);
+    k.dbg_resid = static_cast<float*>(a.g_residual);
+    k.dbg_q = static_cast<float*>(a.g_q);
+    k.dbg_k = static_cast<float*>(a.g_k);
+    k.dbg_v = static_cast<float*>(a.g_v);
+    k.dbg_attn = static_cast<float*>(a.g_attn_out);
+    k.dbg_mlp = static_cast<float*>(a.g_mlp_intermediate);
+    k.dbg_norm = static_cast<float*>(a.g_normalized);
+    k.dbg_bmax = static_cast<float*>(a.block_max_vals);
+    k.dbg_bidx = static_cast<int*>(a.block_max_idxs);
+    k.L = a.num_layers;
+    k.pos = a.position;
+    k.cache_len = a.cache_len;
+    k.S = a.max_seq_len;
+    k.V = s.V;
+    k.attn_scale = a.attn_scale;
+    k.spin_limit = a.spin_limit ? a.spin_limit : (1u << 21);
+    k.hdr = reinterpret_cast<WsHeader*>(ws);
+    k.hid_x = reinterpret_cast<uint64_t*>(ws + lay.hid);
+    k.qkv_x = reinterpret_cast<uint64_t*>(ws + lay.qkv);
+    k.att_x = reinterpret_cast<uint64_t*>(ws + lay.att);
+    k.act_x = reinterpret_cast<uint64_t*>(ws + lay.act);
+    k.mlp_x = reinterpret_cast<uint64_t*>(ws + lay.mlp);
+
+    hipEvent_t t0 = static_cast<hipEvent_t>(a.timing_start), t1 = static_cast<hipEvent_t>(a.timing_stop);
+    if (s.H == 1024 && s.I == 3072) {
+        return int8 ? launch_t<1024, 3072, Int8W>(k, stream, t0, t1) : launch_t<1024, 3072, Bf16W>(k, stream, t0, t1);
+    }
+    if (s.H == 2048 && s.I == 6144 && int8) return launch_t<2048, 6144, Int8W>(k, stream, t0, t1);
+    return set_error(MQ_ERR_UNSUPPORTED, "no decode kernel compiled for H=%d I=%d (%s)", s.H, s.I,
+                     int8 ? "int8" : "bf16");
+}
+
+}  // namespace mq

@@ -1,0 +1,39 @@
+// Host-side declarations shared between the kernel translation units and the
+// C-ABI layer (api.hip). Not part of the public interface.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/megaqwen_a10.h"
+
+namespace mq {
+
+// Records a message for mq_last_error() and returns `status`.
+int set_error(int status, const char* fmt, ...);
+// MQ_OK, or MQ_ERR_HIP with the pending launch error recorded.
+int check_launch(const char* what);
+
+int launch_quantize(const void* w_bf16, int M, int K, int8_t* q, float* scale, hipStream_t stream);
+int launch_int8_gemv(const float* x, const int8_t* w, const float* scale, float* y, int M, int K,
+                     hipStream_t stream);
+
+// Workspace header at the start of every decode workspace (256 bytes).
+struct WsHeader {
+    uint32_t epoch;        // step counter; tags are derived from it (starts at 1)
+    uint32_t abort_flag;   // set by a kernel whose bounded wait expired
+    uint32_t done[2];      // workgroups finished with the LM head, per step parity
+    uint64_t best[2];      // packed (ordered logit, ~token) maximum, per step parity
+    uint32_t pad[56];
+};
+static_assert(sizeof(WsHeader) == 256, "workspace header is 256 bytes");
+
+struct DecodeShape {
+    int H, I, NQ, NKV, D, V;
+};
+
+size_t decode_workspace_bytes(const DecodeShape& s);
+// Launches one decode step; `int8` selects the weight format.
+int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream);
+
+}  // namespace mq

@@ -1,0 +1,364 @@
+"""Drop-in decoder classes for the batch-1 decode path.
+
+* ``A10Int8MegakernelDecoder`` — the INT8 class of bench_int8.py:119-255
+  (same constructor arguments, ``decode_step`` / ``reset`` / ``position``).
+* ``A10MegakernelDecoder`` — the bf16 class of a10_decode.py:87-261, with the
+  debug getters of run_benchmark.py:174-183.
+* ``A10Decoder`` — the Python wrapper of a10_decode.py:35-393 (``.decoder``,
+  ``reset``, ``generate``), which here loads weights from a safetensors
+  checkpoint directory or builds seeded random-init weights.
+
+Each step is ONE launch of the persistent gfx950 kernel (csrc/decode.hip)
+through the C ABI; the returned token is read back like the reference's
+``output_token_.item<int>()`` (bench_int8.py:218). Arguments are validated on
+the host before anything is launched (the reference launches unchecked):
+wrong dtypes/shapes/devices/counts raise ``TypeError``/``ValueError``, a token
+id outside the vocabulary or a full KV cache raise ``ValueError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import time
+from pathlib import Path
+
+import torch
+
+from . import _lib
+from .config import QWEN3_0_6B, ModelConfig
+from .rope import precompute_rope_freqs
+from .weights import pack_bf16, pack_int8, quantize_state, random_init_state
+
+LM_PARTIALS = 256   # per-workgroup LM-head maxima written to block_max_vals/idxs
+
+
+def _check_tensor(t, name, dtype, shape=None, device=None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected dtype {dtype}, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name}: must live on a HIP device")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name}: on {t.device}, expected {device}")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+
+
+def _device_array(structs, device) -> torch.Tensor:
+    raw = bytes(structs)
+    host = torch.frombuffer(bytearray(raw), dtype=torch.uint8)
+    return host.to(device)
+
+
+class _DecoderBase:
+    """Owns the KV cache, the reference's scratch buffers, the workspace and the step state."""
+
+    _int8: bool = True
+
+    def _setup(self, embed, layer_tensors, final_norm, lm_head, cos_table, sin_table, num_layers,
+               max_seq_len, layer_scales=None, lm_head_scale=None):
+        if not isinstance(num_layers, int) or num_layers < 1:
+            raise ValueError(f"num_layers must be a positive int, got {num_layers!r}")
+        if not isinstance(max_seq_len, int) or max_seq_len < 1:
+            raise ValueError(f"max_seq_len must be a positive int, got {max_seq_len!r}")
+        _check_tensor(embed, "embed_weight", torch.bfloat16)
+        if embed.dim() != 2:
+            raise ValueError("embed_weight must be [vocab, hidden]")
+        dev = embed.device
+        V, H = embed.shape
+        if len(layer_tensors) != 11 * num_layers:
+            raise ValueError(f"layer_weights_flat: expected {11 * num_layers} tensors (11 per layer), "
+                             f"got {len(layer_tensors)}")
+        wdt = torch.int8 if self._int8 else torch.bfloat16
+        I = layer_tensors[8].shape[0]
+        D = 128
+        Q, KV = 16 * D, 8 * D
+        shapes = [(H,), (Q, H), (KV, H), (KV, H), (D,), (D,), (H, Q), (H,), (I, H), (I, H), (H, I)]
+        dtypes = [torch.bfloat16, wdt, wdt, wdt, torch.bfloat16, torch.bfloat16, wdt, torch.bfloat16,
+                  wdt, wdt, wdt]
+        for i, t in enumerate(layer_tensors):
+            _check_tensor(t, f"layer_weights_flat[{i}]", dtypes[i % 11], shapes[i % 11], dev)
+        if self._int8:
+            if layer_scales is None or len(layer_scales) != 7 * num_layers:
+                raise ValueError(f"layer_scales_all: expected {7 * num_layers} tensors (7 per layer)")
+            sshapes = [(Q,), (KV,), (KV,), (H,), (I,), (I,), (H,)]
+            for i, t in enumerate(layer_scales):
+                _check_tensor(t, f"layer_scales_all[{i}]", torch.float32, sshapes[i % 7], dev)
+            _check_tensor(lm_head_scale, "lm_head_scale", torch.float32, (V,), dev)
+        _check_tensor(lm_head, "lm_head", wdt, (V, H), dev)
+        _check_tensor(final_norm, "final_norm_weight", torch.bfloat16, (H,), dev)
+        _check_tensor(cos_table, "cos_table", torch.bfloat16, None, dev)
+        _check_tensor(sin_table, "sin_table", torch.bfloat16, None, dev)
+        if cos_table.dim() != 2 or cos_table.shape[1] != D or cos_table.shape[0] < max_seq_len:
+            raise ValueError(f"cos_table must be [>= max_seq_len, {D}], got {tuple(cos_table.shape)}")
+        if tuple(sin_table.shape) != tuple(cos_table.shape):
+            raise ValueError("sin_table must match cos_table")
+
+        self.device = dev
+        self.num_layers = num_layers
+        self.max_seq_len = max_seq_len
+        self.dims = (H, I, V)
+        self._pos = 0
+        self.attn_scale = 1.0 / math.sqrt(float(D))
+        # hold every tensor the kernel reads (the reference's INT8 class drops the scale list)
+        self.embed_weight = embed
+        self.layer_tensors = list(layer_tensors)
+        self.layer_scales = list(layer_scales) if layer_scales is not None else None
+        self.final_norm_weight = final_norm
+        self.lm_head_weight = lm_head
+        self.lm_head_scale = lm_head_scale
+        self.cos_table, self.sin_table = cos_table, sin_table
+
+        lw = (_lib.LayerWeights * num_layers)()
+        for l in range(num_layers):
+            for f, t in zip(_lib.LAYER_FIELDS, layer_tensors[11 * l: 11 * l + 11]):
+                setattr(lw[l], f, t.data_ptr())
+        self.d_layer_weights = _device_array(lw, dev)
+        self.d_layer_scales = None
+        if self._int8:
+            sp = (_lib.ScalePointers * num_layers)()
+            for l in range(num_layers):
+                for f, t in zip(_lib.SCALE_FIELDS, layer_scales[7 * l: 7 * l + 7]):
+                    setattr(sp[l], f, t.data_ptr())
+            self.d_layer_scales = _device_array(sp, dev)
+
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.k_cache = torch.zeros((num_layers, 8, max_seq_len, D), dtype=torch.bfloat16, device=dev)
+        self.v_cache = torch.zeros_like(self.k_cache)
+        self.hidden_buffer = torch.zeros(H, dtype=torch.bfloat16, device=dev)
+        self.g_activations = torch.zeros(H, **f32)
+        self.g_residual = torch.zeros(H, **f32)
+        self.g_q = torch.zeros(Q, **f32)
+        self.g_k = torch.zeros(KV, **f32)
+        self.g_v = torch.zeros(KV, **f32)
+        self.g_attn_out = torch.zeros(Q, **f32)
+        self.g_mlp_intermediate = torch.zeros(I, **f32)
+        self.g_normalized = torch.zeros(H, **f32)
+        self.block_max_vals = torch.zeros(LM_PARTIALS, **f32)
+        self.block_max_idxs = torch.zeros(LM_PARTIALS, dtype=torch.int32, device=dev)
+        self.output_token = torch.zeros(1, dtype=torch.int32, device=dev)
+
+        self._lib = _lib.load()
+        self._dims = _lib.ModelDims(H, I, 16, 8, D, V)
+        ws_bytes = self._lib.mq_decode_workspace_bytes(ctypes.byref(self._dims))
+        if ws_bytes == 0:
+            raise ValueError(f"unsupported model dims H={H} I={I}: {_lib.last_error()}")
+        self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        self._stream = None
+        self._init_workspace()
+
+        a = _lib.DecodeArgs()
+        a.output_token_id = self.output_token.data_ptr()
+        a.embed_weight = embed.data_ptr()
+        a.layer_weights = self.d_layer_weights.data_ptr()
+        a.scales = self.d_layer_scales.data_ptr() if self._int8 else None
+        a.final_norm_weight = final_norm.data_ptr()
+        a.lm_head_weight = lm_head.data_ptr()
+        a.lm_head_scale = lm_head_scale.data_ptr() if self._int8 else None
+        a.cos_table, a.sin_table = cos_table.data_ptr(), sin_table.data_ptr()
+        a.k_cache, a.v_cache = self.k_cache.data_ptr(), self.v_cache.data_ptr()
+        a.hidden_buffer = self.hidden_buffer.data_ptr()
+        a.g_activations = self.g_activations.data_ptr()
+        a.g_residual = self.g_residual.data_ptr()
+        a.g_q, a.g_k, a.g_v = self.g_q.data_ptr(), self.g_k.data_ptr(), self.g_v.data_ptr()
+        a.g_attn_out = self.g_attn_out.data_ptr()
+        a.g_mlp_intermediate = self.g_mlp_intermediate.data_ptr()
+        a.g_normalized = self.g_normalized.data_ptr()
+        a.block_max_vals = self.block_max_vals.data_ptr()
+        a.block_max_idxs = self.block_max_idxs.data_ptr()
+        a.num_layers = num_layers
+        a.max_seq_len = max_seq_len
+        a.attn_scale = self.attn_scale
+        a.dims = ctypes.addressof(self._dims)
+        a.workspace = self.workspace.data_ptr()
+        a.workspace_bytes = ws_bytes
+        a.spin_limit = 0
+        self._args = a
+        self._step_fn = self._lib.mq_int8_decode_step if self._int8 else self._lib.mq_bf16_decode_step
+
+    def _init_workspace(self):
+        with torch.cuda.device(self.device):
+            _lib.check(self._lib.mq_workspace_init(self.workspace.data_ptr(), self.workspace.numel(),
+                                                   _lib.stream_handle()), "mq_workspace_init")
+
+    # -- reference surface ---------------------------------------------------------------
+    def launch_step(self, input_token_id: int) -> None:
+        """Enqueue one decode step on the current stream without waiting for the token."""
+        V = self.dims[2]
+        if not isinstance(input_token_id, int) or not 0 <= input_token_id < V:
+            raise ValueError(f"input_token_id {input_token_id!r} outside [0, {V})")
+        if self._pos >= self.max_seq_len:
+            raise ValueError(f"KV cache full: position {self._pos} == max_seq_len {self.max_seq_len}")
+        a = self._args
+        a.input_token_id = input_token_id
+        a.position = self._pos
+        a.cache_len = self._pos + 1
+        st = self._step_fn(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(self.device)))
+        _lib.check(st, "decode step")
+        self._pos += 1
+
+    def decode_step(self, input_token_id: int) -> int:
+        self.launch_step(input_token_id)
+        tok = int(self.output_token.item())
+        if tok < 0:
+            status = self._lib.mq_decode_check(self.workspace.data_ptr(),
+                                               ctypes.c_void_p(_lib.stream_handle(self.device)))
+            self._init_workspace()
+            _lib.check(status if status != _lib.MQ_OK else _lib.MQ_ERR_TIMEOUT, "decode step")
+        return tok
+
+    def reset(self) -> None:
+        self._pos = 0
+        self.k_cache.zero_()
+        self.v_cache.zero_()
+
+    def position(self) -> int:
+        return self._pos
+
+    def set_timing_events(self, start=None, stop=None) -> None:
+        """Have every following step record ``start``/``stop`` (torch.cuda.Event with
+        timing) at the kernel's own start and end; ``None`` turns it off."""
+        if start is None or stop is None:
+            self._args.timing_start = None
+            self._args.timing_stop = None
+            return
+        for e in (start, stop):
+            if e.cuda_event == 0:
+                e.record()          # torch creates the HIP event lazily
+        self._args.timing_start = start.cuda_event
+        self._args.timing_stop = stop.cuda_event
+
+    def set_spin_limit(self, polls: int) -> None:
+        """Bound on every in-kernel wait (0 = library default)."""
+        self._args.spin_limit = int(polls)
+
+    # debug getters (run_benchmark.py:174-183): the last layer's values after a step
+    def get_hidden(self): return self.hidden_buffer
+    def get_activations(self): return self.g_activations
+    def get_residual(self): return self.g_residual
+    def get_q(self): return self.g_q
+    def get_k(self): return self.g_k
+    def get_v(self): return self.g_v
+    def get_attn_out(self): return self.g_attn_out
+    def get_mlp_int(self): return self.g_mlp_intermediate
+    def get_normalized(self): return self.g_normalized
+
+
+class A10Int8MegakernelDecoder(_DecoderBase):
+    """bench_int8.py:121-130 constructor: (embed_weight, layer_weights_flat,
+    layer_scales_all, lm_head_int8, lm_head_scale, final_norm_weight,
+    cos_table, sin_table, num_layers, max_seq_len)."""
+
+    _int8 = True
+
+    def __init__(self, embed_weight, layer_weights_flat, layer_scales_all, lm_head_int8, lm_head_scale,
+                 final_norm_weight, cos_table, sin_table, num_layers, max_seq_len):
+        self._setup(embed_weight, layer_weights_flat, final_norm_weight, lm_head_int8, cos_table, sin_table,
+                    num_layers, max_seq_len, layer_scales=layer_scales_all, lm_head_scale=lm_head_scale)
+
+
+class A10MegakernelDecoder(_DecoderBase):
+    """a10_decode.py:89-98 constructor: (embed_weight, layer_weights_flat,
+    final_norm_weight, lm_head_weight, cos_table, sin_table, num_layers, max_seq_len)."""
+
+    _int8 = False
+
+    def __init__(self, embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight, cos_table,
+                 sin_table, num_layers, max_seq_len):
+        self._setup(embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight, cos_table, sin_table,
+                    num_layers, max_seq_len)
+
+
+def load_checkpoint_state(model_path, cfg: ModelConfig) -> dict:
+    """bf16 state dict from a local HF safetensors checkpoint directory (no network)."""
+    from safetensors.torch import load_file
+    path = Path(model_path)
+    files = sorted(path.glob("*.safetensors"))
+    if not files:
+        raise FileNotFoundError(f"no *.safetensors under {path}")
+    state = {}
+    for f in files:
+        state.update({k: v.to(torch.bfloat16) for k, v in load_file(str(f)).items()})
+    if "lm_head.weight" not in state:
+        state["lm_head.weight"] = state["model.embed_tokens.weight"]
+    for i in range(cfg.num_layers):
+        p = f"model.layers.{i}.self_attn"
+        state.setdefault(f"{p}.q_norm.weight", torch.ones(cfg.head_dim, dtype=torch.bfloat16))
+        state.setdefault(f"{p}.k_norm.weight", torch.ones(cfg.head_dim, dtype=torch.bfloat16))
+    return state
+
+
+class A10Decoder:
+    """a10_decode.py:35-393. ``A10Decoder(model_path, max_seq_len)`` loads a
+    local checkpoint; ``A10Decoder(seed=0)`` (or a missing ``model_path``)
+    builds seeded random-init weights of ``config``. ``int8=True`` quantizes
+    every linear and the LM head (bench_int8.py:27-55) and drives
+    ``A10Int8MegakernelDecoder``; otherwise the bf16 ``A10MegakernelDecoder``."""
+
+    def __init__(self, model_path=None, max_seq_len: int = 2048, *, seed: int | None = None,
+                 config: ModelConfig = QWEN3_0_6B, int8: bool = False, device="cuda"):
+        self.max_seq_len = max_seq_len
+        self.device = torch.device(device)
+        self.config = config
+        self.tokenizer = None
+        if model_path is not None and Path(model_path).exists():
+            state = load_checkpoint_state(model_path, config)
+            try:
+                from transformers import AutoTokenizer
+                self.tokenizer = AutoTokenizer.from_pretrained(str(model_path), local_files_only=True)
+            except Exception:
+                self.tokenizer = None
+        else:
+            if model_path is not None and seed is None:
+                raise FileNotFoundError(f"checkpoint {model_path} not found (pass seed= for random weights)")
+            state, _ = random_init_state(config, seed=0 if seed is None else seed)
+        self.cos_table, self.sin_table = precompute_rope_freqs(config.head_dim, max_seq_len, config.rope_theta,
+                                                               device=self.device)
+        if int8:
+            qstate = quantize_state(state, config, self.device)
+            embed, layers, scales, lm_q, lm_s, fnorm = pack_int8(qstate, config)
+            self._keep = (embed, layers, scales, lm_q, lm_s, fnorm)
+            self.decoder = A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, self.cos_table,
+                                                    self.sin_table, config.num_layers, max_seq_len)
+        else:
+            embed, layers, fnorm, lm = pack_bf16(state, config, self.device)
+            self._keep = (embed, layers, fnorm, lm)
+            self.decoder = A10MegakernelDecoder(embed, layers, fnorm, lm, self.cos_table, self.sin_table,
+                                                config.num_layers, max_seq_len)
+
+    def reset(self):
+        self.decoder.reset()
+
+    def generate(self, prompt, max_new_tokens: int = 128, temperature: float = 0.0):
+        """Greedy generation. ``prompt`` is a string (needs a tokenizer) or a list of ids.
+        The prompt is prefilled one ``decode_step`` per token and the last prefill
+        output is the first generated token (verify_correctness_a10.py:323-339;
+        a10_decode.py:375 re-feeds the last prompt token instead, which decodes it
+        twice). ``temperature`` is accepted for signature compatibility; decoding is greedy.
+        Returns ``(text_or_ids, tok_per_s, per_token_ms)``."""
+        if isinstance(prompt, str):
+            if self.tokenizer is None:
+                raise ValueError("a string prompt needs a checkpoint with a tokenizer; pass token ids")
+            ids = self.tokenizer.encode(prompt)
+        else:
+            ids = [int(t) for t in prompt]
+        if not ids:
+            raise ValueError("empty prompt")
+        self.reset()
+        tok = None
+        for t in ids:
+            tok = self.decoder.decode_step(t)
+        generated = list(ids) + [tok]
+        times = []
+        eos = getattr(self.tokenizer, "eos_token_id", None)
+        while len(generated) - len(ids) < max_new_tokens and tok != eos:
+            t0 = time.perf_counter()
+            tok = self.decoder.decode_step(tok)
+            times.append((time.perf_counter() - t0) * 1e3)
+            generated.append(tok)
+        tok_s = 1e3 / (sum(times) / len(times)) if times else 0.0
+        out = self.tokenizer.decode(generated) if self.tokenizer is not None else generated
+        return out, tok_s, times

@@ -1,0 +1,219 @@
+"""GPU parity of the persistent decode kernel (run with -m gpu).
+
+Gates: greedy tokens identical to the float64 oracle's
+committed fixtures for 32 steps (INT8 Qwen3-0.6B shape, BF16 Qwen3-0.6B
+shape, a 2-layer INT8 case with non-unit norm gains), per-stage values within
+fp32-accumulation tolerance of the oracle, bitwise run-to-run determinism, the
+reference-signature C launcher agreeing with the class, and the host-forced
+failure paths (bad token, full cache, expired in-kernel wait) raising cleanly.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+
+import pytest
+import torch
+
+from oracle.ref_cpu import Dims, RefDecoder, greedy_generate
+
+from .conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+
+def _fixture(name):
+    return json.loads((GOLDEN / f"tokens_{name}.json").read_text())
+
+
+def _build(mq, dev, name):
+    d = _fixture(name)
+    cfg = mq.ModelConfig(**d["config"])
+    state, prompt = mq.random_init_state(cfg, seed=d["seed"], norm_jitter=d["norm_jitter"])
+    assert mq.state_digest(state) == d["weights_sha256"]
+    S = d["max_seq_len"]
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    if d["int8"]:
+        qstate = mq.quantize_state(state, cfg, dev)
+        embed, layers, scales, lm_q, lm_s, fnorm = mq.pack_int8(qstate, cfg)
+        dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+        keep = (embed, layers, scales, lm_q, lm_s, fnorm, cos, sin)
+    else:
+        embed, layers, fnorm, lm = mq.pack_bf16(state, cfg, dev)
+        dec = mq.A10MegakernelDecoder(embed, layers, fnorm, lm, cos, sin, cfg.num_layers, S)
+        keep = (embed, layers, fnorm, lm, cos, sin)
+    return dec, d, prompt.tolist(), cfg, keep
+
+
+def _greedy(dec, prompt, n):
+    dec.reset()
+    tok = None
+    for t in prompt:
+        tok = dec.decode_step(int(t))
+    out = [tok]
+    while len(out) < n:
+        tok = dec.decode_step(tok)
+        out.append(tok)
+    return out
+
+
+@pytest.fixture(scope="module")
+def small(mq, dev):
+    return _build(mq, dev, "small_int8")
+
+
+def _ref_for(small_case):
+    dec, d, prompt, cfg, keep = small_case
+    embed, layers, scales, lm_q, lm_s, fnorm, cos, sin = keep
+    c = lambda t: t.cpu()
+    return RefDecoder(Dims(vocab_size=cfg.vocab_size), c(embed), [c(t) for t in layers], [c(t) for t in scales],
+                      c(fnorm), c(lm_q), c(lm_s), c(cos), c(sin), cfg.num_layers, d["max_seq_len"])
+
+
+def test_small_int8_tokens_match_fixture(small):
+    dec, d, prompt, cfg, _ = small
+    print("small_int8 32 greedy steps", flush=True)
+    assert _greedy(dec, prompt, 32) == d["tokens"]
+
+
+def test_small_int8_stages_match_oracle(small):
+    """Per-stage values of the last layer (the reference's debug getters) after several steps."""
+    dec, d, prompt, cfg, _ = small
+    ref = _ref_for(small)
+    dec.reset()
+    ref.reset()
+    for t in prompt[:5]:
+        got_tok = dec.decode_step(int(t))
+        ref_logits = ref.step_logits(int(t))
+        assert got_tok == int(torch.argmax(ref_logits))
+    last = ref.last
+
+    def rel(name, t):
+        a = t.detach().cpu().double()
+        b = last[name].double()
+        return float(torch.linalg.norm(a - b) / torch.linalg.norm(b))
+
+    checks = {"q": dec.get_q(), "k": dec.get_k(), "v": dec.get_v(), "attn_out": dec.get_attn_out(),
+              "residual": dec.get_residual(), "activations": dec.get_activations(),
+              "mlp_intermediate": dec.get_mlp_int(), "normalized": dec.get_normalized()}
+    for name, t in checks.items():
+        e = rel(name, t)
+        print(f"stage {name}: rel L2 {e:.2e}")
+        assert e < 1e-4, (name, e)
+    h = dec.get_hidden().cpu().float().double()
+    diff = (h - last["hidden"]).abs()
+    ulp = last["hidden"].abs() * 2.0 ** -7
+    assert torch.all(diff <= ulp + 1e-30)                 # at most one bf16 ulp apart
+    assert float((diff > 0).double().mean()) < 0.01       # and almost all bit-identical
+    # the KV cache rows written at the last position match the oracle's bf16 cache
+    p = dec.position() - 1
+    kc = dec.k_cache[:, :, p].cpu().float()
+    rk = ref.k_cache[:, :, p].float()
+    assert float((kc - rk).abs().max()) <= float(rk.abs().max()) * 2.0 ** -7
+
+
+def test_small_int8_deterministic(small):
+    dec, d, prompt, cfg, _ = small
+    runs = []
+    for _ in range(2):
+        toks = _greedy(dec, prompt, 12)
+        runs.append((toks, dec.get_q().clone(), dec.get_attn_out().clone(), dec.get_mlp_int().clone(),
+                     dec.get_hidden().clone(), dec.k_cache.clone(), dec.block_max_vals.clone()))
+    a, b = runs
+    assert a[0] == b[0]
+    for x, y in zip(a[1:], b[1:]):
+        assert torch.equal(x, y)
+
+
+def test_reset_and_position(small):
+    dec, d, prompt, cfg, _ = small
+    dec.reset()
+    assert dec.position() == 0
+    dec.decode_step(int(prompt[0]))
+    dec.decode_step(int(prompt[1]))
+    assert dec.position() == 2
+    assert dec.k_cache.abs().sum() > 0
+    dec.reset()
+    assert dec.position() == 0 and int(dec.k_cache.abs().sum()) == 0 and int(dec.v_cache.abs().sum()) == 0
+
+
+def test_invalid_inputs_raise(small):
+    dec, d, prompt, cfg, _ = small
+    dec.reset()
+    with pytest.raises(ValueError):
+        dec.decode_step(cfg.vocab_size)
+    with pytest.raises(ValueError):
+        dec.decode_step(-1)
+    for i in range(d["max_seq_len"]):
+        dec.launch_step(int(prompt[i % len(prompt)]))
+    torch.cuda.synchronize()
+    with pytest.raises(ValueError, match="full"):
+        dec.decode_step(int(prompt[0]))
+    dec.reset()
+
+
+def test_expired_wait_reports_timeout_and_recovers(mq, small):
+    """A one-poll spin limit makes every cross-workgroup wait expire: the step must end,
+    report MQ_ERR_TIMEOUT, and the decoder must work again after its workspace reset."""
+    dec, d, prompt, cfg, _ = small
+    dec.reset()
+    dec.set_spin_limit(1)
+    with pytest.raises(mq._lib.MQTimeoutError):
+        for t in prompt:
+            dec.decode_step(int(t))
+    dec.set_spin_limit(0)
+    assert _greedy(dec, prompt, 8) == d["tokens"][:8]
+
+
+def test_full_int8_32_tokens(mq, dev):
+    """BASELINE config 1 gate: Qwen3-0.6B shape, INT8, seed 0, 32 greedy tokens identical to the oracle."""
+    print("building qwen3_0.6b_int8", flush=True)
+    dec, d, prompt, cfg, keep = _build(mq, dev, "qwen3_0.6b_int8")
+    toks = _greedy(dec, prompt, 32)
+    assert toks == d["tokens"], (toks, d["tokens"])
+    # the reference-signature launcher on the same buffers reproduces the last step
+    lib = mq._lib.load()
+    embed, layers, scales, lm_q, lm_s, fnorm, cos, sin = keep
+    dec.reset()
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = ctypes.c_void_p(mq._lib.stream_handle(dev))
+    for pos, t in enumerate(prompt):
+        lib.launch_a10_int8_decode(int(t), out.data_ptr(), embed.data_ptr(), dec.d_layer_weights.data_ptr(),
+                                   fnorm.data_ptr(), lm_q.data_ptr(), lm_s.data_ptr(), cos.data_ptr(),
+                                   sin.data_ptr(), dec.k_cache.data_ptr(), dec.v_cache.data_ptr(),
+                                   None, None, None, None, None, None, None, None, None, None, None,
+                                   cfg.num_layers, pos, pos + 1, d["max_seq_len"], dec.attn_scale,
+                                   dec.d_layer_scales.data_ptr(), stream)
+        assert mq._lib.last_error() == "", mq._lib.last_error()
+    torch.cuda.synchronize()
+    assert int(out.item()) == d["tokens"][0]
+    del dec, keep
+    torch.cuda.empty_cache()
+
+
+def test_full_bf16_32_tokens(mq, dev):
+    """BASELINE config 3 gate: Qwen3-0.6B shape, bf16 weights, 32 greedy tokens identical to the oracle."""
+    print("building qwen3_0.6b_bf16", flush=True)
+    dec, d, prompt, cfg, keep = _build(mq, dev, "qwen3_0.6b_bf16")
+    toks = _greedy(dec, prompt, 32)
+    assert toks == d["tokens"], (toks, d["tokens"])
+    del dec, keep
+    torch.cuda.empty_cache()
+
+
+def test_1p7b_int8_matches_oracle(mq, dev):
+    """Qwen3-1.7B layer shapes (H=2048, I=6144), 2 layers, small vocabulary, live oracle."""
+    cfg = mq.QWEN3_1_7B.with_(num_layers=2, vocab_size=2048)
+    state, prompt = mq.random_init_state(cfg, seed=5, norm_jitter=0.1)
+    qstate = mq.quantize_state(state, cfg, dev)
+    embed, layers, scales, lm_q, lm_s, fnorm = mq.pack_int8(qstate, cfg)
+    S = 32
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+    toks = _greedy(dec, prompt.tolist(), 12)
+    c = lambda t: t.cpu()
+    ref = RefDecoder(Dims(hidden_size=2048, intermediate_size=6144, vocab_size=cfg.vocab_size), c(embed),
+                     [c(t) for t in layers], [c(t) for t in scales], c(fnorm), c(lm_q), c(lm_s), c(cos), c(sin),
+                     cfg.num_layers, S)
+    want, margins = greedy_generate(ref, prompt.tolist(), 12)
+    assert toks == want, (toks, want, margins)

@@ -1,0 +1,146 @@
+"""Host-side checks that need no GPU: the C-ABI library loads and exports what
+include/megaqwen_a10.h declares, struct layouts agree between C and ctypes,
+argument validation rejects bad inputs before any launch, byte accounting,
+packing order, and the seeded weight generator."""
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+
+import pytest
+import torch
+
+from .conftest import ROOT
+
+HEADER = ROOT / "include" / "megaqwen_a10.h"
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*([A-Za-z_][A-Za-z0-9_]*)\s*\(", text, flags=re.M)
+    return sorted(set(n for n in names if n not in ("if", "sizeof")))
+
+
+def test_library_exports_every_declared_symbol(mq):
+    from megaqwen_a10_amd import _lib
+    lib = _lib.load()
+    declared = header_functions()
+    assert sorted(_lib.EXPORTED) == declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.mq_abi_version() == 1
+
+
+def test_struct_layout_matches_c(tmp_path, mq):
+    """offsetof() of every mq_decode_args field from a C program compiled against the header."""
+    from megaqwen_a10_amd import _lib
+    fields = [f for f, _ in _lib.DecodeArgs._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){"]
+    src.append('printf("%zu %zu %zu %zu\\n", sizeof(LayerWeights), sizeof(ScalePointers), sizeof(mq_model_dims), sizeof(mq_decode_args));')
+    for f in fields:
+        src.append(f'printf("%zu\\n", offsetof(mq_decode_args, {f}));')
+    src.append("return 0;}")
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(c)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    sizes = list(map(int, out[:4]))
+    assert sizes == [ctypes.sizeof(_lib.LayerWeights), ctypes.sizeof(_lib.ScalePointers),
+                     ctypes.sizeof(_lib.ModelDims), ctypes.sizeof(_lib.DecodeArgs)]
+    assert sizes[:2] == [88, 56]
+    offs = list(map(int, out[4:]))
+    assert offs == [getattr(_lib.DecodeArgs, f).offset for f in fields]
+
+
+def test_c_api_rejects_bad_arguments_without_launching(mq):
+    from megaqwen_a10_amd import _lib
+    lib = _lib.load()
+    assert lib.mq_int8_gemv(None, None, None, None, 4, 16, None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert "NULL" in _lib.last_error()
+    fake = ctypes.c_void_p(0x1000)
+    assert lib.mq_int8_gemv(fake, fake, fake, fake, 4, 17, None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert lib.mq_quantize_per_channel_bf16(fake, 0, 16, fake, fake, None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    a = _lib.DecodeArgs()
+    a.num_layers, a.max_seq_len, a.position, a.cache_len = 2, 16, 0, 1
+    a.input_token_id = 151936                                  # == vocab: out of range
+    assert lib.mq_int8_decode_step(ctypes.byref(a), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert "input_token_id" in _lib.last_error()
+    a.input_token_id, a.position, a.cache_len = 5, 16, 17        # position == max_seq_len
+    assert lib.mq_int8_decode_step(ctypes.byref(a), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert "position" in _lib.last_error()
+    a.position, a.cache_len = 3, 3                               # cache_len != position + 1
+    assert lib.mq_int8_decode_step(ctypes.byref(a), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert "cache_len" in _lib.last_error()
+    a.cache_len = 4                                              # now only NULL pointers remain
+    assert lib.mq_int8_decode_step(ctypes.byref(a), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    d = _lib.ModelDims(1536, 4096, 16, 8, 128, 1000)
+    assert lib.mq_decode_workspace_bytes(ctypes.byref(d)) == 0   # no kernel for this shape
+    assert lib.mq_decode_workspace_bytes(None) > 0
+
+
+def test_step_byte_accounting(mq):
+    cfg = mq.QWEN3_0_6B
+    assert cfg.int8_step_bytes(cache_len=0) - 114688 == 598_101_504
+    assert cfg.bf16_step_bytes(cache_len=0) - 114688 == 1_192_101_888
+    assert cfg.int8_step_bytes(cache_len=10) - cfg.int8_step_bytes(cache_len=9) == 114_688
+
+
+def test_packing_order_matches_reference(mq):
+    """11 tensors per layer in LayerWeights order and 7 scales (bench_int8.py:291-330)."""
+    cfg = mq.QWEN3_0_6B.with_(num_layers=2, vocab_size=64, hidden_size=8, intermediate_size=12)
+    keys = {}
+    q = {}
+    tag = 0
+    for i in range(cfg.num_layers):
+        p = f"model.layers.{i}"
+        for k in ("input_layernorm", "self_attn.q_norm", "self_attn.k_norm", "post_attention_layernorm"):
+            tag += 1
+            q[f"{p}.{k}.weight"] = torch.full((1,), float(tag))
+            keys[tag] = f"{p}.{k}"
+        for k in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                  "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"):
+            tag += 1
+            q[f"{p}.{k}.weight"] = (torch.full((1,), float(tag)), torch.full((1,), float(-tag)))
+            keys[tag] = f"{p}.{k}"
+    q["model.embed_tokens.weight"] = torch.zeros(1)
+    q["model.norm.weight"] = torch.zeros(1)
+    q["lm_head.weight"] = (torch.zeros(1), torch.zeros(1))
+    _, layers, scales, _, _, _ = mq.pack_int8(q, cfg)
+    names = [keys[int(t.item())].split(".", 3)[3] for t in layers[:11]]
+    assert names == ["input_layernorm", "self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                     "self_attn.q_norm", "self_attn.k_norm", "self_attn.o_proj", "post_attention_layernorm",
+                     "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"]
+    snames = [keys[int(-t.item())].split(".", 3)[3] for t in scales[:7]]
+    assert snames == ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                      "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"]
+    assert keys[int(layers[11].item())].startswith("model.layers.1.")
+
+
+def test_decoder_validation_before_any_launch(mq):
+    cfg = mq.QWEN3_0_6B
+    embed = torch.zeros(16, cfg.hidden_size, dtype=torch.bfloat16)       # CPU tensor
+    with pytest.raises(ValueError, match="HIP device"):
+        mq.A10Int8MegakernelDecoder(embed, [], [], None, None, None, None, None, 1, 8)
+    with pytest.raises(TypeError, match="dtype"):
+        mq.A10Int8MegakernelDecoder(embed.float(), [], [], None, None, None, None, None, 1, 8)
+    with pytest.raises(ValueError, match="num_layers"):
+        mq.A10MegakernelDecoder(embed, [], None, None, None, None, 0, 8)
+    with pytest.raises(ValueError, match="HIP device"):
+        mq.quantize_per_channel(torch.zeros(4, 16, dtype=torch.bfloat16))
+    with pytest.raises(TypeError):
+        mq.quantize_per_channel(torch.zeros(4, 16))
+
+
+def test_random_init_is_deterministic(mq):
+    cfg = mq.QWEN3_0_6B.with_(num_layers=1, vocab_size=512)
+    s1, p1 = mq.random_init_state(cfg, seed=3)
+    s2, p2 = mq.random_init_state(cfg, seed=3)
+    s3, _ = mq.random_init_state(cfg, seed=4)
+    assert mq.state_digest(s1) == mq.state_digest(s2) != mq.state_digest(s3)
+    assert torch.equal(p1, p2) and p1.min() >= 0 and p1.max() < 512 and len(p1) == 8
+    assert s1["lm_head.weight"] is s1["model.embed_tokens.weight"]
+    w = s1["model.layers.0.self_attn.q_proj.weight"]
+    assert w.dtype == torch.bfloat16 and tuple(w.shape) == (2048, 1024)
+    assert abs(float(w.float().std()) - 0.02) < 1e-3
