@@ -124,6 +124,14 @@ typedef struct mq_decode_args {
      * device from the kernel's occupancy. */
     void* timing_start;
     void* timing_stop;
+    /* Optional per-stage timeline: uint64 [(num_layers + 1) * 10 * 256], written
+     * when non-NULL with the 100 MHz real-time counter. Entry
+     * [(l * 10 + p) * 256 + g] is when workgroup g passed point p of layer l:
+     * p = 0/1 QKV input ready/output written, 2/3 attention (workgroups 0-7),
+     * 4/5 O projection, 6/7 gate/up, 8/9 down. Layer num_layers holds p = 0
+     * final-norm input ready, p = 1 LM head done, and [(L*10 + 2) * 256] the
+     * token publication. */
+    void* trace;
 } mq_decode_args;
 
 /* ---- library information ------------------------------------------------ */

@@ -58,7 +58,7 @@ class DecodeArgs(Structure):
         ("num_layers", c_int), ("position", c_int), ("cache_len", c_int), ("max_seq_len", c_int),
         ("attn_scale", c_float), ("dims", c_void_p), ("workspace", c_void_p),
         ("workspace_bytes", c_size_t), ("spin_limit", c_uint),
-        ("timing_start", c_void_p), ("timing_stop", c_void_p),
+        ("timing_start", c_void_p), ("timing_stop", c_void_p), ("trace", c_void_p),
     ]
 
 

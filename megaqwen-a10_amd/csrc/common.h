@@ -227,6 +227,48 @@ struct Waiter {
         return (uint32_t)w;
     }
     __device__ __forceinline__ float getf(const uint64_t* p, uint32_t tag) { return __uint_as_float(get(p, tag)); }
+
+    // N words at p[i * stride]: all N loads are issued before any is checked,
+    // and every retry re-issues the still-missing ones together, so a wait
+    // costs one memory round trip however many words a thread reads.
+    template <int N>
+    __device__ __forceinline__ void get_strided(const uint64_t* p, int stride, uint32_t tag, float (&out)[N]) {
+        uint64_t w[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) w[i] = ll_load(p + i * stride);
+        uint32_t pending = 0;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            out[i] = __uint_as_float((uint32_t)w[i]);
+            if ((uint32_t)(w[i] >> 32) != tag) pending |= 1u << i;
+        }
+        if (pending == 0 || dead) return;
+        uint32_t n = 0;
+        for (;;) {
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int i = 0; i < N; ++i)
+                if (pending & (1u << i)) w[i] = ll_load(p + i * stride);
+#pragma unroll
+            for (int i = 0; i < N; ++i) {
+                if ((pending & (1u << i)) && (uint32_t)(w[i] >> 32) == tag) {
+                    out[i] = __uint_as_float((uint32_t)w[i]);
+                    pending &= ~(1u << i);
+                }
+            }
+            if (pending == 0) return;
+            if (++n >= limit) {
+                dead = true;
+                __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                return;
+            }
+            if ((n & 127u) == 0 &&
+                __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+                dead = true;
+                return;
+            }
+        }
+    }
 };
 
 // Order-preserving map fp32 -> uint32 (larger float -> larger key).

@@ -39,6 +39,9 @@ constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kNWG = 256;
 constexpr int kMaxAttnLen = 4096;     // positions one workgroup attends over (scores in LDS)
+constexpr int kKvLds = 64;            // earlier positions whose K/V rows are prefetched into LDS
+constexpr int kMaxLayers = 64;        // per-layer pointer tables cached in LDS
+constexpr int kTracePoints = 10;      // timestamps per layer in the optional trace
 constexpr float kEps = 1e-6f;
 
 enum Stage { ST_QKV = 0, ST_ATTN = 1, ST_O = 2, ST_GU = 3, ST_DOWN = 4 };
@@ -70,13 +73,26 @@ struct KArgs {
     int L, pos, cache_len, S, V;
     float attn_scale;
     uint32_t spin_limit;
-    WsHeader* hdr;
-    uint64_t* hid_x;
-    uint64_t* qkv_x;
-    uint64_t* att_x;
-    uint64_t* act_x;
-    uint64_t* mlp_x;
+    uint64_t* trace;
+    uint8_t* ws;
 };
+
+// Workspace layout (after the 256-byte header): one 64-bit exchange word per
+// element of each handed-over vector, every region 256-byte aligned.
+struct Layout {
+    size_t hid, qkv, att, act, mlp, total;
+};
+constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+constexpr Layout layout_for(int H, int I, int NQ, int NKV, int D) {
+    Layout o{};
+    o.hid = sizeof(WsHeader);
+    o.qkv = o.hid + round256((size_t)H * 8);
+    o.att = o.qkv + round256(((size_t)NQ * D + 2 * (size_t)NKV * D) * 8);
+    o.act = o.att + round256((size_t)NQ * D * 8);
+    o.mlp = o.act + round256((size_t)H * 8);
+    o.total = o.mlp + round256((size_t)I * 8);
+    return o;
+}
 
 constexpr int pow2ceil(int x) { return x <= 1 ? 1 : 2 * pow2ceil((x + 1) / 2); }
 
@@ -139,18 +155,21 @@ __device__ __forceinline__ float block_sum(float v, float* red, int wave, int la
     return t;
 }
 
-template <int H, int I, class W>
+template <int H, int I, class W, bool kDebug>
 __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
     constexpr int NQ = 16, NKV = 8, D = 128;
+    constexpr Layout kLay = layout_for(H, I, NQ, NKV, D);
     constexpr int QD = NQ * D, KVD = NKV * D, QKV = QD + 2 * KVD;
     constexpr int ES = W::kBytes;
     constexpr bool kInt8 = (ES == 1);
     constexpr int ROWS_QKV = QKV / kNWG;
     constexpr int ROWS_H = H / kNWG;
     constexpr int CPW = I / kNWG;
+    constexpr int PT = H / kThreads;                  // hidden elements per thread
     constexpr int XMAX = (H > QD ? (H > I ? H : I) : (QD > I ? QD : I));
     static_assert(QKV % kNWG == 0 && H % kNWG == 0 && I % kNWG == 0, "rows must split evenly");
     static_assert(H % kThreads == 0 && QD % kThreads == 0 && I % kThreads == 0, "vectors must split evenly");
+    static_assert(ROWS_QKV <= kThreads && CPW <= kThreads, "epilogue threads");
 
     __shared__ float4 xs[XMAX / 4];
     __shared__ float part[256];
@@ -158,11 +177,14 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
     __shared__ float rows_res[ROWS_H];
     __shared__ float att_in[4 * D];
     __shared__ float qrot[2 * D];
-    __shared__ float kv_cur[2 * D];
+    __shared__ uint32_t kv_lds[2][kKvLds][D / 2];      // bf16 pairs of the prefetched K and V rows
+    __shared__ uint32_t kv_curb[2][D / 2];             // this position's K and V (bf16 pairs)
     __shared__ float scores[2 * kMaxAttnLen];
     __shared__ float pv[kWaves * 2 * D];
     __shared__ float lm_best_v[kWaves];
     __shared__ int lm_best_i[kWaves];
+    __shared__ LayerWeights s_lw[kMaxLayers];
+    __shared__ ScalePointers s_sp[kMaxLayers];
 
     const int g = blockIdx.x;
     const int tid = threadIdx.x;
@@ -170,7 +192,27 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
     const int wave = tid / kWave;
     float* xsf = reinterpret_cast<float*>(xs);
 
-    WsHeader* hdr = a.hdr;
+    // step-independent reads first: the embedding row and the per-layer pointer tables
+    float hv0[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) hv0[i] = bf16_bits_to_f32(a.embed[(int64_t)a.token * H + tid + i * kThreads]);
+    {
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.lw);
+        uint64_t* dst = reinterpret_cast<uint64_t*>(s_lw);
+        for (int i = tid; i < a.L * 11; i += kThreads) dst[i] = src[i];
+        if (kInt8) {
+            const uint64_t* ssrc = reinterpret_cast<const uint64_t*>(a.sp);
+            uint64_t* sdst = reinterpret_cast<uint64_t*>(s_sp);
+            for (int i = tid; i < a.L * 7; i += kThreads) sdst[i] = ssrc[i];
+        }
+    }
+
+    WsHeader* hdr = reinterpret_cast<WsHeader*>(a.ws);
+    uint64_t* const hid_x = reinterpret_cast<uint64_t*>(a.ws + kLay.hid);
+    uint64_t* const qkv_x = reinterpret_cast<uint64_t*>(a.ws + kLay.qkv);
+    uint64_t* const att_x = reinterpret_cast<uint64_t*>(a.ws + kLay.att);
+    uint64_t* const act_x = reinterpret_cast<uint64_t*>(a.ws + kLay.act);
+    uint64_t* const mlp_x = reinterpret_cast<uint64_t*>(a.ws + kLay.mlp);
     const uint32_t E = __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (g == 0 && tid == 0) {
         __hip_atomic_store(&hdr->done[(E + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -179,13 +221,18 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
     const uint32_t tps = 5u * (uint32_t)a.L + 4u;
     auto tag = [&](int l, int st) -> uint32_t { return ((E * tps + 5u * (uint32_t)l + (uint32_t)st) << 1) | 1u; };
     Waiter wt(&hdr->abort_flag, a.spin_limit);
+    auto trace = [&](int l, int point) {
+        if (kDebug && a.trace != nullptr && tid == 0)
+            a.trace[((int64_t)l * kTracePoints + point) * kNWG + g] = __builtin_amdgcn_s_memrealtime();
+    };
 
     const int64_t kv_head_stride = (int64_t)a.S * D;
     const int last = a.L - 1;
+    __syncthreads();
 
     for (int l = 0; l < a.L; ++l) {
-        const LayerWeights& lw = a.lw[l];
-        const ScalePointers* sp = kInt8 ? &a.sp[l] : nullptr;
+        const LayerWeights& lw = s_lw[l];
+        const ScalePointers& sp = s_sp[l];
 
         // ---------------- RMSNorm + QKV ----------------
         {
@@ -193,29 +240,35 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             const uint8_t* base;
             const float* sc = nullptr;
             int lrow0;
-            if (row0 < QD) { base = (const uint8_t*)lw.q_proj_weight; lrow0 = row0; if (kInt8) sc = sp->q_scale; }
-            else if (row0 < QD + KVD) { base = (const uint8_t*)lw.k_proj_weight; lrow0 = row0 - QD; if (kInt8) sc = sp->k_scale; }
-            else { base = (const uint8_t*)lw.v_proj_weight; lrow0 = row0 - QD - KVD; if (kInt8) sc = sp->v_scale; }
+            if (row0 < QD) { base = (const uint8_t*)lw.q_proj_weight; lrow0 = row0; if (kInt8) sc = sp.q_scale; }
+            else if (row0 < QD + KVD) { base = (const uint8_t*)lw.k_proj_weight; lrow0 = row0 - QD; if (kInt8) sc = sp.k_scale; }
+            else { base = (const uint8_t*)lw.v_proj_weight; lrow0 = row0 - QD - KVD; if (kInt8) sc = sp.v_scale; }
             Stage_<W, ROWS_QKV, H> st;
             st.load([&](int r) { return base + (int64_t)(lrow0 + r) * H * ES; }, wave, lane);
+            float my_scale = 1.0f;
+            if (kInt8 && tid < ROWS_QKV) my_scale = sc[lrow0 + tid];
+            const uint16_t* lnw = (const uint16_t*)lw.input_layernorm_weight;
+            float wln[PT];
+#pragma unroll
+            for (int i = 0; i < PT; ++i) wln[i] = bf16_bits_to_f32(lnw[tid + i * kThreads]);
 
-            constexpr int PT = H / kThreads;
             float hv[PT];
+            if (l == 0) {
+#pragma unroll
+                for (int i = 0; i < PT; ++i) hv[i] = hv0[i];
+            } else {
+                wt.get_strided<PT>(hid_x + tid, kThreads, tag(l - 1, ST_DOWN), hv);
+            }
             float ss = 0.0f;
 #pragma unroll
-            for (int i = 0; i < PT; ++i) {
-                const int k = tid + i * kThreads;
-                if (l == 0) hv[i] = bf16_bits_to_f32(a.embed[(int64_t)a.token * H + k]);
-                else hv[i] = wt.getf(&a.hid_x[k], tag(l - 1, ST_DOWN));
-                ss += hv[i] * hv[i];
-            }
+            for (int i = 0; i < PT; ++i) ss += hv[i] * hv[i];
             const float tot = block_sum<kWaves>(ss, red, wave, lane);
+            trace(l, 0);
             const float rstd = rsqrtf(tot / (float)H + kEps);
-            const uint16_t* lnw = (const uint16_t*)lw.input_layernorm_weight;
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
                 const int k = tid + i * kThreads;
-                xsf[xs_index<W>(k)] = hv[i] * rstd * bf16_bits_to_f32(lnw[k]);
+                xsf[xs_index<W>(k)] = hv[i] * rstd * wln[i];
                 const int rr = k - g * ROWS_H;
                 if (rr >= 0 && rr < ROWS_H) rows_res[rr] = hv[i];
             }
@@ -224,66 +277,105 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             __syncthreads();
             if (tid < ROWS_QKV) {
                 float v = Stage_<W, ROWS_QKV, H>::row_sum(part, tid);
-                if (kInt8) v = v * sc[lrow0 + tid];
-                ll_put(&a.qkv_x[row0 + tid], __float_as_uint(v), tag(l, ST_QKV));
+                if (kInt8) v = v * my_scale;
+                ll_put(&qkv_x[row0 + tid], __float_as_uint(v), tag(l, ST_QKV));
             }
+            trace(l, 1);
         }
 
         // ---------------- QK-norm + RoPE + KV write + attention (KV head g) ----------------
         if (g < NKV) {
             const int h = g;
+            const int n = a.cache_len;
+            const int64_t cache_base = ((int64_t)l * NKV + h) * kv_head_stride;
+            const int64_t cur = cache_base + (int64_t)a.pos * D;
+            // step-independent inputs: norm gains, the RoPE row, and the K/V rows of
+            // earlier positions (up to kKvLds of them) staged through registers
+            float nw0 = 0.0f, nw1 = 0.0f, c0 = 0.0f, s0 = 0.0f, c1 = 0.0f, s1 = 0.0f;
+            if (wave < 3) {
+                const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
+                nw0 = bf16_bits_to_f32(nw[lane]);
+                nw1 = bf16_bits_to_f32(nw[lane + 64]);
+                const uint16_t* ct = a.cos_t + (int64_t)a.pos * D;
+                const uint16_t* stt = a.sin_t + (int64_t)a.pos * D;
+                c0 = bf16_bits_to_f32(ct[lane]);
+                s0 = bf16_bits_to_f32(stt[lane]);
+                c1 = bf16_bits_to_f32(ct[lane + 64]);
+                s1 = bf16_bits_to_f32(stt[lane + 64]);
+            }
+            const int npre = a.pos < kKvLds ? a.pos : kKvLds;   // earlier positions held in LDS
+            constexpr int kPreU4 = 2 * kKvLds * (D / 8) / kThreads;
+            uint4 pre[kPreU4];
+#pragma unroll
+            for (int i = 0; i < kPreU4; ++i) {
+                const int f = tid + i * kThreads;                 // 16-byte unit: side, position, column
+                const int side = f / (kKvLds * (D / 8));
+                const int rem = f % (kKvLds * (D / 8));
+                const int j = rem / (D / 8), c = rem % (D / 8);
+                pre[i] = make_uint4(0, 0, 0, 0);
+                if (j < npre) {
+                    const uint16_t* src = (side == 0 ? a.kc : a.vc) + cache_base + (int64_t)j * D + c * 8;
+                    pre[i] = *reinterpret_cast<const uint4*>(src);
+                }
+            }
             {
                 int word;
                 if (tid < 2 * D) word = 2 * h * D + tid;
                 else if (tid < 3 * D) word = QD + h * D + (tid - 2 * D);
                 else word = QD + KVD + h * D + (tid - 3 * D);
-                att_in[tid] = wt.getf(&a.qkv_x[word], tag(l, ST_QKV));
+                float v1[1];
+                wt.get_strided<1>(qkv_x + word, 0, tag(l, ST_QKV), v1);
+                att_in[tid] = v1[0];
+            }
+#pragma unroll
+            for (int i = 0; i < kPreU4; ++i) {
+                const int f = tid + i * kThreads;
+                const int side = f / (kKvLds * (D / 8));
+                const int rem = f % (kKvLds * (D / 8));
+                const int j = rem / (D / 8), c = rem % (D / 8);
+                if (j < npre) *reinterpret_cast<uint4*>(&kv_lds[side][j][c * 4]) = pre[i];
             }
             __syncthreads();
-            const int64_t cache_base = ((int64_t)l * NKV + h) * kv_head_stride;
-            const int64_t cur = cache_base + (int64_t)a.pos * D;
+            trace(l, 2);
             if (wave < 3) {
                 const float* src = att_in + wave * D;
                 const float x0 = src[lane], x1 = src[lane + 64];
                 const float ssq = wave_sum(x0 * x0 + x1 * x1);
                 const float sc = rsqrtf(ssq / (float)D + kEps);
-                const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
-                const float y0 = x0 * sc * bf16_bits_to_f32(nw[lane]);
-                const float y1 = x1 * sc * bf16_bits_to_f32(nw[lane + 64]);
-                const uint16_t* ct = a.cos_t + (int64_t)a.pos * D;
-                const uint16_t* stt = a.sin_t + (int64_t)a.pos * D;
-                const float c0 = bf16_bits_to_f32(ct[lane]), s0 = bf16_bits_to_f32(stt[lane]);
-                const float c1 = bf16_bits_to_f32(ct[lane + 64]), s1 = bf16_bits_to_f32(stt[lane + 64]);
+                const float y0 = x0 * sc * nw0;
+                const float y1 = x1 * sc * nw1;
                 const float o0 = y0 * c0 - y1 * s0;
                 const float o1 = y0 * s1 + y1 * c1;
                 if (wave < 2) {
                     qrot[wave * D + lane] = o0;
                     qrot[wave * D + lane + 64] = o1;
-                    if (l == last && a.dbg_q) {
+                    if (l == last && kDebug && a.dbg_q) {
                         a.dbg_q[(2 * h + wave) * D + lane] = o0;
                         a.dbg_q[(2 * h + wave) * D + lane + 64] = o1;
                     }
                 } else {
                     const uint32_t b0 = f32_to_bf16_bits(o0), b1 = f32_to_bf16_bits(o1);
-                    kv_cur[lane] = bf16_bits_to_f32(b0);
-                    kv_cur[lane + 64] = bf16_bits_to_f32(b1);
                     a.kc[cur + lane] = (uint16_t)b0;
                     a.kc[cur + lane + 64] = (uint16_t)b1;
-                    if (l == last && a.dbg_k) { a.dbg_k[h * D + lane] = o0; a.dbg_k[h * D + lane + 64] = o1; }
+                    uint16_t* row = reinterpret_cast<uint16_t*>(kv_curb[0]);
+                    row[lane] = (uint16_t)b0;
+                    row[lane + 64] = (uint16_t)b1;
+                    if (l == last && kDebug && a.dbg_k) { a.dbg_k[h * D + lane] = o0; a.dbg_k[h * D + lane + 64] = o1; }
                 }
             } else if (wave == 3) {
                 const float v0 = att_in[3 * D + lane], v1 = att_in[3 * D + lane + 64];
                 const uint32_t b0 = f32_to_bf16_bits(v0), b1 = f32_to_bf16_bits(v1);
-                kv_cur[D + lane] = bf16_bits_to_f32(b0);
-                kv_cur[D + lane + 64] = bf16_bits_to_f32(b1);
                 a.vc[cur + lane] = (uint16_t)b0;
                 a.vc[cur + lane + 64] = (uint16_t)b1;
-                if (l == last && a.dbg_v) { a.dbg_v[h * D + lane] = v0; a.dbg_v[h * D + lane + 64] = v1; }
+                uint16_t* row = reinterpret_cast<uint16_t*>(kv_curb[1]);
+                row[lane] = (uint16_t)b0;
+                row[lane + 64] = (uint16_t)b1;
+                if (l == last && kDebug && a.dbg_v) { a.dbg_v[h * D + lane] = v0; a.dbg_v[h * D + lane + 64] = v1; }
             }
             __syncthreads();
 
-            // scores: a quad of lanes per position, each lane a quarter of the head dim
-            const int n = a.cache_len;
+            // scores: a quad of lanes per position, each lane a quarter of the head dim.
+            // Positions < kKvLds (and the current one) come from LDS, later ones from HBM.
             {
                 const int qd = tid & 3;
                 float qa[32], qb[32];
@@ -293,28 +385,28 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                     const int j = j0 + (tid >> 2);
                     float d0 = 0.0f, d1 = 0.0f;
                     if (j < n) {
-                        if (j == a.pos) {
+                        uint4 kw[4];
+                        if (j == a.pos || j < kKvLds) {
+                            const uint32_t* rowp = j == a.pos ? kv_curb[0] : kv_lds[0][j];
+                            const uint4* kp = reinterpret_cast<const uint4*>(rowp + qd * 16);
 #pragma unroll
-                            for (int i = 0; i < 32; ++i) {
-                                const float kk = kv_cur[qd * 32 + i];
-                                d0 = fmaf(qa[i], kk, d0);
-                                d1 = fmaf(qb[i], kk, d1);
-                            }
+                            for (int u = 0; u < 4; ++u) kw[u] = kp[u];
                         } else {
                             const uint4* kp = reinterpret_cast<const uint4*>(a.kc + cache_base + (int64_t)j * D + qd * 32);
 #pragma unroll
-                            for (int u = 0; u < 4; ++u) {
-                                const uint4 kw = kp[u];
-                                const uint32_t wv[4] = {kw.x, kw.y, kw.z, kw.w};
+                            for (int u = 0; u < 4; ++u) kw[u] = kp[u];
+                        }
 #pragma unroll
-                                for (int e = 0; e < 4; ++e) {
-                                    const float klo = __uint_as_float(wv[e] << 16);
-                                    const float khi = __uint_as_float(wv[e] & 0xffff0000u);
-                                    d0 = fmaf(qa[u * 8 + 2 * e], klo, d0);
-                                    d0 = fmaf(qa[u * 8 + 2 * e + 1], khi, d0);
-                                    d1 = fmaf(qb[u * 8 + 2 * e], klo, d1);
-                                    d1 = fmaf(qb[u * 8 + 2 * e + 1], khi, d1);
-                                }
+                        for (int u = 0; u < 4; ++u) {
+                            const uint32_t wv[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w};
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const float klo = __uint_as_float(wv[e] << 16);
+                                const float khi = __uint_as_float(wv[e] & 0xffff0000u);
+                                d0 = fmaf(qa[u * 8 + 2 * e], klo, d0);
+                                d0 = fmaf(qa[u * 8 + 2 * e + 1], khi, d0);
+                                d1 = fmaf(qb[u * 8 + 2 * e], klo, d1);
+                                d1 = fmaf(qb[u * 8 + 2 * e + 1], khi, d1);
                             }
                         }
                     }
@@ -359,13 +451,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                 const int dp = lane;
                 float a00 = 0.0f, a01 = 0.0f, a10 = 0.0f, a11 = 0.0f;
                 for (int j = wave; j < n; j += kWaves) {
-                    float v0, v1;
-                    if (j == a.pos) { v0 = kv_cur[D + 2 * dp]; v1 = kv_cur[D + 2 * dp + 1]; }
-                    else {
-                        const uint32_t vw = *reinterpret_cast<const uint32_t*>(a.vc + cache_base + (int64_t)j * D + 2 * dp);
-                        v0 = __uint_as_float(vw << 16);
-                        v1 = __uint_as_float(vw & 0xffff0000u);
-                    }
+                    const uint32_t vw = j == a.pos ? kv_curb[1][dp]
+                                      : j < kKvLds ? kv_lds[1][j][dp]
+                                                   : *reinterpret_cast<const uint32_t*>(a.vc + cache_base + (int64_t)j * D + 2 * dp);
+                    const float v0 = __uint_as_float(vw << 16);
+                    const float v1 = __uint_as_float(vw & 0xffff0000u);
                     const float p0 = scores[j], p1 = scores[kMaxAttnLen + j];
                     a00 = fmaf(p0, v0, a00); a01 = fmaf(p0, v1, a01);
                     a10 = fmaf(p1, v0, a10); a11 = fmaf(p1, v1, a11);
@@ -382,9 +472,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                 for (int w = 0; w < kWaves; ++w) o += pv[w * 2 * D + tid];
                 o = o / (tid < D ? L0 : L1);
                 const int word = 2 * h * D + tid;
-                ll_put(&a.att_x[word], __float_as_uint(o), tag(l, ST_ATTN));
-                if (l == last && a.dbg_attn) a.dbg_attn[word] = o;
+                ll_put(&att_x[word], __float_as_uint(o), tag(l, ST_ATTN));
+                if (l == last && kDebug && a.dbg_attn) a.dbg_attn[word] = o;
             }
+            trace(l, 3);
         }
 
         // ---------------- O projection + residual ----------------
@@ -393,20 +484,25 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             const uint8_t* base = (const uint8_t*)lw.o_proj_weight;
             Stage_<W, ROWS_H, QD> st;
             st.load([&](int r) { return base + (int64_t)(row0 + r) * QD * ES; }, wave, lane);
+            float my_scale = 1.0f;
+            if (kInt8 && tid < ROWS_H) my_scale = sp.o_scale[row0 + tid];
+            {
+                float v[QD / kThreads];
+                wt.get_strided<QD / kThreads>(att_x + tid, kThreads, tag(l, ST_ATTN), v);
 #pragma unroll
-            for (int i = 0; i < QD / kThreads; ++i) {
-                const int k = tid + i * kThreads;
-                xsf[xs_index<W>(k)] = wt.getf(&a.att_x[k], tag(l, ST_ATTN));
+                for (int i = 0; i < QD / kThreads; ++i) xsf[xs_index<W>(tid + i * kThreads)] = v[i];
             }
             __syncthreads();
+            trace(l, 4);
             st.compute(xs, part, wave, lane);
             __syncthreads();
             if (tid < ROWS_H) {
                 float v = Stage_<W, ROWS_H, QD>::row_sum(part, tid);
-                if (kInt8) v = v * sp->o_scale[row0 + tid];
+                if (kInt8) v = v * my_scale;
                 v = v + rows_res[tid];
-                ll_put(&a.act_x[row0 + tid], __float_as_uint(v), tag(l, ST_O));
+                ll_put(&act_x[row0 + tid], __float_as_uint(v), tag(l, ST_O));
             }
+            trace(l, 5);
         }
 
         // ---------------- RMSNorm + gate/up + SwiGLU ----------------
@@ -418,26 +514,28 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             st.load([&](int r) {
                 return r < CPW ? gb + (int64_t)(c0 + r) * H * ES : ub + (int64_t)(c0 + r - CPW) * H * ES;
             }, wave, lane);
-            constexpr int PT = H / kThreads;
+            float gsc = 1.0f, usc = 1.0f;
+            if (kInt8 && tid < CPW) { gsc = sp.gate_scale[c0 + tid]; usc = sp.up_scale[c0 + tid]; }
+            const uint16_t* pnw = (const uint16_t*)lw.post_attn_layernorm_weight;
+            float wpn[PT];
+#pragma unroll
+            for (int i = 0; i < PT; ++i) wpn[i] = bf16_bits_to_f32(pnw[tid + i * kThreads]);
             float av[PT];
+            wt.get_strided<PT>(act_x + tid, kThreads, tag(l, ST_O), av);
             float ss = 0.0f;
 #pragma unroll
-            for (int i = 0; i < PT; ++i) {
-                const int k = tid + i * kThreads;
-                av[i] = wt.getf(&a.act_x[k], tag(l, ST_O));
-                ss += av[i] * av[i];
-            }
+            for (int i = 0; i < PT; ++i) ss += av[i] * av[i];
             const float tot = block_sum<kWaves>(ss, red, wave, lane);
+            trace(l, 6);
             const float rstd = rsqrtf(tot / (float)H + kEps);
-            const uint16_t* pnw = (const uint16_t*)lw.post_attn_layernorm_weight;
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
                 const int k = tid + i * kThreads;
-                const float nv = av[i] * rstd * bf16_bits_to_f32(pnw[k]);
+                const float nv = av[i] * rstd * wpn[i];
                 xsf[xs_index<W>(k)] = nv;
                 const int rr = k - g * ROWS_H;
                 if (rr >= 0 && rr < ROWS_H) rows_res[rr] = av[i];
-                if (l == last && g == 0) {
+                if (kDebug && l == last && g == 0) {
                     if (a.dbg_act) a.dbg_act[k] = nv;
                     if (a.dbg_resid) a.dbg_resid[k] = av[i];
                 }
@@ -448,11 +546,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             if (tid < CPW) {
                 float gs = Stage_<W, 2 * CPW, H>::row_sum(part, tid);
                 float us = Stage_<W, 2 * CPW, H>::row_sum(part, CPW + tid);
-                if (kInt8) { gs = gs * sp->gate_scale[c0 + tid]; us = us * sp->up_scale[c0 + tid]; }
+                if (kInt8) { gs = gs * gsc; us = us * usc; }
                 const float m = gs / (1.0f + expf(-gs)) * us;
-                ll_put(&a.mlp_x[c0 + tid], __float_as_uint(m), tag(l, ST_GU));
-                if (l == last && a.dbg_mlp) a.dbg_mlp[c0 + tid] = m;
+                ll_put(&mlp_x[c0 + tid], __float_as_uint(m), tag(l, ST_GU));
+                if (l == last && kDebug && a.dbg_mlp) a.dbg_mlp[c0 + tid] = m;
             }
+            trace(l, 7);
         }
 
         // ---------------- down projection + residual -> bf16 hidden ----------------
@@ -461,48 +560,31 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             const uint8_t* base = (const uint8_t*)lw.down_proj_weight;
             Stage_<W, ROWS_H, I> st;
             st.load([&](int r) { return base + (int64_t)(row0 + r) * I * ES; }, wave, lane);
+            float my_scale = 1.0f;
+            if (kInt8 && tid < ROWS_H) my_scale = sp.down_scale[row0 + tid];
+            {
+                float v[I / kThreads];
+                wt.get_strided<I / kThreads>(mlp_x + tid, kThreads, tag(l, ST_GU), v);
 #pragma unroll
-            for (int i = 0; i < I / kThreads; ++i) {
-                const int k = tid + i * kThreads;
-                xsf[xs_index<W>(k)] = wt.getf(&a.mlp_x[k], tag(l, ST_GU));
+                for (int i = 0; i < I / kThreads; ++i) xsf[xs_index<W>(tid + i * kThreads)] = v[i];
             }
             __syncthreads();
+            trace(l, 8);
             st.compute(xs, part, wave, lane);
             __syncthreads();
             if (tid < ROWS_H) {
                 float v = Stage_<W, ROWS_H, I>::row_sum(part, tid);
-                if (kInt8) v = v * sp->down_scale[row0 + tid];
+                if (kInt8) v = v * my_scale;
                 v = v + rows_res[tid];
                 const uint32_t hb = f32_to_bf16_bits(v);
-                ll_put(&a.hid_x[row0 + tid], __float_as_uint(bf16_bits_to_f32(hb)), tag(l, ST_DOWN));
-                if (l == last && a.dbg_hidden) a.dbg_hidden[row0 + tid] = (uint16_t)hb;
+                ll_put(&hid_x[row0 + tid], __float_as_uint(bf16_bits_to_f32(hb)), tag(l, ST_DOWN));
+                if (l == last && kDebug && a.dbg_hidden) a.dbg_hidden[row0 + tid] = (uint16_t)hb;
             }
+            trace(l, 9);
         }
     }
 
-    // ---------------- final RMSNorm ----------------
-    {
-        constexpr int PT = H / kThreads;
-        float hv[PT];
-        float ss = 0.0f;
-#pragma unroll
-        for (int i = 0; i < PT; ++i) {
-            hv[i] = wt.getf(&a.hid_x[tid + i * kThreads], tag(last, ST_DOWN));
-            ss += hv[i] * hv[i];
-        }
-        const float tot = block_sum<kWaves>(ss, red, wave, lane);
-        const float rstd = rsqrtf(tot / (float)H + kEps);
-#pragma unroll
-        for (int i = 0; i < PT; ++i) {
-            const int k = tid + i * kThreads;
-            const float nv = hv[i] * rstd * bf16_bits_to_f32(a.final_norm[k]);
-            xsf[xs_index<W>(k)] = nv;
-            if (g == 0 && a.dbg_norm) a.dbg_norm[k] = nv;
-        }
-        __syncthreads();
-    }
-
-    // ---------------- LM head + greedy argmax ----------------
+    // ---------------- final RMSNorm + LM head + greedy argmax ----------------
     {
         constexpr int CH = H / (64 * W::kPerLane);
         constexpr int RB = CH >= 8 ? 1 : 8 / CH;          // rows per wave batch
@@ -512,8 +594,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
         const int r1 = (int)((int64_t)a.V * (g + 1) / kNWG);
         const int nb = (r1 - r0 + RB - 1) / RB;
         const int64_t rowbytes = (int64_t)H * ES;
-        float best_v = -INFINITY;
-        int best_i = 0x7fffffff;
 
         uint4 cur[R], nxt[R];
         float scur = 0.0f, snxt = 0.0f;
@@ -528,8 +608,34 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             s = 1.0f;
             if (kInt8 && myrow < r1) s = a.lm_s[myrow];
         };
+        // the first LM-head batch and the final norm gains do not depend on this step
         int b = wave;
         if (b < nb) fetch(b, cur, scur);
+        float wfn[PT];
+#pragma unroll
+        for (int i = 0; i < PT; ++i) wfn[i] = bf16_bits_to_f32(a.final_norm[tid + i * kThreads]);
+
+        float hv[PT];
+        wt.get_strided<PT>(hid_x + tid, kThreads, tag(last, ST_DOWN), hv);
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PT; ++i) ss += hv[i] * hv[i];
+        const float tot = block_sum<kWaves>(ss, red, wave, lane);
+        trace(a.L, 0);
+        const float rstd = rsqrtf(tot / (float)H + kEps);
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const int k = tid + i * kThreads;
+            const float nv = hv[i] * rstd * wfn[i];
+            xsf[xs_index<W>(k)] = nv;
+            if (g == 0 && kDebug && a.dbg_norm) a.dbg_norm[k] = nv;
+        }
+        __syncthreads();
+
+        float best_v = -INFINITY;
+        int best_i = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < R; ++i) nxt[i] = make_uint4(0, 0, 0, 0);
         for (; b < nb; b += kWaves) {
             if (b + kWaves < nb) fetch(b + kWaves, nxt, snxt);
             float acc[R];
@@ -557,14 +663,15 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
 #undef MQ_ARGMAX_LEVEL
         if (lane == 0) { lm_best_v[wave] = best_v; lm_best_i[wave] = best_i; }
         __syncthreads();
+        trace(a.L, 1);
         if (tid == 0) {
             float bv = lm_best_v[0];
             int bi = lm_best_i[0];
             for (int w = 1; w < kWaves; ++w) {
                 if (lm_best_v[w] > bv || (lm_best_v[w] == bv && lm_best_i[w] < bi)) { bv = lm_best_v[w]; bi = lm_best_i[w]; }
             }
-            if (a.dbg_bmax) a.dbg_bmax[g] = bv;
-            if (a.dbg_bidx) a.dbg_bidx[g] = bi;
+            if (kDebug && a.dbg_bmax) a.dbg_bmax[g] = bv;
+            if (kDebug && a.dbg_bidx) a.dbg_bidx[g] = bi;
             const uint64_t key = ((uint64_t)ordered_key(bv) << 32) | (uint64_t)(~(uint32_t)bi);
             const int slot = E & 1;
             __hip_atomic_fetch_max(&hdr->best[slot], key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -574,6 +681,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                 const bool aborted = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
                 *a.out_token = aborted ? -1 : (int)(~(uint32_t)(k & 0xffffffffu));
                 __hip_atomic_store(&hdr->epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (kDebug && a.trace != nullptr) a.trace[((int64_t)a.L * kTracePoints + 2) * kNWG] = __builtin_amdgcn_s_memrealtime();
             }
         }
     }
@@ -581,32 +689,16 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
 
 // ---------------- host side ----------------
 
-struct Layout {
-    size_t hid, qkv, att, act, mlp, total;
-};
-static Layout layout_of(const DecodeShape& s) {
-    Layout o;
-    size_t off = sizeof(WsHeader);
-    auto take = [&](size_t words) { size_t at = off; off += ((words * 8 + 255) / 256) * 256; return at; };
-    o.hid = take(s.H);
-    o.qkv = take((size_t)s.NQ * s.D + 2 * (size_t)s.NKV * s.D);
-    o.att = take((size_t)s.NQ * s.D);
-    o.act = take(s.H);
-    o.mlp = take(s.I);
-    o.total = off;
-    return o;
-}
-
-size_t decode_workspace_bytes(const DecodeShape& s) { return layout_of(s).total; }
+size_t decode_workspace_bytes(const DecodeShape& s) { return layout_for(s.H, s.I, s.NQ, s.NKV, s.D).total; }
 
 // All kNWG workgroups wait on each other, so they must be resident at once;
 // checked once per (kernel, device) from the occupancy calculator.
-template <int H, int I, class W>
 static int check_residency(const void* fn) {
-    static int checked[64] = {0};
+    static thread_local const void* checked_fn[64] = {nullptr};
+    static thread_local int checked[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(MQ_ERR_HIP, "hipGetDevice failed");
-    if (checked[dev]) return MQ_OK;
+    if (checked[dev] && checked_fn[dev] == fn) return MQ_OK;
     int ncu = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, 0) != hipSuccess)
@@ -615,13 +707,15 @@ static int check_residency(const void* fn) {
         return set_error(MQ_ERR_UNSUPPORTED, "device holds %d x %d resident workgroups, the decode kernel needs %d",
                          ncu, per_cu, kNWG);
     checked[dev] = 1;
+    checked_fn[dev] = fn;
     return MQ_OK;
 }
 
 template <int H, int I, class W>
-static int launch_t(const KArgs& ka, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
-    auto fn = reinterpret_cast<const void*>(&decode_kernel<H, I, W>);
-    int st = check_residency<H, I, W>(fn);
+static int launch_t(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
+    auto fn = debug ? reinterpret_cast<const void*>(&decode_kernel<H, I, W, true>)
+                    : reinterpret_cast<const void*>(&decode_kernel<H, I, W, false>);
+    int st = check_residency(fn);
     if (st != MQ_OK) return st;
     KArgs copy = ka;
     void* args[] = {&copy};
@@ -637,11 +731,11 @@ static int launch_t(const KArgs& ka, hipStream_t stream, hipEvent_t t0, hipEvent
 }
 
 int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream) {
+    if (a.num_layers > kMaxLayers)
+        return set_error(MQ_ERR_UNSUPPORTED, "num_layers %d exceeds %d", a.num_layers, kMaxLayers);
     if (a.cache_len > kMaxAttnLen)
         return set_error(MQ_ERR_UNSUPPORTED, "cache_len %d exceeds the single-workgroup attention limit %d",
                          a.cache_len, kMaxAttnLen);
-    const Layout lay = layout_of(s);
-    uint8_t* ws = static_cast<uint8_t*>(a.workspace);
     KArgs k;
     k.token = a.input_token_id;
     k.out_token = a.output_token_id;
@@ -673,18 +767,17 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
     k.V = s.V;
     k.attn_scale = a.attn_scale;
     k.spin_limit = a.spin_limit ? a.spin_limit : (1u << 21);
-    k.hdr = reinterpret_cast<WsHeader*>(ws);
-    k.hid_x = reinterpret_cast<uint64_t*>(ws + lay.hid);
-    k.qkv_x = reinterpret_cast<uint64_t*>(ws + lay.qkv);
-    k.att_x = reinterpret_cast<uint64_t*>(ws + lay.att);
-    k.act_x = reinterpret_cast<uint64_t*>(ws + lay.act);
-    k.mlp_x = reinterpret_cast<uint64_t*>(ws + lay.mlp);
+    k.trace = static_cast<uint64_t*>(a.trace);
+    k.ws = static_cast<uint8_t*>(a.workspace);
+    const bool debug = a.hidden_buffer || a.g_activations || a.g_residual || a.g_q || a.g_k || a.g_v ||
+                       a.g_attn_out || a.g_mlp_intermediate || a.g_normalized || a.block_max_vals ||
+                       a.block_max_idxs || a.trace;
 
     hipEvent_t t0 = static_cast<hipEvent_t>(a.timing_start), t1 = static_cast<hipEvent_t>(a.timing_stop);
     if (s.H == 1024 && s.I == 3072) {
-        return int8 ? launch_t<1024, 3072, Int8W>(k, stream, t0, t1) : launch_t<1024, 3072, Bf16W>(k, stream, t0, t1);
+        return int8 ? launch_t<1024, 3072, Int8W>(k, debug, stream, t0, t1) : launch_t<1024, 3072, Bf16W>(k, debug, stream, t0, t1);
     }
-    if (s.H == 2048 && s.I == 6144 && int8) return launch_t<2048, 6144, Int8W>(k, stream, t0, t1);
+    if (s.H == 2048 && s.I == 6144 && int8) return launch_t<2048, 6144, Int8W>(k, debug, stream, t0, t1);
     return set_error(MQ_ERR_UNSUPPORTED, "no decode kernel compiled for H=%d I=%d (%s)", s.H, s.I,
                      int8 ? "int8" : "bf16");
 }

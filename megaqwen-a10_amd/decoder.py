@@ -160,15 +160,6 @@ class _DecoderBase:
         a.lm_head_scale = lm_head_scale.data_ptr() if self._int8 else None
         a.cos_table, a.sin_table = cos_table.data_ptr(), sin_table.data_ptr()
         a.k_cache, a.v_cache = self.k_cache.data_ptr(), self.v_cache.data_ptr()
-        a.hidden_buffer = self.hidden_buffer.data_ptr()
-        a.g_activations = self.g_activations.data_ptr()
-        a.g_residual = self.g_residual.data_ptr()
-        a.g_q, a.g_k, a.g_v = self.g_q.data_ptr(), self.g_k.data_ptr(), self.g_v.data_ptr()
-        a.g_attn_out = self.g_attn_out.data_ptr()
-        a.g_mlp_intermediate = self.g_mlp_intermediate.data_ptr()
-        a.g_normalized = self.g_normalized.data_ptr()
-        a.block_max_vals = self.block_max_vals.data_ptr()
-        a.block_max_idxs = self.block_max_idxs.data_ptr()
         a.num_layers = num_layers
         a.max_seq_len = max_seq_len
         a.attn_scale = self.attn_scale
@@ -178,6 +169,7 @@ class _DecoderBase:
         a.spin_limit = 0
         self._args = a
         self._step_fn = self._lib.mq_int8_decode_step if self._int8 else self._lib.mq_bf16_decode_step
+        self._debug = False
 
     def _init_workspace(self):
         with torch.cuda.device(self.device):
@@ -231,11 +223,35 @@ class _DecoderBase:
         self._args.timing_start = start.cuda_event
         self._args.timing_stop = stop.cuda_event
 
+    _DEBUG_FIELDS = ("hidden_buffer", "g_activations", "g_residual", "g_q", "g_k", "g_v", "g_attn_out",
+                     "g_mlp_intermediate", "g_normalized", "block_max_vals", "block_max_idxs")
+
+    def enable_debug(self, on: bool = True) -> None:
+        """Fill the per-stage buffers behind the debug getters on every following step
+        (run_benchmark.py:174-183 semantics: the last layer's values). Off by default:
+        the kernel then carries no debug outputs."""
+        self._debug = bool(on)
+        for f in self._DEBUG_FIELDS:
+            setattr(self._args, f, getattr(self, f).data_ptr() if on else None)
+
+    def set_trace(self, buf) -> None:
+        """Record a per-stage timeline of every following step into ``buf`` (int64 tensor of
+        ``(num_layers + 1) * 10 * 256`` entries on the decoder's device); ``None`` stops it."""
+        if buf is None:
+            self._args.trace = None
+            return
+        need = (self.num_layers + 1) * 10 * 256
+        if buf.dtype != torch.int64 or buf.numel() < need or buf.device != self.device or not buf.is_contiguous():
+            raise ValueError(f"trace buffer must be a contiguous int64 tensor of >= {need} entries on {self.device}")
+        self._trace_buf = buf
+        self._args.trace = buf.data_ptr()
+
     def set_spin_limit(self, polls: int) -> None:
         """Bound on every in-kernel wait (0 = library default)."""
         self._args.spin_limit = int(polls)
 
-    # debug getters (run_benchmark.py:174-183): the last layer's values after a step
+    # debug getters (run_benchmark.py:174-183): the last layer's values after a step,
+    # filled while enable_debug() is on
     def get_hidden(self): return self.hidden_buffer
     def get_activations(self): return self.g_activations
     def get_residual(self): return self.g_residual
