@@ -122,7 +122,12 @@ def run_decode(args, mq, torch):
     dec.set_timing_events(None, None)
     kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     if min(toks) < 0:
-        raise RuntimeError("decode kernel reported a timeout")
+        status = dec._lib.mq_decode_check(dec.workspace.data_ptr(), None)
+        raise RuntimeError(f"decode step {toks.index(min(toks))} of the timed region failed: "
+                           f"status {status}: {mq._lib.last_error()}")
+    variant = mq.decode_variant(cfg.hidden_size, cfg.intermediate_size, int8=True)
+    kernel = {"xcd": "mq::decode_xcd_kernel<1024, 3072, mq::Int8W, false>",
+              "flat": "mq::decode_kernel<1024, 3072, mq::Int8W, false>"}[variant]
 
     # algorithmic bytes of each timed launch: positions PROMPT_LEN .. PROMPT_LEN+K-1
     bytes_total = sum(cfg.int8_step_bytes(cache_len=PROMPT_LEN + i + 1) for i in range(args.steps))
@@ -158,7 +163,7 @@ def run_decode(args, mq, torch):
                    "batch": 1, "prompt_len": PROMPT_LEN, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "mq::decode_kernel<1024, 3072, Int8W>",
+                     "kernel": kernel,
                      "kernel_avg_us": round(sum(kern_ms) / len(kern_ms) * 1e3, 2),
                      "bytes_per_launch_avg": int(bytes_total / args.steps)},
         "device_tok_s": round(args.steps / kern_s, 1),

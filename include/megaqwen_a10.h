@@ -154,6 +154,13 @@ int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream);
  * Synchronises `stream`. */
 int mq_decode_check(void* workspace, hipStream_t stream);
 
+/* Kernel variant for all following steps in this process: 0 = automatic
+ * (default: the XCD-aware kernel when workgroup g is placed on XCD g % 8,
+ * checked once per device), 1 = single-level exchange kernel, 2 = XCD-aware. */
+int mq_decode_set_variant(int variant);
+/* The variant a step with these dims would use now (1 or 2), or -status. */
+int mq_decode_variant(const mq_model_dims* dims, int int8);
+
 /* ---- reference-signature entry points (drop-in for the CUDA launchers) --- */
 /* a10_int8_decode_kernel.cu:821-842. Uses a library-owned workspace per
  * device (allocated on first use): calls that overlap on one device race.

@@ -13,7 +13,8 @@ library (``lib/libmegaqwen_a10.so``, declared in include/megaqwen_a10.h):
   seeded weights and the reference's tensor packing.
 """
 from .config import QWEN3_0_6B, QWEN3_1_7B, ModelConfig
-from .decoder import A10Decoder, A10Int8MegakernelDecoder, A10MegakernelDecoder
+from .decoder import (A10Decoder, A10Int8MegakernelDecoder, A10MegakernelDecoder, decode_variant,
+                      set_decode_variant)
 from .gemv import int8_gemv
 from .quant import quantize_per_channel
 from .rope import make_rope, precompute_rope_freqs
@@ -21,7 +22,7 @@ from .weights import pack_bf16, pack_int8, quantize_state, random_init_state, st
 
 __all__ = [
     "ModelConfig", "QWEN3_0_6B", "QWEN3_1_7B",
-    "A10Decoder", "A10Int8MegakernelDecoder", "A10MegakernelDecoder",
+    "A10Decoder", "A10Int8MegakernelDecoder", "A10MegakernelDecoder", "set_decode_variant", "decode_variant",
     "int8_gemv", "quantize_per_channel", "make_rope", "precompute_rope_freqs",
     "pack_bf16", "pack_int8", "quantize_state", "random_init_state", "state_digest",
 ]

@@ -84,6 +84,8 @@ _SIGNATURES = {
     "mq_int8_decode_step": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mq_bf16_decode_step": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mq_decode_check": (c_int, [c_void_p, c_void_p]),
+    "mq_decode_set_variant": (c_int, [c_int]),
+    "mq_decode_variant": (c_int, [c_void_p, c_int]),
     "launch_a10_int8_decode": (None, [c_int, c_void_p] + [c_void_p] * 20 + [c_int] * 4 + [c_float, c_void_p, c_void_p]),
     "launch_a10_decode": (None, [c_int, c_void_p] + [c_void_p] * 19 + [c_int] * 4 + [c_float, c_void_p]),
     "mq_int8_gemv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),

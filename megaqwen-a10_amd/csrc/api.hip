@@ -167,9 +167,28 @@ int mq_decode_check(void* workspace, hipStream_t stream) {
     e = hipMemcpy(&flag, static_cast<uint8_t*>(workspace) + offsetof(WsHeader, abort_flag), sizeof(flag),
                   hipMemcpyDeviceToHost);
     if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipMemcpy: %s", hipGetErrorString(e));
+    if (flag == 2) {
+        mark_xcd_unusable();
+        return set_error(MQ_ERR_TIMEOUT, "a workgroup ran on an unexpected XCD; the XCD-aware kernel is disabled for "
+                                         "this device, re-initialise the workspace and repeat the step");
+    }
     if (flag != 0)
         return set_error(MQ_ERR_TIMEOUT, "a bounded wait in the decode kernel expired; re-initialise the workspace");
     return MQ_OK;
+}
+
+int mq_decode_set_variant(int variant) {
+    clear_error();
+    return set_decode_variant(variant);
+}
+
+int mq_decode_variant(const mq_model_dims* dims, int int8) {
+    clear_error();
+    DecodeShape s;
+    int st = shape_of(dims, &s);
+    if (st != MQ_OK) return -st;
+    const int v = decode_variant_in_use(s, int8 != 0);
+    return v == 1 || v == 2 ? v : -v;
 }
 
 void launch_a10_int8_decode(int input_token_id, int* output_token_id, const void* embed_weight,

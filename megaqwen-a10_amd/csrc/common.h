@@ -106,6 +106,96 @@ __device__ __forceinline__ float transpose_reduce(float* v, int lane) {
     return x;
 }
 
+// ---- fp64 variants ---------------------------------------------------------------------
+// The decode kernels accumulate in fp64 and round to fp32 / bf16 only where the
+// reference stores a value: int8 x fp32 and bf16 x fp32 products are exact in
+// fp64 and CDNA runs fp64 FMA at the (non-packed) fp32 rate, so every stored
+// intermediate is the correctly rounded value of its defining expression.
+template <int M>
+__device__ __forceinline__ double partner64(double v) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const float lo = partner<M>(__uint_as_float((uint32_t)u));
+    const float hi = partner<M>(__uint_as_float((uint32_t)(u >> 32)));
+    return __longlong_as_double((long long)(((uint64_t)__float_as_uint(hi) << 32) | __float_as_uint(lo)));
+}
+
+__device__ __forceinline__ double wave_sum64(double v) {
+    v += partner64<1>(v);
+    v += partner64<2>(v);
+    v += partner64<4>(v);
+    v += partner64<8>(v);
+    v += partner64<16>(v);
+    v += partner64<32>(v);
+    return v;
+}
+
+__device__ __forceinline__ double wave_max64(double v) {
+    v = fmax(v, partner64<1>(v));
+    v = fmax(v, partner64<2>(v));
+    v = fmax(v, partner64<4>(v));
+    v = fmax(v, partner64<8>(v));
+    v = fmax(v, partner64<16>(v));
+    v = fmax(v, partner64<32>(v));
+    return v;
+}
+
+template <int M, int N>
+__device__ __forceinline__ void transpose_level64(double* v, int lane) {
+    const bool hi = (lane & M) != 0;
+#pragma unroll
+    for (int r = 0; r < N / 2; ++r) {
+        double keep = hi ? v[r + N / 2] : v[r];
+        double send = hi ? v[r] : v[r + N / 2];
+        v[r] = keep + partner64<M>(send);
+    }
+}
+
+// fp64 twin of transpose_reduce.
+template <int R, int G = 1>
+__device__ __forceinline__ double transpose_reduce64(double* v, int lane) {
+    constexpr int T = R / G;
+    if constexpr (T >= 2) transpose_level64<32, R>(v, lane);
+    if constexpr (T >= 4) transpose_level64<16, R / 2>(v, lane);
+    if constexpr (T >= 8) transpose_level64<8, R / 4>(v, lane);
+    if constexpr (T >= 16) transpose_level64<4, R / 8>(v, lane);
+    if constexpr (T >= 32) transpose_level64<2, R / 16>(v, lane);
+    if constexpr (T >= 64) transpose_level64<1, R / 32>(v, lane);
+    double x = v[0];
+#pragma unroll
+    for (int g = 1; g < G; ++g) x += v[g];
+    if constexpr (T < 64) x += partner64<1>(x);
+    if constexpr (T < 32) x += partner64<2>(x);
+    if constexpr (T < 16) x += partner64<4>(x);
+    if constexpr (T < 8) x += partner64<8>(x);
+    if constexpr (T < 4) x += partner64<16>(x);
+    if constexpr (T < 2) x += partner64<32>(x);
+    return x;
+}
+
+// 16 int8 weights against 16 fp64 activations (exact products, fp64 sum).
+__device__ __forceinline__ double dot_i8x16_d(uint4 w, const double2* x, double acc) {
+    const int8_t* b = reinterpret_cast<const int8_t*>(&w);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const double2 xv = x[j];
+        acc = fma((double)(float)b[2 * j], xv.x, acc);
+        acc = fma((double)(float)b[2 * j + 1], xv.y, acc);
+    }
+    return acc;
+}
+
+// 8 bf16 weights against 8 fp64 activations.
+__device__ __forceinline__ double dot_bf16x8_d(uint4 w, const double2* x, double acc) {
+    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const double2 xv = x[j];
+        acc = fma((double)__uint_as_float(wv[j] << 16), xv.x, acc);
+        acc = fma((double)__uint_as_float(wv[j] & 0xffff0000u), xv.y, acc);
+    }
+    return acc;
+}
+
 // ---- 16-byte dot products ----------------------------------------------------------------
 // int8 x16 against 16 fp32 activations (one v_cvt_f32_i32 with a sign-extended
 // byte select plus one FMA per element).
@@ -143,11 +233,13 @@ struct Int8W {
     static constexpr int kBytes = 1;
     static constexpr int kPerLane = 16;
     __device__ static float dot(uint4 w, const float4* x, float acc) { return dot_i8x16(w, x, acc); }
+    __device__ static double dotd(uint4 w, const double2* x, double acc) { return dot_i8x16_d(w, x, acc); }
 };
 struct Bf16W {
     static constexpr int kBytes = 2;
     static constexpr int kPerLane = 8;
     __device__ static float dot(uint4 w, const float4* x, float acc) { return dot_bf16x8(w, x, acc); }
+    __device__ static double dotd(uint4 w, const double2* x, double acc) { return dot_bf16x8_d(w, x, acc); }
 };
 
 // ---- activation vector in LDS, laid out per lane --------------------------------------
@@ -180,6 +272,31 @@ __device__ __forceinline__ float dot_frag(uint4 w, const float4* frag, float acc
         return W::dot(w, x, acc);
     }
 }
+
+// fp64 activation vector in LDS, per-lane order: lane l's P elements of chunk c
+// are P/2 double2 at xd[(c*(P/2) + j)*64 + l].
+template <class W>
+__device__ __forceinline__ int xd_index(int k) {          // double index of element k
+    constexpr int P = W::kPerLane;
+    const int chunk = k / (64 * P);
+    const int e = k % (64 * P);
+    const int lane = e / P;
+    const int t = e % P;
+    return ((chunk * (P / 2) + (t >> 1)) * 64 + lane) * 2 + (t & 1);
+}
+template <class W>
+__device__ __forceinline__ double dot_fragd(uint4 w, const double2* xd, int chunk, int lane, double acc) {
+    constexpr int P = W::kPerLane;
+    const double2* f = xd + (chunk * (P / 2)) * 64 + lane;
+    double2 x[P / 2];
+#pragma unroll
+    for (int j = 0; j < P / 2; ++j) x[j] = f[j * 64];
+    return W::dotd(w, x, acc);
+}
+
+// Keeps the compiler from moving memory accesses across this point (used to
+// issue step-independent loads before a wait instead of where they are used).
+__device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
 
 // ---- tagged exchange words --------------------------------------------------------------
 // A 64-bit word holds a 32-bit payload and a 32-bit tag naming the step,
@@ -231,11 +348,13 @@ struct Waiter {
     // N words at p[i * stride]: all N loads are issued before any is checked,
     // and every retry re-issues the still-missing ones together, so a wait
     // costs one memory round trip however many words a thread reads.
+    // Only the first `count` words are read (count <= N); the rest of `out` is 0.
     template <int N>
-    __device__ __forceinline__ void get_strided(const uint64_t* p, int stride, uint32_t tag, float (&out)[N]) {
+    __device__ __forceinline__ void get_strided(const uint64_t* p, int stride, uint32_t tag, float (&out)[N],
+                                                int count = N) {
         uint64_t w[N];
 #pragma unroll
-        for (int i = 0; i < N; ++i) w[i] = ll_load(p + i * stride);
+        for (int i = 0; i < N; ++i) w[i] = i < count ? ll_load(p + i * stride) : ((uint64_t)tag << 32);
         uint32_t pending = 0;
 #pragma unroll
         for (int i = 0; i < N; ++i) {

@@ -26,63 +26,21 @@
 // The workspace (internal.h: WsHeader + exchange buffers) carries the step
 // counter; the last workgroup to finish the LM head publishes the token and
 // advances it.
-#include "common.h"
-#include "internal.h"
+#include "decode_common.h"
 
 #include <hip/hip_ext.h>
+
+#include <atomic>
 
 #include <algorithm>
 
 namespace mq {
-
-constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / kWave;
-constexpr int kNWG = 256;
-constexpr int kMaxAttnLen = 4096;     // positions one workgroup attends over (scores in LDS)
-constexpr int kKvLds = 64;            // earlier positions whose K/V rows are prefetched into LDS
-constexpr int kMaxLayers = 64;        // per-layer pointer tables cached in LDS
-constexpr int kTracePoints = 10;      // timestamps per layer in the optional trace
-constexpr float kEps = 1e-6f;
-
-enum Stage { ST_QKV = 0, ST_ATTN = 1, ST_O = 2, ST_GU = 3, ST_DOWN = 4 };
-
-struct KArgs {
-    int token;
-    int* out_token;
-    const uint16_t* embed;
-    const LayerWeights* lw;
-    const ScalePointers* sp;
-    const uint16_t* final_norm;
-    const uint8_t* lm_w;
-    const float* lm_s;
-    const uint16_t* cos_t;
-    const uint16_t* sin_t;
-    uint16_t* kc;
-    uint16_t* vc;
-    uint16_t* dbg_hidden;
-    float* dbg_act;
-    float* dbg_resid;
-    float* dbg_q;
-    float* dbg_k;
-    float* dbg_v;
-    float* dbg_attn;
-    float* dbg_mlp;
-    float* dbg_norm;
-    float* dbg_bmax;
-    int* dbg_bidx;
-    int L, pos, cache_len, S, V;
-    float attn_scale;
-    uint32_t spin_limit;
-    uint64_t* trace;
-    uint8_t* ws;
-};
 
 // Workspace layout (after the 256-byte header): one 64-bit exchange word per
 // element of each handed-over vector, every region 256-byte aligned.
 struct Layout {
     size_t hid, qkv, att, act, mlp, total;
 };
-constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 constexpr Layout layout_for(int H, int I, int NQ, int NKV, int D) {
     Layout o{};
     o.hid = sizeof(WsHeader);
@@ -92,67 +50,6 @@ constexpr Layout layout_for(int H, int I, int NQ, int NKV, int D) {
     o.mlp = o.act + round256((size_t)H * 8);
     o.total = o.mlp + round256((size_t)I * 8);
     return o;
-}
-
-constexpr int pow2ceil(int x) { return x <= 1 ? 1 : 2 * pow2ceil((x + 1) / 2); }
-
-// One matvec stage of a workgroup: ROWS rows of K inputs, split into (row,
-// 1 KB chunk) items handed round-robin to the 8 waves. Weights are loaded
-// into registers by load() ahead of the input poll; compute() leaves one
-// partial sum per item in `part`.
-template <class W, int ROWS, int K>
-struct Stage_ {
-    static constexpr int CHUNK = 64 * W::kPerLane;
-    static constexpr int CH = K / CHUNK;
-    static constexpr int ITEMS = ROWS * CH;
-    static constexpr int IPW = (ITEMS + kWaves - 1) / kWaves;
-    static constexpr int R = pow2ceil(IPW);
-    static_assert(K % CHUNK == 0, "row length must be a whole number of 1 KB chunks");
-    uint4 w[IPW];
-
-    template <class RowPtr>
-    __device__ __forceinline__ void load(RowPtr rowptr, int wave, int lane) {
-#pragma unroll
-        for (int j = 0; j < IPW; ++j) {
-            const int it = wave + kWaves * j;
-            if (it < ITEMS)
-                w[j] = *reinterpret_cast<const uint4*>(rowptr(it / CH) + (it % CH) * 1024 + lane * 16);
-        }
-    }
-    __device__ __forceinline__ void compute(const float4* xs, float* part, int wave, int lane) const {
-        float acc[R];
-#pragma unroll
-        for (int j = 0; j < R; ++j) {
-            acc[j] = 0.0f;
-            const int it = wave + kWaves * j;
-            if (j < IPW && it < ITEMS) acc[j] = dot_frag<W>(w[j], xs_frag<W>(xs, it % CH, lane), 0.0f);
-        }
-        const float s = transpose_reduce<R>(acc, lane);
-        constexpr int span = kWave / R;
-        const int j = lane / span;
-        if ((lane % span) == 0 && j < IPW) {
-            const int it = wave + kWaves * j;
-            if (it < ITEMS) part[it] = s;
-        }
-    }
-    __device__ __forceinline__ static float row_sum(const float* part, int row) {
-        float s = 0.0f;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) s += part[row * CH + c];
-        return s;
-    }
-};
-
-template <int N>
-__device__ __forceinline__ float block_sum(float v, float* red, int wave, int lane) {
-    v = wave_sum(v);
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float t = 0.0f;
-#pragma unroll
-    for (int i = 0; i < N; ++i) t += red[i];
-    return t;
 }
 
 template <int H, int I, class W, bool kDebug>
@@ -170,17 +67,20 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
     static_assert(QKV % kNWG == 0 && H % kNWG == 0 && I % kNWG == 0, "rows must split evenly");
     static_assert(H % kThreads == 0 && QD % kThreads == 0 && I % kThreads == 0, "vectors must split evenly");
     static_assert(ROWS_QKV <= kThreads && CPW <= kThreads, "epilogue threads");
+    static_assert(Stage_<W, ROWS_QKV, H>::ITEMS <= 256 && Stage_<W, 2 * CPW, H>::ITEMS <= 256 &&
+                  Stage_<W, ROWS_H, QD>::ITEMS <= 256 && Stage_<W, ROWS_H, I>::ITEMS <= 256, "partials fit");
 
-    __shared__ float4 xs[XMAX / 4];
-    __shared__ float part[256];
-    __shared__ float red[2 * kWaves];
+    __shared__ double2 xd[XMAX / 2];                   // fp64 matvec input in per-lane order
+    __shared__ float4 xs[H / 4];                       // fp32 LM-head input in per-lane order
+    __shared__ double part[256];
+    __shared__ double red[2 * kWaves];
     __shared__ float rows_res[ROWS_H];
     __shared__ float att_in[4 * D];
     __shared__ float qrot[2 * D];
     __shared__ uint32_t kv_lds[2][kKvLds][D / 2];      // bf16 pairs of the prefetched K and V rows
     __shared__ uint32_t kv_curb[2][D / 2];             // this position's K and V (bf16 pairs)
-    __shared__ float scores[2 * kMaxAttnLen];
-    __shared__ float pv[kWaves * 2 * D];
+    __shared__ double scores[2][kMaxAttnLen];
+    __shared__ double pv[kWaves][2 * D];
     __shared__ float lm_best_v[kWaves];
     __shared__ int lm_best_i[kWaves];
     __shared__ LayerWeights s_lw[kMaxLayers];
@@ -191,6 +91,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
     const int lane = tid % kWave;
     const int wave = tid / kWave;
     float* xsf = reinterpret_cast<float*>(xs);
+    double* xdf = reinterpret_cast<double*>(xd);
 
     // step-independent reads first: the embedding row and the per-layer pointer tables
     float hv0[PT];
@@ -219,7 +120,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
         __hip_atomic_store(&hdr->best[(E + 1) & 1], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     const uint32_t tps = 5u * (uint32_t)a.L + 4u;
-    auto tag = [&](int l, int st) -> uint32_t { return ((E * tps + 5u * (uint32_t)l + (uint32_t)st) << 1) | 1u; };
+    // tags end in binary 01 (the XCD-aware kernel's end in 11): no overlap when the
+    // two kernels share a workspace
+    auto tag = [&](int l, int st) -> uint32_t { return ((E * tps + 5u * (uint32_t)l + (uint32_t)st) << 2) | 1u; };
     Waiter wt(&hdr->abort_flag, a.spin_limit);
     auto trace = [&](int l, int point) {
         if (kDebug && a.trace != nullptr && tid == 0)
@@ -228,6 +131,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
 
     const int64_t kv_head_stride = (int64_t)a.S * D;
     const int last = a.L - 1;
+    const double attn_scale = (double)a.attn_scale;
     __syncthreads();
 
     for (int l = 0; l < a.L; ++l) {
@@ -251,6 +155,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             float wln[PT];
 #pragma unroll
             for (int i = 0; i < PT; ++i) wln[i] = bf16_bits_to_f32(lnw[tid + i * kThreads]);
+            issue_fence();
 
             float hv[PT];
             if (l == 0) {
@@ -259,26 +164,26 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             } else {
                 wt.get_strided<PT>(hid_x + tid, kThreads, tag(l - 1, ST_DOWN), hv);
             }
-            float ss = 0.0f;
+            double ss = 0.0;
 #pragma unroll
-            for (int i = 0; i < PT; ++i) ss += hv[i] * hv[i];
-            const float tot = block_sum<kWaves>(ss, red, wave, lane);
+            for (int i = 0; i < PT; ++i) ss = fma((double)hv[i], (double)hv[i], ss);
+            const double tot = block_sum64<kWaves>(ss, red, wave, lane);
             trace(l, 0);
-            const float rstd = rsqrtf(tot / (float)H + kEps);
+            const double rstd = rms_scale(tot, H, kEps);
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
                 const int k = tid + i * kThreads;
-                xsf[xs_index<W>(k)] = hv[i] * rstd * wln[i];
+                xdf[xd_index<W>(k)] = (double)(float)((double)hv[i] * rstd * (double)wln[i]);
                 const int rr = k - g * ROWS_H;
                 if (rr >= 0 && rr < ROWS_H) rows_res[rr] = hv[i];
             }
             __syncthreads();
-            st.compute(xs, part, wave, lane);
+            st.compute(xd, part, wave, lane);
             __syncthreads();
             if (tid < ROWS_QKV) {
-                float v = Stage_<W, ROWS_QKV, H>::row_sum(part, tid);
-                if (kInt8) v = v * my_scale;
-                ll_put(&qkv_x[row0 + tid], __float_as_uint(v), tag(l, ST_QKV));
+                double v = Stage_<W, ROWS_QKV, H>::row_sum(part, tid);
+                if (kInt8) v = v * (double)my_scale;
+                ll_put(&qkv_x[row0 + tid], __float_as_uint((float)v), tag(l, ST_QKV));
             }
             trace(l, 1);
         }
@@ -318,6 +223,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                     pre[i] = *reinterpret_cast<const uint4*>(src);
                 }
             }
+            issue_fence();
             {
                 int word;
                 if (tid < 2 * D) word = 2 * h * D + tid;
@@ -338,14 +244,15 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             __syncthreads();
             trace(l, 2);
             if (wave < 3) {
+                // QK-norm and RoPE in fp64, rounded once to fp32
                 const float* src = att_in + wave * D;
-                const float x0 = src[lane], x1 = src[lane + 64];
-                const float ssq = wave_sum(x0 * x0 + x1 * x1);
-                const float sc = rsqrtf(ssq / (float)D + kEps);
-                const float y0 = x0 * sc * nw0;
-                const float y1 = x1 * sc * nw1;
-                const float o0 = y0 * c0 - y1 * s0;
-                const float o1 = y0 * s1 + y1 * c1;
+                const double x0 = src[lane], x1 = src[lane + 64];
+                const double ssq = wave_sum64(fma(x0, x0, x1 * x1));
+                const double sc = rms_scale(ssq, D, kEps);
+                const double y0 = x0 * sc * (double)nw0;
+                const double y1 = x1 * sc * (double)nw1;
+                const float o0 = (float)(y0 * (double)c0 - y1 * (double)s0);
+                const float o1 = (float)(y0 * (double)s1 + y1 * (double)c1);
                 if (wave < 2) {
                     qrot[wave * D + lane] = o0;
                     qrot[wave * D + lane + 64] = o1;
@@ -378,12 +285,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             // Positions < kKvLds (and the current one) come from LDS, later ones from HBM.
             {
                 const int qd = tid & 3;
-                float qa[32], qb[32];
-#pragma unroll
-                for (int i = 0; i < 32; ++i) { qa[i] = qrot[qd * 32 + i]; qb[i] = qrot[D + qd * 32 + i]; }
+                const float* qa = qrot + qd * 32;          // read from LDS at each use (register budget)
+                const float* qb = qrot + D + qd * 32;
                 for (int j0 = 0; j0 < n; j0 += kThreads / 4) {
                     const int j = j0 + (tid >> 2);
-                    float d0 = 0.0f, d1 = 0.0f;
+                    double d0 = 0.0, d1 = 0.0;
                     if (j < n) {
                         uint4 kw[4];
                         if (j == a.pos || j < kKvLds) {
@@ -401,76 +307,67 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                             const uint32_t wv[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w};
 #pragma unroll
                             for (int e = 0; e < 4; ++e) {
-                                const float klo = __uint_as_float(wv[e] << 16);
-                                const float khi = __uint_as_float(wv[e] & 0xffff0000u);
-                                d0 = fmaf(qa[u * 8 + 2 * e], klo, d0);
-                                d0 = fmaf(qa[u * 8 + 2 * e + 1], khi, d0);
-                                d1 = fmaf(qb[u * 8 + 2 * e], klo, d1);
-                                d1 = fmaf(qb[u * 8 + 2 * e + 1], khi, d1);
+                                const double klo = __uint_as_float(wv[e] << 16);
+                                const double khi = __uint_as_float(wv[e] & 0xffff0000u);
+                                d0 = fma((double)qa[u * 8 + 2 * e], klo, d0);
+                                d0 = fma((double)qa[u * 8 + 2 * e + 1], khi, d0);
+                                d1 = fma((double)qb[u * 8 + 2 * e], klo, d1);
+                                d1 = fma((double)qb[u * 8 + 2 * e + 1], khi, d1);
                             }
                         }
                     }
-                    d0 += partner<1>(d0); d0 += partner<2>(d0);
-                    d1 += partner<1>(d1); d1 += partner<2>(d1);
+                    d0 += partner64<1>(d0); d0 += partner64<2>(d0);
+                    d1 += partner64<1>(d1); d1 += partner64<2>(d1);
                     if (j < n && qd == 0) {
-                        scores[j] = d0 * a.attn_scale;
-                        scores[kMaxAttnLen + j] = d1 * a.attn_scale;
+                        scores[0][j] = d0 * attn_scale;
+                        scores[1][j] = d1 * attn_scale;
                     }
                 }
             }
             __syncthreads();
-            // softmax statistics over the n positions, both heads
-            float m0 = -INFINITY, m1 = -INFINITY;
-            for (int j = tid; j < n; j += kThreads) { m0 = fmaxf(m0, scores[j]); m1 = fmaxf(m1, scores[kMaxAttnLen + j]); }
-            m0 = wave_max(m0);
-            m1 = wave_max(m1);
-            if (lane == 0) { red[wave] = m0; red[kWaves + wave] = m1; }
-            __syncthreads();
-            float M0 = red[0], M1 = red[kWaves];
-#pragma unroll
-            for (int i = 1; i < kWaves; ++i) { M0 = fmaxf(M0, red[i]); M1 = fmaxf(M1, red[kWaves + i]); }
-            float l0 = 0.0f, l1 = 0.0f;
-            for (int j = tid; j < n; j += kThreads) {
-                const float p0 = expf(scores[j] - M0), p1 = expf(scores[kMaxAttnLen + j] - M1);
-                scores[j] = p0;
-                scores[kMaxAttnLen + j] = p1;
-                l0 += p0;
-                l1 += p1;
+            // softmax (fp64): wave 0 handles head 0, wave 1 head 1 (max, exp in place, sum)
+            if (wave < 2) {
+                double* sv = scores[wave];
+                double m = -INFINITY;
+                for (int j = lane; j < n; j += kWave) m = fmax(m, sv[j]);
+                m = wave_max64(m);
+                double lsum = 0.0;
+                for (int j = lane; j < n; j += kWave) {
+                    const double p = exp(sv[j] - m);
+                    sv[j] = p;
+                    lsum += p;
+                }
+                lsum = wave_sum64(lsum);
+                if (lane == 0) red[wave] = lsum;
             }
-            l0 = wave_sum(l0);
-            l1 = wave_sum(l1);
             __syncthreads();
-            if (lane == 0) { red[wave] = l0; red[kWaves + wave] = l1; }
-            __syncthreads();
-            float L0 = 0.0f, L1 = 0.0f;
-#pragma unroll
-            for (int i = 0; i < kWaves; ++i) { L0 += red[i]; L1 += red[kWaves + i]; }
+            const double L0 = red[0], L1 = red[1];
 
             // P @ V: lane owns a pair of dims, the 8 waves split the positions
             {
                 const int dp = lane;
-                float a00 = 0.0f, a01 = 0.0f, a10 = 0.0f, a11 = 0.0f;
+                double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
                 for (int j = wave; j < n; j += kWaves) {
                     const uint32_t vw = j == a.pos ? kv_curb[1][dp]
                                       : j < kKvLds ? kv_lds[1][j][dp]
                                                    : *reinterpret_cast<const uint32_t*>(a.vc + cache_base + (int64_t)j * D + 2 * dp);
-                    const float v0 = __uint_as_float(vw << 16);
-                    const float v1 = __uint_as_float(vw & 0xffff0000u);
-                    const float p0 = scores[j], p1 = scores[kMaxAttnLen + j];
-                    a00 = fmaf(p0, v0, a00); a01 = fmaf(p0, v1, a01);
-                    a10 = fmaf(p1, v0, a10); a11 = fmaf(p1, v1, a11);
+                    const double v0 = __uint_as_float(vw << 16);
+                    const double v1 = __uint_as_float(vw & 0xffff0000u);
+                    const double p0 = scores[0][j], p1 = scores[1][j];
+                    a00 = fma(p0, v0, a00); a01 = fma(p0, v1, a01);
+                    a10 = fma(p1, v0, a10); a11 = fma(p1, v1, a11);
                 }
-                pv[wave * 2 * D + 2 * dp] = a00;
-                pv[wave * 2 * D + 2 * dp + 1] = a01;
-                pv[wave * 2 * D + D + 2 * dp] = a10;
-                pv[wave * 2 * D + D + 2 * dp + 1] = a11;
+                pv[wave][2 * dp] = a00;
+                pv[wave][2 * dp + 1] = a01;
+                pv[wave][D + 2 * dp] = a10;
+                pv[wave][D + 2 * dp + 1] = a11;
             }
             __syncthreads();
             if (tid < 2 * D) {
-                float o = 0.0f;
+                double od = 0.0;
 #pragma unroll
-                for (int w = 0; w < kWaves; ++w) o += pv[w * 2 * D + tid];
-                o = o / (tid < D ? L0 : L1);
+                for (int w = 0; w < kWaves; ++w) od += pv[w][tid];
+                const float o = (float)(od / (tid < D ? L0 : L1));
                 const int word = 2 * h * D + tid;
                 ll_put(&att_x[word], __float_as_uint(o), tag(l, ST_ATTN));
                 if (l == last && kDebug && a.dbg_attn) a.dbg_attn[word] = o;
@@ -486,21 +383,22 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             st.load([&](int r) { return base + (int64_t)(row0 + r) * QD * ES; }, wave, lane);
             float my_scale = 1.0f;
             if (kInt8 && tid < ROWS_H) my_scale = sp.o_scale[row0 + tid];
+            issue_fence();
             {
                 float v[QD / kThreads];
                 wt.get_strided<QD / kThreads>(att_x + tid, kThreads, tag(l, ST_ATTN), v);
 #pragma unroll
-                for (int i = 0; i < QD / kThreads; ++i) xsf[xs_index<W>(tid + i * kThreads)] = v[i];
+                for (int i = 0; i < QD / kThreads; ++i) xdf[xd_index<W>(tid + i * kThreads)] = v[i];
             }
             __syncthreads();
             trace(l, 4);
-            st.compute(xs, part, wave, lane);
+            st.compute(xd, part, wave, lane);
             __syncthreads();
             if (tid < ROWS_H) {
-                float v = Stage_<W, ROWS_H, QD>::row_sum(part, tid);
-                if (kInt8) v = v * my_scale;
-                v = v + rows_res[tid];
-                ll_put(&act_x[row0 + tid], __float_as_uint(v), tag(l, ST_O));
+                double v = Stage_<W, ROWS_H, QD>::row_sum(part, tid);
+                if (kInt8) v = v * (double)my_scale;
+                const float x = (float)(v + (double)rows_res[tid]);
+                ll_put(&act_x[row0 + tid], __float_as_uint(x), tag(l, ST_O));
             }
             trace(l, 5);
         }
@@ -520,19 +418,20 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             float wpn[PT];
 #pragma unroll
             for (int i = 0; i < PT; ++i) wpn[i] = bf16_bits_to_f32(pnw[tid + i * kThreads]);
+            issue_fence();
             float av[PT];
             wt.get_strided<PT>(act_x + tid, kThreads, tag(l, ST_O), av);
-            float ss = 0.0f;
+            double ss = 0.0;
 #pragma unroll
-            for (int i = 0; i < PT; ++i) ss += av[i] * av[i];
-            const float tot = block_sum<kWaves>(ss, red, wave, lane);
+            for (int i = 0; i < PT; ++i) ss = fma((double)av[i], (double)av[i], ss);
+            const double tot = block_sum64<kWaves>(ss, red, wave, lane);
             trace(l, 6);
-            const float rstd = rsqrtf(tot / (float)H + kEps);
+            const double rstd = rms_scale(tot, H, kEps);
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
                 const int k = tid + i * kThreads;
-                const float nv = av[i] * rstd * wpn[i];
-                xsf[xs_index<W>(k)] = nv;
+                const float nv = (float)((double)av[i] * rstd * (double)wpn[i]);
+                xdf[xd_index<W>(k)] = nv;
                 const int rr = k - g * ROWS_H;
                 if (rr >= 0 && rr < ROWS_H) rows_res[rr] = av[i];
                 if (kDebug && l == last && g == 0) {
@@ -541,13 +440,13 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                 }
             }
             __syncthreads();
-            st.compute(xs, part, wave, lane);
+            st.compute(xd, part, wave, lane);
             __syncthreads();
             if (tid < CPW) {
-                float gs = Stage_<W, 2 * CPW, H>::row_sum(part, tid);
-                float us = Stage_<W, 2 * CPW, H>::row_sum(part, CPW + tid);
-                if (kInt8) { gs = gs * gsc; us = us * usc; }
-                const float m = gs / (1.0f + expf(-gs)) * us;
+                double gs = Stage_<W, 2 * CPW, H>::row_sum(part, tid);
+                double us = Stage_<W, 2 * CPW, H>::row_sum(part, CPW + tid);
+                if (kInt8) { gs = gs * (double)gsc; us = us * (double)usc; }
+                const float m = (float)(gs / (1.0 + exp(-gs)) * us);
                 ll_put(&mlp_x[c0 + tid], __float_as_uint(m), tag(l, ST_GU));
                 if (l == last && kDebug && a.dbg_mlp) a.dbg_mlp[c0 + tid] = m;
             }
@@ -562,21 +461,21 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             st.load([&](int r) { return base + (int64_t)(row0 + r) * I * ES; }, wave, lane);
             float my_scale = 1.0f;
             if (kInt8 && tid < ROWS_H) my_scale = sp.down_scale[row0 + tid];
+            issue_fence();
             {
                 float v[I / kThreads];
                 wt.get_strided<I / kThreads>(mlp_x + tid, kThreads, tag(l, ST_GU), v);
 #pragma unroll
-                for (int i = 0; i < I / kThreads; ++i) xsf[xs_index<W>(tid + i * kThreads)] = v[i];
+                for (int i = 0; i < I / kThreads; ++i) xdf[xd_index<W>(tid + i * kThreads)] = v[i];
             }
             __syncthreads();
             trace(l, 8);
-            st.compute(xs, part, wave, lane);
+            st.compute(xd, part, wave, lane);
             __syncthreads();
             if (tid < ROWS_H) {
-                float v = Stage_<W, ROWS_H, I>::row_sum(part, tid);
-                if (kInt8) v = v * my_scale;
-                v = v + rows_res[tid];
-                const uint32_t hb = f32_to_bf16_bits(v);
+                double v = Stage_<W, ROWS_H, I>::row_sum(part, tid);
+                if (kInt8) v = v * (double)my_scale;
+                const uint32_t hb = f32_to_bf16_bits((float)(v + (double)rows_res[tid]));
                 ll_put(&hid_x[row0 + tid], __float_as_uint(bf16_bits_to_f32(hb)), tag(l, ST_DOWN));
                 if (l == last && kDebug && a.dbg_hidden) a.dbg_hidden[row0 + tid] = (uint16_t)hb;
             }
@@ -614,19 +513,20 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
         float wfn[PT];
 #pragma unroll
         for (int i = 0; i < PT; ++i) wfn[i] = bf16_bits_to_f32(a.final_norm[tid + i * kThreads]);
+        issue_fence();
 
         float hv[PT];
         wt.get_strided<PT>(hid_x + tid, kThreads, tag(last, ST_DOWN), hv);
-        float ss = 0.0f;
+        double ss = 0.0;
 #pragma unroll
-        for (int i = 0; i < PT; ++i) ss += hv[i] * hv[i];
-        const float tot = block_sum<kWaves>(ss, red, wave, lane);
+        for (int i = 0; i < PT; ++i) ss = fma((double)hv[i], (double)hv[i], ss);
+        const double tot = block_sum64<kWaves>(ss, red, wave, lane);
         trace(a.L, 0);
-        const float rstd = rsqrtf(tot / (float)H + kEps);
+        const double rstd = rms_scale(tot, H, kEps);
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
             const int k = tid + i * kThreads;
-            const float nv = hv[i] * rstd * wfn[i];
+            const float nv = (float)((double)hv[i] * rstd * (double)wfn[i]);
             xsf[xs_index<W>(k)] = nv;
             if (g == 0 && kDebug && a.dbg_norm) a.dbg_norm[k] = nv;
         }
@@ -689,11 +589,75 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
 
 // ---------------- host side ----------------
 
-size_t decode_workspace_bytes(const DecodeShape& s) { return layout_for(s.H, s.I, s.NQ, s.NKV, s.D).total; }
+size_t decode_workspace_bytes(const DecodeShape& s) {
+    const size_t a = layout_for(s.H, s.I, s.NQ, s.NKV, s.D).total, b = decode_xcd_workspace_bytes(s);
+    return a > b ? a : b;
+}
+
+// ---- kernel variant selection ----
+__global__ void xcc_map_kernel(uint32_t* out) {
+    if (threadIdx.x == 0) {
+        uint32_t v;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+        out[blockIdx.x] = v & 0xfu;
+    }
+}
+
+static std::atomic<int> g_variant{0};
+static std::atomic<int> g_xcd_ok[64];     // 0 unknown, 1 placement verified, 2 not usable
+
+int set_decode_variant(int variant) {
+    if (variant < 0 || variant > 2) return set_error(MQ_ERR_INVALID_ARGUMENT, "variant %d not in {0,1,2}", variant);
+    g_variant = variant;
+    return MQ_OK;
+}
+
+void mark_xcd_unusable() {
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) g_xcd_ok[dev] = 2;
+}
+
+// The XCD-aware kernel takes each workgroup's XCD from the hardware and its
+// rank from g / 8, which needs the workgroups of one residue class of g mod 8
+// to share an XCD and the 8 classes to fill the 8 XCDs; verified once per
+// device with a launch of the same shape.
+static bool xcd_placement_ok() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    int st = g_xcd_ok[dev].load();
+    if (st != 0) return st == 1;
+    bool ok = false;
+    uint32_t* d = nullptr;
+    if (hipMalloc(&d, kNWG * sizeof(uint32_t)) == hipSuccess) {
+        hipLaunchKernelGGL(xcc_map_kernel, dim3(kNWG), dim3(kThreads), 0, 0, d);
+        uint32_t h[kNWG];
+        if (hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
+            hipMemcpy(h, d, sizeof(h), hipMemcpyDeviceToHost) == hipSuccess) {
+            bool seen[8] = {false};
+            ok = true;
+            for (int i = 0; i < 8; ++i) {
+                ok = ok && h[i] < 8 && !seen[h[i]];
+                if (ok) seen[h[i]] = true;
+            }
+            for (int i = 8; i < kNWG; ++i) ok = ok && (h[i] == h[i % 8]);
+        }
+        hipFree(d);
+    }
+    g_xcd_ok[dev] = ok ? 1 : 2;
+    return ok;
+}
+
+int decode_variant_in_use(const DecodeShape& s, bool int8) {
+    const int v = g_variant.load();
+    const bool have_xcd = decode_xcd_kernel_ptr(s, int8, false) != nullptr;
+    if (v == 1) return 1;
+    if (v == 2) return have_xcd ? 2 : set_error(MQ_ERR_UNSUPPORTED, "no XCD-aware kernel for these dims");
+    return (have_xcd && xcd_placement_ok()) ? 2 : 1;
+}
 
 // All kNWG workgroups wait on each other, so they must be resident at once;
 // checked once per (kernel, device) from the occupancy calculator.
-static int check_residency(const void* fn) {
+int check_residency(const void* fn) {
     static thread_local const void* checked_fn[64] = {nullptr};
     static thread_local int checked[64] = {0};
     int dev = 0;
@@ -774,6 +738,9 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
                        a.block_max_idxs || a.trace;
 
     hipEvent_t t0 = static_cast<hipEvent_t>(a.timing_start), t1 = static_cast<hipEvent_t>(a.timing_stop);
+    const int variant = decode_variant_in_use(s, int8);
+    if (variant == 2) return launch_decode_xcd(k, s, int8, debug, stream, t0, t1);
+    if (variant != 1) return variant;
     if (s.H == 1024 && s.I == 3072) {
         return int8 ? launch_t<1024, 3072, Int8W>(k, debug, stream, t0, t1) : launch_t<1024, 3072, Bf16W>(k, debug, stream, t0, t1);
     }

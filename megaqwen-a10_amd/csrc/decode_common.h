@@ -1,0 +1,134 @@
+// Pieces shared by the two decode kernels (decode.hip: one exchange level
+// over all 256 workgroups; decode_xcd.hip: XCD-local exchanges plus two
+// cross-XCD reductions per layer): launch shape, kernel arguments, the
+// register-staged matvec stage and a workgroup sum.
+#pragma once
+
+#include "common.h"
+#include "internal.h"
+
+namespace mq {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kNWG = 256;
+constexpr int kMaxAttnLen = 1024;     // positions one workgroup attends over (fp64 scores in LDS)
+constexpr int kKvLds = 64;            // earlier positions whose K/V rows are prefetched into LDS
+constexpr int kMaxLayers = 64;        // per-layer pointer tables cached in LDS
+constexpr int kTracePoints = 10;      // timestamps per layer in the optional trace
+constexpr double kEps = 1e-6;        // RMSNorm epsilon (config.cuh:40), applied in fp64
+
+enum Stage { ST_QKV = 0, ST_ATTN = 1, ST_O = 2, ST_GU = 3, ST_DOWN = 4 };
+
+struct KArgs {
+    int token;
+    int* out_token;
+    const uint16_t* embed;
+    const LayerWeights* lw;
+    const ScalePointers* sp;
+    const uint16_t* final_norm;
+    const uint8_t* lm_w;
+    const float* lm_s;
+    const uint16_t* cos_t;
+    const uint16_t* sin_t;
+    uint16_t* kc;
+    uint16_t* vc;
+    uint16_t* dbg_hidden;
+    float* dbg_act;
+    float* dbg_resid;
+    float* dbg_q;
+    float* dbg_k;
+    float* dbg_v;
+    float* dbg_attn;
+    float* dbg_mlp;
+    float* dbg_norm;
+    float* dbg_bmax;
+    int* dbg_bidx;
+    int L, pos, cache_len, S, V;
+    float attn_scale;
+    uint32_t spin_limit;
+    uint64_t* trace;
+    uint8_t* ws;
+};
+
+constexpr int pow2ceil(int x) { return x <= 1 ? 1 : 2 * pow2ceil((x + 1) / 2); }
+
+// One matvec stage of a workgroup: ROWS rows of K inputs, split into (row,
+// 1 KB chunk) items handed round-robin to the 8 waves. Weights are loaded
+// into registers by load() ahead of the input wait; compute() leaves one fp64
+// partial sum per item in `part` (the input vector is fp64 in per-lane order,
+// xd_index()).
+template <class W, int ROWS, int K>
+struct Stage_ {
+    static constexpr int CHUNK = 64 * W::kPerLane;
+    static constexpr int CH = K / CHUNK;
+    static constexpr int ITEMS = ROWS * CH;
+    static constexpr int IPW = (ITEMS + kWaves - 1) / kWaves;
+    static constexpr int R = pow2ceil(IPW);
+    static_assert(K % CHUNK == 0, "row length must be a whole number of 1 KB chunks");
+    uint4 w[IPW];
+
+    template <class RowPtr>
+    __device__ __forceinline__ void load(RowPtr rowptr, int wave, int lane) {
+#pragma unroll
+        for (int j = 0; j < IPW; ++j) {
+            const int it = wave + kWaves * j;
+            if (it < ITEMS)
+                w[j] = *reinterpret_cast<const uint4*>(rowptr(it / CH) + (it % CH) * 1024 + lane * 16);
+        }
+    }
+    __device__ __forceinline__ void compute(const double2* xd, double* part, int wave, int lane) const {
+        double acc[R];
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+            acc[j] = 0.0;
+            const int it = wave + kWaves * j;
+            if (j < IPW && it < ITEMS) acc[j] = dot_fragd<W>(w[j], xd, it % CH, lane, 0.0);
+        }
+        const double s = transpose_reduce64<R>(acc, lane);
+        constexpr int span = kWave / R;
+        const int j = lane / span;
+        if ((lane % span) == 0 && j < IPW) {
+            const int it = wave + kWaves * j;
+            if (it < ITEMS) part[it] = s;
+        }
+    }
+    __device__ __forceinline__ static double row_sum(const double* part, int row) {
+        double s = 0.0;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) s += part[row * CH + c];
+        return s;
+    }
+};
+
+// Workgroup sum in fp64 (fixed order over the waves).
+template <int N>
+__device__ __forceinline__ double block_sum64(double v, double* red, int wave, int lane) {
+    v = wave_sum64(v);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) t += red[i];
+    return t;
+}
+
+// RMSNorm scale 1/sqrt(mean + eps) in fp64 (IEEE sqrt and division).
+__device__ __forceinline__ double rms_scale(double sumsq, int n, double eps) {
+    return 1.0 / sqrt(sumsq / (double)n + eps);
+}
+
+constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+// All kNWG workgroups wait on each other, so they must be resident at once:
+// checked once per (kernel, device) with the occupancy calculator.
+int check_residency(const void* fn);
+
+// XCD-aware kernel (decode_xcd.hip).
+size_t decode_xcd_workspace_bytes(const DecodeShape& s);
+const void* decode_xcd_kernel_ptr(const DecodeShape& s, bool int8, bool debug);
+int launch_decode_xcd(const KArgs& k, const DecodeShape& s, bool int8, bool debug, hipStream_t stream,
+                      hipEvent_t t0, hipEvent_t t1);
+
+}  // namespace mq

@@ -1,0 +1,778 @@
+// XCD-aware persistent decode step (the fast path on MI355X).
+//
+// Same computation as decode.hip (a10_int8_decode_kernel.cu:21-815, and the
+// bf16 twin), laid out for 8 XCDs x 32 CUs: workgroup g takes the XCD it runs
+// on, x = HW_REG_XCC_ID, as its group and r = g / 8 as its rank there, and KV
+// head x with its two query heads belongs to XCD x. The dispatcher deals the
+// workgroups of a launch round-robin over the 8 XCDs, so each XCD receives one
+// residue class of g mod 8 and (x, r) covers the 8 x 32 roles exactly once,
+// whichever XCD the round-robin starts on. Per layer:
+//
+//   A  QKV      rank r: 16 of XCD x's 512 q|k|v rows          -> XCD-local words
+//   B  attn     every rank of XCD x: QK-norm, RoPE, attention over the bf16
+//               KV cache for head pair x (redundant; the KV rows are shared
+//               through the XCD's L2); rank 0 writes the cache row
+//   C  O        rank r: rows [H/32 r, +H/32) of O[:, 256x : 256x+256]
+//                                                             -> cross-XCD partials
+//   D  reduce   rank r sums its rows' 8 partials in XCD order, applies the
+//               row scale and the residual                    -> XCD-local act
+//   E  gate/up  rank r: channels [I/8 x + I/256 r, +I/256), SwiGLU
+//                                                             -> XCD-local mlp
+//   F  down     rank r: rows [H/32 r, +H/32) of down[:, I/8 x : I/8 (x+1)]
+//                                                             -> cross-XCD partials
+//   G  reduce   as D, plus bf16 rounding                      -> XCD-local hidden
+//
+// so each layer has four exchanges inside one XCD (plain stores land in the
+// XCD's shared L2; agent-scope loads read it) and two across XCDs
+// (agent-scope stores and loads). Words carry a (step, layer, stage) tag as in
+// decode.hip. Every reduction sums in a fixed order, so all ranks see identical
+// values and results are bitwise reproducible. The LM head is split over all
+// 256 workgroups; its argmax is gathered per XCD and then by workgroup 0.
+//
+// Each stage's weights (and scales / norm gains) are loaded into registers
+// before the preceding wait, so their fetch overlaps the exchange latency.
+#include "decode_common.h"
+
+#include <hip/hip_ext.h>
+
+namespace mq {
+
+constexpr int kNX = 8;                 // XCDs, one KV head each
+constexpr int kGS = kNWG / kNX;        // workgroups per XCD
+
+enum XStage { XS_QKV = 0, XS_PO = 1, XS_ACT = 2, XS_MLP = 3, XS_PD = 4, XS_HID = 5 };
+constexpr uint32_t kXStages = 6;
+
+struct XLayout {
+    size_t qkvx, actx, mlpx, hidx, lmx, po, pd, lmc, total;
+};
+constexpr XLayout xlayout_for(int H, int I) {
+    XLayout o{};
+    size_t off = sizeof(WsHeader);
+    o.qkvx = off; off += round256((size_t)kNX * 512 * 8);
+    o.actx = off; off += round256((size_t)kNX * H * 8);
+    o.mlpx = off; off += round256((size_t)kNX * (I / kNX) * 8);
+    o.hidx = off; off += round256((size_t)kNX * H * 8);
+    o.lmx = off; off += round256((size_t)kNX * kGS * 2 * 8);
+    o.po = off; off += round256((size_t)2 * kNX * H * 8);      // fp64 partials as hi|lo fp32 words
+    o.pd = off; off += round256((size_t)2 * kNX * H * 8);
+    o.lmc = off; off += round256((size_t)kNX * 2 * 8);
+    o.total = off;
+    return o;
+}
+
+// XCD-local exchange store. A wavefront-scope relaxed atomic store is a plain
+// global_store (no cache-scope bits): the CU's L1 is write-through, so the word
+// lands in this XCD's shared L2, where the other ranks' agent-scope loads (which
+// bypass their own L1) read it about twice as fast as an agent-scope store
+// (measured on MI355X: 0.27 us vs 0.52 us one-way). It is not visible to other
+// XCDs, which never read these buffers.
+__device__ __forceinline__ void ll_put_xcd(uint64_t* p, uint32_t payload, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+
+__device__ __forceinline__ uint32_t hw_xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 0xfu;
+}
+
+// Partial-row matvec piece: 16 bytes of weights against the matching fp32
+// activations held contiguously in LDS.
+template <class W>
+__device__ __forceinline__ float dot_piece(uint4 w, const float* x) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    return W::dot(w, x4, 0.0f);
+}
+
+template <int H, int I, class W, bool kDebug>
+__global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
+    constexpr int D = 128;
+    constexpr int ES = W::kBytes;
+    constexpr bool kInt8 = (ES == 1);
+    constexpr XLayout kLay = xlayout_for(H, I);
+    constexpr int GR = 4 * D;               // q|k|v rows of one XCD (2 query heads, 1 K, 1 V)
+    constexpr int ROWS_A = GR / kGS;        // QKV rows per workgroup
+    constexpr int RPW = H / kGS;            // O / down output rows per workgroup
+    constexpr int IX = I / kNX;             // intermediate channels per XCD
+    constexpr int CPW = IX / kGS;           // gate/up channels per workgroup
+    constexpr int PT = H / kThreads;        // hidden elements per thread
+    constexpr int AD = 2 * D;               // attention outputs per XCD
+    constexpr int EPP = 16 / ES;            // weight elements per 16-byte piece
+    constexpr int PC_O = AD / EPP;          // pieces per O row segment
+    constexpr int NIT_O = RPW * PC_O;
+    constexpr int PT_O = (NIT_O + kThreads - 1) / kThreads;
+    constexpr int PC_D = IX / EPP;          // pieces per down row segment
+    constexpr int NIT_D = RPW * PC_D;
+    constexpr int PT_D = (NIT_D + kThreads - 1) / kThreads;
+    constexpr int PARTN = (NIT_D > NIT_O ? NIT_D : NIT_O) > 256 ? (NIT_D > NIT_O ? NIT_D : NIT_O) : 256;
+    constexpr int MLP_PT = (IX + kThreads - 1) / kThreads;
+    static_assert(GR % kGS == 0 && H % kGS == 0 && IX % kGS == 0 && H % kThreads == 0, "even split");
+    static_assert(RPW <= kThreads && AD % EPP == 0 && IX % EPP == 0, "shapes");
+
+    __shared__ double2 xd[H / 2];           // fp64 matvec input in per-lane order (QKV, gate/up)
+    __shared__ float4 xs[H / 4];            // fp32 LM-head input in per-lane order
+    __shared__ float hid[H];                // layer input (bf16 values)
+    __shared__ float act[H];                // post-attention residual stream (fp32 values)
+    __shared__ double attn_d[AD];           // this XCD's attention outputs (fp32 values)
+    __shared__ double mlp_d[IX];            // this XCD's SwiGLU outputs (fp32 values)
+    __shared__ double part[PARTN];
+    __shared__ double red[2 * kWaves];
+    __shared__ float att_in[GR];
+    __shared__ float qrot[2 * D];
+    __shared__ uint32_t kv_lds[2][kKvLds][D / 2];
+    __shared__ uint32_t kv_curb[2][D / 2];
+    __shared__ double scores[2][kMaxAttnLen];
+    __shared__ double pv[kWaves][2 * D];
+    __shared__ float lm_v[kWaves];
+    __shared__ int lm_i[kWaves];
+    __shared__ LayerWeights s_lw[kMaxLayers];
+    __shared__ ScalePointers s_sp[kMaxLayers];
+
+    const int g = blockIdx.x;
+    const int x = (int)hw_xcc_id();
+    const int r = g / kNX;
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
+    const int wave = tid / kWave;
+    double* xdf = reinterpret_cast<double*>(xd);
+    float* xsf = reinterpret_cast<float*>(xs);
+
+    WsHeader* hdr = reinterpret_cast<WsHeader*>(a.ws);
+    uint64_t* const qkvx = reinterpret_cast<uint64_t*>(a.ws + kLay.qkvx) + (size_t)x * GR;
+    uint64_t* const actx = reinterpret_cast<uint64_t*>(a.ws + kLay.actx) + (size_t)x * H;
+    uint64_t* const mlpx = reinterpret_cast<uint64_t*>(a.ws + kLay.mlpx) + (size_t)x * IX;
+    uint64_t* const hidx = reinterpret_cast<uint64_t*>(a.ws + kLay.hidx) + (size_t)x * H;
+    uint64_t* const lmx = reinterpret_cast<uint64_t*>(a.ws + kLay.lmx) + (size_t)x * kGS * 2;
+    uint64_t* const po = reinterpret_cast<uint64_t*>(a.ws + kLay.po);    // [hi|lo][8][H]
+    uint64_t* const pd = reinterpret_cast<uint64_t*>(a.ws + kLay.pd);    // [hi|lo][8][H]
+    uint64_t* const lmc = reinterpret_cast<uint64_t*>(a.ws + kLay.lmc);
+
+    // step-independent reads first
+    float hv0[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) hv0[i] = bf16_bits_to_f32(a.embed[(int64_t)a.token * H + tid + i * kThreads]);
+    {
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.lw);
+        uint64_t* dst = reinterpret_cast<uint64_t*>(s_lw);
+        for (int i = tid; i < a.L * 11; i += kThreads) dst[i] = src[i];
+        if (kInt8) {
+            const uint64_t* ssrc = reinterpret_cast<const uint64_t*>(a.sp);
+            uint64_t* sdst = reinterpret_cast<uint64_t*>(s_sp);
+            for (int i = tid; i < a.L * 7; i += kThreads) sdst[i] = ssrc[i];
+        }
+    }
+    const uint32_t E = __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (g == 0 && tid == 0) {
+        // keep the header slots the single-level kernel counts on in a known state
+        __hip_atomic_store(&hdr->done[(E + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&hdr->best[(E + 1) & 1], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const uint32_t tps = kXStages * (uint32_t)a.L + 4u;
+    // tags end in binary 11 (the single-level kernel's end in 01): no overlap when
+    // the two kernels share a workspace
+    auto tag = [&](int l, int st) -> uint32_t { return ((E * tps + kXStages * (uint32_t)l + (uint32_t)st) << 2) | 3u; };
+    Waiter wt(&hdr->abort_flag, a.spin_limit);
+    auto trace = [&](int l, int point) {
+        if (kDebug && a.trace != nullptr && tid == 0)
+            a.trace[((int64_t)l * kTracePoints + point) * kNWG + g] = __builtin_amdgcn_s_memrealtime();
+    };
+    // A device with other than 8 XCDs cannot run this kernel: flag it (the waits
+    // then end at once and the host switches to the single-level kernel).
+    if (x >= kNX) {
+        if (tid == 0) __hip_atomic_store(&hdr->abort_flag, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+
+    const int64_t kv_head_stride = (int64_t)a.S * D;
+    const int last = a.L - 1;
+    const int R0 = RPW * r;                 // first O / down row of this workgroup
+    const double attn_scale = (double)a.attn_scale;
+    __syncthreads();
+
+    // QKV rows of this workgroup: rank < 16 query rows, < 24 key rows, else value rows
+    auto qkv_rows = [&](const LayerWeights& lw, const ScalePointers& sp, const uint8_t*& base, const float*& sc,
+                        int& mrow0) {
+        if (r < 16) { base = (const uint8_t*)lw.q_proj_weight; mrow0 = 2 * x * D + ROWS_A * r; if (kInt8) sc = sp.q_scale; }
+        else if (r < 24) { base = (const uint8_t*)lw.k_proj_weight; mrow0 = x * D + ROWS_A * (r - 16); if (kInt8) sc = sp.k_scale; }
+        else { base = (const uint8_t*)lw.v_proj_weight; mrow0 = x * D + ROWS_A * (r - 24); if (kInt8) sc = sp.v_scale; }
+    };
+
+    Stage_<W, ROWS_A, H> stA;
+    float scA = 1.0f;
+    float wln[PT];
+    {
+        const uint8_t* base; const float* sc = nullptr; int mrow0;
+        qkv_rows(s_lw[0], s_sp[0], base, sc, mrow0);
+        stA.load([&](int rr) { return base + (int64_t)(mrow0 + rr) * H * ES; }, wave, lane);
+        if (kInt8 && tid < ROWS_A) scA = sc[mrow0 + tid];
+        const uint16_t* lnw = (const uint16_t*)s_lw[0].input_layernorm_weight;
+#pragma unroll
+        for (int i = 0; i < PT; ++i) wln[i] = bf16_bits_to_f32(lnw[tid + i * kThreads]);
+#pragma unroll
+        for (int i = 0; i < PT; ++i) hid[tid + i * kThreads] = hv0[i];
+    }
+    __syncthreads();
+
+    for (int l = 0; l < a.L; ++l) {
+        const LayerWeights& lw = s_lw[l];
+        const ScalePointers& sp = s_sp[l];
+
+        // ---------------- A: RMSNorm + QKV rows -> XCD-local words ----------------
+        {
+            double ss = 0.0;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) { const double v = hid[tid + i * kThreads]; ss = fma(v, v, ss); }
+            const double tot = block_sum64<kWaves>(ss, red, wave, lane);
+            trace(l, 0);
+            const double rstd = rms_scale(tot, H, kEps);
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                const int k = tid + i * kThreads;
+                xdf[xd_index<W>(k)] = (double)(float)((double)hid[k] * rstd * (double)wln[i]);
+            }
+            __syncthreads();
+            stA.compute(xd, part, wave, lane);
+            __syncthreads();
+            if (tid < ROWS_A) {
+                double v = Stage_<W, ROWS_A, H>::row_sum(part, tid);
+                if (kInt8) v = v * (double)scA;
+                ll_put_xcd(&qkvx[ROWS_A * r + tid], __float_as_uint((float)v), tag(l, XS_QKV));
+            }
+            trace(l, 1);
+        }
+
+        // ---------------- B: attention for head pair x (every rank) ----------------
+        const int64_t cache_base = ((int64_t)l * kNX + x) * kv_head_stride;
+        uint4 wo[PT_O];
+        float so = 1.0f;
+        {
+            // step-independent loads: O weights of stage C, the O scale of this rank's
+            // reduction rows, norm gains, the RoPE row and earlier K/V rows
+            const uint8_t* ob = (const uint8_t*)lw.o_proj_weight;
+#pragma unroll
+            for (int i = 0; i < PT_O; ++i) {
+                const int it = tid + i * kThreads;
+                wo[i] = make_uint4(0, 0, 0, 0);
+                if (it < NIT_O) {
+                    const int row = it / PC_O, piece = it % PC_O;
+                    wo[i] = *reinterpret_cast<const uint4*>(ob + (int64_t)(R0 + row) * (16 * D) * ES + (int64_t)AD * x * ES + piece * 16);
+                }
+            }
+            if (kInt8 && tid < RPW) so = sp.o_scale[R0 + tid];
+            float nw0 = 0.0f, nw1 = 0.0f, c0 = 0.0f, s0 = 0.0f, c1 = 0.0f, s1 = 0.0f;
+            if (wave < 3) {
+                const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
+                nw0 = bf16_bits_to_f32(nw[lane]);
+                nw1 = bf16_bits_to_f32(nw[lane + 64]);
+                const uint16_t* ct = a.cos_t + (int64_t)a.pos * D;
+                const uint16_t* stt = a.sin_t + (int64_t)a.pos * D;
+                c0 = bf16_bits_to_f32(ct[lane]);
+                s0 = bf16_bits_to_f32(stt[lane]);
+                c1 = bf16_bits_to_f32(ct[lane + 64]);
+                s1 = bf16_bits_to_f32(stt[lane + 64]);
+            }
+            const int n = a.cache_len;
+            const int npre = a.pos < kKvLds ? a.pos : kKvLds;
+            constexpr int kPreU4 = 2 * kKvLds * (D / 8) / kThreads;
+            uint4 pre[kPreU4];
+#pragma unroll
+            for (int i = 0; i < kPreU4; ++i) {
+                const int f = tid + i * kThreads;
+                const int side = f / (kKvLds * (D / 8));
+                const int rem = f % (kKvLds * (D / 8));
+                const int j = rem / (D / 8), c = rem % (D / 8);
+                pre[i] = make_uint4(0, 0, 0, 0);
+                if (j < npre) pre[i] = *reinterpret_cast<const uint4*>((side == 0 ? a.kc : a.vc) + cache_base + (int64_t)j * D + c * 8);
+            }
+            issue_fence();
+            {
+                float v1[1];
+                wt.get_strided<1>(qkvx + tid, 0, tag(l, XS_QKV), v1);
+                att_in[tid] = v1[0];
+            }
+#pragma unroll
+            for (int i = 0; i < kPreU4; ++i) {
+                const int f = tid + i * kThreads;
+                const int side = f / (kKvLds * (D / 8));
+                const int rem = f % (kKvLds * (D / 8));
+                const int j = rem / (D / 8), c = rem % (D / 8);
+                if (j < npre) *reinterpret_cast<uint4*>(&kv_lds[side][j][c * 4]) = pre[i];
+            }
+            __syncthreads();
+            trace(l, 2);
+            const int64_t cur = cache_base + (int64_t)a.pos * D;
+            const bool writer = (r == 0);
+            if (wave < 3) {
+                // QK-norm and RoPE in fp64, rounded once to fp32
+                const float* src = att_in + wave * D;
+                const double x0 = src[lane], x1 = src[lane + 64];
+                const double ssq = wave_sum64(fma(x0, x0, x1 * x1));
+                const double sc = rms_scale(ssq, D, kEps);
+                const double y0 = x0 * sc * (double)nw0;
+                const double y1 = x1 * sc * (double)nw1;
+                const float o0 = (float)(y0 * (double)c0 - y1 * (double)s0);
+                const float o1 = (float)(y0 * (double)s1 + y1 * (double)c1);
+                if (wave < 2) {
+                    qrot[wave * D + lane] = o0;
+                    qrot[wave * D + lane + 64] = o1;
+                    if (kDebug && writer && l == last && a.dbg_q) {
+                        a.dbg_q[(2 * x + wave) * D + lane] = o0;
+                        a.dbg_q[(2 * x + wave) * D + lane + 64] = o1;
+                    }
+                } else {
+                    const uint32_t b0 = f32_to_bf16_bits(o0), b1 = f32_to_bf16_bits(o1);
+                    if (writer) {
+                        a.kc[cur + lane] = (uint16_t)b0;
+                        a.kc[cur + lane + 64] = (uint16_t)b1;
+                    }
+                    uint16_t* row = reinterpret_cast<uint16_t*>(kv_curb[0]);
+                    row[lane] = (uint16_t)b0;
+                    row[lane + 64] = (uint16_t)b1;
+                    if (kDebug && writer && l == last && a.dbg_k) { a.dbg_k[x * D + lane] = o0; a.dbg_k[x * D + lane + 64] = o1; }
+                }
+            } else if (wave == 3) {
+                const float v0 = att_in[3 * D + lane], v1 = att_in[3 * D + lane + 64];
+                const uint32_t b0 = f32_to_bf16_bits(v0), b1 = f32_to_bf16_bits(v1);
+                if (writer) {
+                    a.vc[cur + lane] = (uint16_t)b0;
+                    a.vc[cur + lane + 64] = (uint16_t)b1;
+                }
+                uint16_t* row = reinterpret_cast<uint16_t*>(kv_curb[1]);
+                row[lane] = (uint16_t)b0;
+                row[lane + 64] = (uint16_t)b1;
+                if (kDebug && writer && l == last && a.dbg_v) { a.dbg_v[x * D + lane] = v0; a.dbg_v[x * D + lane + 64] = v1; }
+            }
+            __syncthreads();
+
+            // scores (fp64): a quad of lanes per position, each lane a quarter of the head dim
+            {
+                const int qd = tid & 3;
+                const float* qa = qrot + qd * 32;          // read from LDS at each use (register budget)
+                const float* qb = qrot + D + qd * 32;
+                for (int j0 = 0; j0 < n; j0 += kThreads / 4) {
+                    const int j = j0 + (tid >> 2);
+                    double d0 = 0.0, d1 = 0.0;
+                    if (j < n) {
+                        uint4 kw[4];
+                        if (j == a.pos || j < kKvLds) {
+                            const uint32_t* rowp = j == a.pos ? kv_curb[0] : kv_lds[0][j];
+                            const uint4* kp = reinterpret_cast<const uint4*>(rowp + qd * 16);
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) kw[u] = kp[u];
+                        } else {
+                            const uint4* kp = reinterpret_cast<const uint4*>(a.kc + cache_base + (int64_t)j * D + qd * 32);
+#pragma unroll
+                            for (int u = 0; u < 4; ++u) kw[u] = kp[u];
+                        }
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const uint32_t wv[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w};
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const double klo = __uint_as_float(wv[e] << 16);
+                                const double khi = __uint_as_float(wv[e] & 0xffff0000u);
+                                d0 = fma((double)qa[u * 8 + 2 * e], klo, d0);
+                                d0 = fma((double)qa[u * 8 + 2 * e + 1], khi, d0);
+                                d1 = fma((double)qb[u * 8 + 2 * e], klo, d1);
+                                d1 = fma((double)qb[u * 8 + 2 * e + 1], khi, d1);
+                            }
+                        }
+                    }
+                    d0 += partner64<1>(d0); d0 += partner64<2>(d0);
+                    d1 += partner64<1>(d1); d1 += partner64<2>(d1);
+                    if (j < n && qd == 0) {
+                        scores[0][j] = d0 * attn_scale;
+                        scores[1][j] = d1 * attn_scale;
+                    }
+                }
+            }
+            __syncthreads();
+            // softmax (fp64): wave 0 handles head 0, wave 1 head 1 (max, exp in place, sum)
+            if (wave < 2) {
+                double* sv = scores[wave];
+                double m = -INFINITY;
+                for (int j = lane; j < n; j += kWave) m = fmax(m, sv[j]);
+                m = wave_max64(m);
+                double lsum = 0.0;
+                for (int j = lane; j < n; j += kWave) {
+                    const double p = exp(sv[j] - m);
+                    sv[j] = p;
+                    lsum += p;
+                }
+                lsum = wave_sum64(lsum);
+                if (lane == 0) red[wave] = lsum;
+            }
+            __syncthreads();
+            const double L0 = red[0], L1 = red[1];
+            // P @ V (fp64): lane owns a pair of dims, the 8 waves split the positions
+            {
+                const int dp = lane;
+                double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
+                for (int j = wave; j < n; j += kWaves) {
+                    const uint32_t vw = j == a.pos ? kv_curb[1][dp]
+                                      : j < kKvLds ? kv_lds[1][j][dp]
+                                                   : *reinterpret_cast<const uint32_t*>(a.vc + cache_base + (int64_t)j * D + 2 * dp);
+                    const double v0 = __uint_as_float(vw << 16);
+                    const double v1 = __uint_as_float(vw & 0xffff0000u);
+                    const double p0 = scores[0][j], p1 = scores[1][j];
+                    a00 = fma(p0, v0, a00); a01 = fma(p0, v1, a01);
+                    a10 = fma(p1, v0, a10); a11 = fma(p1, v1, a11);
+                }
+                pv[wave][2 * dp] = a00;
+                pv[wave][2 * dp + 1] = a01;
+                pv[wave][D + 2 * dp] = a10;
+                pv[wave][D + 2 * dp + 1] = a11;
+            }
+            __syncthreads();
+            if (tid < AD) {
+                double o = 0.0;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) o += pv[w][tid];
+                const float of = (float)(o / (tid < D ? L0 : L1));
+                attn_d[tid] = of;
+                if (kDebug && writer && l == last && a.dbg_attn) a.dbg_attn[AD * x + tid] = of;
+            }
+            __syncthreads();
+            trace(l, 3);
+        }
+
+        // ---------------- C: O partial over this XCD's 256 attention dims -> cross-XCD ----------------
+        {
+#pragma unroll
+            for (int i = 0; i < PT_O; ++i) {
+                const int it = tid + i * kThreads;
+                if (it < NIT_O) {
+                    const double2* xv = reinterpret_cast<const double2*>(attn_d + (it % PC_O) * EPP);
+                    part[it] = W::dotd(wo[i], xv, 0.0);
+                }
+            }
+            __syncthreads();
+            if (tid < RPW) {
+                double p = 0.0;
+#pragma unroll
+                for (int c = 0; c < PC_O; ++c) p += part[tid * PC_O + c];
+                const float hi = (float)p, lo = (float)(p - (double)hi);
+                ll_put(&po[(size_t)x * H + R0 + tid], __float_as_uint(hi), tag(l, XS_PO));
+                ll_put(&po[(size_t)(kNX + x) * H + R0 + tid], __float_as_uint(lo), tag(l, XS_PO));
+            }
+            trace(l, 4);
+        }
+
+        // ---------------- D: reduce O partials -> act rows -> XCD-local all-gather ----------------
+        Stage_<W, 2 * CPW, H> stE;
+        float gsc = 1.0f, usc = 1.0f;
+        float wpn[PT];
+        const int c0 = IX * x + CPW * r;
+        {
+            // stage E's weights, scales and norm gains first
+            const uint8_t* gb = (const uint8_t*)lw.gate_proj_weight;
+            const uint8_t* ub = (const uint8_t*)lw.up_proj_weight;
+            stE.load([&](int rr) {
+                return rr < CPW ? gb + (int64_t)(c0 + rr) * H * ES : ub + (int64_t)(c0 + rr - CPW) * H * ES;
+            }, wave, lane);
+            if (kInt8 && tid < CPW) { gsc = sp.gate_scale[c0 + tid]; usc = sp.up_scale[c0 + tid]; }
+            const uint16_t* pnw = (const uint16_t*)lw.post_attn_layernorm_weight;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) wpn[i] = bf16_bits_to_f32(pnw[tid + i * kThreads]);
+            issue_fence();
+
+            if (tid < RPW) {
+                float v16[2 * kNX];
+                wt.get_strided<2 * kNX>(po + R0 + tid, H, tag(l, XS_PO), v16);
+                double s = 0.0;
+#pragma unroll
+                for (int xx = 0; xx < kNX; ++xx) s += (double)v16[xx] + (double)v16[kNX + xx];
+                if (kInt8) s = s * (double)so;
+                const float av = (float)(s + (double)hid[R0 + tid]);
+                ll_put_xcd(&actx[R0 + tid], __float_as_uint(av), tag(l, XS_ACT));
+            }
+            float av[PT];
+            wt.get_strided<PT>(actx + tid, kThreads, tag(l, XS_ACT), av);
+#pragma unroll
+            for (int i = 0; i < PT; ++i) act[tid + i * kThreads] = av[i];
+            trace(l, 5);
+
+            // ---------------- E: RMSNorm + gate/up + SwiGLU -> XCD-local mlp ----------------
+            double ss = 0.0;
+#pragma unroll
+            for (int i = 0; i < PT; ++i) ss = fma((double)av[i], (double)av[i], ss);
+            const double tot = block_sum64<kWaves>(ss, red, wave, lane);
+            const double rstd = rms_scale(tot, H, kEps);
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                const int k = tid + i * kThreads;
+                const float nv = (float)((double)av[i] * rstd * (double)wpn[i]);
+                xdf[xd_index<W>(k)] = nv;
+                if (kDebug && l == last && g == 0) {
+                    if (a.dbg_act) a.dbg_act[k] = nv;
+                    if (a.dbg_resid) a.dbg_resid[k] = av[i];
+                }
+            }
+            __syncthreads();
+            stE.compute(xd, part, wave, lane);
+            __syncthreads();
+            if (tid < CPW) {
+                double gs = Stage_<W, 2 * CPW, H>::row_sum(part, tid);
+                double us = Stage_<W, 2 * CPW, H>::row_sum(part, CPW + tid);
+                if (kInt8) { gs = gs * (double)gsc; us = us * (double)usc; }
+                const float m = (float)(gs / (1.0 + exp(-gs)) * us);
+                ll_put_xcd(&mlpx[CPW * r + tid], __float_as_uint(m), tag(l, XS_MLP));
+                if (kDebug && l == last && a.dbg_mlp) a.dbg_mlp[c0 + tid] = m;
+            }
+            trace(l, 6);
+        }
+
+        // ---------------- F: down partial over this XCD's channels -> cross-XCD ----------------
+        float sd = 1.0f;
+        {
+            uint4 wd[PT_D];
+            const uint8_t* db = (const uint8_t*)lw.down_proj_weight;
+#pragma unroll
+            for (int i = 0; i < PT_D; ++i) {
+                const int it = tid + i * kThreads;
+                wd[i] = make_uint4(0, 0, 0, 0);
+                if (it < NIT_D) {
+                    const int row = it / PC_D, piece = it % PC_D;
+                    wd[i] = *reinterpret_cast<const uint4*>(db + (int64_t)(R0 + row) * I * ES + (int64_t)IX * x * ES + piece * 16);
+                }
+            }
+            if (kInt8 && tid < RPW) sd = sp.down_scale[R0 + tid];
+            issue_fence();
+            if (tid < IX) {
+                float mv[MLP_PT];
+                wt.get_strided<MLP_PT>(mlpx + tid, kThreads, tag(l, XS_MLP), mv, (IX - tid + kThreads - 1) / kThreads);
+#pragma unroll
+                for (int i = 0; i < MLP_PT; ++i)
+                    if (tid + i * kThreads < IX) mlp_d[tid + i * kThreads] = mv[i];
+            }
+            __syncthreads();
+            trace(l, 7);
+#pragma unroll
+            for (int i = 0; i < PT_D; ++i) {
+                const int it = tid + i * kThreads;
+                if (it < NIT_D) {
+                    const double2* xv = reinterpret_cast<const double2*>(mlp_d + (it % PC_D) * EPP);
+                    part[it] = W::dotd(wd[i], xv, 0.0);
+                }
+            }
+            __syncthreads();
+            if (tid < RPW) {
+                double p = 0.0;
+#pragma unroll
+                for (int c = 0; c < PC_D; ++c) p += part[tid * PC_D + c];
+                const float hi = (float)p, lo = (float)(p - (double)hi);
+                ll_put(&pd[(size_t)x * H + R0 + tid], __float_as_uint(hi), tag(l, XS_PD));
+                ll_put(&pd[(size_t)(kNX + x) * H + R0 + tid], __float_as_uint(lo), tag(l, XS_PD));
+            }
+            trace(l, 8);
+        }
+
+        // ---------------- G: reduce down partials -> bf16 hidden -> XCD-local all-gather ----------------
+        {
+            if (l < last) {
+                // the next layer's QKV weights, scales and input-norm gains first
+                const LayerWeights& nl = s_lw[l + 1];
+                const uint8_t* base; const float* sc = nullptr; int mrow0;
+                qkv_rows(nl, s_sp[l + 1], base, sc, mrow0);
+                stA.load([&](int rr) { return base + (int64_t)(mrow0 + rr) * H * ES; }, wave, lane);
+                if (kInt8 && tid < ROWS_A) scA = sc[mrow0 + tid];
+                const uint16_t* lnw = (const uint16_t*)nl.input_layernorm_weight;
+#pragma unroll
+                for (int i = 0; i < PT; ++i) wln[i] = bf16_bits_to_f32(lnw[tid + i * kThreads]);
+                issue_fence();
+            }
+            if (tid < RPW) {
+                float v16[2 * kNX];
+                wt.get_strided<2 * kNX>(pd + R0 + tid, H, tag(l, XS_PD), v16);
+                double s = 0.0;
+#pragma unroll
+                for (int xx = 0; xx < kNX; ++xx) s += (double)v16[xx] + (double)v16[kNX + xx];
+                if (kInt8) s = s * (double)sd;
+                const float hf = (float)(s + (double)act[R0 + tid]);
+                ll_put_xcd(&hidx[R0 + tid], __float_as_uint(round_bf16(hf)), tag(l, XS_HID));
+            }
+            float hv[PT];
+            wt.get_strided<PT>(hidx + tid, kThreads, tag(l, XS_HID), hv);
+#pragma unroll
+            for (int i = 0; i < PT; ++i) {
+                hid[tid + i * kThreads] = hv[i];
+                if (kDebug && l == last && g == 0 && a.dbg_hidden)
+                    a.dbg_hidden[tid + i * kThreads] = (uint16_t)f32_to_bf16_bits(hv[i]);
+            }
+            __syncthreads();
+            trace(l, 9);
+        }
+    }
+
+    // ---------------- final RMSNorm + LM head + greedy argmax ----------------
+    {
+        constexpr int CH = H / (64 * W::kPerLane);
+        constexpr int RB = CH >= 8 ? 1 : 8 / CH;
+        constexpr int R = RB * CH;
+        constexpr int span = kWave / RB;
+        const int r0 = (int)((int64_t)a.V * g / kNWG);
+        const int r1 = (int)((int64_t)a.V * (g + 1) / kNWG);
+        const int nb = (r1 - r0 + RB - 1) / RB;
+        const int64_t rowbytes = (int64_t)H * ES;
+        uint4 cur[R], nxt[R];
+        float scur = 0.0f, snxt = 0.0f;
+        auto fetch = [&](int b, uint4* dst, float& s) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int row = r0 + b * RB + i / CH;
+                dst[i] = make_uint4(0, 0, 0, 0);
+                if (row < r1) dst[i] = *reinterpret_cast<const uint4*>(a.lm_w + row * rowbytes + (i % CH) * 1024 + lane * 16);
+            }
+            const int myrow = r0 + b * RB + lane / span;
+            s = 1.0f;
+            if (kInt8 && myrow < r1) s = a.lm_s[myrow];
+        };
+        int b = wave;
+        if (b < nb) fetch(b, cur, scur);
+        double ss = 0.0;
+        float wfn[PT];
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            wfn[i] = bf16_bits_to_f32(a.final_norm[tid + i * kThreads]);
+            const double v = hid[tid + i * kThreads];
+            ss = fma(v, v, ss);
+        }
+        const double tot = block_sum64<kWaves>(ss, red, wave, lane);
+        const double rstd = rms_scale(tot, H, kEps);
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const int k = tid + i * kThreads;
+            const float nv = (float)((double)hid[k] * rstd * (double)wfn[i]);
+            xsf[xs_index<W>(k)] = nv;
+            if (kDebug && g == 0 && a.dbg_norm) a.dbg_norm[k] = nv;
+        }
+        __syncthreads();
+        trace(a.L, 0);
+
+        float best_v = -INFINITY;
+        int best_i = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < R; ++i) nxt[i] = make_uint4(0, 0, 0, 0);
+        for (; b < nb; b += kWaves) {
+            if (b + kWaves < nb) fetch(b + kWaves, nxt, snxt);
+            float acc[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) acc[i] = dot_frag<W>(cur[i], xs_frag<W>(xs, i % CH, lane), 0.0f);
+            const float s = transpose_reduce<R, CH>(acc, lane);
+            const int row = r0 + b * RB + lane / span;
+            if ((lane % span) == 0 && row < r1) {
+                const float v = kInt8 ? s * scur : s;
+                if (v > best_v) { best_v = v; best_i = row; }
+            }
+#pragma unroll
+            for (int i = 0; i < R; ++i) cur[i] = nxt[i];
+            scur = snxt;
+        }
+#define MQ_ARGMAX_LEVEL(M)                                                                   \
+        {                                                                                    \
+            const float ov = partner<M>(best_v);                                             \
+            const int oi = __float_as_int(partner<M>(__int_as_float(best_i)));               \
+            if (ov > best_v || (ov == best_v && oi < best_i)) { best_v = ov; best_i = oi; }  \
+        }
+        MQ_ARGMAX_LEVEL(1) MQ_ARGMAX_LEVEL(2) MQ_ARGMAX_LEVEL(4) MQ_ARGMAX_LEVEL(8)
+        MQ_ARGMAX_LEVEL(16) MQ_ARGMAX_LEVEL(32)
+#undef MQ_ARGMAX_LEVEL
+        if (lane == 0) { lm_v[wave] = best_v; lm_i[wave] = best_i; }
+        __syncthreads();
+        trace(a.L, 1);
+        // argmax over the 8 waves, then the XCD's 32 workgroups, then the 8 XCDs
+        const uint32_t tag_l1 = tag(a.L, 0), tag_l2 = tag(a.L, 1);
+        if (tid == 0) {
+            float bv = lm_v[0];
+            int bi = lm_i[0];
+            for (int w = 1; w < kWaves; ++w)
+                if (lm_v[w] > bv || (lm_v[w] == bv && lm_i[w] < bi)) { bv = lm_v[w]; bi = lm_i[w]; }
+            if (kDebug && a.dbg_bmax) a.dbg_bmax[g] = bv;
+            if (kDebug && a.dbg_bidx) a.dbg_bidx[g] = bi;
+            ll_put_xcd(&lmx[2 * r], ordered_key(bv), tag_l1);
+            ll_put_xcd(&lmx[2 * r + 1], (uint32_t)bi, tag_l1);
+        }
+        if (r == 0 && wave == 0) {
+            // XCD leader: one lane per rank
+            uint32_t kv = 0, iv = 0x7fffffffu;
+            if (lane < kGS) {
+                kv = wt.get(&lmx[2 * lane], tag_l1);
+                iv = wt.get(&lmx[2 * lane + 1], tag_l1);
+            }
+#define MQ_KEY_LEVEL(M)                                                                      \
+            {                                                                                \
+                const uint32_t ok = __float_as_uint(partner<M>(__uint_as_float(kv)));        \
+                const uint32_t oi = __float_as_uint(partner<M>(__uint_as_float(iv)));        \
+                if (ok > kv || (ok == kv && oi < iv)) { kv = ok; iv = oi; }                  \
+            }
+            MQ_KEY_LEVEL(1) MQ_KEY_LEVEL(2) MQ_KEY_LEVEL(4) MQ_KEY_LEVEL(8) MQ_KEY_LEVEL(16) MQ_KEY_LEVEL(32)
+            if (lane == 0) {
+                ll_put(&lmc[2 * x], kv, tag_l2);
+                ll_put(&lmc[2 * x + 1], iv, tag_l2);
+            }
+            if (x == 0) {
+                uint32_t k2 = 0, i2 = 0x7fffffffu;
+                if (lane < kNX) {
+                    k2 = wt.get(&lmc[2 * lane], tag_l2);
+                    i2 = wt.get(&lmc[2 * lane + 1], tag_l2);
+                }
+                kv = k2;
+                iv = i2;
+                MQ_KEY_LEVEL(1) MQ_KEY_LEVEL(2) MQ_KEY_LEVEL(4) MQ_KEY_LEVEL(8) MQ_KEY_LEVEL(16) MQ_KEY_LEVEL(32)
+                if (lane == 0) {
+                    const bool aborted = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+                    *a.out_token = (aborted || wt.dead) ? -1 : (int)iv;
+                    __hip_atomic_store(&hdr->epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (kDebug && a.trace != nullptr)
+                        a.trace[((int64_t)a.L * kTracePoints + 2) * kNWG] = __builtin_amdgcn_s_memrealtime();
+                }
+            }
+#undef MQ_KEY_LEVEL
+        }
+    }
+}
+
+// ---------------- host side ----------------
+
+size_t decode_xcd_workspace_bytes(const DecodeShape& s) { return xlayout_for(s.H, s.I).total; }
+
+template <int H, int I, class W>
+static int launch_xcd_t(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
+    auto fn = debug ? reinterpret_cast<const void*>(&decode_xcd_kernel<H, I, W, true>)
+                    : reinterpret_cast<const void*>(&decode_xcd_kernel<H, I, W, false>);
+    int st = check_residency(fn);
+    if (st != MQ_OK) return st;
+    KArgs copy = ka;
+    void* args[] = {&copy};
+    hipError_t e;
+    if (t0 != nullptr && t1 != nullptr) {
+        e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
+        if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode_xcd): %s", hipGetErrorString(e));
+    } else {
+        e = hipLaunchCooperativeKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream);
+        if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipLaunchCooperativeKernel(decode_xcd): %s", hipGetErrorString(e));
+    }
+    return MQ_OK;
+}
+
+const void* decode_xcd_kernel_ptr(const DecodeShape& s, bool int8, bool debug) {
+    if (s.H == 1024 && s.I == 3072) {
+        if (int8) return debug ? (const void*)&decode_xcd_kernel<1024, 3072, Int8W, true> : (const void*)&decode_xcd_kernel<1024, 3072, Int8W, false>;
+        return debug ? (const void*)&decode_xcd_kernel<1024, 3072, Bf16W, true> : (const void*)&decode_xcd_kernel<1024, 3072, Bf16W, false>;
+    }
+    if (s.H == 2048 && s.I == 6144 && int8)
+        return debug ? (const void*)&decode_xcd_kernel<2048, 6144, Int8W, true> : (const void*)&decode_xcd_kernel<2048, 6144, Int8W, false>;
+    return nullptr;
+}
+
+int launch_decode_xcd(const KArgs& k, const DecodeShape& s, bool int8, bool debug, hipStream_t stream,
+                      hipEvent_t t0, hipEvent_t t1) {
+    if (s.H == 1024 && s.I == 3072)
+        return int8 ? launch_xcd_t<1024, 3072, Int8W>(k, debug, stream, t0, t1)
+                    : launch_xcd_t<1024, 3072, Bf16W>(k, debug, stream, t0, t1);
+    if (s.H == 2048 && s.I == 6144 && int8) return launch_xcd_t<2048, 6144, Int8W>(k, debug, stream, t0, t1);
+    return set_error(MQ_ERR_UNSUPPORTED, "no XCD decode kernel for H=%d I=%d (%s)", s.H, s.I, int8 ? "int8" : "bf16");
+}
+
+}  // namespace mq

@@ -33,6 +33,12 @@ struct DecodeShape {
 };
 
 size_t decode_workspace_bytes(const DecodeShape& s);
+// Kernel variant: 0 = automatic (XCD-aware when the device places workgroup g
+// on XCD g % 8), 1 = single-level exchange kernel, 2 = XCD-aware kernel.
+int set_decode_variant(int variant);
+int decode_variant_in_use(const DecodeShape& s, bool int8);
+// After an in-kernel placement failure: use the single-level kernel from now on.
+void mark_xcd_unusable();
 // Launches one decode step; `int8` selects the weight format.
 int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream);
 

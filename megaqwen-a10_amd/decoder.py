@@ -31,6 +31,26 @@ from .weights import pack_bf16, pack_int8, quantize_state, random_init_state
 
 LM_PARTIALS = 256   # per-workgroup LM-head maxima written to block_max_vals/idxs
 
+VARIANTS = {"auto": 0, "flat": 1, "xcd": 2}
+
+
+def set_decode_variant(name: str) -> None:
+    """Select the decode kernel for all following steps in this process:
+    ``"auto"`` (default; the XCD-aware kernel when the device places workgroup g
+    on XCD g % 8), ``"flat"`` (single-level exchanges) or ``"xcd"``."""
+    lib = _lib.load()
+    _lib.check(lib.mq_decode_set_variant(VARIANTS[name]), "mq_decode_set_variant")
+
+
+def decode_variant(hidden_size: int = 1024, intermediate_size: int = 3072, int8: bool = True) -> str:
+    """The kernel a step with these dims would use now."""
+    lib = _lib.load()
+    dims = _lib.ModelDims(hidden_size, intermediate_size, 16, 8, 128, 151936)
+    v = lib.mq_decode_variant(ctypes.byref(dims), int(int8))
+    if v < 0:
+        _lib.check(-v, "mq_decode_variant")
+    return {1: "flat", 2: "xcd"}[v]
+
 
 def _check_tensor(t, name, dtype, shape=None, device=None):
     if not isinstance(t, torch.Tensor):

@@ -57,6 +57,15 @@ def _greedy(dec, prompt, n):
     return out
 
 
+@pytest.fixture(params=["flat", "xcd"])
+def variant(request, mq, dev):
+    """Runs a test once per decode kernel (single-level exchanges / XCD-aware)."""
+    mq.set_decode_variant(request.param)
+    assert mq.decode_variant() == request.param
+    yield request.param
+    mq.set_decode_variant("auto")
+
+
 @pytest.fixture(scope="module")
 def small(mq, dev):
     return _build(mq, dev, "small_int8")
@@ -70,13 +79,13 @@ def _ref_for(small_case):
                       c(fnorm), c(lm_q), c(lm_s), c(cos), c(sin), cfg.num_layers, d["max_seq_len"])
 
 
-def test_small_int8_tokens_match_fixture(small):
+def test_small_int8_tokens_match_fixture(variant, small):
     dec, d, prompt, cfg, _ = small
     print("small_int8 32 greedy steps", flush=True)
     assert _greedy(dec, prompt, 32) == d["tokens"]
 
 
-def test_small_int8_stages_match_oracle(small):
+def test_small_int8_stages_match_oracle(variant, small):
     """Per-stage values of the last layer (the reference's debug getters) after several steps."""
     dec, d, prompt, cfg, _ = small
     ref = _ref_for(small)
@@ -115,7 +124,7 @@ def test_small_int8_stages_match_oracle(small):
     assert float((kc - rk).abs().max()) <= float(rk.abs().max()) * 2.0 ** -7
 
 
-def test_one_layer_stages_tight(mq, dev):
+def test_one_layer_stages_tight(variant, mq, dev):
     """One layer, first position: every stage input is bit-identical to the oracle's, so the
     fp32 stages must agree to accumulation error (1e-5) and the bf16 outputs to one ulp."""
     cfg = mq.QWEN3_0_6B.with_(num_layers=1, vocab_size=3000)
@@ -150,7 +159,7 @@ def test_one_layer_stages_tight(mq, dev):
         assert e < 1e-3, e
 
 
-def test_small_int8_deterministic(small):
+def test_small_int8_deterministic(variant, small):
     dec, d, prompt, cfg, _ = small
     dec.enable_debug()
     runs = []
@@ -194,7 +203,7 @@ def test_invalid_inputs_raise(small):
     dec.reset()
 
 
-def test_expired_wait_reports_timeout_and_recovers(mq, small):
+def test_expired_wait_reports_timeout_and_recovers(variant, mq, small):
     """A one-poll spin limit makes every cross-workgroup wait expire: the step must end,
     report MQ_ERR_TIMEOUT, and the decoder must work again after its workspace reset."""
     dec, d, prompt, cfg, _ = small
@@ -207,7 +216,7 @@ def test_expired_wait_reports_timeout_and_recovers(mq, small):
     assert _greedy(dec, prompt, 8) == d["tokens"][:8]
 
 
-def test_full_int8_32_tokens(mq, dev):
+def test_full_int8_32_tokens(variant, mq, dev):
     """BASELINE config 1 gate: Qwen3-0.6B shape, INT8, seed 0, 32 greedy tokens identical to the oracle."""
     print("building qwen3_0.6b_int8", flush=True)
     dec, d, prompt, cfg, keep = _build(mq, dev, "qwen3_0.6b_int8")
@@ -233,7 +242,7 @@ def test_full_int8_32_tokens(mq, dev):
     torch.cuda.empty_cache()
 
 
-def test_full_bf16_32_tokens(mq, dev):
+def test_full_bf16_32_tokens(variant, mq, dev):
     """BASELINE config 3 gate: Qwen3-0.6B shape, bf16 weights, 32 greedy tokens identical to the oracle."""
     print("building qwen3_0.6b_bf16", flush=True)
     dec, d, prompt, cfg, keep = _build(mq, dev, "qwen3_0.6b_bf16")
@@ -243,7 +252,7 @@ def test_full_bf16_32_tokens(mq, dev):
     torch.cuda.empty_cache()
 
 
-def test_1p7b_int8_matches_oracle(mq, dev):
+def test_1p7b_int8_matches_oracle(variant, mq, dev):
     """Qwen3-1.7B layer shapes (H=2048, I=6144), 2 layers, small vocabulary, live oracle."""
     cfg = mq.QWEN3_1_7B.with_(num_layers=2, vocab_size=2048)
     state, prompt = mq.random_init_state(cfg, seed=5, norm_jitter=0.1)
