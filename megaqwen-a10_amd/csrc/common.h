@@ -172,28 +172,35 @@ __device__ __forceinline__ double transpose_reduce64(double* v, int lane) {
     return x;
 }
 
-// 16 int8 weights against 16 fp64 activations (exact products, fp64 sum).
+// 16 int8 weights against 16 fp64 activations (exact products, fp64 sum). The
+// activations are 8 double2 at x[0], x[S], ..., x[7S]. Four independent
+// accumulators keep the dependent fp64 FMA chain short (its latency, not the
+// FMA rate, bounds these small dot products).
+template <int S = 1>
 __device__ __forceinline__ double dot_i8x16_d(uint4 w, const double2* x, double acc) {
     const int8_t* b = reinterpret_cast<const int8_t*>(&w);
+    double s[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const double2 xv = x[j];
-        acc = fma((double)(float)b[2 * j], xv.x, acc);
-        acc = fma((double)(float)b[2 * j + 1], xv.y, acc);
+        const double2 xv = x[j * S];
+        s[(2 * j) & 3] = fma((double)(float)b[2 * j], xv.x, s[(2 * j) & 3]);
+        s[(2 * j + 1) & 3] = fma((double)(float)b[2 * j + 1], xv.y, s[(2 * j + 1) & 3]);
     }
-    return acc;
+    return acc + ((s[0] + s[1]) + (s[2] + s[3]));
 }
 
-// 8 bf16 weights against 8 fp64 activations.
+// 8 bf16 weights against 8 fp64 activations (4 double2 at x[0], x[S], ...).
+template <int S = 1>
 __device__ __forceinline__ double dot_bf16x8_d(uint4 w, const double2* x, double acc) {
     const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    double s[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const double2 xv = x[j];
-        acc = fma((double)__uint_as_float(wv[j] << 16), xv.x, acc);
-        acc = fma((double)__uint_as_float(wv[j] & 0xffff0000u), xv.y, acc);
+        const double2 xv = x[j * S];
+        s[(2 * j) & 3] = fma((double)__uint_as_float(wv[j] << 16), xv.x, s[(2 * j) & 3]);
+        s[(2 * j + 1) & 3] = fma((double)__uint_as_float(wv[j] & 0xffff0000u), xv.y, s[(2 * j + 1) & 3]);
     }
-    return acc;
+    return acc + ((s[0] + s[1]) + (s[2] + s[3]));
 }
 
 // ---- 16-byte dot products ----------------------------------------------------------------
@@ -233,13 +240,15 @@ struct Int8W {
     static constexpr int kBytes = 1;
     static constexpr int kPerLane = 16;
     __device__ static float dot(uint4 w, const float4* x, float acc) { return dot_i8x16(w, x, acc); }
-    __device__ static double dotd(uint4 w, const double2* x, double acc) { return dot_i8x16_d(w, x, acc); }
+    template <int S = 1>
+    __device__ static double dotd(uint4 w, const double2* x, double acc) { return dot_i8x16_d<S>(w, x, acc); }
 };
 struct Bf16W {
     static constexpr int kBytes = 2;
     static constexpr int kPerLane = 8;
     __device__ static float dot(uint4 w, const float4* x, float acc) { return dot_bf16x8(w, x, acc); }
-    __device__ static double dotd(uint4 w, const double2* x, double acc) { return dot_bf16x8_d(w, x, acc); }
+    template <int S = 1>
+    __device__ static double dotd(uint4 w, const double2* x, double acc) { return dot_bf16x8_d<S>(w, x, acc); }
 };
 
 // ---- activation vector in LDS, laid out per lane --------------------------------------
@@ -287,16 +296,77 @@ __device__ __forceinline__ int xd_index(int k) {          // double index of ele
 template <class W>
 __device__ __forceinline__ double dot_fragd(uint4 w, const double2* xd, int chunk, int lane, double acc) {
     constexpr int P = W::kPerLane;
-    const double2* f = xd + (chunk * (P / 2)) * 64 + lane;
-    double2 x[P / 2];
-#pragma unroll
-    for (int j = 0; j < P / 2; ++j) x[j] = f[j * 64];
-    return W::dotd(w, x, acc);
+    return W::template dotd<64>(w, xd + (chunk * (P / 2)) * 64 + lane, acc);
+}
+
+// Piece-major fp64 activation layout for matvecs whose row segment is split
+// into 16-byte weight "pieces" handed to consecutive lanes: element k of the
+// segment (piece p = k / EPP, e = k % EPP) is stored as double e of double2
+// (e / 2) * NP + p, so the lanes of a wave read consecutive double2 values.
+__device__ __forceinline__ int piece_index(int k, int epp, int np) {     // double index of element k
+    const int p = k / epp, e = k % epp;
+    return ((e >> 1) * np + p) * 2 + (e & 1);
+}
+
+// Sum of v over aligned groups of N consecutive lanes (N a power of two <= 64);
+// every lane of a group receives its group's sum. Butterfly order, so the
+// result is bitwise reproducible.
+template <int N>
+__device__ __forceinline__ double group_sum64(double v) {
+    if constexpr (N >= 2) v += partner64<1>(v);
+    if constexpr (N >= 4) v += partner64<2>(v);
+    if constexpr (N >= 8) v += partner64<4>(v);
+    if constexpr (N >= 16) v += partner64<8>(v);
+    if constexpr (N >= 32) v += partner64<16>(v);
+    if constexpr (N >= 64) v += partner64<32>(v);
+    return v;
 }
 
 // Keeps the compiler from moving memory accesses across this point (used to
 // issue step-independent loads before a wait instead of where they are used).
 __device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
+
+// The value of v, hidden from the optimiser. Taken once per iteration of a long
+// loop, it keeps per-lane addresses derived from v from being hoisted out of
+// the loop and held (or spilled to scratch) for its whole length: they are
+// recomputed at their use with a couple of integer operations instead.
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// A prefetched 32-bit value, released for use at this point. Without it the
+// compiler converts a loaded value right after its load, and the wait for that
+// load (loads return in order, so it also waits for every load issued before
+// it, such as a stage's weight prefetch) lands ahead of the exchange the
+// prefetch is meant to overlap. Prefetched scalars are therefore kept as raw
+// bits and pass through here after the wait.
+__device__ __forceinline__ uint32_t after_wait(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ float after_wait_f(uint32_t v) { return __uint_as_float(after_wait(v)); }
+__device__ __forceinline__ float after_wait_bf16(uint32_t v) { return bf16_bits_to_f32(after_wait(v)); }
+
+// Global-memory view of a pointer. A pointer the kernel reads from memory (the
+// per-layer pointer tables) is generic to the compiler, which then emits flat
+// loads; a flat load counts against the LDS counter as well, so every later LDS
+// wait would also wait for it and a weight prefetch could not overlap the
+// exchange that follows. Loads through this view are global loads.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gview(const T* p) {
+    return (const __attribute__((address_space(1))) T*)p;
+}
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+// 16-byte global load (gview() for uint4, whose assignment operators take
+// generic references only).
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+    const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t*)p;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+// Raw 32-bit load of a float / bf16 value for after_wait().
+__device__ __forceinline__ uint32_t ldg_bits(const float* p) { return *gview(reinterpret_cast<const uint32_t*>(p)); }
+__device__ __forceinline__ uint32_t ldg_bits(const uint16_t* p) { return *gview(p); }
 
 // ---- tagged exchange words --------------------------------------------------------------
 // A 64-bit word holds a 32-bit payload and a 32-bit tag naming the step,
@@ -306,6 +376,18 @@ __device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
 // access, so no fence is needed between them.
 __device__ __forceinline__ void ll_put(uint64_t* p, uint32_t payload, uint32_t tag) {
     __hip_atomic_store(p, ((uint64_t)tag << 32) | payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A packed word: an fp64 value whose lowest mantissa bit is replaced by a
+// one-bit tag. A buffer of packed words is written once per use and the tag
+// alternates between uses (first use 1, the workspace starts zeroed), so a
+// reader tells this use's value from the previous one's. That needs every
+// reader of a use to have read before the slot is written again, which the
+// writers' data dependencies guarantee where these words are used.
+__device__ __forceinline__ uint64_t pack_tagged(double v, uint32_t pbit) {
+    return ((uint64_t)__double_as_longlong(v) & ~(uint64_t)1) | (uint64_t)(pbit & 1u);
+}
+__device__ __forceinline__ void ll_put64(uint64_t* p, uint64_t w) {
+    __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -344,6 +426,40 @@ struct Waiter {
         return (uint32_t)w;
     }
     __device__ __forceinline__ float getf(const uint64_t* p, uint32_t tag) { return __uint_as_float(get(p, tag)); }
+
+    // N packed words at p[i * stride] (see pack_tagged): waits until bit 0 of
+    // each equals `pbit` and returns the fp64 values with that bit cleared.
+    template <int N>
+    __device__ __forceinline__ void get_packed(const uint64_t* p, int stride, uint32_t pbit, double (&out)[N]) {
+        uint64_t w[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) w[i] = ll_load(p + i * stride);
+        uint32_t pending = 0;
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            if ((uint32_t)(w[i] & 1u) != pbit) pending |= 1u << i;
+        uint32_t n = 0;
+        while (pending != 0 && !dead) {
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int i = 0; i < N; ++i)
+                if (pending & (1u << i)) w[i] = ll_load(p + i * stride);
+#pragma unroll
+            for (int i = 0; i < N; ++i)
+                if ((pending & (1u << i)) && (uint32_t)(w[i] & 1u) == pbit) pending &= ~(1u << i);
+            if (pending == 0) break;
+            if (++n >= limit) {
+                dead = true;
+                __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            if ((n & 127u) == 0 &&
+                __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
+                dead = true;
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) out[i] = __longlong_as_double((long long)(w[i] & ~(uint64_t)1));
+    }
 
     // N words at p[i * stride]: all N loads are issued before any is checked,
     // and every retry re-issues the still-missing ones together, so a wait

@@ -36,22 +36,6 @@
 
 namespace mq {
 
-// Workspace layout (after the 256-byte header): one 64-bit exchange word per
-// element of each handed-over vector, every region 256-byte aligned.
-struct Layout {
-    size_t hid, qkv, att, act, mlp, total;
-};
-constexpr Layout layout_for(int H, int I, int NQ, int NKV, int D) {
-    Layout o{};
-    o.hid = sizeof(WsHeader);
-    o.qkv = o.hid + round256((size_t)H * 8);
-    o.att = o.qkv + round256(((size_t)NQ * D + 2 * (size_t)NKV * D) * 8);
-    o.act = o.att + round256((size_t)NQ * D * 8);
-    o.mlp = o.act + round256((size_t)H * 8);
-    o.total = o.mlp + round256((size_t)I * 8);
-    return o;
-}
-
 template <int H, int I, class W, bool kDebug>
 __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
     constexpr int NQ = 16, NKV = 8, D = 128;
@@ -96,7 +80,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
     // step-independent reads first: the embedding row and the per-layer pointer tables
     float hv0[PT];
 #pragma unroll
-    for (int i = 0; i < PT; ++i) hv0[i] = bf16_bits_to_f32(a.embed[(int64_t)a.token * H + tid + i * kThreads]);
+    for (int i = 0; i < PT; ++i) hv0[i] = bf16_bits_to_f32(gview(a.embed)[(int64_t)a.token * H + tid + i * kThreads]);
     {
         const uint64_t* src = reinterpret_cast<const uint64_t*>(a.lw);
         uint64_t* dst = reinterpret_cast<uint64_t*>(s_lw);
@@ -134,9 +118,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
     const double attn_scale = (double)a.attn_scale;
     __syncthreads();
 
+    const int tid_all = tid;
     for (int l = 0; l < a.L; ++l) {
         const LayerWeights& lw = s_lw[l];
         const ScalePointers& sp = s_sp[l];
+        const int tid = opaque(tid_all);
+        const int lane = tid % kWave;
 
         // ---------------- RMSNorm + QKV ----------------
         {
@@ -149,12 +136,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             else { base = (const uint8_t*)lw.v_proj_weight; lrow0 = row0 - QD - KVD; if (kInt8) sc = sp.v_scale; }
             Stage_<W, ROWS_QKV, H> st;
             st.load([&](int r) { return base + (int64_t)(lrow0 + r) * H * ES; }, wave, lane);
-            float my_scale = 1.0f;
-            if (kInt8 && tid < ROWS_QKV) my_scale = sc[lrow0 + tid];
+            uint32_t my_scale = 0x3f800000u;            // prefetched raw bits (after_wait at use)
+            if (kInt8 && tid < ROWS_QKV) my_scale = ldg_bits(sc + lrow0 + tid);
             const uint16_t* lnw = (const uint16_t*)lw.input_layernorm_weight;
-            float wln[PT];
+            uint32_t wln[PT];
 #pragma unroll
-            for (int i = 0; i < PT; ++i) wln[i] = bf16_bits_to_f32(lnw[tid + i * kThreads]);
+            for (int i = 0; i < PT; ++i) wln[i] = ldg_bits(lnw + tid + i * kThreads);
             issue_fence();
 
             float hv[PT];
@@ -173,7 +160,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
                 const int k = tid + i * kThreads;
-                xdf[xd_index<W>(k)] = (double)(float)((double)hv[i] * rstd * (double)wln[i]);
+                xdf[xd_index<W>(k)] = (double)(float)((double)hv[i] * rstd * (double)after_wait_bf16(wln[i]));
                 const int rr = k - g * ROWS_H;
                 if (rr >= 0 && rr < ROWS_H) rows_res[rr] = hv[i];
             }
@@ -182,7 +169,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             __syncthreads();
             if (tid < ROWS_QKV) {
                 double v = Stage_<W, ROWS_QKV, H>::row_sum(part, tid);
-                if (kInt8) v = v * (double)my_scale;
+                if (kInt8) v = v * (double)after_wait_f(my_scale);
                 ll_put(&qkv_x[row0 + tid], __float_as_uint((float)v), tag(l, ST_QKV));
             }
             trace(l, 1);
@@ -196,17 +183,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             const int64_t cur = cache_base + (int64_t)a.pos * D;
             // step-independent inputs: norm gains, the RoPE row, and the K/V rows of
             // earlier positions (up to kKvLds of them) staged through registers
-            float nw0 = 0.0f, nw1 = 0.0f, c0 = 0.0f, s0 = 0.0f, c1 = 0.0f, s1 = 0.0f;
+            uint32_t nw0 = 0, nw1 = 0, c0 = 0, s0 = 0, c1 = 0, s1 = 0;
             if (wave < 3) {
                 const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
-                nw0 = bf16_bits_to_f32(nw[lane]);
-                nw1 = bf16_bits_to_f32(nw[lane + 64]);
+                nw0 = ldg_bits(nw + lane);
+                nw1 = ldg_bits(nw + lane + 64);
                 const uint16_t* ct = a.cos_t + (int64_t)a.pos * D;
                 const uint16_t* stt = a.sin_t + (int64_t)a.pos * D;
-                c0 = bf16_bits_to_f32(ct[lane]);
-                s0 = bf16_bits_to_f32(stt[lane]);
-                c1 = bf16_bits_to_f32(ct[lane + 64]);
-                s1 = bf16_bits_to_f32(stt[lane + 64]);
+                c0 = ldg_bits(ct + lane);
+                s0 = ldg_bits(stt + lane);
+                c1 = ldg_bits(ct + lane + 64);
+                s1 = ldg_bits(stt + lane + 64);
             }
             const int npre = a.pos < kKvLds ? a.pos : kKvLds;   // earlier positions held in LDS
             constexpr int kPreU4 = 2 * kKvLds * (D / 8) / kThreads;
@@ -220,7 +207,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                 pre[i] = make_uint4(0, 0, 0, 0);
                 if (j < npre) {
                     const uint16_t* src = (side == 0 ? a.kc : a.vc) + cache_base + (int64_t)j * D + c * 8;
-                    pre[i] = *reinterpret_cast<const uint4*>(src);
+                    pre[i] = ldg16(src);
                 }
             }
             issue_fence();
@@ -249,10 +236,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                 const double x0 = src[lane], x1 = src[lane + 64];
                 const double ssq = wave_sum64(fma(x0, x0, x1 * x1));
                 const double sc = rms_scale(ssq, D, kEps);
-                const double y0 = x0 * sc * (double)nw0;
-                const double y1 = x1 * sc * (double)nw1;
-                const float o0 = (float)(y0 * (double)c0 - y1 * (double)s0);
-                const float o1 = (float)(y0 * (double)s1 + y1 * (double)c1);
+                const double y0 = x0 * sc * (double)after_wait_bf16(nw0);
+                const double y1 = x1 * sc * (double)after_wait_bf16(nw1);
+                const double cd0 = after_wait_bf16(c0), sd0 = after_wait_bf16(s0);
+                const double cd1 = after_wait_bf16(c1), sd1 = after_wait_bf16(s1);
+                const float o0 = (float)(y0 * cd0 - y1 * sd0);
+                const float o1 = (float)(y0 * sd1 + y1 * cd1);
                 if (wave < 2) {
                     qrot[wave * D + lane] = o0;
                     qrot[wave * D + lane + 64] = o1;
@@ -298,9 +287,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
 #pragma unroll
                             for (int u = 0; u < 4; ++u) kw[u] = kp[u];
                         } else {
-                            const uint4* kp = reinterpret_cast<const uint4*>(a.kc + cache_base + (int64_t)j * D + qd * 32);
+                            const uint16_t* kp = a.kc + cache_base + (int64_t)j * D + qd * 32;
 #pragma unroll
-                            for (int u = 0; u < 4; ++u) kw[u] = kp[u];
+                            for (int u = 0; u < 4; ++u) kw[u] = ldg16(kp + 8 * u);
                         }
 #pragma unroll
                         for (int u = 0; u < 4; ++u) {
@@ -350,7 +339,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                 for (int j = wave; j < n; j += kWaves) {
                     const uint32_t vw = j == a.pos ? kv_curb[1][dp]
                                       : j < kKvLds ? kv_lds[1][j][dp]
-                                                   : *reinterpret_cast<const uint32_t*>(a.vc + cache_base + (int64_t)j * D + 2 * dp);
+                                                   : *gview(reinterpret_cast<const uint32_t*>(a.vc + cache_base + (int64_t)j * D + 2 * dp));
                     const double v0 = __uint_as_float(vw << 16);
                     const double v1 = __uint_as_float(vw & 0xffff0000u);
                     const double p0 = scores[0][j], p1 = scores[1][j];
@@ -381,8 +370,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             const uint8_t* base = (const uint8_t*)lw.o_proj_weight;
             Stage_<W, ROWS_H, QD> st;
             st.load([&](int r) { return base + (int64_t)(row0 + r) * QD * ES; }, wave, lane);
-            float my_scale = 1.0f;
-            if (kInt8 && tid < ROWS_H) my_scale = sp.o_scale[row0 + tid];
+            uint32_t my_scale = 0x3f800000u;
+            if (kInt8 && tid < ROWS_H) my_scale = ldg_bits(sp.o_scale + row0 + tid);
             issue_fence();
             {
                 float v[QD / kThreads];
@@ -396,7 +385,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             __syncthreads();
             if (tid < ROWS_H) {
                 double v = Stage_<W, ROWS_H, QD>::row_sum(part, tid);
-                if (kInt8) v = v * (double)my_scale;
+                if (kInt8) v = v * (double)after_wait_f(my_scale);
                 const float x = (float)(v + (double)rows_res[tid]);
                 ll_put(&act_x[row0 + tid], __float_as_uint(x), tag(l, ST_O));
             }
@@ -412,12 +401,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             st.load([&](int r) {
                 return r < CPW ? gb + (int64_t)(c0 + r) * H * ES : ub + (int64_t)(c0 + r - CPW) * H * ES;
             }, wave, lane);
-            float gsc = 1.0f, usc = 1.0f;
-            if (kInt8 && tid < CPW) { gsc = sp.gate_scale[c0 + tid]; usc = sp.up_scale[c0 + tid]; }
+            uint32_t gsc = 0x3f800000u, usc = 0x3f800000u;
+            if (kInt8 && tid < CPW) { gsc = ldg_bits(sp.gate_scale + c0 + tid); usc = ldg_bits(sp.up_scale + c0 + tid); }
             const uint16_t* pnw = (const uint16_t*)lw.post_attn_layernorm_weight;
-            float wpn[PT];
+            uint32_t wpn[PT];
 #pragma unroll
-            for (int i = 0; i < PT; ++i) wpn[i] = bf16_bits_to_f32(pnw[tid + i * kThreads]);
+            for (int i = 0; i < PT; ++i) wpn[i] = ldg_bits(pnw + tid + i * kThreads);
             issue_fence();
             float av[PT];
             wt.get_strided<PT>(act_x + tid, kThreads, tag(l, ST_O), av);
@@ -430,7 +419,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
                 const int k = tid + i * kThreads;
-                const float nv = (float)((double)av[i] * rstd * (double)wpn[i]);
+                const float nv = (float)((double)av[i] * rstd * (double)after_wait_bf16(wpn[i]));
                 xdf[xd_index<W>(k)] = nv;
                 const int rr = k - g * ROWS_H;
                 if (rr >= 0 && rr < ROWS_H) rows_res[rr] = av[i];
@@ -445,7 +434,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             if (tid < CPW) {
                 double gs = Stage_<W, 2 * CPW, H>::row_sum(part, tid);
                 double us = Stage_<W, 2 * CPW, H>::row_sum(part, CPW + tid);
-                if (kInt8) { gs = gs * (double)gsc; us = us * (double)usc; }
+                if (kInt8) { gs = gs * (double)after_wait_f(gsc); us = us * (double)after_wait_f(usc); }
                 const float m = (float)(gs / (1.0 + exp(-gs)) * us);
                 ll_put(&mlp_x[c0 + tid], __float_as_uint(m), tag(l, ST_GU));
                 if (l == last && kDebug && a.dbg_mlp) a.dbg_mlp[c0 + tid] = m;
@@ -459,8 +448,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             const uint8_t* base = (const uint8_t*)lw.down_proj_weight;
             Stage_<W, ROWS_H, I> st;
             st.load([&](int r) { return base + (int64_t)(row0 + r) * I * ES; }, wave, lane);
-            float my_scale = 1.0f;
-            if (kInt8 && tid < ROWS_H) my_scale = sp.down_scale[row0 + tid];
+            uint32_t my_scale = 0x3f800000u;
+            if (kInt8 && tid < ROWS_H) my_scale = ldg_bits(sp.down_scale + row0 + tid);
             issue_fence();
             {
                 float v[I / kThreads];
@@ -474,7 +463,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             __syncthreads();
             if (tid < ROWS_H) {
                 double v = Stage_<W, ROWS_H, I>::row_sum(part, tid);
-                if (kInt8) v = v * (double)my_scale;
+                if (kInt8) v = v * (double)after_wait_f(my_scale);
                 const uint32_t hb = f32_to_bf16_bits((float)(v + (double)rows_res[tid]));
                 ll_put(&hid_x[row0 + tid], __float_as_uint(bf16_bits_to_f32(hb)), tag(l, ST_DOWN));
                 if (l == last && kDebug && a.dbg_hidden) a.dbg_hidden[row0 + tid] = (uint16_t)hb;
@@ -501,18 +490,18 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             for (int i = 0; i < R; ++i) {
                 const int row = r0 + b * RB + i / CH;
                 dst[i] = make_uint4(0, 0, 0, 0);
-                if (row < r1) dst[i] = *reinterpret_cast<const uint4*>(a.lm_w + row * rowbytes + (i % CH) * 1024 + lane * 16);
+                if (row < r1) dst[i] = ldg16(a.lm_w + row * rowbytes + (i % CH) * 1024 + lane * 16);
             }
             const int myrow = r0 + b * RB + lane / span;
             s = 1.0f;
-            if (kInt8 && myrow < r1) s = a.lm_s[myrow];
+            if (kInt8 && myrow < r1) s = gview(a.lm_s)[myrow];
         };
         // the first LM-head batch and the final norm gains do not depend on this step
         int b = wave;
         if (b < nb) fetch(b, cur, scur);
-        float wfn[PT];
+        uint32_t wfn[PT];
 #pragma unroll
-        for (int i = 0; i < PT; ++i) wfn[i] = bf16_bits_to_f32(a.final_norm[tid + i * kThreads]);
+        for (int i = 0; i < PT; ++i) wfn[i] = ldg_bits(a.final_norm + tid + i * kThreads);
         issue_fence();
 
         float hv[PT];
@@ -526,7 +515,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
             const int k = tid + i * kThreads;
-            const float nv = (float)((double)hv[i] * rstd * (double)wfn[i]);
+            const float nv = (float)((double)hv[i] * rstd * (double)after_wait_bf16(wfn[i]));
             xsf[xs_index<W>(k)] = nv;
             if (g == 0 && kDebug && a.dbg_norm) a.dbg_norm[k] = nv;
         }
@@ -641,7 +630,7 @@ static bool xcd_placement_ok() {
             }
             for (int i = 8; i < kNWG; ++i) ok = ok && (h[i] == h[i % 8]);
         }
-        hipFree(d);
+        (void)hipFree(d);
     }
     g_xcd_ok[dev] = ok ? 1 : 2;
     return ok;

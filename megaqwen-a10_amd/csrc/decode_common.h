@@ -51,45 +51,68 @@ struct KArgs {
     uint8_t* ws;
 };
 
+constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
+
+// Workspace layout (after the 256-byte header): one 64-bit exchange word per
+// element of each handed-over vector, every region 256-byte aligned.
+struct Layout {
+    size_t hid, qkv, att, act, mlp, total;
+};
+constexpr Layout layout_for(int H, int I, int NQ, int NKV, int D) {
+    Layout o{};
+    o.hid = sizeof(WsHeader);
+    o.qkv = o.hid + round256((size_t)H * 8);
+    o.att = o.qkv + round256(((size_t)NQ * D + 2 * (size_t)NKV * D) * 8);
+    o.act = o.att + round256((size_t)NQ * D * 8);
+    o.mlp = o.act + round256((size_t)H * 8);
+    o.total = o.mlp + round256((size_t)I * 8);
+    return o;
+}
+
 constexpr int pow2ceil(int x) { return x <= 1 ? 1 : 2 * pow2ceil((x + 1) / 2); }
 
 // One matvec stage of a workgroup: ROWS rows of K inputs, split into (row,
-// 1 KB chunk) items handed round-robin to the 8 waves. Weights are loaded
-// into registers by load() ahead of the input wait; compute() leaves one fp64
+// 1 KB chunk) items handed round-robin to waves W0..7 (a stage whose wave 0
+// polls a cross-XCD exchange leaves it out, so that its polls are not queued
+// behind weight loads: loads return in order). Weights are loaded into
+// registers by load() ahead of the input wait; compute() leaves one fp64
 // partial sum per item in `part` (the input vector is fp64 in per-lane order,
-// xd_index()).
-template <class W, int ROWS, int K>
+// xd_index()). Items past the end get zero weights, so compute() runs every
+// item slot without branches and the FMA chains of the items interleave.
+template <class W, int ROWS, int K, int W0 = 0>
 struct Stage_ {
+    static constexpr int NWV = kWaves - W0;
     static constexpr int CHUNK = 64 * W::kPerLane;
     static constexpr int CH = K / CHUNK;
     static constexpr int ITEMS = ROWS * CH;
-    static constexpr int IPW = (ITEMS + kWaves - 1) / kWaves;
+    static constexpr int IPW = (ITEMS + NWV - 1) / NWV;
     static constexpr int R = pow2ceil(IPW);
     static_assert(K % CHUNK == 0, "row length must be a whole number of 1 KB chunks");
     uint4 w[IPW];
 
     template <class RowPtr>
     __device__ __forceinline__ void load(RowPtr rowptr, int wave, int lane) {
+        if (wave < W0) return;
 #pragma unroll
         for (int j = 0; j < IPW; ++j) {
-            const int it = wave + kWaves * j;
-            if (it < ITEMS)
-                w[j] = *reinterpret_cast<const uint4*>(rowptr(it / CH) + (it % CH) * 1024 + lane * 16);
+            const int it = (wave - W0) + NWV * j;
+            w[j] = make_uint4(0, 0, 0, 0);
+            if (it < ITEMS) w[j] = ldg16(rowptr(it / CH) + (it % CH) * 1024 + lane * 16);
         }
     }
     __device__ __forceinline__ void compute(const double2* xd, double* part, int wave, int lane) const {
+        if (wave < W0) return;
         double acc[R];
 #pragma unroll
         for (int j = 0; j < R; ++j) {
-            acc[j] = 0.0;
-            const int it = wave + kWaves * j;
-            if (j < IPW && it < ITEMS) acc[j] = dot_fragd<W>(w[j], xd, it % CH, lane, 0.0);
+            const int it = (wave - W0) + NWV * j;
+            acc[j] = j < IPW ? dot_fragd<W>(w[j], xd, it % CH, lane, 0.0) : 0.0;
         }
         const double s = transpose_reduce64<R>(acc, lane);
         constexpr int span = kWave / R;
         const int j = lane / span;
         if ((lane % span) == 0 && j < IPW) {
-            const int it = wave + kWaves * j;
+            const int it = (wave - W0) + NWV * j;
             if (it < ITEMS) part[it] = s;
         }
     }
@@ -119,7 +142,6 @@ __device__ __forceinline__ double rms_scale(double sumsq, int n, double eps) {
     return 1.0 / sqrt(sumsq / (double)n + eps);
 }
 
-constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
 // All kNWG workgroups wait on each other, so they must be resident at once:
 // checked once per (kernel, device) with the occupancy calculator.

@@ -46,16 +46,19 @@ constexpr uint32_t kXStages = 6;
 struct XLayout {
     size_t qkvx, actx, mlpx, hidx, lmx, po, pd, lmc, total;
 };
+// The regions follow the single-level kernel's (layout_for), so neither kernel
+// writes words the other could take for its own: the packed words below carry
+// a one-bit tag only.
 constexpr XLayout xlayout_for(int H, int I) {
     XLayout o{};
-    size_t off = sizeof(WsHeader);
+    size_t off = layout_for(H, I, 16, 8, 128).total;
     o.qkvx = off; off += round256((size_t)kNX * 512 * 8);
     o.actx = off; off += round256((size_t)kNX * H * 8);
     o.mlpx = off; off += round256((size_t)kNX * (I / kNX) * 8);
     o.hidx = off; off += round256((size_t)kNX * H * 8);
     o.lmx = off; off += round256((size_t)kNX * kGS * 2 * 8);
-    o.po = off; off += round256((size_t)2 * kNX * H * 8);      // fp64 partials as hi|lo fp32 words
-    o.pd = off; off += round256((size_t)2 * kNX * H * 8);
+    o.po = off; off += round256((size_t)kNX * H * 8);          // packed fp64 partials [xcd][row]
+    o.pd = off; off += round256((size_t)kNX * H * 8);
     o.lmc = off; off += round256((size_t)kNX * 2 * 8);
     o.total = off;
     return o;
@@ -99,14 +102,16 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     constexpr int PT = H / kThreads;        // hidden elements per thread
     constexpr int AD = 2 * D;               // attention outputs per XCD
     constexpr int EPP = 16 / ES;            // weight elements per 16-byte piece
+    // stages C and F: LPR consecutive lanes per output row, each taking every
+    // LPR-th 16-byte piece of the row's segment; the row sum is a DPP butterfly
+    // inside the lane group
+    constexpr int LPR = kThreads / RPW;
     constexpr int PC_O = AD / EPP;          // pieces per O row segment
-    constexpr int NIT_O = RPW * PC_O;
-    constexpr int PT_O = (NIT_O + kThreads - 1) / kThreads;
+    constexpr int PPL_O = (PC_O + LPR - 1) / LPR;
     constexpr int PC_D = IX / EPP;          // pieces per down row segment
-    constexpr int NIT_D = RPW * PC_D;
-    constexpr int PT_D = (NIT_D + kThreads - 1) / kThreads;
-    constexpr int PARTN = (NIT_D > NIT_O ? NIT_D : NIT_O) > 256 ? (NIT_D > NIT_O ? NIT_D : NIT_O) : 256;
+    constexpr int PPL_D = (PC_D + LPR - 1) / LPR;
     constexpr int MLP_PT = (IX + kThreads - 1) / kThreads;
+    static_assert(RPW * LPR == kThreads && (LPR & (LPR - 1)) == 0 && LPR <= kWave, "C/F lane groups");
     static_assert(GR % kGS == 0 && H % kGS == 0 && IX % kGS == 0 && H % kThreads == 0, "even split");
     static_assert(RPW <= kThreads && AD % EPP == 0 && IX % EPP == 0, "shapes");
 
@@ -114,9 +119,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     __shared__ float4 xs[H / 4];            // fp32 LM-head input in per-lane order
     __shared__ float hid[H];                // layer input (bf16 values)
     __shared__ float act[H];                // post-attention residual stream (fp32 values)
-    __shared__ double attn_d[AD];           // this XCD's attention outputs (fp32 values)
-    __shared__ double mlp_d[IX];            // this XCD's SwiGLU outputs (fp32 values)
-    __shared__ double part[PARTN];
+    __shared__ double attn_d[AD];           // this XCD's attention outputs (fp32 values), piece-major
+    __shared__ double mlp_d[IX];            // this XCD's SwiGLU outputs (fp32 values), piece-major
+    __shared__ double part[256];
     __shared__ double red[2 * kWaves];
     __shared__ float att_in[GR];
     __shared__ float qrot[2 * D];
@@ -144,14 +149,14 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     uint64_t* const mlpx = reinterpret_cast<uint64_t*>(a.ws + kLay.mlpx) + (size_t)x * IX;
     uint64_t* const hidx = reinterpret_cast<uint64_t*>(a.ws + kLay.hidx) + (size_t)x * H;
     uint64_t* const lmx = reinterpret_cast<uint64_t*>(a.ws + kLay.lmx) + (size_t)x * kGS * 2;
-    uint64_t* const po = reinterpret_cast<uint64_t*>(a.ws + kLay.po);    // [hi|lo][8][H]
-    uint64_t* const pd = reinterpret_cast<uint64_t*>(a.ws + kLay.pd);    // [hi|lo][8][H]
+    uint64_t* const po = reinterpret_cast<uint64_t*>(a.ws + kLay.po);    // packed [8][H]
+    uint64_t* const pd = reinterpret_cast<uint64_t*>(a.ws + kLay.pd);    // packed [8][H]
     uint64_t* const lmc = reinterpret_cast<uint64_t*>(a.ws + kLay.lmc);
 
     // step-independent reads first
     float hv0[PT];
 #pragma unroll
-    for (int i = 0; i < PT; ++i) hv0[i] = bf16_bits_to_f32(a.embed[(int64_t)a.token * H + tid + i * kThreads]);
+    for (int i = 0; i < PT; ++i) hv0[i] = bf16_bits_to_f32(gview(a.embed)[(int64_t)a.token * H + tid + i * kThreads]);
     {
         const uint64_t* src = reinterpret_cast<const uint64_t*>(a.lw);
         uint64_t* dst = reinterpret_cast<uint64_t*>(s_lw);
@@ -163,6 +168,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         }
     }
     const uint32_t E = __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t XS = __hip_atomic_load(&hdr->xsteps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (g == 0 && tid == 0) {
         // keep the header slots the single-level kernel counts on in a known state
         __hip_atomic_store(&hdr->done[(E + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -172,6 +178,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     // tags end in binary 11 (the single-level kernel's end in 01): no overlap when
     // the two kernels share a workspace
     auto tag = [&](int l, int st) -> uint32_t { return ((E * tps + kXStages * (uint32_t)l + (uint32_t)st) << 2) | 3u; };
+    // one-bit tag of the packed cross-XCD words: po and pd are each written once
+    // per layer, so their use count is XS * L + l + 1
+    auto pbit = [&](int l) -> uint32_t { return (XS * (uint32_t)a.L + (uint32_t)l + 1u) & 1u; };
     Waiter wt(&hdr->abort_flag, a.spin_limit);
     auto trace = [&](int l, int point) {
         if (kDebug && a.trace != nullptr && tid == 0)
@@ -198,25 +207,28 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         else { base = (const uint8_t*)lw.v_proj_weight; mrow0 = x * D + ROWS_A * (r - 24); if (kInt8) sc = sp.v_scale; }
     };
 
-    Stage_<W, ROWS_A, H> stA;
-    float scA = 1.0f;
-    float wln[PT];
+    Stage_<W, ROWS_A, H, 1> stA;            // wave 0 polls stage G's cross-XCD words
+    uint32_t scA = 0x3f800000u;             // prefetched raw bits (after_wait at use)
+    uint32_t wln[PT];
     {
         const uint8_t* base; const float* sc = nullptr; int mrow0;
         qkv_rows(s_lw[0], s_sp[0], base, sc, mrow0);
         stA.load([&](int rr) { return base + (int64_t)(mrow0 + rr) * H * ES; }, wave, lane);
-        if (kInt8 && tid < ROWS_A) scA = sc[mrow0 + tid];
+        if (kInt8 && tid < ROWS_A) scA = ldg_bits(sc + mrow0 + tid);
         const uint16_t* lnw = (const uint16_t*)s_lw[0].input_layernorm_weight;
 #pragma unroll
-        for (int i = 0; i < PT; ++i) wln[i] = bf16_bits_to_f32(lnw[tid + i * kThreads]);
+        for (int i = 0; i < PT; ++i) wln[i] = ldg_bits(lnw + tid + i * kThreads);
 #pragma unroll
         for (int i = 0; i < PT; ++i) hid[tid + i * kThreads] = hv0[i];
     }
     __syncthreads();
 
+    const int tid_all = tid;
     for (int l = 0; l < a.L; ++l) {
         const LayerWeights& lw = s_lw[l];
         const ScalePointers& sp = s_sp[l];
+        const int tid = opaque(tid_all);
+        const int lane = tid % kWave;
 
         // ---------------- A: RMSNorm + QKV rows -> XCD-local words ----------------
         {
@@ -229,14 +241,14 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
                 const int k = tid + i * kThreads;
-                xdf[xd_index<W>(k)] = (double)(float)((double)hid[k] * rstd * (double)wln[i]);
+                xdf[xd_index<W>(k)] = (double)(float)((double)hid[k] * rstd * (double)after_wait_bf16(wln[i]));
             }
             __syncthreads();
             stA.compute(xd, part, wave, lane);
             __syncthreads();
             if (tid < ROWS_A) {
-                double v = Stage_<W, ROWS_A, H>::row_sum(part, tid);
-                if (kInt8) v = v * (double)scA;
+                double v = Stage_<W, ROWS_A, H, 1>::row_sum(part, tid);
+                if (kInt8) v = v * (double)after_wait_f(scA);
                 ll_put_xcd(&qkvx[ROWS_A * r + tid], __float_as_uint((float)v), tag(l, XS_QKV));
             }
             trace(l, 1);
@@ -244,33 +256,31 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 
         // ---------------- B: attention for head pair x (every rank) ----------------
         const int64_t cache_base = ((int64_t)l * kNX + x) * kv_head_stride;
-        uint4 wo[PT_O];
-        float so = 1.0f;
+        const int crow = tid_all / LPR, clr = tid_all % LPR;   // stages C and F: row, lane in row group
+        uint4 wo[PPL_O];
+        uint32_t so = 0x3f800000u;
         {
             // step-independent loads: O weights of stage C, the O scale of this rank's
             // reduction rows, norm gains, the RoPE row and earlier K/V rows
             const uint8_t* ob = (const uint8_t*)lw.o_proj_weight;
 #pragma unroll
-            for (int i = 0; i < PT_O; ++i) {
-                const int it = tid + i * kThreads;
-                wo[i] = make_uint4(0, 0, 0, 0);
-                if (it < NIT_O) {
-                    const int row = it / PC_O, piece = it % PC_O;
-                    wo[i] = *reinterpret_cast<const uint4*>(ob + (int64_t)(R0 + row) * (16 * D) * ES + (int64_t)AD * x * ES + piece * 16);
-                }
+            for (int k = 0; k < PPL_O; ++k) {
+                const int pc = clr + LPR * k;
+                wo[k] = make_uint4(0, 0, 0, 0);
+                if (pc < PC_O) wo[k] = ldg16(ob + (int64_t)(R0 + crow) * (16 * D) * ES + (int64_t)AD * x * ES + pc * 16);
             }
-            if (kInt8 && tid < RPW) so = sp.o_scale[R0 + tid];
-            float nw0 = 0.0f, nw1 = 0.0f, c0 = 0.0f, s0 = 0.0f, c1 = 0.0f, s1 = 0.0f;
+            if (kInt8 && tid < RPW) so = ldg_bits(sp.o_scale + R0 + tid);
+            uint32_t nw0 = 0, nw1 = 0, c0 = 0, s0 = 0, c1 = 0, s1 = 0;
             if (wave < 3) {
                 const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
-                nw0 = bf16_bits_to_f32(nw[lane]);
-                nw1 = bf16_bits_to_f32(nw[lane + 64]);
+                nw0 = ldg_bits(nw + lane);
+                nw1 = ldg_bits(nw + lane + 64);
                 const uint16_t* ct = a.cos_t + (int64_t)a.pos * D;
                 const uint16_t* stt = a.sin_t + (int64_t)a.pos * D;
-                c0 = bf16_bits_to_f32(ct[lane]);
-                s0 = bf16_bits_to_f32(stt[lane]);
-                c1 = bf16_bits_to_f32(ct[lane + 64]);
-                s1 = bf16_bits_to_f32(stt[lane + 64]);
+                c0 = ldg_bits(ct + lane);
+                s0 = ldg_bits(stt + lane);
+                c1 = ldg_bits(ct + lane + 64);
+                s1 = ldg_bits(stt + lane + 64);
             }
             const int n = a.cache_len;
             const int npre = a.pos < kKvLds ? a.pos : kKvLds;
@@ -283,7 +293,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 const int rem = f % (kKvLds * (D / 8));
                 const int j = rem / (D / 8), c = rem % (D / 8);
                 pre[i] = make_uint4(0, 0, 0, 0);
-                if (j < npre) pre[i] = *reinterpret_cast<const uint4*>((side == 0 ? a.kc : a.vc) + cache_base + (int64_t)j * D + c * 8);
+                if (j < npre) pre[i] = ldg16((side == 0 ? a.kc : a.vc) + cache_base + (int64_t)j * D + c * 8);
             }
             issue_fence();
             {
@@ -309,10 +319,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 const double x0 = src[lane], x1 = src[lane + 64];
                 const double ssq = wave_sum64(fma(x0, x0, x1 * x1));
                 const double sc = rms_scale(ssq, D, kEps);
-                const double y0 = x0 * sc * (double)nw0;
-                const double y1 = x1 * sc * (double)nw1;
-                const float o0 = (float)(y0 * (double)c0 - y1 * (double)s0);
-                const float o1 = (float)(y0 * (double)s1 + y1 * (double)c1);
+                const double y0 = x0 * sc * (double)after_wait_bf16(nw0);
+                const double y1 = x1 * sc * (double)after_wait_bf16(nw1);
+                const double cd0 = after_wait_bf16(c0), sd0 = after_wait_bf16(s0);
+                const double cd1 = after_wait_bf16(c1), sd1 = after_wait_bf16(s1);
+                const float o0 = (float)(y0 * cd0 - y1 * sd0);
+                const float o1 = (float)(y0 * sd1 + y1 * cd1);
                 if (wave < 2) {
                     qrot[wave * D + lane] = o0;
                     qrot[wave * D + lane + 64] = o1;
@@ -361,9 +373,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 #pragma unroll
                             for (int u = 0; u < 4; ++u) kw[u] = kp[u];
                         } else {
-                            const uint4* kp = reinterpret_cast<const uint4*>(a.kc + cache_base + (int64_t)j * D + qd * 32);
+                            const uint16_t* kp = a.kc + cache_base + (int64_t)j * D + qd * 32;
 #pragma unroll
-                            for (int u = 0; u < 4; ++u) kw[u] = kp[u];
+                            for (int u = 0; u < 4; ++u) kw[u] = ldg16(kp + 8 * u);
                         }
 #pragma unroll
                         for (int u = 0; u < 4; ++u) {
@@ -412,7 +424,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 for (int j = wave; j < n; j += kWaves) {
                     const uint32_t vw = j == a.pos ? kv_curb[1][dp]
                                       : j < kKvLds ? kv_lds[1][j][dp]
-                                                   : *reinterpret_cast<const uint32_t*>(a.vc + cache_base + (int64_t)j * D + 2 * dp);
+                                                   : *gview(reinterpret_cast<const uint32_t*>(a.vc + cache_base + (int64_t)j * D + 2 * dp));
                     const double v0 = __uint_as_float(vw << 16);
                     const double v1 = __uint_as_float(vw & 0xffff0000u);
                     const double p0 = scores[0][j], p1 = scores[1][j];
@@ -430,7 +442,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 #pragma unroll
                 for (int w = 0; w < kWaves; ++w) o += pv[w][tid];
                 const float of = (float)(o / (tid < D ? L0 : L1));
-                attn_d[tid] = of;
+                attn_d[piece_index(tid, EPP, PC_O)] = of;
                 if (kDebug && writer && l == last && a.dbg_attn) a.dbg_attn[AD * x + tid] = of;
             }
             __syncthreads();
@@ -439,30 +451,21 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 
         // ---------------- C: O partial over this XCD's 256 attention dims -> cross-XCD ----------------
         {
+            double p = 0.0;
 #pragma unroll
-            for (int i = 0; i < PT_O; ++i) {
-                const int it = tid + i * kThreads;
-                if (it < NIT_O) {
-                    const double2* xv = reinterpret_cast<const double2*>(attn_d + (it % PC_O) * EPP);
-                    part[it] = W::dotd(wo[i], xv, 0.0);
-                }
+            for (int k = 0; k < PPL_O; ++k) {
+                const int pc = clr + LPR * k;
+                if (pc < PC_O) p = W::template dotd<PC_O>(wo[k], reinterpret_cast<const double2*>(attn_d) + pc, p);
             }
-            __syncthreads();
-            if (tid < RPW) {
-                double p = 0.0;
-#pragma unroll
-                for (int c = 0; c < PC_O; ++c) p += part[tid * PC_O + c];
-                const float hi = (float)p, lo = (float)(p - (double)hi);
-                ll_put(&po[(size_t)x * H + R0 + tid], __float_as_uint(hi), tag(l, XS_PO));
-                ll_put(&po[(size_t)(kNX + x) * H + R0 + tid], __float_as_uint(lo), tag(l, XS_PO));
-            }
+            p = group_sum64<LPR>(p);
+            if (clr == 0) ll_put64(&po[(size_t)x * H + R0 + crow], pack_tagged(p, pbit(l)));
             trace(l, 4);
         }
 
         // ---------------- D: reduce O partials -> act rows -> XCD-local all-gather ----------------
-        Stage_<W, 2 * CPW, H> stE;
-        float gsc = 1.0f, usc = 1.0f;
-        float wpn[PT];
+        Stage_<W, 2 * CPW, H, 1> stE;       // wave 0 polls stage D's cross-XCD words
+        uint32_t gsc = 0x3f800000u, usc = 0x3f800000u;
+        uint32_t wpn[PT];
         const int c0 = IX * x + CPW * r;
         {
             // stage E's weights, scales and norm gains first
@@ -471,19 +474,19 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             stE.load([&](int rr) {
                 return rr < CPW ? gb + (int64_t)(c0 + rr) * H * ES : ub + (int64_t)(c0 + rr - CPW) * H * ES;
             }, wave, lane);
-            if (kInt8 && tid < CPW) { gsc = sp.gate_scale[c0 + tid]; usc = sp.up_scale[c0 + tid]; }
+            if (kInt8 && tid < CPW) { gsc = ldg_bits(sp.gate_scale + c0 + tid); usc = ldg_bits(sp.up_scale + c0 + tid); }
             const uint16_t* pnw = (const uint16_t*)lw.post_attn_layernorm_weight;
 #pragma unroll
-            for (int i = 0; i < PT; ++i) wpn[i] = bf16_bits_to_f32(pnw[tid + i * kThreads]);
+            for (int i = 0; i < PT; ++i) wpn[i] = ldg_bits(pnw + tid + i * kThreads);
             issue_fence();
 
             if (tid < RPW) {
-                float v16[2 * kNX];
-                wt.get_strided<2 * kNX>(po + R0 + tid, H, tag(l, XS_PO), v16);
+                double v8[kNX];
+                wt.get_packed<kNX>(po + R0 + tid, H, pbit(l), v8);
                 double s = 0.0;
 #pragma unroll
-                for (int xx = 0; xx < kNX; ++xx) s += (double)v16[xx] + (double)v16[kNX + xx];
-                if (kInt8) s = s * (double)so;
+                for (int xx = 0; xx < kNX; ++xx) s += v8[xx];
+                if (kInt8) s = s * (double)after_wait_f(so);
                 const float av = (float)(s + (double)hid[R0 + tid]);
                 ll_put_xcd(&actx[R0 + tid], __float_as_uint(av), tag(l, XS_ACT));
             }
@@ -502,7 +505,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
                 const int k = tid + i * kThreads;
-                const float nv = (float)((double)av[i] * rstd * (double)wpn[i]);
+                const float nv = (float)((double)av[i] * rstd * (double)after_wait_bf16(wpn[i]));
                 xdf[xd_index<W>(k)] = nv;
                 if (kDebug && l == last && g == 0) {
                     if (a.dbg_act) a.dbg_act[k] = nv;
@@ -513,9 +516,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             stE.compute(xd, part, wave, lane);
             __syncthreads();
             if (tid < CPW) {
-                double gs = Stage_<W, 2 * CPW, H>::row_sum(part, tid);
-                double us = Stage_<W, 2 * CPW, H>::row_sum(part, CPW + tid);
-                if (kInt8) { gs = gs * (double)gsc; us = us * (double)usc; }
+                double gs = Stage_<W, 2 * CPW, H, 1>::row_sum(part, tid);
+                double us = Stage_<W, 2 * CPW, H, 1>::row_sum(part, CPW + tid);
+                if (kInt8) { gs = gs * (double)after_wait_f(gsc); us = us * (double)after_wait_f(usc); }
                 const float m = (float)(gs / (1.0 + exp(-gs)) * us);
                 ll_put_xcd(&mlpx[CPW * r + tid], __float_as_uint(m), tag(l, XS_MLP));
                 if (kDebug && l == last && a.dbg_mlp) a.dbg_mlp[c0 + tid] = m;
@@ -524,47 +527,35 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         }
 
         // ---------------- F: down partial over this XCD's channels -> cross-XCD ----------------
-        float sd = 1.0f;
+        uint32_t sd = 0x3f800000u;
         {
-            uint4 wd[PT_D];
+            uint4 wd[PPL_D];
             const uint8_t* db = (const uint8_t*)lw.down_proj_weight;
 #pragma unroll
-            for (int i = 0; i < PT_D; ++i) {
-                const int it = tid + i * kThreads;
-                wd[i] = make_uint4(0, 0, 0, 0);
-                if (it < NIT_D) {
-                    const int row = it / PC_D, piece = it % PC_D;
-                    wd[i] = *reinterpret_cast<const uint4*>(db + (int64_t)(R0 + row) * I * ES + (int64_t)IX * x * ES + piece * 16);
-                }
+            for (int k = 0; k < PPL_D; ++k) {
+                const int pc = clr + LPR * k;
+                wd[k] = make_uint4(0, 0, 0, 0);
+                if (pc < PC_D) wd[k] = ldg16(db + (int64_t)(R0 + crow) * I * ES + (int64_t)IX * x * ES + pc * 16);
             }
-            if (kInt8 && tid < RPW) sd = sp.down_scale[R0 + tid];
+            if (kInt8 && tid < RPW) sd = ldg_bits(sp.down_scale + R0 + tid);
             issue_fence();
             if (tid < IX) {
                 float mv[MLP_PT];
                 wt.get_strided<MLP_PT>(mlpx + tid, kThreads, tag(l, XS_MLP), mv, (IX - tid + kThreads - 1) / kThreads);
 #pragma unroll
                 for (int i = 0; i < MLP_PT; ++i)
-                    if (tid + i * kThreads < IX) mlp_d[tid + i * kThreads] = mv[i];
+                    if (tid + i * kThreads < IX) mlp_d[piece_index(tid + i * kThreads, EPP, PC_D)] = mv[i];
             }
             __syncthreads();
             trace(l, 7);
+            double p = 0.0;
 #pragma unroll
-            for (int i = 0; i < PT_D; ++i) {
-                const int it = tid + i * kThreads;
-                if (it < NIT_D) {
-                    const double2* xv = reinterpret_cast<const double2*>(mlp_d + (it % PC_D) * EPP);
-                    part[it] = W::dotd(wd[i], xv, 0.0);
-                }
+            for (int k = 0; k < PPL_D; ++k) {
+                const int pc = clr + LPR * k;
+                if (pc < PC_D) p = W::template dotd<PC_D>(wd[k], reinterpret_cast<const double2*>(mlp_d) + pc, p);
             }
-            __syncthreads();
-            if (tid < RPW) {
-                double p = 0.0;
-#pragma unroll
-                for (int c = 0; c < PC_D; ++c) p += part[tid * PC_D + c];
-                const float hi = (float)p, lo = (float)(p - (double)hi);
-                ll_put(&pd[(size_t)x * H + R0 + tid], __float_as_uint(hi), tag(l, XS_PD));
-                ll_put(&pd[(size_t)(kNX + x) * H + R0 + tid], __float_as_uint(lo), tag(l, XS_PD));
-            }
+            p = group_sum64<LPR>(p);
+            if (clr == 0) ll_put64(&pd[(size_t)x * H + R0 + crow], pack_tagged(p, pbit(l)));
             trace(l, 8);
         }
 
@@ -576,19 +567,19 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 const uint8_t* base; const float* sc = nullptr; int mrow0;
                 qkv_rows(nl, s_sp[l + 1], base, sc, mrow0);
                 stA.load([&](int rr) { return base + (int64_t)(mrow0 + rr) * H * ES; }, wave, lane);
-                if (kInt8 && tid < ROWS_A) scA = sc[mrow0 + tid];
+                if (kInt8 && tid < ROWS_A) scA = ldg_bits(sc + mrow0 + tid);
                 const uint16_t* lnw = (const uint16_t*)nl.input_layernorm_weight;
 #pragma unroll
-                for (int i = 0; i < PT; ++i) wln[i] = bf16_bits_to_f32(lnw[tid + i * kThreads]);
+                for (int i = 0; i < PT; ++i) wln[i] = ldg_bits(lnw + tid + i * kThreads);
                 issue_fence();
             }
             if (tid < RPW) {
-                float v16[2 * kNX];
-                wt.get_strided<2 * kNX>(pd + R0 + tid, H, tag(l, XS_PD), v16);
+                double v8[kNX];
+                wt.get_packed<kNX>(pd + R0 + tid, H, pbit(l), v8);
                 double s = 0.0;
 #pragma unroll
-                for (int xx = 0; xx < kNX; ++xx) s += (double)v16[xx] + (double)v16[kNX + xx];
-                if (kInt8) s = s * (double)sd;
+                for (int xx = 0; xx < kNX; ++xx) s += v8[xx];
+                if (kInt8) s = s * (double)after_wait_f(sd);
                 const float hf = (float)(s + (double)act[R0 + tid]);
                 ll_put_xcd(&hidx[R0 + tid], __float_as_uint(round_bf16(hf)), tag(l, XS_HID));
             }
@@ -622,19 +613,19 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             for (int i = 0; i < R; ++i) {
                 const int row = r0 + b * RB + i / CH;
                 dst[i] = make_uint4(0, 0, 0, 0);
-                if (row < r1) dst[i] = *reinterpret_cast<const uint4*>(a.lm_w + row * rowbytes + (i % CH) * 1024 + lane * 16);
+                if (row < r1) dst[i] = ldg16(a.lm_w + row * rowbytes + (i % CH) * 1024 + lane * 16);
             }
             const int myrow = r0 + b * RB + lane / span;
             s = 1.0f;
-            if (kInt8 && myrow < r1) s = a.lm_s[myrow];
+            if (kInt8 && myrow < r1) s = gview(a.lm_s)[myrow];
         };
         int b = wave;
         if (b < nb) fetch(b, cur, scur);
         double ss = 0.0;
-        float wfn[PT];
+        uint32_t wfn[PT];
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
-            wfn[i] = bf16_bits_to_f32(a.final_norm[tid + i * kThreads]);
+            wfn[i] = ldg_bits(a.final_norm + tid + i * kThreads);
             const double v = hid[tid + i * kThreads];
             ss = fma(v, v, ss);
         }
@@ -643,7 +634,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
             const int k = tid + i * kThreads;
-            const float nv = (float)((double)hid[k] * rstd * (double)wfn[i]);
+            const float nv = (float)((double)hid[k] * rstd * (double)after_wait_bf16(wfn[i]));
             xsf[xs_index<W>(k)] = nv;
             if (kDebug && g == 0 && a.dbg_norm) a.dbg_norm[k] = nv;
         }
@@ -723,6 +714,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 if (lane == 0) {
                     const bool aborted = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
                     *a.out_token = (aborted || wt.dead) ? -1 : (int)iv;
+                    __hip_atomic_store(&hdr->xsteps, XS + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     __hip_atomic_store(&hdr->epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     if (kDebug && a.trace != nullptr)
                         a.trace[((int64_t)a.L * kTracePoints + 2) * kNWG] = __builtin_amdgcn_s_memrealtime();

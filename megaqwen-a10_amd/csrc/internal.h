@@ -24,7 +24,8 @@ struct WsHeader {
     uint32_t abort_flag;   // set by a kernel whose bounded wait expired
     uint32_t done[2];      // workgroups finished with the LM head, per step parity
     uint64_t best[2];      // packed (ordered logit, ~token) maximum, per step parity
-    uint32_t pad[56];
+    uint32_t xsteps;       // steps run by the XCD-aware kernel (parity tags of its packed words)
+    uint32_t pad[55];
 };
 static_assert(sizeof(WsHeader) == 256, "workspace header is 256 bytes");
 
