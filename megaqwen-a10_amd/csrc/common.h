@@ -31,11 +31,19 @@ __device__ __forceinline__ float dpp(float v) {
 // Value held by this lane's partner at level M of a 64-lane butterfly. Every
 // level pairs a lane whose bit M is clear with one whose bit M is set, inside
 // the same 2M-lane group: xor for M = 32, 16, 2, 1 and the (half-)row mirrors
-// for M = 8, 4 (lane i <-> 15-i, lane i <-> 7-i).
+// for M = 8, 4 (lane i <-> 15-i, lane i <-> 7-i). The xor-32 and xor-16
+// exchanges use gfx950's v_permlane32_swap / v_permlane16_swap (VALU, no LDS
+// round trip): swapping a register with itself leaves the partner's value in
+// one of the two results, chosen by the lane's bit M.
 template <int M>
 __device__ __forceinline__ float partner(float v) {
-    if constexpr (M == 32) return __shfl_xor(v, 32);
-    else if constexpr (M == 16) return __shfl_xor(v, 16);
+    if constexpr (M == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+    } else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+    }
     else if constexpr (M == 8) return dpp<0x140>(v);   // row_mirror
     else if constexpr (M == 4) return dpp<0x141>(v);   // row_half_mirror
     else if constexpr (M == 2) return dpp<0x4E>(v);    // quad_perm [2,3,0,1]

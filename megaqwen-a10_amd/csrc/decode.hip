@@ -26,7 +26,7 @@
 // The workspace (internal.h: WsHeader + exchange buffers) carries the step
 // counter; the last workgroup to finish the LM head publishes the token and
 // advances it.
-#include "decode_common.h"
+#include "attention.h"
 
 #include <hip/hip_ext.h>
 
@@ -60,11 +60,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
     __shared__ double red[2 * kWaves];
     __shared__ float rows_res[ROWS_H];
     __shared__ float att_in[4 * D];
-    __shared__ float qrot[2 * D];
-    __shared__ uint32_t kv_lds[2][kKvLds][D / 2];      // bf16 pairs of the prefetched K and V rows
-    __shared__ uint32_t kv_curb[2][D / 2];             // this position's K and V (bf16 pairs)
-    __shared__ double scores[2][kMaxAttnLen];
-    __shared__ double pv[kWaves][2 * D];
+    __shared__ __align__(16) AttnShared at;
     __shared__ float lm_best_v[kWaves];
     __shared__ int lm_best_i[kWaves];
     __shared__ LayerWeights s_lw[kMaxLayers];
@@ -226,141 +222,22 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                 const int side = f / (kKvLds * (D / 8));
                 const int rem = f % (kKvLds * (D / 8));
                 const int j = rem / (D / 8), c = rem % (D / 8);
-                if (j < npre) *reinterpret_cast<uint4*>(&kv_lds[side][j][c * 4]) = pre[i];
+                if (j < npre) *reinterpret_cast<uint4*>(&at.kv_pre[side][j][c * 4]) = pre[i];
             }
             __syncthreads();
             trace(l, 2);
-            if (wave < 3) {
-                // QK-norm and RoPE in fp64, rounded once to fp32
-                const float* src = att_in + wave * D;
-                const double x0 = src[lane], x1 = src[lane + 64];
-                const double ssq = wave_sum64(fma(x0, x0, x1 * x1));
-                const double sc = rms_scale(ssq, D, kEps);
-                const double y0 = x0 * sc * (double)after_wait_bf16(nw0);
-                const double y1 = x1 * sc * (double)after_wait_bf16(nw1);
-                const double cd0 = after_wait_bf16(c0), sd0 = after_wait_bf16(s0);
-                const double cd1 = after_wait_bf16(c1), sd1 = after_wait_bf16(s1);
-                const float o0 = (float)(y0 * cd0 - y1 * sd0);
-                const float o1 = (float)(y0 * sd1 + y1 * cd1);
-                if (wave < 2) {
-                    qrot[wave * D + lane] = o0;
-                    qrot[wave * D + lane + 64] = o1;
-                    if (l == last && kDebug && a.dbg_q) {
-                        a.dbg_q[(2 * h + wave) * D + lane] = o0;
-                        a.dbg_q[(2 * h + wave) * D + lane + 64] = o1;
-                    }
-                } else {
-                    const uint32_t b0 = f32_to_bf16_bits(o0), b1 = f32_to_bf16_bits(o1);
-                    a.kc[cur + lane] = (uint16_t)b0;
-                    a.kc[cur + lane + 64] = (uint16_t)b1;
-                    uint16_t* row = reinterpret_cast<uint16_t*>(kv_curb[0]);
-                    row[lane] = (uint16_t)b0;
-                    row[lane + 64] = (uint16_t)b1;
-                    if (l == last && kDebug && a.dbg_k) { a.dbg_k[h * D + lane] = o0; a.dbg_k[h * D + lane + 64] = o1; }
-                }
-            } else if (wave == 3) {
-                const float v0 = att_in[3 * D + lane], v1 = att_in[3 * D + lane + 64];
-                const uint32_t b0 = f32_to_bf16_bits(v0), b1 = f32_to_bf16_bits(v1);
-                a.vc[cur + lane] = (uint16_t)b0;
-                a.vc[cur + lane + 64] = (uint16_t)b1;
-                uint16_t* row = reinterpret_cast<uint16_t*>(kv_curb[1]);
-                row[lane] = (uint16_t)b0;
-                row[lane + 64] = (uint16_t)b1;
-                if (l == last && kDebug && a.dbg_v) { a.dbg_v[h * D + lane] = v0; a.dbg_v[h * D + lane + 64] = v1; }
-            }
+            const bool dbg = kDebug && l == last;
+            attn_qk_rope(at, att_in, nw0, nw1, c0, s0, c1, s1, a.kc + cur, a.vc + cur,
+                         (dbg && a.dbg_q) ? a.dbg_q + 2 * h * D : nullptr, (dbg && a.dbg_k) ? a.dbg_k + h * D : nullptr,
+                         (dbg && a.dbg_v) ? a.dbg_v + h * D : nullptr, wave, lane);
             __syncthreads();
-
-            // scores: a quad of lanes per position, each lane a quarter of the head dim.
-            // Positions < kKvLds (and the current one) come from LDS, later ones from HBM.
-            {
-                const int qd = tid & 3;
-                const float* qa = qrot + qd * 32;          // read from LDS at each use (register budget)
-                const float* qb = qrot + D + qd * 32;
-                for (int j0 = 0; j0 < n; j0 += kThreads / 4) {
-                    const int j = j0 + (tid >> 2);
-                    double d0 = 0.0, d1 = 0.0;
-                    if (j < n) {
-                        uint4 kw[4];
-                        if (j == a.pos || j < kKvLds) {
-                            const uint32_t* rowp = j == a.pos ? kv_curb[0] : kv_lds[0][j];
-                            const uint4* kp = reinterpret_cast<const uint4*>(rowp + qd * 16);
-#pragma unroll
-                            for (int u = 0; u < 4; ++u) kw[u] = kp[u];
-                        } else {
-                            const uint16_t* kp = a.kc + cache_base + (int64_t)j * D + qd * 32;
-#pragma unroll
-                            for (int u = 0; u < 4; ++u) kw[u] = ldg16(kp + 8 * u);
-                        }
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            const uint32_t wv[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w};
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const double klo = __uint_as_float(wv[e] << 16);
-                                const double khi = __uint_as_float(wv[e] & 0xffff0000u);
-                                d0 = fma((double)qa[u * 8 + 2 * e], klo, d0);
-                                d0 = fma((double)qa[u * 8 + 2 * e + 1], khi, d0);
-                                d1 = fma((double)qb[u * 8 + 2 * e], klo, d1);
-                                d1 = fma((double)qb[u * 8 + 2 * e + 1], khi, d1);
-                            }
-                        }
-                    }
-                    d0 += partner64<1>(d0); d0 += partner64<2>(d0);
-                    d1 += partner64<1>(d1); d1 += partner64<2>(d1);
-                    if (j < n && qd == 0) {
-                        scores[0][j] = d0 * attn_scale;
-                        scores[1][j] = d1 * attn_scale;
-                    }
-                }
-            }
-            __syncthreads();
-            // softmax (fp64): wave 0 handles head 0, wave 1 head 1 (max, exp in place, sum)
-            if (wave < 2) {
-                double* sv = scores[wave];
-                double m = -INFINITY;
-                for (int j = lane; j < n; j += kWave) m = fmax(m, sv[j]);
-                m = wave_max64(m);
-                double lsum = 0.0;
-                for (int j = lane; j < n; j += kWave) {
-                    const double p = exp(sv[j] - m);
-                    sv[j] = p;
-                    lsum += p;
-                }
-                lsum = wave_sum64(lsum);
-                if (lane == 0) red[wave] = lsum;
-            }
-            __syncthreads();
-            const double L0 = red[0], L1 = red[1];
-
-            // P @ V: lane owns a pair of dims, the 8 waves split the positions
-            {
-                const int dp = lane;
-                double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
-                for (int j = wave; j < n; j += kWaves) {
-                    const uint32_t vw = j == a.pos ? kv_curb[1][dp]
-                                      : j < kKvLds ? kv_lds[1][j][dp]
-                                                   : *gview(reinterpret_cast<const uint32_t*>(a.vc + cache_base + (int64_t)j * D + 2 * dp));
-                    const double v0 = __uint_as_float(vw << 16);
-                    const double v1 = __uint_as_float(vw & 0xffff0000u);
-                    const double p0 = scores[0][j], p1 = scores[1][j];
-                    a00 = fma(p0, v0, a00); a01 = fma(p0, v1, a01);
-                    a10 = fma(p1, v0, a10); a11 = fma(p1, v1, a11);
-                }
-                pv[wave][2 * dp] = a00;
-                pv[wave][2 * dp + 1] = a01;
-                pv[wave][D + 2 * dp] = a10;
-                pv[wave][D + 2 * dp + 1] = a11;
-            }
-            __syncthreads();
-            if (tid < 2 * D) {
-                double od = 0.0;
-#pragma unroll
-                for (int w = 0; w < kWaves; ++w) od += pv[w][tid];
-                const float o = (float)(od / (tid < D ? L0 : L1));
-                const int word = 2 * h * D + tid;
-                ll_put(&att_x[word], __float_as_uint(o), tag(l, ST_ATTN));
-                if (l == last && kDebug && a.dbg_attn) a.dbg_attn[word] = o;
-            }
+            attn_core(at, a.kc + cache_base, a.vc + cache_base, n, a.pos, attn_scale, tid, lane, wave,
+                      [&](int i, float v) {
+                          const int word = 2 * h * D + i;
+                          ll_put(&att_x[word], __float_as_uint(v), tag(l, ST_ATTN));
+                          if (dbg && a.dbg_attn) a.dbg_attn[word] = v;
+                      },
+                      [](int) {});
             trace(l, 3);
         }
 
@@ -435,7 +312,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                 double gs = Stage_<W, 2 * CPW, H>::row_sum(part, tid);
                 double us = Stage_<W, 2 * CPW, H>::row_sum(part, CPW + tid);
                 if (kInt8) { gs = gs * (double)after_wait_f(gsc); us = us * (double)after_wait_f(usc); }
-                const float m = (float)(gs / (1.0 + exp(-gs)) * us);
+                const float m = (float)(gs * rcp_nr(1.0 + exp(-gs)) * us);
                 ll_put(&mlp_x[c0 + tid], __float_as_uint(m), tag(l, ST_GU));
                 if (l == last && kDebug && a.dbg_mlp) a.dbg_mlp[c0 + tid] = m;
             }

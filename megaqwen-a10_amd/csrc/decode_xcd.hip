@@ -31,7 +31,7 @@
 //
 // Each stage's weights (and scales / norm gains) are loaded into registers
 // before the preceding wait, so their fetch overlaps the exchange latency.
-#include "decode_common.h"
+#include "attention.h"
 
 #include <hip/hip_ext.h>
 
@@ -124,11 +124,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     __shared__ double part[256];
     __shared__ double red[2 * kWaves];
     __shared__ float att_in[GR];
-    __shared__ float qrot[2 * D];
-    __shared__ uint32_t kv_lds[2][kKvLds][D / 2];
-    __shared__ uint32_t kv_curb[2][D / 2];
-    __shared__ double scores[2][kMaxAttnLen];
-    __shared__ double pv[kWaves][2 * D];
+    __shared__ __align__(16) AttnShared at;
     __shared__ float lm_v[kWaves];
     __shared__ int lm_i[kWaves];
     __shared__ LayerWeights s_lw[kMaxLayers];
@@ -223,6 +219,53 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     }
     __syncthreads();
 
+    // Stage B's step-independent inputs for a layer, loaded one stage ahead of
+    // its QKV wait: O weights (consumed in stage C), the O scale, the QK-norm
+    // gains and the K/V rows of the first kKvLds earlier positions.
+    const int crow = tid / LPR, clr = tid % LPR;   // stages C and F: row, lane in the row's group
+    constexpr int kPreU4 = 2 * kKvLds * (D / 8) / kThreads;
+    uint4 wo[PPL_O];
+    uint4 pre[kPreU4];
+    uint32_t so = 0x3f800000u, nw0 = 0, nw1 = 0;
+    auto prefetch_b = [&](int ll) {
+        const LayerWeights& lw = s_lw[ll];
+        const uint8_t* ob = (const uint8_t*)lw.o_proj_weight;
+#pragma unroll
+        for (int k = 0; k < PPL_O; ++k) {
+            const int pc = clr + LPR * k;
+            wo[k] = make_uint4(0, 0, 0, 0);
+            if (pc < PC_O) wo[k] = ldg16(ob + (int64_t)(R0 + crow) * (16 * D) * ES + (int64_t)AD * x * ES + pc * 16);
+        }
+        if (kInt8 && tid < RPW) so = ldg_bits(s_sp[ll].o_scale + R0 + tid);
+        if (wave < 3) {
+            const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
+            nw0 = ldg_bits(nw + lane);
+            nw1 = ldg_bits(nw + lane + 64);
+        }
+        const int64_t cb = ((int64_t)ll * kNX + x) * kv_head_stride;
+        const int npre = a.pos < kKvLds ? a.pos : kKvLds;
+#pragma unroll
+        for (int i = 0; i < kPreU4; ++i) {
+            const int f = tid + i * kThreads;
+            const int side = f / (kKvLds * (D / 8));
+            const int rem = f % (kKvLds * (D / 8));
+            const int j = rem / (D / 8), c = rem % (D / 8);
+            pre[i] = make_uint4(0, 0, 0, 0);
+            if (j < npre) pre[i] = ldg16((side == 0 ? a.kc : a.vc) + cb + (int64_t)j * D + c * 8);
+        }
+    };
+    // the RoPE row of this position is the same for every layer
+    uint32_t c0 = 0, s0 = 0, c1 = 0, s1 = 0;
+    if (wave < 3) {
+        const uint16_t* ct = a.cos_t + (int64_t)a.pos * D;
+        const uint16_t* stt = a.sin_t + (int64_t)a.pos * D;
+        c0 = ldg_bits(ct + lane);
+        s0 = ldg_bits(stt + lane);
+        c1 = ldg_bits(ct + lane + 64);
+        s1 = ldg_bits(stt + lane + 64);
+    }
+    prefetch_b(0);
+
     const int tid_all = tid;
     for (int l = 0; l < a.L; ++l) {
         const LayerWeights& lw = s_lw[l];
@@ -256,46 +299,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 
         // ---------------- B: attention for head pair x (every rank) ----------------
         const int64_t cache_base = ((int64_t)l * kNX + x) * kv_head_stride;
-        const int crow = tid_all / LPR, clr = tid_all % LPR;   // stages C and F: row, lane in row group
-        uint4 wo[PPL_O];
-        uint32_t so = 0x3f800000u;
         {
-            // step-independent loads: O weights of stage C, the O scale of this rank's
-            // reduction rows, norm gains, the RoPE row and earlier K/V rows
-            const uint8_t* ob = (const uint8_t*)lw.o_proj_weight;
-#pragma unroll
-            for (int k = 0; k < PPL_O; ++k) {
-                const int pc = clr + LPR * k;
-                wo[k] = make_uint4(0, 0, 0, 0);
-                if (pc < PC_O) wo[k] = ldg16(ob + (int64_t)(R0 + crow) * (16 * D) * ES + (int64_t)AD * x * ES + pc * 16);
-            }
-            if (kInt8 && tid < RPW) so = ldg_bits(sp.o_scale + R0 + tid);
-            uint32_t nw0 = 0, nw1 = 0, c0 = 0, s0 = 0, c1 = 0, s1 = 0;
-            if (wave < 3) {
-                const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
-                nw0 = ldg_bits(nw + lane);
-                nw1 = ldg_bits(nw + lane + 64);
-                const uint16_t* ct = a.cos_t + (int64_t)a.pos * D;
-                const uint16_t* stt = a.sin_t + (int64_t)a.pos * D;
-                c0 = ldg_bits(ct + lane);
-                s0 = ldg_bits(stt + lane);
-                c1 = ldg_bits(ct + lane + 64);
-                s1 = ldg_bits(stt + lane + 64);
-            }
+            // this stage's step-independent inputs (O weights, K/V rows of earlier
+            // positions, QK-norm gains) were loaded during the previous layer
             const int n = a.cache_len;
             const int npre = a.pos < kKvLds ? a.pos : kKvLds;
-            constexpr int kPreU4 = 2 * kKvLds * (D / 8) / kThreads;
-            uint4 pre[kPreU4];
-#pragma unroll
-            for (int i = 0; i < kPreU4; ++i) {
-                const int f = tid + i * kThreads;
-                const int side = f / (kKvLds * (D / 8));
-                const int rem = f % (kKvLds * (D / 8));
-                const int j = rem / (D / 8), c = rem % (D / 8);
-                pre[i] = make_uint4(0, 0, 0, 0);
-                if (j < npre) pre[i] = ldg16((side == 0 ? a.kc : a.vc) + cache_base + (int64_t)j * D + c * 8);
-            }
-            issue_fence();
             {
                 float v1[1];
                 wt.get_strided<1>(qkvx + tid, 0, tag(l, XS_QKV), v1);
@@ -307,144 +315,24 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 const int side = f / (kKvLds * (D / 8));
                 const int rem = f % (kKvLds * (D / 8));
                 const int j = rem / (D / 8), c = rem % (D / 8);
-                if (j < npre) *reinterpret_cast<uint4*>(&kv_lds[side][j][c * 4]) = pre[i];
+                if (j < npre) *reinterpret_cast<uint4*>(&at.kv_pre[side][j][c * 4]) = pre[i];
             }
             __syncthreads();
             trace(l, 2);
             const int64_t cur = cache_base + (int64_t)a.pos * D;
-            const bool writer = (r == 0);
-            if (wave < 3) {
-                // QK-norm and RoPE in fp64, rounded once to fp32
-                const float* src = att_in + wave * D;
-                const double x0 = src[lane], x1 = src[lane + 64];
-                const double ssq = wave_sum64(fma(x0, x0, x1 * x1));
-                const double sc = rms_scale(ssq, D, kEps);
-                const double y0 = x0 * sc * (double)after_wait_bf16(nw0);
-                const double y1 = x1 * sc * (double)after_wait_bf16(nw1);
-                const double cd0 = after_wait_bf16(c0), sd0 = after_wait_bf16(s0);
-                const double cd1 = after_wait_bf16(c1), sd1 = after_wait_bf16(s1);
-                const float o0 = (float)(y0 * cd0 - y1 * sd0);
-                const float o1 = (float)(y0 * sd1 + y1 * cd1);
-                if (wave < 2) {
-                    qrot[wave * D + lane] = o0;
-                    qrot[wave * D + lane + 64] = o1;
-                    if (kDebug && writer && l == last && a.dbg_q) {
-                        a.dbg_q[(2 * x + wave) * D + lane] = o0;
-                        a.dbg_q[(2 * x + wave) * D + lane + 64] = o1;
-                    }
-                } else {
-                    const uint32_t b0 = f32_to_bf16_bits(o0), b1 = f32_to_bf16_bits(o1);
-                    if (writer) {
-                        a.kc[cur + lane] = (uint16_t)b0;
-                        a.kc[cur + lane + 64] = (uint16_t)b1;
-                    }
-                    uint16_t* row = reinterpret_cast<uint16_t*>(kv_curb[0]);
-                    row[lane] = (uint16_t)b0;
-                    row[lane + 64] = (uint16_t)b1;
-                    if (kDebug && writer && l == last && a.dbg_k) { a.dbg_k[x * D + lane] = o0; a.dbg_k[x * D + lane + 64] = o1; }
-                }
-            } else if (wave == 3) {
-                const float v0 = att_in[3 * D + lane], v1 = att_in[3 * D + lane + 64];
-                const uint32_t b0 = f32_to_bf16_bits(v0), b1 = f32_to_bf16_bits(v1);
-                if (writer) {
-                    a.vc[cur + lane] = (uint16_t)b0;
-                    a.vc[cur + lane + 64] = (uint16_t)b1;
-                }
-                uint16_t* row = reinterpret_cast<uint16_t*>(kv_curb[1]);
-                row[lane] = (uint16_t)b0;
-                row[lane + 64] = (uint16_t)b1;
-                if (kDebug && writer && l == last && a.dbg_v) { a.dbg_v[x * D + lane] = v0; a.dbg_v[x * D + lane + 64] = v1; }
-            }
+            const bool writer = (r == 0);           // rank 0 writes the cache rows
+            const bool dbg = kDebug && writer && l == last;
+            attn_qk_rope(at, att_in, nw0, nw1, c0, s0, c1, s1, writer ? a.kc + cur : nullptr,
+                         writer ? a.vc + cur : nullptr, (dbg && a.dbg_q) ? a.dbg_q + 2 * x * D : nullptr,
+                         (dbg && a.dbg_k) ? a.dbg_k + x * D : nullptr, (dbg && a.dbg_v) ? a.dbg_v + x * D : nullptr,
+                         wave, lane);
             __syncthreads();
-
-            // scores (fp64): a quad of lanes per position, each lane a quarter of the head dim
-            {
-                const int qd = tid & 3;
-                const float* qa = qrot + qd * 32;          // read from LDS at each use (register budget)
-                const float* qb = qrot + D + qd * 32;
-                for (int j0 = 0; j0 < n; j0 += kThreads / 4) {
-                    const int j = j0 + (tid >> 2);
-                    double d0 = 0.0, d1 = 0.0;
-                    if (j < n) {
-                        uint4 kw[4];
-                        if (j == a.pos || j < kKvLds) {
-                            const uint32_t* rowp = j == a.pos ? kv_curb[0] : kv_lds[0][j];
-                            const uint4* kp = reinterpret_cast<const uint4*>(rowp + qd * 16);
-#pragma unroll
-                            for (int u = 0; u < 4; ++u) kw[u] = kp[u];
-                        } else {
-                            const uint16_t* kp = a.kc + cache_base + (int64_t)j * D + qd * 32;
-#pragma unroll
-                            for (int u = 0; u < 4; ++u) kw[u] = ldg16(kp + 8 * u);
-                        }
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            const uint32_t wv[4] = {kw[u].x, kw[u].y, kw[u].z, kw[u].w};
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const double klo = __uint_as_float(wv[e] << 16);
-                                const double khi = __uint_as_float(wv[e] & 0xffff0000u);
-                                d0 = fma((double)qa[u * 8 + 2 * e], klo, d0);
-                                d0 = fma((double)qa[u * 8 + 2 * e + 1], khi, d0);
-                                d1 = fma((double)qb[u * 8 + 2 * e], klo, d1);
-                                d1 = fma((double)qb[u * 8 + 2 * e + 1], khi, d1);
-                            }
-                        }
-                    }
-                    d0 += partner64<1>(d0); d0 += partner64<2>(d0);
-                    d1 += partner64<1>(d1); d1 += partner64<2>(d1);
-                    if (j < n && qd == 0) {
-                        scores[0][j] = d0 * attn_scale;
-                        scores[1][j] = d1 * attn_scale;
-                    }
-                }
-            }
-            __syncthreads();
-            // softmax (fp64): wave 0 handles head 0, wave 1 head 1 (max, exp in place, sum)
-            if (wave < 2) {
-                double* sv = scores[wave];
-                double m = -INFINITY;
-                for (int j = lane; j < n; j += kWave) m = fmax(m, sv[j]);
-                m = wave_max64(m);
-                double lsum = 0.0;
-                for (int j = lane; j < n; j += kWave) {
-                    const double p = exp(sv[j] - m);
-                    sv[j] = p;
-                    lsum += p;
-                }
-                lsum = wave_sum64(lsum);
-                if (lane == 0) red[wave] = lsum;
-            }
-            __syncthreads();
-            const double L0 = red[0], L1 = red[1];
-            // P @ V (fp64): lane owns a pair of dims, the 8 waves split the positions
-            {
-                const int dp = lane;
-                double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
-                for (int j = wave; j < n; j += kWaves) {
-                    const uint32_t vw = j == a.pos ? kv_curb[1][dp]
-                                      : j < kKvLds ? kv_lds[1][j][dp]
-                                                   : *gview(reinterpret_cast<const uint32_t*>(a.vc + cache_base + (int64_t)j * D + 2 * dp));
-                    const double v0 = __uint_as_float(vw << 16);
-                    const double v1 = __uint_as_float(vw & 0xffff0000u);
-                    const double p0 = scores[0][j], p1 = scores[1][j];
-                    a00 = fma(p0, v0, a00); a01 = fma(p0, v1, a01);
-                    a10 = fma(p1, v0, a10); a11 = fma(p1, v1, a11);
-                }
-                pv[wave][2 * dp] = a00;
-                pv[wave][2 * dp + 1] = a01;
-                pv[wave][D + 2 * dp] = a10;
-                pv[wave][D + 2 * dp + 1] = a11;
-            }
-            __syncthreads();
-            if (tid < AD) {
-                double o = 0.0;
-#pragma unroll
-                for (int w = 0; w < kWaves; ++w) o += pv[w][tid];
-                const float of = (float)(o / (tid < D ? L0 : L1));
-                attn_d[piece_index(tid, EPP, PC_O)] = of;
-                if (kDebug && writer && l == last && a.dbg_attn) a.dbg_attn[AD * x + tid] = of;
-            }
+            attn_core(at, a.kc + cache_base, a.vc + cache_base, n, a.pos, attn_scale, tid, lane, wave,
+                      [&](int i, float v) {
+                          attn_d[piece_index(i, EPP, PC_O)] = v;
+                          if (dbg && a.dbg_attn) a.dbg_attn[AD * x + i] = v;
+                      },
+                      [](int) {});
             __syncthreads();
             trace(l, 3);
         }
@@ -464,11 +352,13 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 
         // ---------------- D: reduce O partials -> act rows -> XCD-local all-gather ----------------
         Stage_<W, 2 * CPW, H, 1> stE;       // wave 0 polls stage D's cross-XCD words
+        uint32_t sd = 0x3f800000u;
+        uint4 wd[PPL_D];                    // stage F's down weights
         uint32_t gsc = 0x3f800000u, usc = 0x3f800000u;
         uint32_t wpn[PT];
         const int c0 = IX * x + CPW * r;
         {
-            // stage E's weights, scales and norm gains first
+            // stage E's weights (waves 1-7), scales and norm gains
             const uint8_t* gb = (const uint8_t*)lw.gate_proj_weight;
             const uint8_t* ub = (const uint8_t*)lw.up_proj_weight;
             stE.load([&](int rr) {
@@ -490,11 +380,25 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 const float av = (float)(s + (double)hid[R0 + tid]);
                 ll_put_xcd(&actx[R0 + tid], __float_as_uint(av), tag(l, XS_ACT));
             }
+
             float av[PT];
             wt.get_strided<PT>(actx + tid, kThreads, tag(l, XS_ACT), av);
 #pragma unroll
             for (int i = 0; i < PT; ++i) act[tid + i * kThreads] = av[i];
             trace(l, 5);
+            issue_fence();
+            {
+                // stage F's down weights: issued after the act gather (so that
+                // neither exchange waits for them), consumed after stage E
+                const uint8_t* db = (const uint8_t*)lw.down_proj_weight;
+#pragma unroll
+                for (int k = 0; k < PPL_D; ++k) {
+                    const int pc = clr + LPR * k;
+                    wd[k] = make_uint4(0, 0, 0, 0);
+                    if (pc < PC_D) wd[k] = ldg16(db + (int64_t)(R0 + crow) * I * ES + (int64_t)IX * x * ES + pc * 16);
+                }
+                if (kInt8 && tid < RPW) sd = ldg_bits(sp.down_scale + R0 + tid);
+            }
 
             // ---------------- E: RMSNorm + gate/up + SwiGLU -> XCD-local mlp ----------------
             double ss = 0.0;
@@ -519,7 +423,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 double gs = Stage_<W, 2 * CPW, H, 1>::row_sum(part, tid);
                 double us = Stage_<W, 2 * CPW, H, 1>::row_sum(part, CPW + tid);
                 if (kInt8) { gs = gs * (double)after_wait_f(gsc); us = us * (double)after_wait_f(usc); }
-                const float m = (float)(gs / (1.0 + exp(-gs)) * us);
+                const float m = (float)(gs * rcp_nr(1.0 + exp(-gs)) * us);
                 ll_put_xcd(&mlpx[CPW * r + tid], __float_as_uint(m), tag(l, XS_MLP));
                 if (kDebug && l == last && a.dbg_mlp) a.dbg_mlp[c0 + tid] = m;
             }
@@ -527,18 +431,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         }
 
         // ---------------- F: down partial over this XCD's channels -> cross-XCD ----------------
-        uint32_t sd = 0x3f800000u;
         {
-            uint4 wd[PPL_D];
-            const uint8_t* db = (const uint8_t*)lw.down_proj_weight;
-#pragma unroll
-            for (int k = 0; k < PPL_D; ++k) {
-                const int pc = clr + LPR * k;
-                wd[k] = make_uint4(0, 0, 0, 0);
-                if (pc < PC_D) wd[k] = ldg16(db + (int64_t)(R0 + crow) * I * ES + (int64_t)IX * x * ES + pc * 16);
-            }
-            if (kInt8 && tid < RPW) sd = ldg_bits(sp.down_scale + R0 + tid);
-            issue_fence();
+
             if (tid < IX) {
                 float mv[MLP_PT];
                 wt.get_strided<MLP_PT>(mlpx + tid, kThreads, tag(l, XS_MLP), mv, (IX - tid + kThreads - 1) / kThreads);
@@ -562,7 +456,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         // ---------------- G: reduce down partials -> bf16 hidden -> XCD-local all-gather ----------------
         {
             if (l < last) {
-                // the next layer's QKV weights, scales and input-norm gains first
+                // the next layer's QKV weights (waves 1-7), scales and input-norm gains
                 const LayerWeights& nl = s_lw[l + 1];
                 const uint8_t* base; const float* sc = nullptr; int mrow0;
                 qkv_rows(nl, s_sp[l + 1], base, sc, mrow0);
@@ -583,6 +477,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 const float hf = (float)(s + (double)act[R0 + tid]);
                 ll_put_xcd(&hidx[R0 + tid], __float_as_uint(round_bf16(hf)), tag(l, XS_HID));
             }
+
             float hv[PT];
             wt.get_strided<PT>(hidx + tid, kThreads, tag(l, XS_HID), hv);
 #pragma unroll
@@ -591,6 +486,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 if (kDebug && l == last && g == 0 && a.dbg_hidden)
                     a.dbg_hidden[tid + i * kThreads] = (uint16_t)f32_to_bf16_bits(hv[i]);
             }
+            // the next layer's stage B inputs: after the hidden gather, so that
+            // neither exchange waits for them; stage A covers their latency
+            issue_fence();
+            if (l < last) prefetch_b(l + 1);
             __syncthreads();
             trace(l, 9);
         }

@@ -176,6 +176,23 @@ def test_small_int8_deterministic(variant, small):
     assert _greedy(dec, prompt, 12) == a[0]
 
 
+def test_trace_without_debug_outputs(variant, small, dev):
+    """The timing trace alone selects the instrumented kernel with every debug
+    output pointer null: it must write through none of them and give the same tokens."""
+    dec, d, prompt, cfg, _ = small
+    dec.enable_debug(False)
+    L = cfg.num_layers
+    buf = torch.zeros((L + 1) * 10 * 256, dtype=torch.int64, device=dev)
+    dec.set_trace(buf)
+    try:
+        toks = _greedy(dec, prompt, 12)
+    finally:
+        dec.set_trace(None)
+    assert toks == d["tokens"][:12]
+    t = buf.view(L + 1, 10, 256)
+    assert bool((t[:L, 0, :] > 0).all()) and bool((t[:L, 1, :] > 0).all())
+
+
 def test_reset_and_position(small):
     dec, d, prompt, cfg, _ = small
     dec.reset()
