@@ -18,7 +18,10 @@ The JSON line also carries:
 * ``parity`` — the timed tokens against the committed oracle fixture.
 
 Other workloads (parity-case shapes, one JSON line each): ``matvec``
-``positions`` (config 3 positions, bf16 weights).
+``positions`` (config 3 positions, bf16 weights), and
+``traffic``: a uint8 add over a 256 MiB buffer (reads and writes exactly
+256 MiB, the calibration for the FETCH_SIZE / WRITE_SIZE counters) followed
+by 8 decode steps, for ``rocprofv3 --pmc`` runs.
 """
 from __future__ import annotations
 
@@ -34,6 +37,10 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 PROMPT_LEN = 8
+# Memory traffic per decode launch of this kernel, measured with rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE runs of megaqwen-a10_amd/profile_decode.py, each scaled by the counter's reading for a
+# 256 MiB copy (the commands and numbers are in profiles/decode_xcd_kernel_int8_qwen3-0.6b_traffic.txt).
+MEASURED_TRAFFIC = {"mq::decode_xcd_kernel<1024, 3072, mq::Int8W, false>": 638_600_000}
 
 
 def parse():
@@ -43,8 +50,12 @@ def parse():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-steps", type=int, default=32, help="greedy steps of the CPU baseline sample")
-    ap.add_argument("--workload", default="decode", choices=["decode", "matvec", "positions"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "matvec", "positions", "traffic"])
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-kernel-events", action="store_true",
+                    help="do not attach timing events to the decode launches (for runs under rocprofv3 "
+                         "--kernel-trace, which supplies the kernel durations itself); roofline.achieved then "
+                         "uses the wall time per step")
     return ap.parse_args()
 
 
@@ -103,24 +114,31 @@ def run_decode(args, mq, torch):
     torch.cuda.synchronize()
 
     # timed region: K greedy steps through the drop-in API
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    for e in starts + ends:
-        e.record()                     # create the HIP events before the timed region
+    starts, ends = [], []
+    if not args.no_kernel_events:
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+        for e in starts + ends:
+            e.record()                 # create the HIP events before the timed region
     toks = []
     tok = first
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         # the dispatch itself records the pair at the kernel's start and end (hipExtLaunchKernel)
-        dec.set_timing_events(starts[i], ends[i])
+        if not args.no_kernel_events:
+            dec.set_timing_events(starts[i], ends[i])
         dec.launch_step(tok)
         tok = int(dec.output_token.item())
         toks.append(tok)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    dec.set_timing_events(None, None)
-    kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    if not args.no_kernel_events:
+        dec.set_timing_events(None, None)
+    if args.no_kernel_events:
+        kern_ms = [wall * 1e3 / args.steps] * args.steps
+    else:
+        kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     if min(toks) < 0:
         status = dec._lib.mq_decode_check(dec.workspace.data_ptr(), None)
         raise RuntimeError(f"decode step {toks.index(min(toks))} of the timed region failed: "
@@ -154,17 +172,20 @@ def run_decode(args, mq, torch):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "f64",
         "data": "synthetic",
         "config": {"workload": "config 1: INT8 greedy decode, Qwen3-0.6B architecture random-init (seed 0), "
                                "bs=1, 8-token random prompt prefilled untimed, K greedy steps timed",
                    "weights": "int8 per-output-channel (scale=bf16(absmax/127)); embed/norms/RoPE/KV bf16",
+                   "arithmetic": "layer stages fp64 (rounded to fp32/bf16 where the reference stores), LM head fp32",
                    "layers": cfg.num_layers, "hidden": cfg.hidden_size, "vocab": cfg.vocab_size,
                    "batch": 1, "prompt_len": PROMPT_LEN, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(kernel),
                      "kernel": kernel,
                      "kernel_avg_us": round(sum(kern_ms) / len(kern_ms) * 1e3, 2),
+                     "timing": "wall per step" if args.no_kernel_events else
+                               "HIP events recorded by the dispatch itself (hipExtLaunchKernel), launch stream",
                      "bytes_per_launch_avg": int(bytes_total / args.steps)},
         "device_tok_s": round(args.steps / kern_s, 1),
         "parity": parity,
@@ -187,7 +208,6 @@ def run_decode(args, mq, torch):
 
 def run_matvec(args, mq, torch):
     """per-shape INT8 matvec GB/s, rotating weight copies past the 256 MB MALL."""
-    from oracle import quant as oquant  # noqa: F401  (not used for timing)
     dev = torch.device("cuda:0")
     shapes = {"qkv": (4096, 1024), "o": (1024, 2048), "gate_up": (6144, 1024), "down": (1024, 3072),
               "lm_head": (151936, 1024)}
@@ -257,11 +277,43 @@ def run_positions(args, mq, torch):
                        "tok_s_at_position": res}}
 
 
+def run_traffic(args, mq, torch):
+    """Counter calibration plus decode steps for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs."""
+    dev = torch.device("cuda:0")
+    nbytes = 256 * 2 ** 20
+    a = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(4):
+        torch.add(a, 1, out=b)              # reads nbytes, writes nbytes
+    torch.cuda.synchronize()
+    del a, b
+    cfg = mq.QWEN3_0_6B
+    state, prompt = mq.random_init_state(cfg, seed=args.seed)
+    S = PROMPT_LEN + 16
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    qstate = mq.quantize_state(state, cfg, dev)
+    del state
+    embed, layers, scales, lm_q, lm_s, fnorm = mq.pack_int8(qstate, cfg)
+    dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+    tok = None
+    for t in prompt.tolist():
+        tok = dec.decode_step(int(t))
+    for _ in range(8):
+        tok = dec.decode_step(tok)
+    torch.cuda.synchronize()
+    return {"metric": "counter calibration run", "value": 0, "unit": "none", "n_gpus": 1, "steps": 8, "warmup": 0,
+            "ms_per_step": 0, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f64",
+            "data": "synthetic",
+            "config": {"workload": "traffic: 4 x uint8 add over 256 MiB (256 MiB read + 256 MiB written each), "
+                                   "then 8-token prefill + 8 decode steps of config 1",
+                       "copy_bytes": nbytes, "decode_steps": 16, "variant": mq.decode_variant()}}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the decode path is single-device, "
-              "see DESIGN.md for how it would shard", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}): the batch-1 decode step runs on a "
+              "single device", file=sys.stderr)
         return 2
     import torch
     import __graft_entry__
@@ -269,11 +321,14 @@ def main():
     if not torch.cuda.is_available():
         print("no HIP device visible", file=sys.stderr)
         return 1
-    fn = {"decode": run_decode, "matvec": run_matvec, "positions": run_positions}[args.workload]
+    fn = {"decode": run_decode, "matvec": run_matvec, "positions": run_positions, "traffic": run_traffic}[args.workload]
     out = fn(args, mq, torch)
     print(json.dumps(out), flush=True)
     return 0
 
 
 if __name__ == "__main__":
-    sys.exit(main())
+    # return normally on success (the interpreter-shutdown path profilers finalise on)
+    status = main()
+    if status:
+        sys.exit(status)
