@@ -126,11 +126,15 @@ typedef struct mq_decode_args {
     void* timing_stop;
     /* Optional per-stage timeline: uint64 [(num_layers + 1) * 10 * 256], written
      * when non-NULL with the 100 MHz real-time counter. Entry
-     * [(l * 10 + p) * 256 + g] is when workgroup g passed point p of layer l:
-     * p = 0/1 QKV input ready/output written, 2/3 attention (workgroups 0-7),
-     * 4/5 O projection, 6/7 gate/up, 8/9 down. Layer num_layers holds p = 0
-     * final-norm input ready, p = 1 LM head done, and [(L*10 + 2) * 256] the
-     * token publication. */
+     * [(l * 10 + p) * 256 + g] is when workgroup g passed point p of layer l.
+     * Single-level kernel: p = 0/1 QKV input ready/output written, 2/3
+     * attention (workgroups 0-7), 4/5 O projection, 6/7 gate/up, 8/9 down.
+     * XCD-aware kernel: p = 0/1 QKV input ready/output written, 2/3 attention
+     * inputs ready/output in LDS (every workgroup), 4 O partial written,
+     * 5 residual rows gathered, 6 gate/up output written, 7 SwiGLU outputs
+     * gathered, 8 down partial written, 9 hidden rows gathered.
+     * Layer num_layers holds p = 0 final-norm input ready, p = 1 LM head done,
+     * and [(L*10 + 2) * 256] the token publication. */
     void* trace;
 } mq_decode_args;
 
@@ -155,8 +159,9 @@ int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream);
 int mq_decode_check(void* workspace, hipStream_t stream);
 
 /* Kernel variant for all following steps in this process: 0 = automatic
- * (default: the XCD-aware kernel when workgroup g is placed on XCD g % 8,
- * checked once per device), 1 = single-level exchange kernel, 2 = XCD-aware. */
+ * (default: the XCD-aware kernel when the workgroups of each residue class
+ * g mod 8 share one XCD and the 8 classes cover the 8 XCDs, checked once per
+ * device), 1 = single-level exchange kernel, 2 = XCD-aware. */
 int mq_decode_set_variant(int variant);
 /* The variant a step with these dims would use now (1 or 2), or -status. */
 int mq_decode_variant(const mq_model_dims* dims, int int8);

@@ -34,8 +34,8 @@ struct DecodeShape {
 };
 
 size_t decode_workspace_bytes(const DecodeShape& s);
-// Kernel variant: 0 = automatic (XCD-aware when the device places workgroup g
-// on XCD g % 8), 1 = single-level exchange kernel, 2 = XCD-aware kernel.
+// Kernel variant: 0 = automatic (XCD-aware when the workgroups of each residue
+// class g mod 8 share one XCD), 1 = single-level exchange kernel, 2 = XCD-aware.
 int set_decode_variant(int variant);
 int decode_variant_in_use(const DecodeShape& s, bool int8);
 // After an in-kernel placement failure: use the single-level kernel from now on.

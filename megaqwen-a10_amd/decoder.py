@@ -36,8 +36,9 @@ VARIANTS = {"auto": 0, "flat": 1, "xcd": 2}
 
 def set_decode_variant(name: str) -> None:
     """Select the decode kernel for all following steps in this process:
-    ``"auto"`` (default; the XCD-aware kernel when the device places workgroup g
-    on XCD g % 8), ``"flat"`` (single-level exchanges) or ``"xcd"``."""
+    ``"auto"`` (default; the XCD-aware kernel when the workgroups of each
+    residue class g mod 8 share one XCD, checked once per device), ``"flat"``
+    (single-level exchanges) or ``"xcd"``."""
     lib = _lib.load()
     _lib.check(lib.mq_decode_set_variant(VARIANTS[name]), "mq_decode_set_variant")
 
