@@ -18,18 +18,10 @@ struct AttnShared {
     double q[2][kHD];                      // rotated queries (fp32 values)
     uint32_t kv_cur[2][kHD / 2];           // this position's K and V rows (bf16 pairs)
     uint32_t kv_pre[2][kKvLds][kHD / 2];   // K and V rows of the first kKvLds positions
-    double p[2][kMaxAttnLen];              // scores, then unnormalised probabilities
+    double p[2][kMaxAttnLen];              // scores
     double pv[kWaves][2 * kHD];            // per-wave partial P @ V
     double wred[4][kWaves];                // per-wave score maxima, then probability sums (2 heads each)
 };
-
-// 1/v for v > 0: hardware estimate and two Newton steps r <- r (2 - v r).
-__device__ __forceinline__ double rcp_nr(double v) {
-    double r = __builtin_amdgcn_rcp(v);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) r = fma(r, fma(-v, r, 1.0), r);
-    return r;
-}
 
 // QK-RMSNorm and RoPE (split-half rotation) of the new q and k rows, and the
 // bf16 K/V rows of this position. Waves 0 and 1 take the two query heads,
@@ -83,7 +75,8 @@ __device__ __forceinline__ const uint32_t* attn_k_row_lds(const AttnShared& at, 
 
 // Scores of both heads for all n positions with G lanes per position (each
 // lane a 128/G-element slice of the head dim), scaled, into at.p; each wave's
-// maxima into at.wred[0..1].
+// maxima, rounded to fp32, into at.wred[0..1] (the softmax only needs a value
+// close to the maximum: exp(s - m) / sum exp(s - m) does not depend on m).
 template <int G>
 __device__ __forceinline__ void attn_scores(AttnShared& at, const uint16_t* kh, int n, int pos, double scale,
                                             int tid, int lane, int wave) {
@@ -93,7 +86,7 @@ __device__ __forceinline__ void attn_scores(AttnShared& at, const uint16_t* kh, 
     const int gi = tid % G;
     const double* q0 = at.q[0] + gi * EPL;
     const double* q1 = at.q[1] + gi * EPL;
-    double m0 = -INFINITY, m1 = -INFINITY;
+    float m0 = -INFINITY, m1 = -INFINITY;
     for (int j0 = 0; j0 < n; j0 += P) {
         const int j = j0 + tid / G;
         double d0[2] = {0.0, 0.0}, d1[2] = {0.0, 0.0};
@@ -127,21 +120,28 @@ __device__ __forceinline__ void attn_scores(AttnShared& at, const uint16_t* kh, 
         const double s1 = group_sum64<G>(d1[0] + d1[1]) * scale;
         if (j < n) {
             if (gi == 0) { at.p[0][j] = s0; at.p[1][j] = s1; }
-            m0 = fmax(m0, s0);
-            m1 = fmax(m1, s1);
+            m0 = fmaxf(m0, (float)s0);
+            m1 = fmaxf(m1, (float)s1);
         }
     }
-    m0 = wave_max64(m0);
-    m1 = wave_max64(m1);
+    m0 = wave_max(m0);
+    m1 = wave_max(m1);
     if (lane == 0) { at.wred[0][wave] = m0; at.wred[1][wave] = m1; }
+}
+
+__device__ __forceinline__ double readlane64(double v, int l) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)u, l);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(u >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
 // Scores, softmax and P @ V of both query heads over positions [0, n) (the
 // current one, `pos`, from at.kv_cur). at.q / kv_cur / kv_pre must be written
 // and visible (barrier) on entry. Calls emit(i, value) for output element
 // i = head * 128 + dim on threads tid < 256, then returns without a barrier.
-// mark(k) is called after sub-stage k (0 scores, 1 softmax, 2 P @ V) for
-// timing instrumentation.
+// mark(k) is called after sub-stage k (0 scores, 1 and 2 softmax with P @ V)
+// for timing instrumentation.
 template <class Emit, class Mark>
 __device__ __forceinline__ void attn_core(AttnShared& at, const uint16_t* kh, const uint16_t* vh, int n, int pos,
                                           double scale, int tid, int lane, int wave, Emit emit, Mark mark) {
@@ -151,33 +151,37 @@ __device__ __forceinline__ void attn_core(AttnShared& at, const uint16_t* kh, co
     else attn_scores<4>(at, kh, n, pos, scale, tid, lane, wave);
     __syncthreads();
     mark(0);
-    // unnormalised probabilities exp(s - max), all threads
-    {
-        double m0 = at.wred[0][0], m1 = at.wred[1][0];
+    double M0 = at.wred[0][0], M1 = at.wred[1][0];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) { m0 = fmax(m0, at.wred[0][w]); m1 = fmax(m1, at.wred[1][w]); }
-        for (int j = tid; j < n; j += kThreads) {
-            at.p[0][j] = exp(at.p[0][j] - m0);
-            at.p[1][j] = exp(at.p[1][j] - m1);
-        }
-    }
-    __syncthreads();
-    mark(1);
-    // P @ V: wave w takes positions j = w mod 8, lane the dims 2*lane, 2*lane+1 of
-    // both heads; the probability sums ride along
+    for (int w = 1; w < kWaves; ++w) { M0 = fmax(M0, at.wred[0][w]); M1 = fmax(M1, at.wred[1][w]); }
+    // softmax numerators and P @ V. Wave w takes positions j = w + 8t: lane t
+    // computes exp(s_j - m) for its t (64 positions per chunk) and the loop hands
+    // the values to every lane with readlane; lane l accumulates dims 2l, 2l+1 of
+    // both heads, and the probability sums ride along.
     {
         double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0, l0 = 0.0, l1 = 0.0;
-        for (int j = wave; j < n; j += kWaves) {
-            const uint32_t vw = j == pos ? at.kv_cur[1][lane]
-                              : j < kKvLds ? at.kv_pre[1][j][lane]
-                                           : *gview(reinterpret_cast<const uint32_t*>(vh + (int64_t)j * kHD + 2 * lane));
-            const double v0 = __uint_as_float(vw << 16);
-            const double v1 = __uint_as_float(vw & 0xffff0000u);
-            const double p0 = at.p[0][j], p1 = at.p[1][j];
-            a00 = fma(p0, v0, a00); a01 = fma(p0, v1, a01);
-            a10 = fma(p1, v0, a10); a11 = fma(p1, v1, a11);
-            l0 += p0;
-            l1 += p1;
+        for (int c0 = wave; c0 < n; c0 += kWaves * kWave) {
+            const int jl = c0 + kWaves * lane;
+            double p0 = 0.0, p1 = 0.0;
+            if (jl < n) {
+                p0 = exp(at.p[0][jl] - M0);
+                p1 = exp(at.p[1][jl] - M1);
+            }
+            const int rem = (n - c0 + kWaves - 1) / kWaves;
+            const int T = rem < kWave ? rem : kWave;
+            for (int t = 0; t < T; ++t) {
+                const int j = c0 + kWaves * t;
+                const uint32_t vw = j == pos ? at.kv_cur[1][lane]
+                                  : j < kKvLds ? at.kv_pre[1][j][lane]
+                                               : *gview(reinterpret_cast<const uint32_t*>(vh + (int64_t)j * kHD + 2 * lane));
+                const double q0 = readlane64(p0, t), q1 = readlane64(p1, t);
+                const double v0 = __uint_as_float(vw << 16);
+                const double v1 = __uint_as_float(vw & 0xffff0000u);
+                a00 = fma(q0, v0, a00); a01 = fma(q0, v1, a01);
+                a10 = fma(q1, v0, a10); a11 = fma(q1, v1, a11);
+                l0 += q0;
+                l1 += q1;
+            }
         }
         at.pv[wave][2 * lane] = a00;
         at.pv[wave][2 * lane + 1] = a01;
@@ -186,13 +190,18 @@ __device__ __forceinline__ void attn_core(AttnShared& at, const uint16_t* kh, co
         if (lane == 0) { at.wred[2][wave] = l0; at.wred[3][wave] = l1; }
     }
     __syncthreads();
+    mark(1);
     mark(2);
     if (tid < 2 * kHD) {
         const int h = tid / kHD;
-        double o = 0.0, L = 0.0;
+        double o[kWaves];
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) { o += at.pv[w][tid]; L += at.wred[2 + h][w]; }
-        emit(tid, (float)(o * rcp_nr(L)));
+        for (int w = 0; w < kWaves; ++w) o[w] = at.pv[w][tid];
+#pragma unroll
+        for (int s2 = kWaves / 2; s2 > 0; s2 /= 2)
+#pragma unroll
+            for (int w = 0; w < s2; ++w) o[w] += o[w + s2];
+        emit(tid, (float)(o[0] * rcp_nr(tree_sum<kWaves>(at.wred[2 + h]))));
     }
 }
 

@@ -150,7 +150,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             double ss = 0.0;
 #pragma unroll
             for (int i = 0; i < PT; ++i) ss = fma((double)hv[i], (double)hv[i], ss);
-            const double tot = block_sum64<kWaves>(ss, red, wave, lane);
+            const double tot = block_sum64<kWaves>(ss, red, 0, wave, lane);
             trace(l, 0);
             const double rstd = rms_scale(tot, H, kEps);
 #pragma unroll
@@ -290,7 +290,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             double ss = 0.0;
 #pragma unroll
             for (int i = 0; i < PT; ++i) ss = fma((double)av[i], (double)av[i], ss);
-            const double tot = block_sum64<kWaves>(ss, red, wave, lane);
+            const double tot = block_sum64<kWaves>(ss, red, 1, wave, lane);
             trace(l, 6);
             const double rstd = rms_scale(tot, H, kEps);
 #pragma unroll
@@ -312,7 +312,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
                 double gs = Stage_<W, 2 * CPW, H>::row_sum(part, tid);
                 double us = Stage_<W, 2 * CPW, H>::row_sum(part, CPW + tid);
                 if (kInt8) { gs = gs * (double)after_wait_f(gsc); us = us * (double)after_wait_f(usc); }
-                const float m = (float)(gs * rcp_nr(1.0 + exp(-gs)) * us);
+                const float m = (float)silu_mul(gs, us);
                 ll_put(&mlp_x[c0 + tid], __float_as_uint(m), tag(l, ST_GU));
                 if (l == last && kDebug && a.dbg_mlp) a.dbg_mlp[c0 + tid] = m;
             }
@@ -386,7 +386,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
         double ss = 0.0;
 #pragma unroll
         for (int i = 0; i < PT; ++i) ss = fma((double)hv[i], (double)hv[i], ss);
-        const double tot = block_sum64<kWaves>(ss, red, wave, lane);
+        const double tot = block_sum64<kWaves>(ss, red, 0, wave, lane);
         trace(a.L, 0);
         const double rstd = rms_scale(tot, H, kEps);
 #pragma unroll

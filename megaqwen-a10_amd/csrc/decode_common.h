@@ -124,17 +124,30 @@ struct Stage_ {
     }
 };
 
-// Workgroup sum in fp64 (fixed order over the waves).
+// Sum of N doubles held in LDS, as a fixed pairwise tree (3 levels for 8).
 template <int N>
-__device__ __forceinline__ double block_sum64(double v, double* red, int wave, int lane) {
-    v = wave_sum64(v);
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    double t = 0.0;
+__device__ __forceinline__ double tree_sum(const double* r) {
+    double t[N];
 #pragma unroll
-    for (int i = 0; i < N; ++i) t += red[i];
-    return t;
+    for (int i = 0; i < N; ++i) t[i] = r[i];
+#pragma unroll
+    for (int s = N / 2; s > 0; s /= 2)
+#pragma unroll
+        for (int i = 0; i < s; ++i) t[i] += t[i + s];
+    return t[0];
+}
+
+// Workgroup sum in fp64: wave sums, then a fixed tree over the N wave sums
+// (every thread gets the same value). `red` holds 2N doubles; consecutive
+// calls use different halves (`half`), so the previous call's readers are
+// ordered by that call's barrier and no leading barrier is needed.
+template <int N>
+__device__ __forceinline__ double block_sum64(double v, double* red, int half, int wave, int lane) {
+    v = wave_sum64(v);
+    double* r = red + half * N;
+    if (lane == 0) r[wave] = v;
+    __syncthreads();
+    return tree_sum<N>(r);
 }
 
 // 1/sqrt(v) for v > 0 in fp64: the hardware estimate refined by two Newton
@@ -148,6 +161,20 @@ __device__ __forceinline__ double rsqrt_nr(double v) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) y = fma(y, fma(-h * y, y, 0.5), y);
     return y;
+}
+
+// 1/v for finite v > 0: hardware estimate and two Newton steps r <- r (2 - v r).
+__device__ __forceinline__ double rcp_nr(double v) {
+    double r = __builtin_amdgcn_rcp(v);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) r = fma(r, fma(-v, r, 1.0), r);
+    return r;
+}
+
+// SiLU(g) * u = g / (1 + e^-g) * u in fp64 (config.cuh:81-83); 0 where e^-g overflows.
+__device__ __forceinline__ double silu_mul(double g, double u) {
+    const double e = exp(-g);
+    return e == INFINITY ? 0.0 : g * rcp_nr(1.0 + e) * u;
 }
 
 // RMSNorm scale 1/sqrt(mean + eps) in fp64.

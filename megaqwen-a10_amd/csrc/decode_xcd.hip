@@ -37,7 +37,7 @@
 
 namespace mq {
 
-constexpr int kNX = 8;                 // XCDs, one KV head each
+constexpr int kNX = 8;                 // XCDs, one KV head each (the 8-term reductions below assume 8)
 constexpr int kGS = kNWG / kNX;        // workgroups per XCD
 
 enum XStage { XS_QKV = 0, XS_PO = 1, XS_ACT = 2, XS_MLP = 3, XS_PD = 4, XS_HID = 5 };
@@ -278,7 +278,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             double ss = 0.0;
 #pragma unroll
             for (int i = 0; i < PT; ++i) { const double v = hid[tid + i * kThreads]; ss = fma(v, v, ss); }
-            const double tot = block_sum64<kWaves>(ss, red, wave, lane);
+            const double tot = block_sum64<kWaves>(ss, red, 0, wave, lane);
             trace(l, 0);
             const double rstd = rms_scale(tot, H, kEps);
 #pragma unroll
@@ -373,9 +373,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             if (tid < RPW) {
                 double v8[kNX];
                 wt.get_packed<kNX>(po + R0 + tid, H, pbit(l), v8);
-                double s = 0.0;
-#pragma unroll
-                for (int xx = 0; xx < kNX; ++xx) s += v8[xx];
+                double s = ((v8[0] + v8[1]) + (v8[2] + v8[3])) + ((v8[4] + v8[5]) + (v8[6] + v8[7]));
                 if (kInt8) s = s * (double)after_wait_f(so);
                 const float av = (float)(s + (double)hid[R0 + tid]);
                 ll_put_xcd(&actx[R0 + tid], __float_as_uint(av), tag(l, XS_ACT));
@@ -404,7 +402,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             double ss = 0.0;
 #pragma unroll
             for (int i = 0; i < PT; ++i) ss = fma((double)av[i], (double)av[i], ss);
-            const double tot = block_sum64<kWaves>(ss, red, wave, lane);
+            const double tot = block_sum64<kWaves>(ss, red, 1, wave, lane);
             const double rstd = rms_scale(tot, H, kEps);
 #pragma unroll
             for (int i = 0; i < PT; ++i) {
@@ -423,7 +421,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 double gs = Stage_<W, 2 * CPW, H, 1>::row_sum(part, tid);
                 double us = Stage_<W, 2 * CPW, H, 1>::row_sum(part, CPW + tid);
                 if (kInt8) { gs = gs * (double)after_wait_f(gsc); us = us * (double)after_wait_f(usc); }
-                const float m = (float)(gs * rcp_nr(1.0 + exp(-gs)) * us);
+                const float m = (float)silu_mul(gs, us);
                 ll_put_xcd(&mlpx[CPW * r + tid], __float_as_uint(m), tag(l, XS_MLP));
                 if (kDebug && l == last && a.dbg_mlp) a.dbg_mlp[c0 + tid] = m;
             }
@@ -470,9 +468,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             if (tid < RPW) {
                 double v8[kNX];
                 wt.get_packed<kNX>(pd + R0 + tid, H, pbit(l), v8);
-                double s = 0.0;
-#pragma unroll
-                for (int xx = 0; xx < kNX; ++xx) s += v8[xx];
+                double s = ((v8[0] + v8[1]) + (v8[2] + v8[3])) + ((v8[4] + v8[5]) + (v8[6] + v8[7]));
                 if (kInt8) s = s * (double)after_wait_f(sd);
                 const float hf = (float)(s + (double)act[R0 + tid]);
                 ll_put_xcd(&hidx[R0 + tid], __float_as_uint(round_bf16(hf)), tag(l, XS_HID));
@@ -528,7 +524,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             const double v = hid[tid + i * kThreads];
             ss = fma(v, v, ss);
         }
-        const double tot = block_sum64<kWaves>(ss, red, wave, lane);
+        const double tot = block_sum64<kWaves>(ss, red, 0, wave, lane);
         const double rstd = rms_scale(tot, H, kEps);
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
