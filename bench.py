@@ -18,7 +18,8 @@ The JSON line also carries:
 * ``parity`` — the timed tokens against the committed oracle fixture.
 
 Other workloads (parity-case shapes, one JSON line each): ``matvec``
-``positions`` (config 3 positions, bf16 weights), and
+``positions`` (config 3 positions, bf16 weights),
+``longctx`` (config 4: KV pre-filled to 1024 / 4096 / 8192, ``--steps 64``), and
 ``traffic``: a uint8 add over a 256 MiB buffer (reads and writes exactly
 256 MiB, the calibration for the FETCH_SIZE / WRITE_SIZE counters) followed
 by 8 decode steps, for ``rocprofv3 --pmc`` runs.
@@ -50,7 +51,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-steps", type=int, default=32, help="greedy steps of the CPU baseline sample")
-    ap.add_argument("--workload", default="decode", choices=["decode", "matvec", "positions", "traffic"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "matvec", "positions", "longctx", "traffic"])
+    ap.add_argument("--depths", default="1024,4096,8192", help="longctx: KV depths")
+    ap.add_argument("--split-min", type=int, default=0,
+                    help="longctx: attention split threshold (0 = library default, -1 = never)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-kernel-events", action="store_true",
                     help="do not attach timing events to the decode launches (for runs under rocprofv3 "
@@ -277,6 +281,72 @@ def run_positions(args, mq, torch):
                        "tok_s_at_position": res}}
 
 
+def run_longctx(args, mq, torch):
+    """INT8 Qwen3-0.6B shape with the KV cache pre-filled by seeded N(0,1) bf16
+    rows to each depth, then 64 timed greedy steps per depth (kernel time from HIP events)."""
+    dev = torch.device("cuda:0")
+    cfg = mq.QWEN3_0_6B
+    depths = [int(d) for d in args.depths.split(",")]
+    steps = args.steps
+    state, prompt = mq.random_init_state(cfg, seed=args.seed)
+    S = max(depths) + max(steps, args.warmup) + 8
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    qstate = mq.quantize_state(state, cfg, dev)
+    del state
+    embed, layers, scales, lm_q, lm_s, fnorm = mq.pack_int8(qstate, cfg)
+    dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+    dec.set_attn_split(args.split_min)
+    first = int(prompt[-1])
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for e in starts + ends:
+        e.record()
+    per_depth = {}
+    for depth in depths:
+        dec.prefill_random_kv(depth, seed=args.seed)
+        tok = first
+        for _ in range(args.warmup):
+            tok = dec.decode_step(tok)
+        dec.prefill_random_kv(depth, seed=args.seed)
+        torch.cuda.synchronize()
+        tok = first
+        toks = []
+        t0 = time.perf_counter()
+        for i in range(steps):
+            dec.set_timing_events(starts[i], ends[i])
+            dec.launch_step(tok)
+            tok = int(dec.output_token.item())
+            toks.append(tok)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        dec.set_timing_events(None, None)
+        if min(toks) < 0:
+            raise RuntimeError(f"a timed decode step at depth {depth} failed: {mq._lib.last_error()}")
+        kern_ms = [a.elapsed_time(b) for a, b in zip(starts, ends)]
+        bytes_total = sum(cfg.int8_step_bytes(cache_len=depth + i + 1) for i in range(steps))
+        achieved = bytes_total / (sum(kern_ms) / 1e3) / 1e9
+        roof_tok_s = steps / (bytes_total / (HBM_PEAK_GBS * 1e9))
+        per_depth[str(depth)] = {
+            "tok_s": round(steps / wall, 1), "kernel_avg_us": round(sum(kern_ms) / steps * 1e3, 2),
+            "device_tok_s": round(steps / (sum(kern_ms) / 1e3), 1), "achieved_GBs": round(achieved, 1),
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "roofline_tok_s": round(roof_tok_s, 1),
+            "bytes_per_launch_avg": int(bytes_total / steps)}
+        print(f"depth {depth}: {per_depth[str(depth)]}", file=sys.stderr, flush=True)
+    top = per_depth[str(max(depths))]
+    variant = mq.decode_variant(cfg.hidden_size, cfg.intermediate_size, int8=True)
+    return {"metric": f"INT8 decode tok/s at KV depth {max(depths)}, Qwen3-0.6B shape bs=1 (BASELINE config 4)",
+            "value": top["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+            "ms_per_step": round(1e3 / top["tok_s"], 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f64", "data": "synthetic",
+            "config": {"workload": "config 4: KV cache pre-filled with seeded N(0,1) bf16 rows to each depth, "
+                                   "then K greedy steps timed per depth",
+                       "depths": depths, "variant": variant,
+                       "attn_split_min": args.split_min or "library default", "per_depth": per_depth},
+            "roofline": {"bound": "hbm", "achieved": top["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": top["frac"], "traffic": None, "kernel_avg_us": top["kernel_avg_us"],
+                         "timing": "HIP events recorded by the dispatch itself (hipExtLaunchKernel), launch stream"}}
+
+
 def run_traffic(args, mq, torch):
     """Counter calibration plus decode steps for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs."""
     dev = torch.device("cuda:0")
@@ -321,7 +391,8 @@ def main():
     if not torch.cuda.is_available():
         print("no HIP device visible", file=sys.stderr)
         return 1
-    fn = {"decode": run_decode, "matvec": run_matvec, "positions": run_positions, "traffic": run_traffic}[args.workload]
+    fn = {"decode": run_decode, "matvec": run_matvec, "positions": run_positions, "longctx": run_longctx,
+          "traffic": run_traffic}[args.workload]
     out = fn(args, mq, torch)
     print(json.dumps(out), flush=True)
     return 0

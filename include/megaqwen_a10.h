@@ -136,6 +136,13 @@ typedef struct mq_decode_args {
      * Layer num_layers holds p = 0 final-norm input ready, p = 1 LM head done,
      * and [(L*10 + 2) * 256] the token publication. */
     void* trace;
+    /* Attention split (XCD-aware kernel): from cache_len >= attn_split_min on,
+     * each of the 32 workgroups sharing a KV head attends over 1/32 of the
+     * positions and the softmax partials are merged (log-sum-exp), which lifts
+     * the context limit from 1024 to 32768 positions. 0 = library default
+     * (256), > 1025 is taken as 1025, < 0 = never split. The single-level
+     * kernel never splits (cache_len <= 1024). */
+    int attn_split_min;
 } mq_decode_args;
 
 /* ---- library information ------------------------------------------------ */

@@ -59,6 +59,7 @@ class DecodeArgs(Structure):
         ("attn_scale", c_float), ("dims", c_void_p), ("workspace", c_void_p),
         ("workspace_bytes", c_size_t), ("spin_limit", c_uint),
         ("timing_start", c_void_p), ("timing_stop", c_void_p), ("trace", c_void_p),
+        ("attn_split_min", c_int),
     ]
 
 

@@ -121,7 +121,7 @@ using namespace mq;
 
 extern "C" {
 
-int mq_abi_version(void) { return 1; }
+int mq_abi_version(void) { return 2; }
 
 const char* mq_last_error(void) { return g_err; }
 

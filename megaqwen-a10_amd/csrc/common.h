@@ -330,6 +330,18 @@ __device__ __forceinline__ double group_sum64(double v) {
     return v;
 }
 
+// Maximum over aligned groups of N lanes (N a power of two <= 64).
+template <int N>
+__device__ __forceinline__ double group_max64(double v) {
+    if constexpr (N >= 2) v = fmax(v, partner64<1>(v));
+    if constexpr (N >= 4) v = fmax(v, partner64<2>(v));
+    if constexpr (N >= 8) v = fmax(v, partner64<4>(v));
+    if constexpr (N >= 16) v = fmax(v, partner64<8>(v));
+    if constexpr (N >= 32) v = fmax(v, partner64<16>(v));
+    if constexpr (N >= 64) v = fmax(v, partner64<32>(v));
+    return v;
+}
+
 // Keeps the compiler from moving memory accesses across this point (used to
 // issue step-independent loads before a wait instead of where they are used).
 __device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }

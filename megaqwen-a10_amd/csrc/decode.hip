@@ -33,6 +33,7 @@
 #include <atomic>
 
 #include <algorithm>
+#include <climits>
 
 namespace mq {
 
@@ -60,7 +61,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
     __shared__ double red[2 * kWaves];
     __shared__ float rows_res[ROWS_H];
     __shared__ float att_in[4 * D];
-    __shared__ __align__(16) AttnShared at;
+    __shared__ __align__(16) AttnShared<128> at;   // never splits: kst stays inside the kv_pre/pv union
     __shared__ float lm_best_v[kWaves];
     __shared__ int lm_best_i[kWaves];
     __shared__ LayerWeights s_lw[kMaxLayers];
@@ -563,9 +564,16 @@ static int launch_t(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t 
 int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream) {
     if (a.num_layers > kMaxLayers)
         return set_error(MQ_ERR_UNSUPPORTED, "num_layers %d exceeds %d", a.num_layers, kMaxLayers);
-    if (a.cache_len > kMaxAttnLen)
-        return set_error(MQ_ERR_UNSUPPORTED, "cache_len %d exceeds the single-workgroup attention limit %d",
-                         a.cache_len, kMaxAttnLen);
+    const int variant = decode_variant_in_use(s, int8);
+    if (variant != 1 && variant != 2) return variant;
+    // split attention (XCD kernel only): a slice of at most kMaxAttnLen positions per workgroup
+    int split_min = a.attn_split_min == 0 ? kDefaultSplitMin : a.attn_split_min;
+    split_min = split_min > 0 ? std::min(split_min, kMaxAttnLen + 1) : INT_MAX;
+    const int max_len = (variant == 2 && split_min != INT_MAX) ? kSplitRanks * kMaxAttnLen : kMaxAttnLen;
+    if (a.cache_len > max_len)
+        return set_error(MQ_ERR_UNSUPPORTED, "cache_len %d exceeds the attention limit %d of the %s kernel%s",
+                         a.cache_len, max_len, variant == 2 ? "XCD-aware" : "single-level",
+                         variant == 2 ? " without split attention" : "");
     KArgs k;
     k.token = a.input_token_id;
     k.out_token = a.output_token_id;
@@ -595,6 +603,7 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
     k.cache_len = a.cache_len;
     k.S = a.max_seq_len;
     k.V = s.V;
+    k.split_min = split_min;
     k.attn_scale = a.attn_scale;
     k.spin_limit = a.spin_limit ? a.spin_limit : (1u << 21);
     k.trace = static_cast<uint64_t*>(a.trace);
@@ -604,9 +613,7 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
                        a.block_max_idxs || a.trace;
 
     hipEvent_t t0 = static_cast<hipEvent_t>(a.timing_start), t1 = static_cast<hipEvent_t>(a.timing_stop);
-    const int variant = decode_variant_in_use(s, int8);
     if (variant == 2) return launch_decode_xcd(k, s, int8, debug, stream, t0, t1);
-    if (variant != 1) return variant;
     if (s.H == 1024 && s.I == 3072) {
         return int8 ? launch_t<1024, 3072, Int8W>(k, debug, stream, t0, t1) : launch_t<1024, 3072, Bf16W>(k, debug, stream, t0, t1);
     }

@@ -14,6 +14,8 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kNWG = 256;
 constexpr int kMaxAttnLen = 1024;     // positions one workgroup attends over (fp64 scores in LDS)
 constexpr int kKvLds = 64;            // earlier positions whose K/V rows are prefetched into LDS
+constexpr int kSplitRanks = 32;       // XCD kernel: workgroups sharing one KV head's split attention
+constexpr int kDefaultSplitMin = 48;  // XCD kernel: default cache_len from which attention is split
 constexpr int kMaxLayers = 64;        // per-layer pointer tables cached in LDS
 constexpr int kTracePoints = 10;      // timestamps per layer in the optional trace
 constexpr double kEps = 1e-6;        // RMSNorm epsilon (config.cuh:40), applied in fp64
@@ -45,6 +47,7 @@ struct KArgs {
     float* dbg_bmax;
     int* dbg_bidx;
     int L, pos, cache_len, S, V;
+    int split_min;                         // XCD kernel: split attention over the ranks from this cache_len on
     float attn_scale;
     uint32_t spin_limit;
     uint64_t* trace;

@@ -11,7 +11,12 @@
 //   A  QKV      rank r: 16 of XCD x's 512 q|k|v rows          -> XCD-local words
 //   B  attn     every rank of XCD x: QK-norm, RoPE, attention over the bf16
 //               KV cache for head pair x (redundant; the KV rows are shared
-//               through the XCD's L2); rank 0 writes the cache row
+//               through the XCD's L2); rank 0 writes the cache row. From
+//               split_min positions on, rank r takes the r-th 1/32 of the
+//               positions instead: its softmax partial (max, sum, weighted V)
+//               goes to XCD-local words, rank r merges output dims
+//               [8r, 8r+8) over the 32 partials, and an XCD-local all-gather
+//               hands every rank the 256 outputs
 //   C  O        rank r: rows [H/32 r, +H/32) of O[:, 256x : 256x+256]
 //                                                             -> cross-XCD partials
 //   D  reduce   rank r sums its rows' 8 partials in XCD order, applies the
@@ -40,11 +45,14 @@ namespace mq {
 constexpr int kNX = 8;                 // XCDs, one KV head each (the 8-term reductions below assume 8)
 constexpr int kGS = kNWG / kNX;        // workgroups per XCD
 
-enum XStage { XS_QKV = 0, XS_PO = 1, XS_ACT = 2, XS_MLP = 3, XS_PD = 4, XS_HID = 5 };
-constexpr uint32_t kXStages = 6;
+enum XStage { XS_QKV = 0, XS_PO = 1, XS_ACT = 2, XS_MLP = 3, XS_PD = 4, XS_HID = 5, XS_ATP = 6, XS_ATO = 7 };
+constexpr uint32_t kXStages = 8;
+// split attention partial of one rank: 256 fp64 weighted sums (low word, high
+// word), then per head the fp32 maximum and the fp64 probability sum (3 words)
+constexpr int kAttWords = 2 * 256 + 2 * 3;
 
 struct XLayout {
-    size_t qkvx, actx, mlpx, hidx, lmx, po, pd, lmc, total;
+    size_t qkvx, actx, mlpx, hidx, lmx, po, pd, lmc, attp, atto, total;
 };
 // The regions follow the single-level kernel's (layout_for), so neither kernel
 // writes words the other could take for its own: the packed words below carry
@@ -60,6 +68,8 @@ constexpr XLayout xlayout_for(int H, int I) {
     o.po = off; off += round256((size_t)kNX * H * 8);          // packed fp64 partials [xcd][row]
     o.pd = off; off += round256((size_t)kNX * H * 8);
     o.lmc = off; off += round256((size_t)kNX * 2 * 8);
+    o.attp = off; off += round256((size_t)kNX * kGS * kAttWords * 8);
+    o.atto = off; off += round256((size_t)kNX * 256 * 8);
     o.total = off;
     return o;
 }
@@ -124,7 +134,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     __shared__ double part[256];
     __shared__ double red[2 * kWaves];
     __shared__ float att_in[GR];
-    __shared__ __align__(16) AttnShared at;
+    __shared__ uint32_t mrg[kGS * 19];      // split attention: the 32 partials of this rank's 8 dims
+    // split slices staged in LDS: up to 320 positions (context 10240) at H = 1024,
+    // 256 (context 8192) at H = 2048, whose other buffers leave less LDS
+    constexpr int kSlice = H <= 1024 ? 320 : 256;
+    __shared__ __align__(16) AttnShared<kSlice> at;
     __shared__ float lm_v[kWaves];
     __shared__ int lm_i[kWaves];
     __shared__ LayerWeights s_lw[kMaxLayers];
@@ -148,6 +162,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     uint64_t* const po = reinterpret_cast<uint64_t*>(a.ws + kLay.po);    // packed [8][H]
     uint64_t* const pd = reinterpret_cast<uint64_t*>(a.ws + kLay.pd);    // packed [8][H]
     uint64_t* const lmc = reinterpret_cast<uint64_t*>(a.ws + kLay.lmc);
+    uint64_t* const attp = reinterpret_cast<uint64_t*>(a.ws + kLay.attp) + (size_t)x * kGS * kAttWords;
+    uint64_t* const atto = reinterpret_cast<uint64_t*>(a.ws + kLay.atto) + (size_t)x * AD;
 
     // step-independent reads first
     float hv0[PT];
@@ -191,6 +207,20 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 
     const int64_t kv_head_stride = (int64_t)a.S * D;
     const int last = a.L - 1;
+    // attention positions of this workgroup: all of them, or the r-th slice
+    const bool split = a.cache_len >= a.split_min;
+    const int cs = (a.cache_len + kGS - 1) / kGS;
+    const int sj0 = split ? min(a.cache_len, r * cs) : 0;
+    const int sj1 = split ? min(a.cache_len, sj0 + cs) : a.cache_len;
+    // split slices of at most kKvLds positions come wholly from the rows
+    // prefetched during the previous layer (spre); up to kSlice positions, the
+    // K rows go straight to LDS and the V words to registers ahead of the QKV
+    // wait (sdma); longer slices read the cache inside the loop
+    const bool spre = split && cs <= kKvLds;
+    const bool sdma = split && !spre && cs <= kSlice;
+    // the range's first npre earlier positions prefetched into registers, staged
+    // in LDS (the current one comes from the QKV words)
+    const int npre = sdma ? 0 : max(0, min(kKvLds, min(sj1, a.pos) - sj0));
     const int R0 = RPW * r;                 // first O / down row of this workgroup
     const double attn_scale = (double)a.attn_scale;
     __syncthreads();
@@ -221,7 +251,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 
     // Stage B's step-independent inputs for a layer, loaded one stage ahead of
     // its QKV wait: O weights (consumed in stage C), the O scale, the QK-norm
-    // gains and the K/V rows of the first kKvLds earlier positions.
+    // gains and the K/V rows of the range's first npre positions.
     const int crow = tid / LPR, clr = tid % LPR;   // stages C and F: row, lane in the row's group
     constexpr int kPreU4 = 2 * kKvLds * (D / 8) / kThreads;
     uint4 wo[PPL_O];
@@ -242,8 +272,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             nw0 = ldg_bits(nw + lane);
             nw1 = ldg_bits(nw + lane + 64);
         }
-        const int64_t cb = ((int64_t)ll * kNX + x) * kv_head_stride;
-        const int npre = a.pos < kKvLds ? a.pos : kKvLds;
+        const int64_t cb = ((int64_t)ll * kNX + x) * kv_head_stride + (int64_t)opaque(sj0) * D;
 #pragma unroll
         for (int i = 0; i < kPreU4; ++i) {
             const int f = tid + i * kThreads;
@@ -302,21 +331,34 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         {
             // this stage's step-independent inputs (O weights, K/V rows of earlier
             // positions, QK-norm gains) were loaded during the previous layer
-            const int n = a.cache_len;
-            const int npre = a.pos < kKvLds ? a.pos : kKvLds;
-            {
-                float v1[1];
-                wt.get_strided<1>(qkvx + tid, 0, tag(l, XS_QKV), v1);
-                att_in[tid] = v1[0];
-            }
+            // the K/V rows prefetched during the previous layer go to LDS (read
+            // after the barrier below); a split slice's K rows with their chunks
+            // permuted for the matrix-core reads (kv_pre[0] is kst's first rows)
 #pragma unroll
             for (int i = 0; i < kPreU4; ++i) {
                 const int f = tid + i * kThreads;
                 const int side = f / (kKvLds * (D / 8));
                 const int rem = f % (kKvLds * (D / 8));
                 const int j = rem / (D / 8), c = rem % (D / 8);
-                if (j < npre) *reinterpret_cast<uint4*>(&at.kv_pre[side][j][c * 4]) = pre[i];
+                const int cc = (spre && side == 0) ? kst_chunk(c, j) : c;
+                if (j < npre) *reinterpret_cast<uint4*>(&at.kv_pre[side][j][cc * 4]) = pre[i];
             }
+            // split slices: the K rows (to LDS) and V words, all loads in flight
+            // at once (opaque offsets keep the addresses from being hoisted out
+            // of the layer loop). A __syncthreads would wait for the LDS-direct
+            // loads, so they are issued after the last barrier before the QKV wait.
+            SliceRegs<kSlice> sr;
+            if (sdma) {
+                const int oj0 = opaque(sj0);
+                attn_slice_k(at, a.kc + cache_base, oj0, min(sj1, a.pos), lane, tid / kWave);
+                attn_slice_v(sr, a.vc + cache_base, oj0, min(sj1, a.pos), lane, tid / kWave);
+            }
+            {
+                float v1[1];
+                wt.get_strided<1>(qkvx + tid, 0, tag(l, XS_QKV), v1);
+                att_in[tid] = v1[0];
+            }
+            if (sdma) wait_vmem();              // the K rows are in LDS after the barrier
             __syncthreads();
             trace(l, 2);
             const int64_t cur = cache_base + (int64_t)a.pos * D;
@@ -325,14 +367,70 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             attn_qk_rope(at, att_in, nw0, nw1, c0, s0, c1, s1, writer ? a.kc + cur : nullptr,
                          writer ? a.vc + cur : nullptr, (dbg && a.dbg_q) ? a.dbg_q + 2 * x * D : nullptr,
                          (dbg && a.dbg_k) ? a.dbg_k + x * D : nullptr, (dbg && a.dbg_v) ? a.dbg_v + x * D : nullptr,
-                         wave, lane);
+                         wave, lane, spre || sdma);
             __syncthreads();
-            attn_core(at, a.kc + cache_base, a.vc + cache_base, n, a.pos, attn_scale, tid, lane, wave,
-                      [&](int i, float v) {
-                          attn_d[piece_index(i, EPP, PC_O)] = v;
-                          if (dbg && a.dbg_attn) a.dbg_attn[AD * x + i] = v;
-                      },
-                      [](int) {});
+            if (!split) {
+                attn_core(at, a.kc + cache_base, a.vc + cache_base, sj1, a.pos, attn_scale, tid, lane, wave,
+                          [&](int i, float v) {
+                              attn_d[piece_index(i, EPP, PC_O)] = v;
+                              if (dbg && a.dbg_attn) a.dbg_attn[AD * x + i] = v;
+                          },
+                          [](int) {});
+            } else {
+                const uint32_t tp = tag(l, XS_ATP);
+                uint64_t* const mine = attp + (size_t)r * kAttWords;
+                auto publish = [&](int i, double acc, double psum, double m) {
+                    const uint64_t u = (uint64_t)__double_as_longlong(acc);
+                    ll_put_xcd(&mine[2 * i], (uint32_t)u, tp);
+                    ll_put_xcd(&mine[2 * i + 1], (uint32_t)(u >> 32), tp);
+                    if ((i & (D - 1)) == 0) {
+                        const int h = i / D;
+                        const uint64_t su = (uint64_t)__double_as_longlong(psum);
+                        ll_put_xcd(&mine[2 * AD + 3 * h], __float_as_uint((float)m), tp);
+                        ll_put_xcd(&mine[2 * AD + 3 * h + 1], (uint32_t)su, tp);
+                        ll_put_xcd(&mine[2 * AD + 3 * h + 2], (uint32_t)(su >> 32), tp);
+                    }
+                };
+                if (spre) {
+                    attn_partial_lds(at, sj0, sj1, a.pos, attn_scale, tid, lane, wave, publish, [](int) {});
+                } else if (sdma) {
+                    attn_partial_regs(at, sr, sj0, sj1, a.pos, attn_scale, tid, lane, wave, publish, [](int) {});
+                } else
+                    attn_partial(at, a.kc + cache_base, a.vc + cache_base, sj0, sj1, a.pos, attn_scale, tid, lane,
+                                 wave, publish, [](int) {});
+                // merge output dims [8r, 8r+8) (query head r / 16) over the 32
+                // partials: thread (s, k) reads word k of rank s's slice, and
+                // threads below 96 rank s2's maximum and probability sum
+                {
+                    const int hh = r / (kGS / 2);
+                    const uint64_t* pa = attp + (size_t)(tid >> 4) * kAttWords + 16 * r + (tid & 15);
+                    const uint64_t* pb = attp + (size_t)(tid / 3) * kAttWords + 2 * AD + 3 * hh + tid % 3;
+                    float w2[2];
+                    wt.get_strided<2>(pa, (int)(pb - pa), tp, w2, tid < 3 * kGS ? 2 : 1);
+                    mrg[tid] = __float_as_uint(w2[0]);
+                    if (tid < 3 * kGS) mrg[16 * kGS + tid] = __float_as_uint(w2[1]);
+                }
+                __syncthreads();
+                if (tid < 8 * kGS) {
+                    const int k = tid / kGS, s = tid % kGS;
+                    auto word64 = [&](int w) {
+                        return __longlong_as_double((long long)(((uint64_t)mrg[w + 1] << 32) | mrg[w]));
+                    };
+                    const double ms = __uint_as_float(mrg[16 * kGS + 3 * s]);
+                    const double ls = word64(16 * kGS + 3 * s + 1);
+                    const double acc = word64(16 * s + 2 * k);
+                    const double M = group_max64<kGS>(ms);
+                    const double c = exp(ms - M);        // 0 for an empty slice (m = -inf)
+                    const double num = group_sum64<kGS>(c * acc);
+                    const double den = group_sum64<kGS>(c * ls);
+                    if (s == 0) {
+                        const float o = (float)(num * rcp_nr(den));
+                        ll_put_xcd(&atto[8 * r + k], __float_as_uint(o), tag(l, XS_ATO));
+                        if (kDebug && l == last && a.dbg_attn) a.dbg_attn[AD * x + 8 * r + k] = o;
+                    }
+                }
+                if (tid < AD) attn_d[piece_index(tid, EPP, PC_O)] = wt.getf(atto + tid, tag(l, XS_ATO));
+            }
             __syncthreads();
             trace(l, 3);
         }
@@ -356,7 +454,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         uint4 wd[PPL_D];                    // stage F's down weights
         uint32_t gsc = 0x3f800000u, usc = 0x3f800000u;
         uint32_t wpn[PT];
-        const int c0 = IX * x + CPW * r;
+        const int c0 = opaque(IX * x + CPW * r);
         {
             // stage E's weights (waves 1-7), scales and norm gains
             const uint8_t* gb = (const uint8_t*)lw.gate_proj_weight;

@@ -271,6 +271,31 @@ class _DecoderBase:
         """Bound on every in-kernel wait (0 = library default)."""
         self._args.spin_limit = int(polls)
 
+    def set_attn_split(self, min_len: int) -> None:
+        """Context length from which the XCD-aware kernel splits each KV head's attention
+        over its 32 workgroups (0 = library default, negative = never; the unsplit
+        path attends over at most 1024 positions)."""
+        self._args.attn_split_min = int(min_len)
+
+    def prefill_random_kv(self, depth: int, seed: int = 0) -> None:
+        """Long-context set-up (the reference has no counterpart):
+        K and V cache rows of positions [0, depth) of every layer and KV head become
+        seeded N(0, 1) values rounded to bf16, later rows zero, and the next step
+        decodes at position ``depth``. The rows come from a generator on the
+        decoder's device seeded with ``seed``, one layer at a time."""
+        if not isinstance(depth, int) or not 0 <= depth < self.max_seq_len:
+            raise ValueError(f"depth {depth!r} outside [0, {self.max_seq_len})")
+        g = torch.Generator(device=self.device)
+        g.manual_seed(int(seed))
+        shape = (self.k_cache.shape[1], depth, self.k_cache.shape[3])
+        with torch.cuda.device(self.device):
+            for cache in (self.k_cache, self.v_cache):
+                cache.zero_()
+                for l in range(self.num_layers):
+                    cache[l, :, :depth].copy_(torch.randn(shape, generator=g, device=self.device,
+                                                          dtype=torch.float32))
+        self._pos = depth
+
     # debug getters (run_benchmark.py:174-183): the last layer's values after a step,
     # filled while enable_debug() is on
     def get_hidden(self): return self.hidden_buffer

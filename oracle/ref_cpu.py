@@ -109,6 +109,14 @@ class RefDecoder:
     def position(self) -> int:
         return self._pos
 
+    def load_kv(self, k_cache, v_cache, position: int) -> None:
+        """Start from a given cache (e.g. a long-context pre-fill): rows [0, position)
+        of every layer / KV head are copied, the next step decodes at ``position``."""
+        self.reset()
+        self.k_cache[:, :, :position] = k_cache[:, :, :position].detach().cpu().to(self.k_cache.dtype)
+        self.v_cache[:, :, :position] = v_cache[:, :, :position].detach().cpu().to(self.v_cache.dtype)
+        self._pos = position
+
     def decode_step(self, token: int) -> int:
         logits = self.step_logits(token)
         return int(torch.argmax(logits))
