@@ -19,7 +19,8 @@ The JSON line also carries:
 
 Other workloads (parity-case shapes, one JSON line each): ``matvec``
 ``positions`` (config 3 positions, bf16 weights),
-``longctx`` (config 4: KV pre-filled to 1024 / 4096 / 8192, ``--steps 64``), and
+``longctx`` (config 4: KV pre-filled to 1024 / 4096 / 8192, ``--steps 64``),
+``batched`` (config 5: Qwen3-1.7B shape, B = 1 / 4 / 8 / 16, ``--steps 128``), and
 ``traffic``: a uint8 add over a 256 MiB buffer (reads and writes exactly
 256 MiB, the calibration for the FETCH_SIZE / WRITE_SIZE counters) followed
 by 8 decode steps, for ``rocprofv3 --pmc`` runs.
@@ -37,6 +38,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0          # dense int8 MFMA, MI355X
 PROMPT_LEN = 8
 # Memory traffic per decode launch of this kernel, measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE runs of megaqwen-a10_amd/profile_decode.py, each scaled by the counter's reading for a
@@ -51,8 +53,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-steps", type=int, default=32, help="greedy steps of the CPU baseline sample")
-    ap.add_argument("--workload", default="decode", choices=["decode", "matvec", "positions", "longctx", "traffic"])
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "matvec", "positions", "longctx", "batched", "traffic"])
     ap.add_argument("--depths", default="1024,4096,8192", help="longctx: KV depths")
+    ap.add_argument("--batches", default="1,4,8,16", help="batched: batch sizes")
     ap.add_argument("--split-min", type=int, default=0,
                     help="longctx: attention split threshold (0 = library default, -1 = never)")
     ap.add_argument("--seed", type=int, default=0)
@@ -347,6 +351,85 @@ def run_longctx(args, mq, torch):
                          "timing": "HIP events recorded by the dispatch itself (hipExtLaunchKernel), launch stream"}}
 
 
+def run_batched(args, mq, torch):
+    """batched INT8 decode of the Qwen3-1.7B shape, B independent seeded
+    8-token prompts, then K greedy steps timed per batch size (kernel time from HIP events)."""
+    dev = torch.device("cuda:0")
+    cfg = mq.QWEN3_1_7B
+    batches = [int(b) for b in args.batches.split(",")]
+    steps = args.steps
+    state, _ = mq.random_init_state(cfg, seed=args.seed)
+    S = PROMPT_LEN + steps + max(args.warmup, 1) + 8
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    qstate = mq.quantize_state(state, cfg, dev)
+    del state
+    packed = mq.pack_int8(qstate, cfg)
+    del qstate
+    g = torch.Generator().manual_seed(args.seed + 100)
+    prompts_all = torch.randint(0, cfg.vocab_size, (max(batches), PROMPT_LEN), generator=g).tolist()
+    weight_bytes = cfg.int8_step_bytes(cache_len=0) - cfg.num_layers * 2 * cfg.num_kv_heads * cfg.head_dim * 2
+    # useful int8 multiply-adds per sequence and step: every projection and the LM head once
+    H, I, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_layers
+    macs = L * (H * (cfg.q_size + 2 * cfg.kv_size) + cfg.q_size * H + 3 * H * I) + V * H
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for e in starts + ends:
+        e.record()
+    per_batch = {}
+    for B in batches:
+        prompts = prompts_all[:B]
+        dec = mq.A10Int8BatchDecoder(*packed, cos, sin, L, S, B)
+
+        def prefill():
+            dec.reset()
+            out = None
+            for i in range(PROMPT_LEN):
+                out = dec.decode_step([p[i] for p in prompts])
+            return out
+
+        out = prefill()
+        for _ in range(args.warmup):
+            out = dec.decode_step(out)
+        out = prefill()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            dec.set_timing_events(starts[i], ends[i])
+            dec.launch_step(out)
+            out = dec.output_tokens.tolist()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        dec.set_timing_events(None, None)
+        if min(out) < 0:
+            raise RuntimeError(f"a timed batched step (B={B}) failed: {mq._lib.last_error()}")
+        kern_s = sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / 1e3
+        kv_bytes = sum(B * L * 2 * cfg.num_kv_heads * cfg.head_dim * 2 * (PROMPT_LEN + i + 1) for i in range(steps))
+        achieved = (steps * weight_bytes + kv_bytes) / kern_s / 1e9
+        mfma_tops = 2.0 * macs * B * steps / kern_s / 1e12
+        per_batch[str(B)] = {
+            "tok_s": round(B * steps / wall, 1), "kernel_avg_us": round(kern_s / steps * 1e6, 2),
+            "device_tok_s": round(B * steps / kern_s, 1), "achieved_GBs": round(achieved, 1),
+            "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
+            "roofline_tok_s": round(B * HBM_PEAK_GBS * 1e9 / (weight_bytes + kv_bytes / steps / 1.0), 1),
+            "useful_int8_TOPs": round(mfma_tops, 2), "mfma_util": round(mfma_tops / INT8_PEAK_TOPS, 5)}
+        print(f"batch {B}: {per_batch[str(B)]}", file=sys.stderr, flush=True)
+        del dec
+        torch.cuda.empty_cache()
+    top = per_batch[str(max(batches))]
+    return {"metric": f"batched INT8 decode aggregate tok/s, Qwen3-1.7B shape, batch {max(batches)} (BASELINE config 5)",
+            "value": top["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+            "ms_per_step": round(1e3 * max(batches) / top["tok_s"], 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int8 x 4-digit int8 (int32 sums), fp64 recombination", "data": "synthetic",
+            "config": {"workload": "config 5: Qwen3-1.7B architecture random-init (seed 0), independent seeded 8-token "
+                                   "prompts per sequence prefilled untimed, K greedy steps timed per batch size",
+                       "batches": batches, "per_batch": per_batch,
+                       "weight_bytes_per_step": weight_bytes, "useful_int8_macs_per_token": macs},
+            "roofline": {"bound": "hbm", "achieved": top["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": top["hbm_frac"], "traffic": None, "kernel_avg_us": top["kernel_avg_us"],
+                         "mfma_util": top["mfma_util"],
+                         "timing": "HIP events recorded by the dispatch itself (hipExtLaunchKernel), launch stream"}}
+
+
 def run_traffic(args, mq, torch):
     """Counter calibration plus decode steps for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs."""
     dev = torch.device("cuda:0")
@@ -392,7 +475,7 @@ def main():
         print("no HIP device visible", file=sys.stderr)
         return 1
     fn = {"decode": run_decode, "matvec": run_matvec, "positions": run_positions, "longctx": run_longctx,
-          "traffic": run_traffic}[args.workload]
+          "batched": run_batched, "traffic": run_traffic}[args.workload]
     out = fn(args, mq, torch)
     print(json.dumps(out), flush=True)
     return 0

@@ -140,10 +140,65 @@ typedef struct mq_decode_args {
      * each of the 32 workgroups sharing a KV head attends over 1/32 of the
      * positions and the softmax partials are merged (log-sum-exp), which lifts
      * the context limit from 1024 to 32768 positions. 0 = library default
-     * (256), > 1025 is taken as 1025, < 0 = never split. The single-level
+     * (48), > 1025 is taken as 1025, < 0 = never split. The single-level
      * kernel never splits (cache_len <= 1024). */
     int attn_split_min;
 } mq_decode_args;
+
+/* ---- batched INT8 decode (no counterpart in the reference) ---------------
+ * B <= MQ_MAX_BATCH independent sequences share one pass over the weights per
+ * step; each has its own KV cache slice and position. The semantics are B
+ * copies of mq_int8_decode_step's; the matrix products run on the int8 matrix
+ * cores with each activation vector split into four int8 digits (per-sequence
+ * power-of-two scale, 28 significant bits) and the RMSNorm scale applied after
+ * the product, so projections differ from the single-sequence path by ~1e-8
+ * relative and an occasional bf16 rounding (K/V rows, hidden state) lands one
+ * ulp apart: agreement is within bf16 tolerance, not bitwise. Only the
+ * Qwen3-1.7B layer shapes (hidden 2048, intermediate 6144, 16 / 8 heads of
+ * 128) are compiled. */
+#define MQ_MAX_BATCH 16
+typedef struct mq_batch_args {
+    int batch;                        /* 1..MQ_MAX_BATCH; the same for every step on a workspace */
+    int input_token_ids[MQ_MAX_BATCH];/* per sequence, 0 <= id < vocab_size                   */
+    int positions[MQ_MAX_BATCH];      /* per sequence, 0 <= position < min(max_seq_len, 1024) */
+    int* output_token_ids;            /* device int32[batch]: greedy argmax per sequence        */
+    const void* embed_weight;         /* bf16 [V, H]                                           */
+    const LayerWeights* layer_weights;/* DEVICE array [num_layers] (int8 projections)          */
+    const ScalePointers* scales;      /* DEVICE array [num_layers]                              */
+    const void* final_norm_weight;    /* bf16 [H]                                              */
+    const void* lm_head_weight;       /* int8 [V, H]                                           */
+    const float* lm_head_scale;       /* fp32 [V]                                              */
+    const void* cos_table;            /* bf16 [max_seq_len, D]                                 */
+    const void* sin_table;            /* bf16 [max_seq_len, D]                                 */
+    void* k_cache;                    /* bf16 [batch, num_layers, NKV, max_seq_len, D]         */
+    void* v_cache;                    /* bf16 [batch, num_layers, NKV, max_seq_len, D]         */
+    int num_layers;
+    int max_seq_len;
+    float attn_scale;
+    const mq_model_dims* dims;        /* NULL: Qwen3-1.7B                                      */
+    void* workspace;                  /* device memory of mq_batch_workspace_bytes(dims)       */
+    size_t workspace_bytes;
+    unsigned int spin_limit;          /* bound on each in-kernel wait (polls); 0 = default     */
+    void* timing_start;               /* optional hipEvent_t pair, as in mq_decode_args        */
+    void* timing_stop;
+    /* Optional per-sequence values of the last layer (NULL: not written):
+     * hidden_out bf16 [batch, H] (layer output), qkv_out fp32 [batch, NKV, 512]
+     * (each KV head's two query heads, key and value projections before QK-norm),
+     * attn_out fp32 [batch, NQ * D], act_out fp32 [batch, H] (post-attention
+     * residual), mlp_out fp32 [batch, I] (SwiGLU output). */
+    void* hidden_out;
+    void* qkv_out;
+    void* attn_out;
+    void* act_out;
+    void* mlp_out;
+    /* Optional timeline, uint64 [(num_layers + 1) * 10 * 256] of the 100 MHz
+     * real-time counter: [(l * 10 + p) * 256 + g] is when workgroup g passed
+     * point p of layer l: 0 layer start, 1 QKV partials written, 2 QKV rows
+     * reduced, 3 attention done, 4 O partials written, 5 O rows reduced, 6
+     * gate/up partials written, 7 SwiGLU outputs written, 8 down partials
+     * written, 9 layer done; layer num_layers: 0 LM head start, 1 LM products done. */
+    void* trace;
+} mq_batch_args;
 
 /* ---- library information ------------------------------------------------ */
 int mq_abi_version(void);
@@ -164,6 +219,14 @@ int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream);
 /* After a completed step: MQ_ERR_TIMEOUT if a bounded wait of that step expired, else MQ_OK.
  * Synchronises `stream`. */
 int mq_decode_check(void* workspace, hipStream_t stream);
+
+/* Batched decode: workspace size for any batch up to MQ_MAX_BATCH (0 for
+ * unsupported dims), and one step of `batch` sequences (mq_batch_args).
+ * Initialise the workspace with mq_workspace_init; a workspace serves one
+ * batch size (re-initialise it to change the size). Needs the XCD-aware
+ * workgroup placement (mq_decode_variant() == 2). */
+size_t mq_batch_workspace_bytes(const mq_model_dims* dims);
+int mq_int8_decode_batch_step(const mq_batch_args* args, hipStream_t stream);
 
 /* Kernel variant for all following steps in this process: 0 = automatic
  * (default: the XCD-aware kernel when the workgroups of each residue class

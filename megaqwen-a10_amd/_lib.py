@@ -63,6 +63,24 @@ class DecodeArgs(Structure):
     ]
 
 
+MAX_BATCH = 16
+
+
+class BatchArgs(Structure):
+    _fields_ = [
+        ("batch", c_int), ("input_token_ids", c_int * MAX_BATCH), ("positions", c_int * MAX_BATCH),
+        ("output_token_ids", c_void_p),
+        ("embed_weight", c_void_p), ("layer_weights", c_void_p), ("scales", c_void_p),
+        ("final_norm_weight", c_void_p), ("lm_head_weight", c_void_p), ("lm_head_scale", c_void_p),
+        ("cos_table", c_void_p), ("sin_table", c_void_p), ("k_cache", c_void_p), ("v_cache", c_void_p),
+        ("num_layers", c_int), ("max_seq_len", c_int), ("attn_scale", c_float), ("dims", c_void_p),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t), ("spin_limit", c_uint),
+        ("timing_start", c_void_p), ("timing_stop", c_void_p), ("hidden_out", c_void_p),
+        ("qkv_out", c_void_p), ("attn_out", c_void_p), ("act_out", c_void_p), ("mlp_out", c_void_p),
+        ("trace", c_void_p),
+    ]
+
+
 assert ctypes.sizeof(LayerWeights) == 88 and ctypes.sizeof(ScalePointers) == 56
 
 
@@ -87,6 +105,8 @@ _SIGNATURES = {
     "mq_decode_check": (c_int, [c_void_p, c_void_p]),
     "mq_decode_set_variant": (c_int, [c_int]),
     "mq_decode_variant": (c_int, [c_void_p, c_int]),
+    "mq_batch_workspace_bytes": (c_size_t, [c_void_p]),
+    "mq_int8_decode_batch_step": (c_int, [POINTER(BatchArgs), c_void_p]),
     "launch_a10_int8_decode": (None, [c_int, c_void_p] + [c_void_p] * 20 + [c_int] * 4 + [c_float, c_void_p, c_void_p]),
     "launch_a10_decode": (None, [c_int, c_void_p] + [c_void_p] * 19 + [c_int] * 4 + [c_float, c_void_p]),
     "mq_int8_gemv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),

@@ -172,9 +172,35 @@ int mq_decode_check(void* workspace, hipStream_t stream) {
         return set_error(MQ_ERR_TIMEOUT, "a workgroup ran on an unexpected XCD; the XCD-aware kernel is disabled for "
                                          "this device, re-initialise the workspace and repeat the step");
     }
+    if (flag == 3)
+        return set_error(MQ_ERR_TIMEOUT, "the workspace was used with another batch size; re-initialise it");
     if (flag != 0)
         return set_error(MQ_ERR_TIMEOUT, "a bounded wait in the decode kernel expired; re-initialise the workspace");
     return MQ_OK;
+}
+
+size_t mq_batch_workspace_bytes(const mq_model_dims* dims) {
+    clear_error();
+    DecodeShape s{2048, 6144, 16, 8, 128, 151936};
+    if (dims != nullptr && shape_of(dims, &s) != MQ_OK) return 0;
+    const size_t n = decode_batch_workspace_bytes(s);
+    if (n == 0) set_error(MQ_ERR_UNSUPPORTED, "no batched decode kernel for hidden %d / intermediate %d", s.H, s.I);
+    return n;
+}
+
+int mq_int8_decode_batch_step(const mq_batch_args* args, hipStream_t stream) {
+    clear_error();
+    if (args == nullptr) return set_error(MQ_ERR_INVALID_ARGUMENT, "args is NULL");
+    DecodeShape s{2048, 6144, 16, 8, 128, 151936};
+    if (args->dims != nullptr) {
+        const int st = shape_of(args->dims, &s);
+        if (st != MQ_OK) return st;
+    }
+    if (args->max_seq_len < 1) return set_error(MQ_ERR_INVALID_ARGUMENT, "max_seq_len %d < 1", args->max_seq_len);
+    if (!aligned16(args->lm_head_weight) || !aligned16(args->k_cache) || !aligned16(args->v_cache) ||
+        !aligned16(args->workspace) || !aligned16(args->embed_weight))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "weights, KV caches and workspace must be 16-byte aligned");
+    return launch_decode_batch(*args, s, stream);
 }
 
 int mq_decode_set_variant(int variant) {

@@ -488,7 +488,7 @@ void mark_xcd_unusable() {
 // rank from g / 8, which needs the workgroups of one residue class of g mod 8
 // to share an XCD and the 8 classes to fill the 8 XCDs; verified once per
 // device with a launch of the same shape.
-static bool xcd_placement_ok() {
+bool xcd_placement_ok() {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
     int st = g_xcd_ok[dev].load();

@@ -166,6 +166,22 @@ __device__ __forceinline__ double rsqrt_nr(double v) {
     return y;
 }
 
+// XCD-local exchange store. A wavefront-scope relaxed atomic store is a plain
+// global_store (no cache-scope bits): the CU's L1 is write-through, so the word
+// lands in this XCD's shared L2, where the other ranks' agent-scope loads (which
+// bypass their own L1) read it about twice as fast as an agent-scope store
+// (measured on MI355X: 0.27 us vs 0.52 us one-way). It is not visible to other
+// XCDs, which never read these buffers.
+__device__ __forceinline__ void ll_put_xcd(uint64_t* p, uint32_t payload, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | payload, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WAVEFRONT);
+}
+
+__device__ __forceinline__ uint32_t hw_xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 0xfu;
+}
+
 // 1/v for finite v > 0: hardware estimate and two Newton steps r <- r (2 - v r).
 __device__ __forceinline__ double rcp_nr(double v) {
     double r = __builtin_amdgcn_rcp(v);

@@ -25,7 +25,9 @@ struct WsHeader {
     uint32_t done[2];      // workgroups finished with the LM head, per step parity
     uint64_t best[2];      // packed (ordered logit, ~token) maximum, per step parity
     uint32_t xsteps;       // steps run by the XCD-aware kernel (parity tags of its packed words)
-    uint32_t pad[55];
+    uint32_t bsteps;       // steps run by the batched kernel (parity tags of its packed words)
+    uint32_t batch;        // sequences per step of the batched kernel (0 until its first step)
+    uint32_t pad[53];
 };
 static_assert(sizeof(WsHeader) == 256, "workspace header is 256 bytes");
 
@@ -42,5 +44,11 @@ int decode_variant_in_use(const DecodeShape& s, bool int8);
 void mark_xcd_unusable();
 // Launches one decode step; `int8` selects the weight format.
 int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream);
+// True when the workgroups of each residue class g mod 8 run on one XCD (checked once per device).
+bool xcd_placement_ok();
+
+// Batched INT8 decode (decode_batch.hip).
+size_t decode_batch_workspace_bytes(const DecodeShape& s);
+int launch_decode_batch(const mq_batch_args& a, const DecodeShape& s, hipStream_t stream);
 
 }  // namespace mq

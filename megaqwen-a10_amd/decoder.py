@@ -81,6 +81,14 @@ class _DecoderBase:
 
     def _setup(self, embed, layer_tensors, final_norm, lm_head, cos_table, sin_table, num_layers,
                max_seq_len, layer_scales=None, lm_head_scale=None):
+        self._hold_weights(embed, layer_tensors, final_norm, lm_head, cos_table, sin_table, num_layers,
+                           max_seq_len, layer_scales, lm_head_scale)
+        self._alloc_state()
+
+    def _hold_weights(self, embed, layer_tensors, final_norm, lm_head, cos_table, sin_table, num_layers,
+                      max_seq_len, layer_scales=None, lm_head_scale=None):
+        """Validate the reference's constructor arguments and keep them (with the device
+        LayerWeights / ScalePointers arrays) alive on the decoder."""
         if not isinstance(num_layers, int) or num_layers < 1:
             raise ValueError(f"num_layers must be a positive int, got {num_layers!r}")
         if not isinstance(max_seq_len, int) or max_seq_len < 1:
@@ -146,6 +154,14 @@ class _DecoderBase:
                     setattr(sp[l], f, t.data_ptr())
             self.d_layer_scales = _device_array(sp, dev)
 
+    def _alloc_state(self):
+        dev, num_layers, max_seq_len = self.device, self.num_layers, self.max_seq_len
+        H, I, V = self.dims
+        D = 128
+        Q, KV = 16 * D, 8 * D
+        embed, final_norm, lm_head, lm_head_scale = (self.embed_weight, self.final_norm_weight, self.lm_head_weight,
+                                                     self.lm_head_scale)
+        cos_table, sin_table = self.cos_table, self.sin_table
         f32 = dict(dtype=torch.float32, device=dev)
         self.k_cache = torch.zeros((num_layers, 8, max_seq_len, D), dtype=torch.bfloat16, device=dev)
         self.v_cache = torch.zeros_like(self.k_cache)
@@ -332,6 +348,151 @@ class A10MegakernelDecoder(_DecoderBase):
                  sin_table, num_layers, max_seq_len):
         self._setup(embed_weight, layer_weights_flat, final_norm_weight, lm_head_weight, cos_table, sin_table,
                     num_layers, max_seq_len)
+
+
+class A10Int8BatchDecoder(_DecoderBase):
+    """Batched INT8 decode (the reference has no batched path):
+    ``batch`` independent sequences share one pass over the weights per step, each
+    with its own KV cache and position. Constructor arguments are those of
+    A10Int8MegakernelDecoder plus ``batch`` (1..16); Qwen3-1.7B layer shapes only.
+
+    ``decode_step(tokens)`` feeds one token per sequence and returns the next
+    greedy token of each. The matrix products run on the int8 matrix cores with
+    28-bit activations (four int8 digits) and the RMSNorm scale applied after the
+    product, so results agree with the single-sequence path within bf16 rounding
+    of intermediate values rather than bitwise."""
+
+    def __init__(self, embed_weight, layer_weights_flat, layer_scales_all, lm_head_int8, lm_head_scale,
+                 final_norm_weight, cos_table, sin_table, num_layers, max_seq_len, batch):
+        if not isinstance(batch, int) or not 1 <= batch <= _lib.MAX_BATCH:
+            raise ValueError(f"batch must be an int in [1, {_lib.MAX_BATCH}], got {batch!r}")
+        self._hold_weights(embed_weight, layer_weights_flat, final_norm_weight, lm_head_int8, cos_table, sin_table,
+                           num_layers, max_seq_len, layer_scales_all, lm_head_scale)
+        H, I, V = self.dims
+        if (H, I) != (2048, 6144):
+            raise ValueError(f"the batched kernel is compiled for hidden 2048 / intermediate 6144, got {H} / {I}")
+        if max_seq_len > 1024:
+            raise ValueError(f"max_seq_len {max_seq_len} > 1024: the batched path attends within one workgroup")
+        dev = self.device
+        self.batch = batch
+        D = 128
+        self.k_cache = torch.zeros((batch, num_layers, 8, max_seq_len, D), dtype=torch.bfloat16, device=dev)
+        self.v_cache = torch.zeros_like(self.k_cache)
+        self.output_tokens = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.hidden_buffer = torch.zeros((batch, H), dtype=torch.bfloat16, device=dev)
+        f32 = dict(dtype=torch.float32, device=dev)
+        self.qkv_buffer = torch.zeros((batch, 8, 512), **f32)
+        self.attn_buffer = torch.zeros((batch, 16 * D), **f32)
+        self.act_buffer = torch.zeros((batch, H), **f32)
+        self.mlp_buffer = torch.zeros((batch, I), **f32)
+        self._lib = _lib.load()
+        self._dims = _lib.ModelDims(H, I, 16, 8, D, V)
+        ws_bytes = self._lib.mq_batch_workspace_bytes(ctypes.byref(self._dims))
+        if ws_bytes == 0:
+            raise ValueError(f"unsupported model dims H={H} I={I}: {_lib.last_error()}")
+        self.workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        self._init_workspace()
+        a = _lib.BatchArgs()
+        a.batch = batch
+        a.output_token_ids = self.output_tokens.data_ptr()
+        a.embed_weight = self.embed_weight.data_ptr()
+        a.layer_weights = self.d_layer_weights.data_ptr()
+        a.scales = self.d_layer_scales.data_ptr()
+        a.final_norm_weight = self.final_norm_weight.data_ptr()
+        a.lm_head_weight = self.lm_head_weight.data_ptr()
+        a.lm_head_scale = self.lm_head_scale.data_ptr()
+        a.cos_table, a.sin_table = self.cos_table.data_ptr(), self.sin_table.data_ptr()
+        a.k_cache, a.v_cache = self.k_cache.data_ptr(), self.v_cache.data_ptr()
+        a.num_layers = num_layers
+        a.max_seq_len = max_seq_len
+        a.attn_scale = self.attn_scale
+        a.dims = ctypes.addressof(self._dims)
+        a.workspace = self.workspace.data_ptr()
+        a.workspace_bytes = ws_bytes
+        self._args = a
+        self._positions = [0] * batch
+
+    def launch_step(self, tokens) -> None:
+        """Enqueue one step (one token per sequence) on the current stream."""
+        tokens = [int(t) for t in tokens]
+        if len(tokens) != self.batch:
+            raise ValueError(f"expected {self.batch} tokens, got {len(tokens)}")
+        V = self.dims[2]
+        for b, t in enumerate(tokens):
+            if not 0 <= t < V:
+                raise ValueError(f"sequence {b}: token {t} outside [0, {V})")
+            if self._positions[b] >= self.max_seq_len:
+                raise ValueError(f"sequence {b}: KV cache full at position {self._positions[b]}")
+        a = self._args
+        for b in range(self.batch):
+            a.input_token_ids[b] = tokens[b]
+            a.positions[b] = self._positions[b]
+        st = self._lib.mq_int8_decode_batch_step(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(self.device)))
+        _lib.check(st, "batched decode step")
+        self._positions = [p + 1 for p in self._positions]
+
+    def decode_step(self, tokens) -> list:
+        self.launch_step(tokens)
+        out = self.output_tokens.tolist()
+        if min(out) < 0:
+            status = self._lib.mq_decode_check(self.workspace.data_ptr(),
+                                               ctypes.c_void_p(_lib.stream_handle(self.device)))
+            self._init_workspace()
+            _lib.check(status if status != _lib.MQ_OK else _lib.MQ_ERR_TIMEOUT, "batched decode step")
+        return out
+
+    def reset(self) -> None:
+        self._positions = [0] * self.batch
+        self.k_cache.zero_()
+        self.v_cache.zero_()
+
+    def positions(self) -> list:
+        return list(self._positions)
+
+    def position(self) -> int:
+        return self._positions[0]
+
+    def set_timing_events(self, start=None, stop=None) -> None:
+        if start is None or stop is None:
+            self._args.timing_start = None
+            self._args.timing_stop = None
+            return
+        for e in (start, stop):
+            if e.cuda_event == 0:
+                e.record()
+        self._args.timing_start = start.cuda_event
+        self._args.timing_stop = stop.cuda_event
+
+    def set_spin_limit(self, polls: int) -> None:
+        self._args.spin_limit = int(polls)
+
+    def enable_debug(self, on: bool = True) -> None:
+        """Write each sequence's last-layer values on every following step: ``get_hidden()``
+        (bf16 [batch, H]), ``get_qkv()`` ([batch, 8, 512]: per KV head the two query heads,
+        key and value before QK-norm), ``get_attn_out()``, ``get_activations()`` (the
+        post-attention residual) and ``get_mlp_int()``."""
+        a = self._args
+        for f, t in (("hidden_out", self.hidden_buffer), ("qkv_out", self.qkv_buffer),
+                     ("attn_out", self.attn_buffer), ("act_out", self.act_buffer), ("mlp_out", self.mlp_buffer)):
+            setattr(a, f, t.data_ptr() if on else None)
+
+    def set_trace(self, buf) -> None:
+        """Record a per-stage timeline of every following step into ``buf`` (int64, at least
+        ``(num_layers + 1) * 10 * 256`` entries on the decoder's device); ``None`` stops it."""
+        if buf is None:
+            self._args.trace = None
+            return
+        need = (self.num_layers + 1) * 10 * 256
+        if buf.dtype != torch.int64 or buf.numel() < need or buf.device != self.device or not buf.is_contiguous():
+            raise ValueError(f"trace buffer must be a contiguous int64 tensor of >= {need} entries on {self.device}")
+        self._trace_buf = buf
+        self._args.trace = buf.data_ptr()
+
+    def get_hidden(self): return self.hidden_buffer
+    def get_qkv(self): return self.qkv_buffer
+    def get_attn_out(self): return self.attn_buffer
+    def get_activations(self): return self.act_buffer
+    def get_mlp_int(self): return self.mlp_buffer
 
 
 def load_checkpoint_state(model_path, cfg: ModelConfig) -> dict:

@@ -54,6 +54,48 @@ def test_struct_layout_matches_c(tmp_path, mq):
     assert offs == [getattr(_lib.DecodeArgs, f).offset for f in fields]
 
 
+def test_batch_struct_layout_matches_c(tmp_path, mq):
+    """offsetof() of every mq_batch_args field from a C program compiled against the header."""
+    from megaqwen_a10_amd import _lib
+    fields = [f for f, _ in _lib.BatchArgs._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){"]
+    src.append('printf("%zu %d\\n", sizeof(mq_batch_args), MQ_MAX_BATCH);')
+    for f in fields:
+        src.append(f'printf("%zu\\n", offsetof(mq_batch_args, {f}));')
+    src.append("return 0;}")
+    c = tmp_path / "blayout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "blayout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(c)], check=True)
+    out = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()))
+    assert out[:2] == [ctypes.sizeof(_lib.BatchArgs), _lib.MAX_BATCH]
+    assert out[2:] == [getattr(_lib.BatchArgs, f).offset for f in fields]
+
+
+def test_batch_api_rejects_bad_arguments_without_launching(mq):
+    from megaqwen_a10_amd import _lib
+    lib = _lib.load()
+    assert lib.mq_batch_workspace_bytes(None) > 0
+    assert lib.mq_batch_workspace_bytes(ctypes.byref(_lib.ModelDims(1024, 3072, 16, 8, 128, 151936))) == 0
+    a = _lib.BatchArgs()
+    a.num_layers, a.max_seq_len = 2, 64
+    for bad in (0, 17):
+        a.batch = bad
+        assert lib.mq_int8_decode_batch_step(ctypes.byref(a), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+        assert "batch" in _lib.last_error()
+    a.batch = 2
+    a.input_token_ids[1] = 151936                              # == vocab
+    assert lib.mq_int8_decode_batch_step(ctypes.byref(a), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert "sequence 1" in _lib.last_error()
+    a.input_token_ids[1] = 7
+    a.positions[0] = 64                                        # == max_seq_len
+    assert lib.mq_int8_decode_batch_step(ctypes.byref(a), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert "position" in _lib.last_error()
+    a.positions[0] = 3
+    assert lib.mq_int8_decode_batch_step(ctypes.byref(a), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert "null" in _lib.last_error()
+
+
 def test_c_api_rejects_bad_arguments_without_launching(mq):
     from megaqwen_a10_amd import _lib
     lib = _lib.load()
