@@ -413,6 +413,25 @@ __device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
     return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// 16-byte agent-coherent reads of an exchange region: one buffer load with
+// agent scope (sc1) returns two adjacent 64-bit words, so lanes that read
+// consecutive 16-byte chunks coalesce into whole cache lines. A 16-byte access
+// is one transaction, so each aligned 8-byte word comes back as one store
+// wrote it (a word is checked on its own tag). The base must be the same in
+// every lane of the wave (the buffer resource lives in scalar registers); reads
+// past `nwords` return zero, which is never a tagged word's tag.
+struct XRegion {
+    __amdgpu_buffer_rsrc_t rs;
+    __device__ __forceinline__ XRegion(const uint64_t* base, uint32_t nwords)
+        : rs(__builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(base), (short)0, (int)(nwords * 8u),
+                                               0x00020000 /* 32-bit data format, no swizzle */)) {}
+    // words w and w + 1 (w even)
+    __device__ __forceinline__ uint4 load2(uint32_t w) const {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(w * 8u), 0, 16 /* sc1 */);
+        return make_uint4(v[0], v[1], v[2], v[3]);
+    }
+};
+
 // Bounded polling. After `limit` unsuccessful polls of one word, or once any
 // workgroup has raised the abort flag, every further wait returns at once, so
 // a grid whose producers stalled still drains in bounded time and the host
@@ -522,6 +541,84 @@ struct Waiter {
                 dead = true;
                 return;
             }
+        }
+    }
+
+    // Chunks of two tagged words: chunk i is words w[i], w[i] + 1 of R (w[i] even),
+    // payloads to out[2i], out[2i + 1]. Only the first `count` chunks are read (the
+    // rest of `out` is 0); all loads are issued before any check, and every retry
+    // re-issues the still-missing chunks together.
+    template <int N>
+    __device__ __forceinline__ void get_pairs(const XRegion& R, const uint32_t (&w)[N], uint32_t tag,
+                                              float (&out)[2 * N], int count = N) {
+        uint4 c[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) c[i] = i < count ? R.load2(w[i]) : make_uint4(0, tag, 0, tag);
+        uint32_t pending = 0;
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            if (c[i].y != tag || c[i].w != tag) pending |= 1u << i;
+        uint32_t n = 0;
+        while (pending != 0 && !dead) {
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int i = 0; i < N; ++i)
+                if (pending & (1u << i)) c[i] = R.load2(w[i]);
+#pragma unroll
+            for (int i = 0; i < N; ++i)
+                if ((pending & (1u << i)) && c[i].y == tag && c[i].w == tag) pending &= ~(1u << i);
+            if (pending == 0) break;
+            if (++n >= limit) {
+                dead = true;
+                __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            if ((n & 127u) == 0 &&
+                __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
+                dead = true;
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            out[2 * i] = __uint_as_float(c[i].x);
+            out[2 * i + 1] = __uint_as_float(c[i].z);
+        }
+    }
+
+    // Chunks of two packed words (see pack_tagged), as get_pairs: waits until bit 0
+    // of both words of each chunk equals `pbit`; values with that bit cleared.
+    template <int N>
+    __device__ __forceinline__ void get_packed_pairs(const XRegion& R, const uint32_t (&w)[N], uint32_t pbit,
+                                                     double (&out)[2 * N], int count = N) {
+        uint4 c[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) c[i] = i < count ? R.load2(w[i]) : make_uint4(pbit, 0, pbit, 0);
+        uint32_t pending = 0;
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            if ((c[i].x & 1u) != pbit || (c[i].z & 1u) != pbit) pending |= 1u << i;
+        uint32_t n = 0;
+        while (pending != 0 && !dead) {
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int i = 0; i < N; ++i)
+                if (pending & (1u << i)) c[i] = R.load2(w[i]);
+#pragma unroll
+            for (int i = 0; i < N; ++i)
+                if ((pending & (1u << i)) && (c[i].x & 1u) == pbit && (c[i].z & 1u) == pbit) pending &= ~(1u << i);
+            if (pending == 0) break;
+            if (++n >= limit) {
+                dead = true;
+                __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            if ((n & 127u) == 0 &&
+                __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u)
+                dead = true;
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            out[2 * i] = __longlong_as_double((long long)((((uint64_t)c[i].y) << 32) | (c[i].x & ~1u)));
+            out[2 * i + 1] = __longlong_as_double((long long)((((uint64_t)c[i].w) << 32) | (c[i].z & ~1u)));
         }
     }
 };

@@ -123,18 +123,25 @@ __device__ __forceinline__ int digit_exp(double mx) {
     return e;
 }
 
-// X = trunc(v 2^(28-e)), |X| < 2^28 for |v| < 2^e.
+// X = trunc(v 2^(28-e)), |X| < 2^28 for |v| < 2^e (the scaling is exact).
 __device__ __forceinline__ int fixed28(double v, int e) { return (int)ldexp(v, 28 - e); }
 
 // The four digit bytes of X0..X3 packed per digit: out[d] holds digit d of
-// X0 | X1 << 8 | X2 << 16 | X3 << 24.
+// X0 | X1 << 8 | X2 << 16 | X3 << 24. Digit d of X is byte 3 - d of X << (3 - d)
+// (bits 21 - 7d .. 28 - 7d of X), masked to 7 bits for d > 0.
 __device__ __forceinline__ void digit_words(const int* X, uint32_t* out) {
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-        const int sh = 21 - 7 * d;
-        const uint32_t m = d == 0 ? 0xffu : 0x7fu;
-        out[d] = ((uint32_t)(X[0] >> sh) & m) | (((uint32_t)(X[1] >> sh) & m) << 8) |
-                 (((uint32_t)(X[2] >> sh) & m) << 16) | (((uint32_t)(X[3] >> sh) & m) << 24);
+        const int sh = 3 - d;
+        const uint32_t y0 = (uint32_t)X[0] << sh, y1 = (uint32_t)X[1] << sh;
+        const uint32_t y2 = (uint32_t)X[2] << sh, y3 = (uint32_t)X[3] << sh;
+        // byte sh of each y into bytes 0..3 (v_perm_b32 picks byte i of {src0:src1} for
+        // selector value i, src1 holding bytes 0-3)
+        const uint32_t sel = 0x0c0c0400u + 0x0101u * (uint32_t)sh;
+        const uint32_t t01 = __builtin_amdgcn_perm(y1, y0, sel);
+        const uint32_t t23 = __builtin_amdgcn_perm(y3, y2, sel);
+        const uint32_t w = __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+        out[d] = d == 0 ? w : (w & 0x7f7f7f7fu);
     }
 }
 
@@ -163,6 +170,28 @@ __device__ __forceinline__ double sum_tree(double (&v)[N]) {
     return v[0];
 }
 
+// Chunked vector layout of the gathers: lane c (0..31) of a sequence's 32-lane
+// group holds elements 2 (c + 32 j) and 2 (c + 32 j) + 1 for j = 0, 1, ..., so
+// every 16-byte exchange read (two words) of the group is contiguous with its
+// neighbours'. The bf16 pairs at those elements of p, as 4 words (j = 0..3).
+__device__ __forceinline__ uint4 slice_pairs(const uint16_t* p, int c) {
+    const __attribute__((address_space(1))) uint32_t* q = gview(reinterpret_cast<const uint32_t*>(p));
+    return make_uint4(q[c], q[c + 32], q[c + 64], q[c + 96]);
+}
+
+// Digit rows of 8 chunked values (two groups of 4: v[4h..4h+3] are chunks 2h and
+// 2h + 1): digit d of chunk j goes to the 16-bit slot c + 32 j of row d.
+__device__ __forceinline__ void put_digit_chunks(uint8_t* row0, int pitch, int c, const int (&X)[4], int h) {
+    uint32_t dw[4];
+    digit_words(X, dw);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        uint16_t* row = reinterpret_cast<uint16_t*>(row0 + d * pitch);
+        row[c + 32 * (2 * h)] = (uint16_t)dw[d];
+        row[c + 32 * (2 * h + 1)] = (uint16_t)(dw[d] >> 16);
+    }
+}
+
 }  // namespace
 
 template <int H, int I>
@@ -180,6 +209,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     static_assert(IX == kBG * 24 && IX % 64 == 0 && 2 * IX == 4 * 16 * kWaves * NTE, "gate/up split");
     static_assert(512 == 4 * 16 * kWaves, "QKV split: 16 rows per wave and row group");
     static_assert(RPW / 16 * 2 == kWaves && KSC % 2 == 0 && KSF % 2 == 0, "row-split stages: 2 waves per tile");
+    static_assert(kKS == 64 * 4 && KC == 64 * 4 && IX == 64 * 12, "chunked gathers: 4, 4 and 12 chunks per lane");
+    static_assert(RPW == 64 && kBX == 8 && kThreads == 4 * RPW * 2, "D/G reductions: 4 lanes per row, 2 sequences per pass");
 
     // LDS
     __shared__ LayerWeights s_lw[kMaxLayers];
@@ -309,7 +340,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     // stage A weights: wave w takes rows 128 rg + 16 w + lane % 16 of XCD x's 512, the 16
     // bytes at k = 256 sl + 64 ks + 16 (lane / 16) for k-step ks
     uint4 wA[4];
-    uint4 win8;                               // input-norm gains of this thread's 8 slice elements
+    uint4 win8;                               // input-norm gains of this thread's 8 slice elements (slice_chunks)
     uint32_t scA = 0x3f800000u;               // stage A reducer: its row's scale
     auto load_a = [&](int ll) {
         const LayerWeights& lw = s_lw[ll];
@@ -325,18 +356,18 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             qkv_row(lw, sp, 16 * r + (tid & 15), w, sc);
             scA = ldg_bits(sc);
         }
-        win8 = ldg16((const uint16_t*)lw.input_layernorm_weight + kKS * sl + 8 * (tid & 31));
+        win8 = slice_pairs((const uint16_t*)lw.input_layernorm_weight + kKS * sl, tid & 31);
     };
     // stage C weights: wave w, O rows 64 r + 16 (w / 2) + lane % 16, k-steps 2 (w % 2) + s
     uint4 wC[2];
-    uint32_t soD = 0x3f800000u;               // stage D: O scale of row 64 r + tid % 64
+    uint32_t soD = 0x3f800000u;               // stage D: O scale of row 64 r + (tid / 4) % 64
     auto load_c = [&](int ll) {
         const uint8_t* ob = (const uint8_t*)s_lw[ll].o_proj_weight;
         const int row = RPW * r + 16 * (wave >> 1) + lane % 16;
 #pragma unroll
         for (int s = 0; s < 2; ++s)
             wC[s] = ldg16(ob + (int64_t)row * (16 * kD) + KC * x + 64 * (2 * (wave & 1) + s) + 16 * (lane / 16));
-        soD = ldg_bits(s_sp[ll].o_scale + RPW * r + (tid & 63));
+        soD = ldg_bits(s_sp[ll].o_scale + RPW * r + ((tid >> 2) & 63));
     };
     // stage E weights: wave w, tiles j: rows 384 rg + 16 (NTE w + j) + lane % 16 of XCD x's
     // gate (< IX) / up rows, k-steps as in stage A
@@ -353,7 +384,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) wE[4 * j + ks] = ldg16(w + kKS * sl + 64 * ks + 16 * (lane / 16));
         }
-        wpost8 = ldg16((const uint16_t*)lw.post_attn_layernorm_weight + kKS * sl + 8 * (tid & 31));
+        wpost8 = slice_pairs((const uint16_t*)lw.post_attn_layernorm_weight + kKS * sl, tid & 31);
         if (tid < 24 * kBMax) {
             gsc = ldg_bits(s_sp[ll].gate_scale + IX * x + 24 * r + tid % 24);
             usc = ldg_bits(s_sp[ll].up_scale + IX * x + 24 * r + tid % 24);
@@ -361,22 +392,22 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     };
     // stage F weights: wave w, down rows 64 r + 16 (w / 2) + lane % 16, k-steps 6 (w % 2) + s
     uint4 wF[KSF / 2];
-    uint32_t sdG = 0x3f800000u;               // stage G: down scale of row 64 r + tid % 64
+    uint32_t sdG = 0x3f800000u;               // stage G: down scale of row 64 r + (tid / 4) % 64
     auto load_f = [&](int ll) {
         const uint8_t* db = (const uint8_t*)s_lw[ll].down_proj_weight;
         const int row = RPW * r + 16 * (wave >> 1) + lane % 16;
 #pragma unroll
         for (int s = 0; s < KSF / 2; ++s)
             wF[s] = ldg16(db + (int64_t)row * I + IX * x + 64 * ((KSF / 2) * (wave & 1) + s) + 16 * (lane / 16));
-        sdG = ldg_bits(s_sp[ll].down_scale + RPW * r + (tid & 63));
+        sdG = ldg_bits(s_sp[ll].down_scale + RPW * r + ((tid >> 2) & 63));
     };
 
     // Digits of v = h * gain for the K slice [256 sl, +256) of every sequence: thread
-    // t: sequence t / 32, elements 8 (t % 32) .. + 7 with values hv and gains g8. Writes
-    // digit rows 4b + d (pitch KPA) and es[b]; returns the thread's group sum of h^2
-    // over the slice (32 lanes).
+    // t: sequence t / 32, the 8 slice elements of chunks j = 0..3 of lane t % 32
+    // (slice_pairs) with values hv and gains g8. Writes digit rows 4b + d (pitch KPA)
+    // and es[b]; returns the thread's group sum of h^2 over the slice (32 lanes).
     auto slice_digits = [&](const float (&hv)[8], uint4 g8) -> double {
-        const int b = tid >> 5, k0 = 8 * (tid & 31);
+        const int b = tid >> 5, c = tid & 31;
         const uint32_t gw[4] = {g8.x, g8.y, g8.z, g8.w};
         double v[8], ss = 0.0, mx = 0.0;
 #pragma unroll
@@ -396,10 +427,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 int X[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) X[j] = b < B ? fixed28(v[4 * h + j], e) : 0;
-                uint32_t dw[4];
-                digit_words(X, dw);
-#pragma unroll
-                for (int d = 0; d < 4; ++d) reinterpret_cast<uint32_t*>(dg + (4 * b + d) * KPA)[(k0 >> 2) + h] = dw[d];
+                put_digit_chunks(dg + 4 * b * KPA, KPA, c, X, h);
             }
         }
         if (b < B && (tid & 31) == 0) es[b] = e;
@@ -424,16 +452,19 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
         trace(l, 0);
         {
             // the slice of every sequence's layer input (the embedding rows at layer 0)
-            const int b = tid >> 5, k0 = 8 * (tid & 31);
+            const int b = tid >> 5, c = tid & 31;
             float hv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
             if (b < B) {
                 if (l == 0) {
-                    const uint4 e8 = ldg16(a.embed + (int64_t)a.tok[b] * H + kKS * sl + k0);
+                    const uint4 e8 = slice_pairs(a.embed + (int64_t)a.tok[b] * H + kKS * sl, c);
                     const uint32_t ew[4] = {e8.x, e8.y, e8.z, e8.w};
 #pragma unroll
                     for (int j = 0; j < 8; ++j) hv[j] = bf16_bits_to_f32((j & 1) ? (ew[j >> 1] >> 16) : (ew[j >> 1] & 0xffffu));
                 } else {
-                    wt.get_strided<8>(&hidx[b * H + kKS * sl + k0], 1, tag(l - 1, BS_HID), hv);
+                    uint32_t w[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) w[j] = (uint32_t)(b * H + kKS * sl + 2 * (c + 32 * j));
+                    wt.get_pairs<4>(XRegion(hidx, kBMax * H), w, tag(l - 1, BS_HID), hv);
                 }
             }
             const double ss = slice_digits(hv, win8);
@@ -521,10 +552,15 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
         trace(l, 3);
         // ---------------- C: O partials, rows [64r, +64) x XCD x's attention dims ----------------
         {
-            // gather: thread t: sequence t / 32, dims 8 (t % 32) .. + 7
-            const int b = tid >> 5, k0 = 8 * (tid & 31);
+            // gather: thread t: sequence t / 32, the dims of chunks j = 0..3 of lane t % 32
+            const int b = tid >> 5, c = tid & 31;
             float v8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            if (b < B) wt.get_strided<8>(&atto[b * 256 + k0], 1, tag(l, BS_ATT), v8);
+            if (b < B) {
+                uint32_t w[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[j] = (uint32_t)(b * 256 + 2 * (c + 32 * j));
+                wt.get_pairs<4>(XRegion(atto, kBMax * 256), w, tag(l, BS_ATT), v8);
+            }
             double mx = 0.0;
 #pragma unroll
             for (int j = 0; j < 8; ++j) mx = fmax(mx, fabs((double)v8[j]));
@@ -536,11 +572,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                     int X[4];
 #pragma unroll
                     for (int j = 0; j < 4; ++j) X[j] = b < B ? fixed28(v8[4 * h + j], e) : 0;
-                    uint32_t dw[4];
-                    digit_words(X, dw);
-#pragma unroll
-                    for (int d = 0; d < 4; ++d)
-                        reinterpret_cast<uint32_t*>(dg + (4 * b + d) * KPC)[(k0 >> 2) + h] = dw[d];
+                    put_digit_chunks(dg + 4 * b * KPC, KPC, c, X, h);
                 }
             }
             if (b < B && (tid & 31) == 0) es[b] = e;
@@ -585,27 +617,43 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
 
         trace(l, 4);
         // ---------------- D: O rows [64r, +64) over the 8 XCDs, scale, residual ----------------
+        {
+            // thread t: row rl = (t / 4) % 64 of sequences t / 256 + 2 i, quarter u = t % 4 (the
+            // partials of XCDs 2u, 2u + 1, one 16-byte chunk); the 4 lanes of a row add up
+            const int rl = (tid >> 2) & 63, u = tid & 3, b0 = tid >> 8;
+            const int nb = (B - b0 + 1) >> 1;                 // sequences of this wave
+            uint32_t w[kBMax / 2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int p = tid + kThreads * i;
-            const int rl = p & 63, b = p >> 6;
-            if (b < B) {
-                double v8[kBX];
-                wt.get_packed<kBX>(&po[((size_t)b * H + RPW * r + rl) * kBX], 1, pb, v8);
-                const double sv = sum_tree(v8) * (double)after_wait_f(soD);
-                const float av = (float)(sv + (double)hid_s[b][rl]);
-                act_s[b][rl] = av;
-                ll_put_xcd(&actx[b * H + RPW * r + rl], __float_as_uint(av), tag(l, BS_ACT));
-                if (l == last && x == 0 && a.dbg_act != nullptr) a.dbg_act[(int64_t)b * H + RPW * r + rl] = av;
+            for (int i = 0; i < kBMax / 2; ++i) w[i] = (uint32_t)(((b0 + 2 * i) * H + RPW * r + rl) * kBX + 2 * u);
+            double v[kBMax];
+            wt.get_packed_pairs<kBMax / 2>(XRegion(po, kBMax * H * kBX), w, pb, v, nb);
+            const double so = (double)after_wait_f(soD);
+#pragma unroll
+            for (int i = 0; i < kBMax / 2; ++i) {
+                if (i < nb) {
+                    const int b = b0 + 2 * i;
+                    const double sv = group_sum64<4>(v[2 * i] + v[2 * i + 1]) * so;
+                    if (u == 0) {
+                        const float av = (float)(sv + (double)hid_s[b][rl]);
+                        act_s[b][rl] = av;
+                        ll_put_xcd(&actx[b * H + RPW * r + rl], __float_as_uint(av), tag(l, BS_ACT));
+                        if (l == last && x == 0 && a.dbg_act != nullptr) a.dbg_act[(int64_t)b * H + RPW * r + rl] = av;
+                    }
+                }
             }
         }
         __syncthreads();
         trace(l, 5);
         // ---------------- E: gate/up partials over the slice [256 sl, +256) ----------------
         {
-            const int b = tid >> 5, k0 = 8 * (tid & 31);
+            const int b = tid >> 5, c = tid & 31;
             float hv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-            if (b < B) wt.get_strided<8>(&actx[b * H + kKS * sl + k0], 1, tag(l, BS_ACT), hv);
+            if (b < B) {
+                uint32_t w[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w[j] = (uint32_t)(b * H + kKS * sl + 2 * (c + 32 * j));
+                wt.get_pairs<4>(XRegion(actx, kBMax * H), w, tag(l, BS_ACT), hv);
+            }
             const double ss = slice_digits(hv, wpost8);
             if (b < B && (tid & 31) == 0 && rg == 0) ll_put64(&ess[b * kNSl + sl], pack_tagged(ss, pb));
             __syncthreads();
@@ -669,12 +717,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
         trace(l, 7);
         // ---------------- F: down partials, rows [64r, +64) x XCD x's channels ----------------
         {
-            // gather: thread t: sequence t / 32, channels 24 (t % 32) .. + 23
-            const int b = tid >> 5, k0 = 24 * (tid & 31);
+            // gather: thread t: sequence t / 32, the channels of chunks j = 0..11 of lane t % 32
+            const int b = tid >> 5, c = tid & 31;
             float v24[24];
 #pragma unroll
             for (int j = 0; j < 24; ++j) v24[j] = 0.0f;
-            if (b < B) wt.get_strided<24>(&mlpx[b * IX + k0], 1, tag(l, BS_MLP), v24);
+            if (b < B) {
+                uint32_t w[12];
+#pragma unroll
+                for (int j = 0; j < 12; ++j) w[j] = (uint32_t)(b * IX + 2 * (c + 32 * j));
+                wt.get_pairs<12>(XRegion(mlpx, kBMax * IX), w, tag(l, BS_MLP), v24);
+            }
             double mx = 0.0;
 #pragma unroll
             for (int j = 0; j < 24; ++j) mx = fmax(mx, fabs((double)v24[j]));
@@ -687,11 +740,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                     int X[4];
 #pragma unroll
                     for (int j = 0; j < 4; ++j) X[j] = b < B ? fixed28(v24[4 * h + j], e) : 0;
-                    uint32_t dw[4];
-                    digit_words(X, dw);
-#pragma unroll
-                    for (int d = 0; d < 4; ++d)
-                        reinterpret_cast<uint32_t*>(dg + (4 * b + d) * KPF)[(k0 >> 2) + h] = dw[d];
+                    put_digit_chunks(dg + 4 * b * KPF, KPF, c, X, h);
                 }
             }
             if (b < B && (tid & 31) == 0) es[b] = e;
@@ -736,19 +785,29 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
 
         trace(l, 8);
         // ---------------- G: down rows [64r, +64) over the 8 XCDs, scale, residual, bf16 ----------------
+        {
+            // as stage D
+            const int rl = (tid >> 2) & 63, u = tid & 3, b0 = tid >> 8;
+            const int nb = (B - b0 + 1) >> 1;
+            uint32_t w[kBMax / 2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int p = tid + kThreads * i;
-            const int rl = p & 63, b = p >> 6;
-            if (b < B) {
-                double v8[kBX];
-                wt.get_packed<kBX>(&pd[((size_t)b * H + RPW * r + rl) * kBX], 1, pb, v8);
-                const double sv = sum_tree(v8) * (double)after_wait_f(sdG);
-                const float hf = round_bf16((float)(sv + (double)act_s[b][rl]));
-                hid_s[b][rl] = hf;
-                if (l < last) ll_put_xcd(&hidx[b * H + RPW * r + rl], __float_as_uint(hf), tag(l, BS_HID));
-                if (l == last && x == 0 && a.dbg_hidden != nullptr)
-                    a.dbg_hidden[(int64_t)b * H + RPW * r + rl] = (uint16_t)f32_to_bf16_bits(hf);
+            for (int i = 0; i < kBMax / 2; ++i) w[i] = (uint32_t)(((b0 + 2 * i) * H + RPW * r + rl) * kBX + 2 * u);
+            double v[kBMax];
+            wt.get_packed_pairs<kBMax / 2>(XRegion(pd, kBMax * H * kBX), w, pb, v, nb);
+            const double sd = (double)after_wait_f(sdG);
+#pragma unroll
+            for (int i = 0; i < kBMax / 2; ++i) {
+                if (i < nb) {
+                    const int b = b0 + 2 * i;
+                    const double sv = group_sum64<4>(v[2 * i] + v[2 * i + 1]) * sd;
+                    if (u == 0) {
+                        const float hf = round_bf16((float)(sv + (double)act_s[b][rl]));
+                        hid_s[b][rl] = hf;
+                        if (l < last) ll_put_xcd(&hidx[b * H + RPW * r + rl], __float_as_uint(hf), tag(l, BS_HID));
+                        if (l == last && x == 0 && a.dbg_hidden != nullptr)
+                            a.dbg_hidden[(int64_t)b * H + RPW * r + rl] = (uint16_t)f32_to_bf16_bits(hf);
+                    }
+                }
             }
         }
         __syncthreads();
@@ -813,25 +872,36 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 if (row < r1) dst[i] = ldg16(a.lm_w + (int64_t)row * H + 64 * ks + 16 * (lane / 16));
             }
         };
-        uint4 wcur[TPW], wnxt[TPW];
-        lm_load(0, wcur);
+        // weights two k-steps ahead: wb0 holds even k-steps, wb1 odd ones (k-step ks + 2
+        // is loaded into the buffer ks has just used)
+        uint4 wb0[TPW], wb1[TPW];
+        lm_load(0, wb0);
+        lm_load(1, wb1);
         for (int q = 0; q < kBG / 8; ++q) {
             // digit rows of k-steps 8q .. 8q + 7 (hidden slices of ranks 8q ..): 8 x 64 rows x 16 words
             __syncthreads();                  // the previous chunk's digits are consumed
             {
-                const int s8 = tid >> 6, rowd = tid & 63;
-                if (rowd < 16 * MG) {
-                    float w16[16];
-                    wt.get_strided<16>(&lmd[((size_t)(8 * q + s8) * 64 + rowd) * 16], 1, tl1, w16);
-                    uint32_t* dst = reinterpret_cast<uint32_t*>(dg + ((size_t)s8 * 64 + rowd) * 64);
+                // wave s8 takes k-step 8q + s8: lane l reads words 2 (l % 8), +1 of digit rows
+                // 8 i + l / 8 (rows < 16 MG are in use), a contiguous 1 KB per i and wave
+                const int s8 = tid >> 6, pr = lane & 7;
+                uint32_t w[8];
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) dst[j] = __float_as_uint(w16[j]);
+                for (int i = 0; i < 8; ++i) w[i] = (uint32_t)(((8 * q + s8) * 64 + 8 * i + (lane >> 3)) * 16 + 2 * pr);
+                float v16[16];
+                wt.get_pairs<8>(XRegion(lmd, kBG * 64 * 16), w, tl1, v16, 2 * MG);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    if (i < 2 * MG) {
+                        uint2* dst = reinterpret_cast<uint2*>(dg + ((size_t)s8 * 64 + 8 * i + (lane >> 3)) * 64 + 8 * pr);
+                        *dst = make_uint2(__float_as_uint(v16[2 * i]), __float_as_uint(v16[2 * i + 1]));
+                    }
                 }
             }
             __syncthreads();
+#pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const int ks = 8 * q + s;
-                if (ks + 1 < kBG) lm_load(ks + 1, wnxt);
+                uint4 (&wcur)[TPW] = (s & 1) ? wb1 : wb0;
 #pragma unroll
                 for (int mg = 0; mg < 4; ++mg) {
                     if (mg < MG) {
@@ -841,8 +911,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                             if (wave + kWaves * i < ntl) acc[i][mg] = mfma8(av, as_i32x4(wcur[i]), acc[i][mg]);
                     }
                 }
-#pragma unroll
-                for (int i = 0; i < TPW; ++i) wcur[i] = wnxt[i];
+                if (ks + 2 < kBG) lm_load(ks + 2, wcur);
             }
         }
         trace(a.L, 1);
