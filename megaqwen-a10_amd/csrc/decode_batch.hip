@@ -101,12 +101,12 @@ constexpr BLayout blayout_for(int H, int I) {
     o.qss = off;  off += round256((size_t)kBX * kBMax * kNSl * 8);           // [x][b][slice]
     o.qkvx = off; off += round256((size_t)kBX * kBMax * 512 * 8);            // [x][b][row 512]
     o.atto = off; off += round256((size_t)kBX * kBMax * 256 * 8);            // [x][b][dim 256]
-    o.po = off;   off += round256((size_t)kBMax * H * kBX * 8);              // [b][row][xcd]
+    o.po = off;   off += round256((size_t)kBX * kBMax * H * 8);              // [xcd][b][row]
     o.actx = off; off += round256((size_t)kBX * kBMax * H * 8);              // [x][b][row]
     o.ep = off;   off += round256((size_t)kBX * kNSl * kBMax * 2 * IX * 8);  // [x][slice][b][row 2 IX]
     o.ess = off;  off += round256((size_t)kBX * kBMax * kNSl * 8);           // [x][b][slice]
     o.mlpx = off; off += round256((size_t)kBX * kBMax * IX * 8);             // [x][b][channel]
-    o.pd = off;   off += round256((size_t)kBMax * H * kBX * 8);              // [b][row][xcd]
+    o.pd = off;   off += round256((size_t)kBX * kBMax * H * 8);              // [xcd][b][row]
     o.hidx = off; off += round256((size_t)kBX * kBMax * H * 8);              // [x][b][row]
     o.lme = off;  off += round256((size_t)kBX * kBMax * kBG * 8);           // [x][b][src]
     o.lmd = off;  off += round256((size_t)kBX * kBG * 64 * 16 * 8);         // [x][src][digit row][word]
@@ -192,6 +192,15 @@ __device__ __forceinline__ void put_digit_chunks(uint8_t* row0, int pitch, int c
     }
 }
 
+// Sums of v[0..15] over the 8 lanes of each aligned lane octet, transposed:
+// afterwards v[0], v[1] of lane j (j = lane % 8) hold the octet's sums of
+// entries 2j and 2j + 1 (three halving exchange levels, lane bits 4, 2, 1).
+__device__ __forceinline__ void xcd_transpose_sum(double (&v)[kBMax], int lane) {
+    transpose_level64<4, 16>(v, lane);
+    transpose_level64<2, 8>(v, lane);
+    transpose_level64<1, 4>(v, lane);
+}
+
 }  // namespace
 
 template <int H, int I>
@@ -210,7 +219,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     static_assert(512 == 4 * 16 * kWaves, "QKV split: 16 rows per wave and row group");
     static_assert(RPW / 16 * 2 == kWaves && KSC % 2 == 0 && KSF % 2 == 0, "row-split stages: 2 waves per tile");
     static_assert(kKS == 64 * 4 && KC == 64 * 4 && IX == 64 * 12, "chunked gathers: 4, 4 and 12 chunks per lane");
-    static_assert(RPW == 64 && kBX == 8 && kThreads == 4 * RPW * 2, "D/G reductions: 4 lanes per row, 2 sequences per pass");
+    static_assert(RPW == 64 && kBX == 8 && kWaves == 8 && kWave == 64, "D/G reductions: 8 XCDs x 32 row pairs x 2 sequences per pass");
 
     // LDS
     __shared__ LayerWeights s_lw[kMaxLayers];
@@ -360,14 +369,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     };
     // stage C weights: wave w, O rows 64 r + 16 (w / 2) + lane % 16, k-steps 2 (w % 2) + s
     uint4 wC[2];
-    uint32_t soD = 0x3f800000u;               // stage D: O scale of row 64 r + (tid / 4) % 64
+    // stages D and G: thread t reduces rows 2 cD, 2 cD + 1 of the rank's 64 (see stage D)
+    const int cD = ((tid & 63) >> 3) + 8 * ((tid >> 6) & 3);
+    uint32_t soD0 = 0x3f800000u, soD1 = 0x3f800000u;     // stage D: O scales of those rows
     auto load_c = [&](int ll) {
         const uint8_t* ob = (const uint8_t*)s_lw[ll].o_proj_weight;
         const int row = RPW * r + 16 * (wave >> 1) + lane % 16;
 #pragma unroll
         for (int s = 0; s < 2; ++s)
             wC[s] = ldg16(ob + (int64_t)row * (16 * kD) + KC * x + 64 * (2 * (wave & 1) + s) + 16 * (lane / 16));
-        soD = ldg_bits(s_sp[ll].o_scale + RPW * r + ((tid >> 2) & 63));
+        soD0 = ldg_bits(s_sp[ll].o_scale + RPW * r + 2 * cD);
+        soD1 = ldg_bits(s_sp[ll].o_scale + RPW * r + 2 * cD + 1);
     };
     // stage E weights: wave w, tiles j: rows 384 rg + 16 (NTE w + j) + lane % 16 of XCD x's
     // gate (< IX) / up rows, k-steps as in stage A
@@ -392,14 +404,15 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     };
     // stage F weights: wave w, down rows 64 r + 16 (w / 2) + lane % 16, k-steps 6 (w % 2) + s
     uint4 wF[KSF / 2];
-    uint32_t sdG = 0x3f800000u;               // stage G: down scale of row 64 r + (tid / 4) % 64
+    uint32_t sdG0 = 0x3f800000u, sdG1 = 0x3f800000u;     // stage G: down scales of rows 2 cD, 2 cD + 1
     auto load_f = [&](int ll) {
         const uint8_t* db = (const uint8_t*)s_lw[ll].down_proj_weight;
         const int row = RPW * r + 16 * (wave >> 1) + lane % 16;
 #pragma unroll
         for (int s = 0; s < KSF / 2; ++s)
             wF[s] = ldg16(db + (int64_t)row * I + IX * x + 64 * ((KSF / 2) * (wave & 1) + s) + 16 * (lane / 16));
-        sdG = ldg_bits(s_sp[ll].down_scale + RPW * r + ((tid >> 2) & 63));
+        sdG0 = ldg_bits(s_sp[ll].down_scale + RPW * r + 2 * cD);
+        sdG1 = ldg_bits(s_sp[ll].down_scale + RPW * r + 2 * cD + 1);
     };
 
     // Digits of v = h * gain for the K slice [256 sl, +256) of every sequence: thread
@@ -609,7 +622,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                     if (mg < MG && bb < B) {
                         const i32x4_t c = cm[mg] + cred[(nt * 4 + mg) * kWave + lane];
                         const int row = RPW * r + 16 * nt + lane % 16;
-                        ll_put64(&po[((size_t)bb * H + row) * kBX + x], pack_tagged(digit_value(c, es[bb]), pb));
+                        ll_put64(&po[((size_t)x * kBMax + bb) * H + row], pack_tagged(digit_value(c, es[bb]), pb));
                     }
                 }
             }
@@ -618,27 +631,28 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
         trace(l, 4);
         // ---------------- D: O rows [64r, +64) over the 8 XCDs, scale, residual ----------------
         {
-            // thread t: row rl = (t / 4) % 64 of sequences t / 256 + 2 i, quarter u = t % 4 (the
-            // partials of XCDs 2u, 2u + 1, one 16-byte chunk); the 4 lanes of a row add up
-            const int rl = (tid >> 2) & 63, u = tid & 3, b0 = tid >> 8;
+            // thread t: the partials of XCD xs = t % 8 for rows 2 cD, 2 cD + 1 of sequences
+            // t / 256 + 2 i, one 16-byte chunk each (a wave reads 8 runs of 128 bytes). A
+            // transpose-reduction over the 8 lanes of a row pair (one per XCD) leaves lane xs
+            // with both rows' sums of sequence t / 256 + 2 xs.
+            const int xs = lane & 7, b0 = wave >> 2;
             const int nb = (B - b0 + 1) >> 1;                 // sequences of this wave
             uint32_t w[kBMax / 2];
 #pragma unroll
-            for (int i = 0; i < kBMax / 2; ++i) w[i] = (uint32_t)(((b0 + 2 * i) * H + RPW * r + rl) * kBX + 2 * u);
+            for (int i = 0; i < kBMax / 2; ++i) w[i] = (uint32_t)((xs * kBMax + b0 + 2 * i) * H + RPW * r + 2 * cD);
             double v[kBMax];
-            wt.get_packed_pairs<kBMax / 2>(XRegion(po, kBMax * H * kBX), w, pb, v, nb);
-            const double so = (double)after_wait_f(soD);
+            wt.get_packed_pairs<kBMax / 2>(XRegion(po, kBX * kBMax * H), w, pb, v, nb);
+            xcd_transpose_sum(v, lane);
+            if (xs < nb) {
+                const int b = b0 + 2 * xs;
+                const double sv[2] = {v[0] * (double)after_wait_f(soD0), v[1] * (double)after_wait_f(soD1)};
 #pragma unroll
-            for (int i = 0; i < kBMax / 2; ++i) {
-                if (i < nb) {
-                    const int b = b0 + 2 * i;
-                    const double sv = group_sum64<4>(v[2 * i] + v[2 * i + 1]) * so;
-                    if (u == 0) {
-                        const float av = (float)(sv + (double)hid_s[b][rl]);
-                        act_s[b][rl] = av;
-                        ll_put_xcd(&actx[b * H + RPW * r + rl], __float_as_uint(av), tag(l, BS_ACT));
-                        if (l == last && x == 0 && a.dbg_act != nullptr) a.dbg_act[(int64_t)b * H + RPW * r + rl] = av;
-                    }
+                for (int h = 0; h < 2; ++h) {
+                    const int rl = 2 * cD + h;
+                    const float av = (float)(sv[h] + (double)hid_s[b][rl]);
+                    act_s[b][rl] = av;
+                    ll_put_xcd(&actx[b * H + RPW * r + rl], __float_as_uint(av), tag(l, BS_ACT));
+                    if (l == last && x == 0 && a.dbg_act != nullptr) a.dbg_act[(int64_t)b * H + RPW * r + rl] = av;
                 }
             }
         }
@@ -777,7 +791,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                     if (mg < MG && bb < B) {
                         const i32x4_t c = cm[mg] + cred[(nt * 4 + mg) * kWave + lane];
                         const int row = RPW * r + 16 * nt + lane % 16;
-                        ll_put64(&pd[((size_t)bb * H + row) * kBX + x], pack_tagged(digit_value(c, es[bb]), pb));
+                        ll_put64(&pd[((size_t)x * kBMax + bb) * H + row], pack_tagged(digit_value(c, es[bb]), pb));
                     }
                 }
             }
@@ -787,26 +801,25 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
         // ---------------- G: down rows [64r, +64) over the 8 XCDs, scale, residual, bf16 ----------------
         {
             // as stage D
-            const int rl = (tid >> 2) & 63, u = tid & 3, b0 = tid >> 8;
+            const int xs = lane & 7, b0 = wave >> 2;
             const int nb = (B - b0 + 1) >> 1;
             uint32_t w[kBMax / 2];
 #pragma unroll
-            for (int i = 0; i < kBMax / 2; ++i) w[i] = (uint32_t)(((b0 + 2 * i) * H + RPW * r + rl) * kBX + 2 * u);
+            for (int i = 0; i < kBMax / 2; ++i) w[i] = (uint32_t)((xs * kBMax + b0 + 2 * i) * H + RPW * r + 2 * cD);
             double v[kBMax];
-            wt.get_packed_pairs<kBMax / 2>(XRegion(pd, kBMax * H * kBX), w, pb, v, nb);
-            const double sd = (double)after_wait_f(sdG);
+            wt.get_packed_pairs<kBMax / 2>(XRegion(pd, kBX * kBMax * H), w, pb, v, nb);
+            xcd_transpose_sum(v, lane);
+            if (xs < nb) {
+                const int b = b0 + 2 * xs;
+                const double sv[2] = {v[0] * (double)after_wait_f(sdG0), v[1] * (double)after_wait_f(sdG1)};
 #pragma unroll
-            for (int i = 0; i < kBMax / 2; ++i) {
-                if (i < nb) {
-                    const int b = b0 + 2 * i;
-                    const double sv = group_sum64<4>(v[2 * i] + v[2 * i + 1]) * sd;
-                    if (u == 0) {
-                        const float hf = round_bf16((float)(sv + (double)act_s[b][rl]));
-                        hid_s[b][rl] = hf;
-                        if (l < last) ll_put_xcd(&hidx[b * H + RPW * r + rl], __float_as_uint(hf), tag(l, BS_HID));
-                        if (l == last && x == 0 && a.dbg_hidden != nullptr)
-                            a.dbg_hidden[(int64_t)b * H + RPW * r + rl] = (uint16_t)f32_to_bf16_bits(hf);
-                    }
+                for (int h = 0; h < 2; ++h) {
+                    const int rl = 2 * cD + h;
+                    const float hf = round_bf16((float)(sv[h] + (double)act_s[b][rl]));
+                    hid_s[b][rl] = hf;
+                    if (l < last) ll_put_xcd(&hidx[b * H + RPW * r + rl], __float_as_uint(hf), tag(l, BS_HID));
+                    if (l == last && x == 0 && a.dbg_hidden != nullptr)
+                        a.dbg_hidden[(int64_t)b * H + RPW * r + rl] = (uint16_t)f32_to_bf16_bits(hf);
                 }
             }
         }
