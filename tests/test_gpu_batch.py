@@ -5,33 +5,43 @@ the single-sequence step sharing the weights. Each sequence of a batch must
 therefore produce the float64 oracle's greedy tokens for its own prompt, and a
 sequence's tokens must not depend on which slot or batch size it runs in.
 The batched kernel computes products on the int8 matrix cores with 28-bit
-(four-digit) activations, so agreement is checked on tokens, with the oracle's
-top-2 margins: a divergence is allowed only where the oracle's top-2 logit
-margin is below 1e-4. The hidden state after the last layer is compared with
-the oracle's directly (relative L2, and most bf16 values identical).
+(four-digit) activations and applies the RMSNorm scale after the product, so
+its intermediate values carry bf16-level differences from the oracle's (a
+flipped bf16 rounding is 2^-8 relative), and those accumulate in the KV cache
+over a long run. Parity is therefore checked teacher-forced: the oracle is fed
+each sequence's own GPU tokens, and at every step the GPU's token must be the
+oracle's argmax up to the bf16-activation tolerance carried to the logits
+(its logit at most 2^-7 of the logits' standard deviation below the maximum,
+twice the 2^-8 relative error of one bf16 rounding). After the last step the
+hidden state must be within 2^-8 relative L2 of the oracle's. A wrong token
+from a real fault falls short of the maximum by about 3 logit standard
+deviations.
 """
 from __future__ import annotations
 
 import pytest
 import torch
 
-from oracle.ref_cpu import Dims, RefDecoder, greedy_generate
+from oracle.ref_cpu import Dims, RefDecoder
 
 pytestmark = pytest.mark.gpu
 
 STEPS = 12
-MARGIN_TOL = 1e-4      # logit units; the oracle fixtures' smallest margins are ~1e-3
+LOGIT_TOL = 2.0 ** -7  # x the logits' standard deviation at that step
+
+
+def _model(mq, dev, S, seed=5):
+    cfg = mq.QWEN3_1_7B.with_(num_layers=2, vocab_size=4096)
+    state, _ = mq.random_init_state(cfg, seed=seed, norm_jitter=0.1)
+    qstate = mq.quantize_state(state, cfg, dev)
+    packed = mq.pack_int8(qstate, cfg)
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    return cfg, packed, cos, sin, S
 
 
 @pytest.fixture(scope="module")
 def model(mq, dev):
-    cfg = mq.QWEN3_1_7B.with_(num_layers=2, vocab_size=4096)
-    state, _ = mq.random_init_state(cfg, seed=5, norm_jitter=0.1)
-    qstate = mq.quantize_state(state, cfg, dev)
-    packed = mq.pack_int8(qstate, cfg)
-    S = 64
-    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
-    return cfg, packed, cos, sin, S
+    return _model(mq, dev, 64)
 
 
 def _prompts(n, vocab, seed=21):
@@ -39,9 +49,11 @@ def _prompts(n, vocab, seed=21):
     return torch.randint(0, vocab, (n, 8), generator=g).tolist()
 
 
-def _run_batch(mq, model, prompts, steps=STEPS):
+def _run_batch(mq, model, prompts, steps=STEPS, debug=False):
     cfg, (embed, layers, scales, lm_q, lm_s, fnorm), cos, sin, S = model
     dec = mq.A10Int8BatchDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S, len(prompts))
+    if debug:
+        dec.enable_debug()
     out = None
     for i in range(len(prompts[0])):
         out = dec.decode_step([p[i] for p in prompts])
@@ -53,37 +65,55 @@ def _run_batch(mq, model, prompts, steps=STEPS):
     return dec, toks
 
 
-_oracle_cache = {}
-
-
-def _oracle(model, prompt, steps=STEPS):
-    key = tuple(prompt)
-    if key not in _oracle_cache:
-        cfg, (embed, layers, scales, lm_q, lm_s, fnorm), cos, sin, S = model
-        c = lambda t: t.cpu()
-        ref = RefDecoder(Dims(hidden_size=2048, intermediate_size=6144, vocab_size=cfg.vocab_size), c(embed),
-                         [c(t) for t in layers], [c(t) for t in scales], c(fnorm), c(lm_q), c(lm_s), c(cos), c(sin),
-                         cfg.num_layers, S)
-        _oracle_cache[key] = greedy_generate(ref, prompt, steps)
-    return _oracle_cache[key]
+def _ref(model):
+    cfg, (embed, layers, scales, lm_q, lm_s, fnorm), cos, sin, S = model
+    c = lambda t: t.cpu()
+    return RefDecoder(Dims(hidden_size=2048, intermediate_size=6144, vocab_size=cfg.vocab_size), c(embed),
+                      [c(t) for t in layers], [c(t) for t in scales], c(fnorm), c(lm_q), c(lm_s), c(cos), c(sin),
+                      cfg.num_layers, S)
 
 
 @pytest.mark.parametrize("batch", [1, 3, 4, 8, 16])
 def test_batch_matches_oracle_per_sequence(mq, dev, model, batch):
     prompts = _prompts(batch, model[0].vocab_size)
     print(f"batch {batch}", flush=True)
-    dec, toks = _run_batch(mq, model, prompts)
-    assert dec.positions() == [8 + STEPS - 1] * batch
-    # tokens equal the oracle's up to the first step whose top-2 logit margin is below
-    # MARGIN_TOL (a near-tie that the batched path's slightly different rounding may
-    # resolve either way); past such a step the sequences legitimately differ
-    bad, ties = [], []
+    _check_against_oracle(mq, model, prompts, STEPS)
+
+
+def test_batch_long_positions_match_oracle(mq, dev):
+    """Past the positions the config-5 benchmark reaches (8 prompt tokens + 128 steps): three
+    sequences, 8 prompt tokens and 142 greedy steps, up to position 149."""
+    long_model = _model(mq, dev, 160, seed=6)
+    prompts = _prompts(3, long_model[0].vocab_size, seed=29)
+    print("batch 3, 142 steps", flush=True)
+    _check_against_oracle(mq, long_model, prompts, 142)
+
+
+def _check_against_oracle(mq, model, prompts, steps):
+    """Teacher-forced parity of every sequence (module docstring)."""
+    dec, toks = _run_batch(mq, model, prompts, steps, debug=True)
+    assert dec.positions() == [8 + steps - 1] * len(prompts)
+    hidden = dec.get_hidden().float().cpu().double()
+    bad, worst, differ = [], 0.0, 0
     for b, p in enumerate(prompts):
-        want, margins = _oracle(model, p)
-        if toks[b] != want:
-            i = next(j for j in range(len(want)) if toks[b][j] != want[j])
-            (ties if margins[i] < MARGIN_TOL else bad).append((b, i, toks[b][i], want[i], f"{margins[i]:.3e}"))
-    print("divergent at near-ties (sequence, step, got, oracle, margin):", ties, flush=True)
+        ref = _ref(model)
+        for i, t in enumerate(list(p) + toks[b][:-1]):
+            logits = ref.step_logits(int(t))
+            j = i - (len(p) - 1)
+            if j < 0:
+                continue
+            got = toks[b][j]
+            deficit = float(logits.max() - logits[got]) / float(logits.std())
+            worst = max(worst, deficit)
+            differ += int(got != int(logits.argmax()))
+            if deficit > LOGIT_TOL:
+                bad.append((b, j, got, int(logits.argmax()), f"{deficit:.2e}"))
+        want = ref.last["hidden"].double()
+        e = float(torch.linalg.norm(hidden[b] - want) / torch.linalg.norm(want))
+        if e >= 2.0 ** -8:
+            bad.append((b, "hidden rel L2", f"{e:.2e}"))
+    print(f"{len(prompts)} sequences x {steps} steps: {differ} tokens differ from the oracle's argmax, "
+          f"largest logit deficit {worst:.2e} std", flush=True)
     assert not bad, bad
 
 
