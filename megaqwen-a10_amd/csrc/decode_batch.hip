@@ -348,44 +348,32 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     const int sl = r % kNSl, rg = r / kNSl;
     // stage A weights: wave w takes rows 128 rg + 16 w + lane % 16 of XCD x's 512, the 16
     // bytes at k = 256 sl + 64 ks + 16 (lane / 16) for k-step ks
+    //
+    // Only weights are loaded ahead. A stage's scales and norm gains are loaded just
+    // before the exchange poll that precedes their use: a value loaded ahead would be
+    // live across stages and may be spilled, and a spill store waits for its load,
+    // which (loads returning in order) waits for the whole weight batch before it.
     uint4 wA[4];
-    uint4 win8;                               // input-norm gains of this thread's 8 slice elements (slice_chunks)
-    uint32_t scA = 0x3f800000u;               // stage A reducer: its row's scale
     auto load_a = [&](int ll) {
-        const LayerWeights& lw = s_lw[ll];
-        const ScalePointers& sp = s_sp[ll];
-        {
-            const uint8_t* w; const float* sc;
-            qkv_row(lw, sp, 128 * rg + 16 * wave + lane % 16, w, sc);
+        const uint8_t* w; const float* sc;
+        qkv_row(s_lw[ll], s_sp[ll], 128 * rg + 16 * wave + lane % 16, w, sc);
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) wA[ks] = ldg16(w + kKS * sl + 64 * ks + 16 * (lane / 16));
-        }
-        {
-            const uint8_t* w; const float* sc;
-            qkv_row(lw, sp, 16 * r + (tid & 15), w, sc);
-            scA = ldg_bits(sc);
-        }
-        win8 = slice_pairs((const uint16_t*)lw.input_layernorm_weight + kKS * sl, tid & 31);
+        for (int ks = 0; ks < 4; ++ks) wA[ks] = ldg16(w + kKS * sl + 64 * ks + 16 * (lane / 16));
     };
     // stage C weights: wave w, O rows 64 r + 16 (w / 2) + lane % 16, k-steps 2 (w % 2) + s
     uint4 wC[2];
     // stages D and G: thread t reduces rows 2 cD, 2 cD + 1 of the rank's 64 (see stage D)
     const int cD = ((tid & 63) >> 3) + 8 * ((tid >> 6) & 3);
-    uint32_t soD0 = 0x3f800000u, soD1 = 0x3f800000u;     // stage D: O scales of those rows
     auto load_c = [&](int ll) {
         const uint8_t* ob = (const uint8_t*)s_lw[ll].o_proj_weight;
         const int row = RPW * r + 16 * (wave >> 1) + lane % 16;
 #pragma unroll
         for (int s = 0; s < 2; ++s)
             wC[s] = ldg16(ob + (int64_t)row * (16 * kD) + KC * x + 64 * (2 * (wave & 1) + s) + 16 * (lane / 16));
-        soD0 = ldg_bits(s_sp[ll].o_scale + RPW * r + 2 * cD);
-        soD1 = ldg_bits(s_sp[ll].o_scale + RPW * r + 2 * cD + 1);
     };
     // stage E weights: wave w, tiles j: rows 384 rg + 16 (NTE w + j) + lane % 16 of XCD x's
     // gate (< IX) / up rows, k-steps as in stage A
     uint4 wE[NTE * 4];
-    uint4 wpost8;
-    uint32_t gsc = 0x3f800000u, usc = 0x3f800000u;
     auto load_e = [&](int ll) {
         const LayerWeights& lw = s_lw[ll];
 #pragma unroll
@@ -396,23 +384,15 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) wE[4 * j + ks] = ldg16(w + kKS * sl + 64 * ks + 16 * (lane / 16));
         }
-        wpost8 = slice_pairs((const uint16_t*)lw.post_attn_layernorm_weight + kKS * sl, tid & 31);
-        if (tid < 24 * kBMax) {
-            gsc = ldg_bits(s_sp[ll].gate_scale + IX * x + 24 * r + tid % 24);
-            usc = ldg_bits(s_sp[ll].up_scale + IX * x + 24 * r + tid % 24);
-        }
     };
     // stage F weights: wave w, down rows 64 r + 16 (w / 2) + lane % 16, k-steps 6 (w % 2) + s
     uint4 wF[KSF / 2];
-    uint32_t sdG0 = 0x3f800000u, sdG1 = 0x3f800000u;     // stage G: down scales of rows 2 cD, 2 cD + 1
     auto load_f = [&](int ll) {
         const uint8_t* db = (const uint8_t*)s_lw[ll].down_proj_weight;
         const int row = RPW * r + 16 * (wave >> 1) + lane % 16;
 #pragma unroll
         for (int s = 0; s < KSF / 2; ++s)
             wF[s] = ldg16(db + (int64_t)row * I + IX * x + 64 * ((KSF / 2) * (wave & 1) + s) + 16 * (lane / 16));
-        sdG0 = ldg_bits(s_sp[ll].down_scale + RPW * r + 2 * cD);
-        sdG1 = ldg_bits(s_sp[ll].down_scale + RPW * r + 2 * cD + 1);
     };
 
     // Digits of v = h * gain for the K slice [256 sl, +256) of every sequence: thread
@@ -466,6 +446,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
         {
             // the slice of every sequence's layer input (the embedding rows at layer 0)
             const int b = tid >> 5, c = tid & 31;
+            const uint4 win8 = slice_pairs((const uint16_t*)lw.input_layernorm_weight + kKS * sl, c);
             float hv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
             if (b < B) {
                 if (l == 0) {
@@ -506,6 +487,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             // reduce rows [16r, +16) over the 8 slices: thread t < 256: row 16 r + t % 16, sequence t / 16
             {
                 const int rl = tid & 15, bb = tid >> 4;
+                uint32_t scA = 0x3f800000u;
+                {
+                    const uint8_t* w; const float* sc;
+                    qkv_row(lw, sp, 16 * r + rl, w, sc);
+                    scA = ldg_bits(sc);
+                }
                 double s8 = 0.0;
                 if (tid < 256 && bb < B) {
                     double v8[kNSl];
@@ -640,6 +627,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             uint32_t w[kBMax / 2];
 #pragma unroll
             for (int i = 0; i < kBMax / 2; ++i) w[i] = (uint32_t)((xs * kBMax + b0 + 2 * i) * H + RPW * r + 2 * cD);
+            const uint32_t soD0 = ldg_bits(sp.o_scale + RPW * r + 2 * cD);
+            const uint32_t soD1 = ldg_bits(sp.o_scale + RPW * r + 2 * cD + 1);
             double v[kBMax];
             wt.get_packed_pairs<kBMax / 2>(XRegion(po, kBX * kBMax * H), w, pb, v, nb);
             xcd_transpose_sum(v, lane);
@@ -661,6 +650,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
         // ---------------- E: gate/up partials over the slice [256 sl, +256) ----------------
         {
             const int b = tid >> 5, c = tid & 31;
+            const uint4 wpost8 = slice_pairs((const uint16_t*)lw.post_attn_layernorm_weight + kKS * sl, c);
             float hv[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
             if (b < B) {
                 uint32_t w[4];
@@ -695,6 +685,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             }
             trace(l, 6);
             // reduce channels [24r, +24) (gate rows 24 r + c, up rows IX + 24 r + c) over the 8 slices
+            const uint32_t gsc = ldg_bits(sp.gate_scale + IX * x + 24 * r + tid % 24);
+            const uint32_t usc = ldg_bits(sp.up_scale + IX * x + 24 * r + tid % 24);
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int p = tid + kThreads * i;
@@ -806,6 +798,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             uint32_t w[kBMax / 2];
 #pragma unroll
             for (int i = 0; i < kBMax / 2; ++i) w[i] = (uint32_t)((xs * kBMax + b0 + 2 * i) * H + RPW * r + 2 * cD);
+            const uint32_t sdG0 = ldg_bits(sp.down_scale + RPW * r + 2 * cD);
+            const uint32_t sdG1 = ldg_bits(sp.down_scale + RPW * r + 2 * cD + 1);
             double v[kBMax];
             wt.get_packed_pairs<kBMax / 2>(XRegion(pd, kBX * kBMax * H), w, pb, v, nb);
             xcd_transpose_sum(v, lane);
