@@ -231,6 +231,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     __shared__ float att_in[512];
     __shared__ float lm_v[kWaves][kBMax];
     __shared__ int lm_i[kWaves][kBMax];
+    __shared__ uint32_t rope_s[2][kD];        // attention rank: cos / sin row of its position (bf16 bits)
     constexpr size_t kBigF = (size_t)64 * KPF + (size_t)4 * 4 * 64 * 16;          // F digits + pair partials
     constexpr size_t kBigLM = (size_t)8 * 64 * 64;                                  // 8 k-steps of LM digits
     constexpr size_t kBig0 = sizeof(AttnShared<128>) > kBigF ? sizeof(AttnShared<128>) : kBigF;
@@ -301,31 +302,21 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     const int64_t head_stride = (int64_t)a.S * kD;                 // one KV head of one layer
     const int64_t seq_stride = (int64_t)a.L * 8 * head_stride;     // one sequence's cache
 
-    // stage-B inputs of the attention rank (sequence r): RoPE row, K/V rows of
-    // the first kKvLds earlier positions (prefetched a layer ahead), QK-norm gains
+    // stage-B inputs of the attention rank (sequence r): the RoPE row of its
+    // position (in LDS for the whole step) and the K/V rows of the first kKvLds
+    // earlier positions (prefetched a layer ahead); the QK-norm gains are loaded
+    // in stage B with the query gather
     const bool attn = r < B;
     const int apos = attn ? a.pos[r] : 0;
-    uint32_t c0 = 0, s0 = 0, c1 = 0, s1 = 0;
-    if (attn && wave < 3) {
-        const uint16_t* ct = a.cos_t + (int64_t)apos * kD;
-        const uint16_t* stt = a.sin_t + (int64_t)apos * kD;
-        c0 = ldg_bits(ct + lane);
-        s0 = ldg_bits(stt + lane);
-        c1 = ldg_bits(ct + lane + 64);
-        s1 = ldg_bits(stt + lane + 64);
+    if (attn && tid < 2 * kD) {
+        const uint16_t* row = (tid < kD ? a.cos_t : a.sin_t) + (int64_t)apos * kD;
+        rope_s[tid / kD][tid % kD] = ldg_bits(row + tid % kD);
     }
     constexpr int kPreU4 = 2 * kKvLds * (kD / 8) / kThreads;
     uint4 pre[kPreU4];
-    uint32_t nw0 = 0, nw1 = 0;
     const int npre = attn ? min(apos, kKvLds) : 0;
     auto prefetch_attn = [&](int ll) {
         if (!attn) return;
-        const LayerWeights& lw = s_lw[ll];
-        if (wave < 3) {
-            const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
-            nw0 = ldg_bits(nw + lane);
-            nw1 = ldg_bits(nw + lane + 64);
-        }
         const int64_t cb = (int64_t)r * seq_stride + ((int64_t)ll * 8 + x) * head_stride;
 #pragma unroll
         for (int i = 0; i < kPreU4; ++i) {
@@ -521,6 +512,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
         trace(l, 2);
         // ---------------- B: attention of sequence r (ranks r < B) ----------------
         if (attn) {
+            uint32_t nw0 = 0, nw1 = 0;
+            if (wave < 3) {
+                const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
+                nw0 = ldg_bits(nw + lane);
+                nw1 = ldg_bits(nw + lane + 64);
+            }
             {
                 float v1[1];
                 wt.get_strided<1>(qkvx + r * 512 + tid, 0, tag(l, BS_QKV), v1);
@@ -537,8 +534,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             __syncthreads();
             const int64_t cache_base = (int64_t)r * seq_stride + ((int64_t)l * 8 + x) * head_stride;
             const int64_t cur = cache_base + (int64_t)apos * kD;
-            attn_qk_rope(at, att_in, nw0, nw1, c0, s0, c1, s1, a.kc + cur, a.vc + cur, nullptr, nullptr, nullptr,
-                         wave, lane);
+            attn_qk_rope(at, att_in, nw0, nw1, rope_s[0][lane], rope_s[1][lane], rope_s[0][lane + 64],
+                         rope_s[1][lane + 64], a.kc + cur, a.vc + cur, nullptr, nullptr, nullptr, wave, lane);
             __syncthreads();
             attn_core(at, a.kc + cache_base, a.vc + cache_base, apos + 1, apos, (double)a.attn_scale, tid, lane,
                       wave, [&](int i, float v) {
