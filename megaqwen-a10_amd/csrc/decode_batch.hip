@@ -576,9 +576,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             // the next stages' inputs of the attention rank (its layer l + 1 rows)
             if (l < last) prefetch_attn(l + 1);
             __syncthreads();
-            // stage E's weights
-            load_e(l);
-            issue_fence();
             const int nt = wave >> 1;
             i32x4_t cm[4];
 #pragma unroll
@@ -610,6 +607,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                     }
                 }
             }
+            // stage E's weights, behind this stage's stores: a weight batch fills the CU's
+            // memory pipeline for microseconds, and the stores are on the critical path
+            issue_fence();
+            load_e(l);
+            issue_fence();
         }
 
         trace(l, 4);
@@ -658,9 +660,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             const double ss = slice_digits(hv, wpost8);
             if (b < B && (tid & 31) == 0 && rg == 0) ll_put64(&ess[b * kNSl + sl], pack_tagged(ss, pb));
             __syncthreads();
-            // stage F's weights
-            load_f(l);
-            issue_fence();
 #pragma unroll
             for (int mg = 0; mg < 4; ++mg) {
                 if (mg < MG) {
@@ -680,6 +679,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                     }
                 }
             }
+            // stage F's weights, behind the stores
+            issue_fence();
+            load_f(l);
+            issue_fence();
             trace(l, 6);
             // reduce channels [24r, +24) (gate rows 24 r + c, up rows IX + 24 r + c) over the 8 slices
             const uint32_t gsc = ldg_bits(sp.gate_scale + IX * x + 24 * r + tid % 24);
@@ -748,11 +751,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             }
             if (b < B && (tid & 31) == 0) es[b] = e;
             __syncthreads();
-            // the next layer's stage A weights
-            if (l < last) {
-                load_a(l + 1);
-                issue_fence();
-            }
             const int nt = wave >> 1;
             i32x4_t cm[4];
 #pragma unroll
@@ -783,6 +781,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                         ll_put64(&pd[((size_t)x * kBMax + bb) * H + row], pack_tagged(digit_value(c, es[bb]), pb));
                     }
                 }
+            }
+            // the next layer's stage A weights, behind the stores
+            if (l < last) {
+                issue_fence();
+                load_a(l + 1);
+                issue_fence();
             }
         }
 
