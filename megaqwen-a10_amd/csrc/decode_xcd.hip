@@ -125,6 +125,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     __shared__ __align__(16) AttnShared<kSlice> at;
     __shared__ float lm_v[kWaves];
     __shared__ int lm_i[kWaves];
+    __shared__ uint32_t rope_s[2][D];       // cos / sin row of this step's position (bf16 bits)
     __shared__ LayerWeights s_lw[kMaxLayers];
     __shared__ ScalePointers s_sp[kMaxLayers];
 
@@ -240,7 +241,21 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     constexpr int kPreU4 = 2 * kKvLds * (D / 8) / kThreads;
     uint4 wo[PPL_O];
     uint4 pre[kPreU4];
+    // Where stage B's QK-norm gains and RoPE row live: the int8 instantiations have
+    // registers to spare and load the gains a layer ahead (with the O scale) and hold
+    // the RoPE row in registers. The bf16 instantiation spills, and a spilled value
+    // costs more than it saves: the spill store waits for its load, and the reload
+    // waits, in order, behind every weight load issued before it. It keeps the RoPE
+    // row in LDS and loads the gains at the start of stage A.
+    constexpr bool kLateInputs = !kInt8;
     uint32_t so = 0x3f800000u, nw0 = 0, nw1 = 0;
+    auto load_gains = [&](const LayerWeights& lw) {
+        if (wave < 3) {
+            const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
+            nw0 = ldg_bits(nw + lane);
+            nw1 = ldg_bits(nw + lane + 64);
+        }
+    };
     auto prefetch_b = [&](int ll) {
         const LayerWeights& lw = s_lw[ll];
         const uint8_t* ob = (const uint8_t*)lw.o_proj_weight;
@@ -251,11 +266,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             if (pc < PC_O) wo[k] = ldg16(ob + (int64_t)(R0 + crow) * (16 * D) * ES + (int64_t)AD * x * ES + pc * 16);
         }
         if (kInt8 && tid < RPW) so = ldg_bits(s_sp[ll].o_scale + R0 + tid);
-        if (wave < 3) {
-            const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
-            nw0 = ldg_bits(nw + lane);
-            nw1 = ldg_bits(nw + lane + 64);
-        }
+        if constexpr (!kLateInputs) load_gains(lw);
         const int64_t cb = ((int64_t)ll * kNX + x) * kv_head_stride + (int64_t)opaque(sj0) * D;
 #pragma unroll
         for (int i = 0; i < kPreU4; ++i) {
@@ -267,9 +278,15 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             if (j < npre) pre[i] = ldg16((side == 0 ? a.kc : a.vc) + cb + (int64_t)j * D + c * 8);
         }
     };
-    // the RoPE row of this position is the same for every layer
+    // the RoPE row of this position is the same for every layer (in LDS: stage A's
+    // barriers order these writes before the first read)
     uint32_t c0 = 0, s0 = 0, c1 = 0, s1 = 0;
-    if (wave < 3) {
+    if constexpr (kLateInputs) {
+        if (tid < 2 * D) {
+            const uint16_t* row = (tid < D ? a.cos_t : a.sin_t) + (int64_t)a.pos * D;
+            rope_s[tid / D][tid % D] = ldg_bits(row + tid % D);
+        }
+    } else if (wave < 3) {
         const uint16_t* ct = a.cos_t + (int64_t)a.pos * D;
         const uint16_t* stt = a.sin_t + (int64_t)a.pos * D;
         c0 = ldg_bits(ct + lane);
@@ -285,6 +302,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         const ScalePointers& sp = s_sp[l];
         const int tid = opaque(tid_all);
         const int lane = tid % kWave;
+        // bf16: stage B's QK-norm gains, at the start of stage A (no exchange poll before
+        // their use, so the loads overlap stage A's work)
+        if constexpr (kLateInputs) load_gains(lw);
 
         // ---------------- A: RMSNorm + QKV rows -> XCD-local words ----------------
         {
@@ -348,6 +368,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             const int64_t cur = cache_base + (int64_t)a.pos * D;
             const bool writer = (r == 0);           // rank 0 writes the cache rows
             const bool dbg = kDebug && writer && l == last;
+            if constexpr (kLateInputs) {
+                c0 = rope_s[0][lane];
+                s0 = rope_s[1][lane];
+                c1 = rope_s[0][lane + 64];
+                s1 = rope_s[1][lane + 64];
+            }
             attn_qk_rope(at, att_in, nw0, nw1, c0, s0, c1, s1, writer ? a.kc + cur : nullptr,
                          writer ? a.vc + cur : nullptr, (dbg && a.dbg_q) ? a.dbg_q + 2 * x * D : nullptr,
                          (dbg && a.dbg_k) ? a.dbg_k + x * D : nullptr, (dbg && a.dbg_v) ? a.dbg_v + x * D : nullptr,
