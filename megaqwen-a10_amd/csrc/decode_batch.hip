@@ -9,10 +9,10 @@
 //   A  QKV, K-sliced   rank r = 8q + s: rows [128q, +128) of XCD x's 512 q|k|v
 //                      rows x hidden elements [256s, +256) (gathered from the 4
 //                      ranks owning them, times the input-norm gains) -> XCD-
-//                      local partials; rank r sums rows [16r, +16) over the 8
-//                      slices, applies the RMSNorm scale and the row scale
-//   B  attention       rank b < B: sequence b (QK-norm, RoPE, cache write,
-//                      softmax over its KV cache; attention.h)
+//                      local partials
+//   B  attention       rank b < B: sequence b -- sums its 512 rows over the 8
+//                      slices, applies the RMSNorm and row scales, then QK-norm,
+//                      RoPE, cache write, softmax over its KV cache (attention.h)
 //   C  O, row-split    rank r: rows [64r, +64) x XCD x's 256 attention dims
 //                                                             -> cross-XCD partials
 //   D  reduce          rank r: its 64 rows over the 8 XCDs, scale, residual
@@ -52,7 +52,7 @@ constexpr int kD = 128;                 // head dim
 constexpr int kLmTiles = 5;             // LM-head 16-row tiles per wave
 constexpr int kLmRowsPerWG = 16 * kLmTiles * kWaves;
 
-enum BStage { BS_QKV = 0, BS_ATT = 1, BS_MLP = 2, BS_ACT = 3, BS_HID = 4 };
+enum BStage { BS_ATT = 1, BS_MLP = 2, BS_ACT = 3, BS_HID = 4 };    // tag stages (0 unused)
 constexpr uint32_t kBStages = 5;
 constexpr int kKS = 256;                // stages A and E: K slice of a rank
 constexpr int kNSl = 8;                 // K slices (rank r takes slice r % 8, row group r / 8)
@@ -89,7 +89,7 @@ struct BArgs {
 // one-bit parity tag (pack_tagged), written exactly once per layer; the others
 // carry a 32-bit payload and a (step, layer, stage) tag.
 struct BLayout {
-    size_t qp, qss, qkvx, atto, po, actx, ep, ess, mlpx, pd, hidx, lme, lmd, lmx, lmc, total;
+    size_t qp, qss, atto, po, actx, ep, ess, mlpx, pd, hidx, lme, lmd, lmx, lmc, total;
 };
 // Every layout puts the index that consecutive lanes of the writer and of the
 // reader step through last (coalesced stores and loads).
@@ -99,7 +99,6 @@ constexpr BLayout blayout_for(int H, int I) {
     size_t off = 256;
     o.qp = off;   off += round256((size_t)kBX * kNSl * kBMax * 512 * 8);     // [x][slice][b][row 512]
     o.qss = off;  off += round256((size_t)kBX * kBMax * kNSl * 8);           // [x][b][slice]
-    o.qkvx = off; off += round256((size_t)kBX * kBMax * 512 * 8);            // [x][b][row 512]
     o.atto = off; off += round256((size_t)kBX * kBMax * 256 * 8);            // [x][b][dim 256]
     o.po = off;   off += round256((size_t)kBX * kBMax * H * 8);              // [xcd][b][row]
     o.actx = off; off += round256((size_t)kBX * kBMax * H * 8);              // [x][b][row]
@@ -254,7 +253,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     WsHeader* hdr = reinterpret_cast<WsHeader*>(a.ws);
     uint64_t* const qp = reinterpret_cast<uint64_t*>(a.ws + kLay.qp) + (size_t)x * kNSl * kBMax * 512;
     uint64_t* const qss = reinterpret_cast<uint64_t*>(a.ws + kLay.qss) + (size_t)x * kBMax * kNSl;
-    uint64_t* const qkvx = reinterpret_cast<uint64_t*>(a.ws + kLay.qkvx) + (size_t)x * kBMax * 512;
     uint64_t* const atto = reinterpret_cast<uint64_t*>(a.ws + kLay.atto) + (size_t)x * kBMax * 256;
     uint64_t* const po = reinterpret_cast<uint64_t*>(a.ws + kLay.po);
     uint64_t* const ep = reinterpret_cast<uint64_t*>(a.ws + kLay.ep) + (size_t)x * kNSl * kBMax * 2 * IX;
@@ -475,38 +473,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 }
             }
             trace(l, 1);
-            // reduce rows [16r, +16) over the 8 slices: thread t < 256: row 16 r + t % 16, sequence t / 16
-            {
-                const int rl = tid & 15, bb = tid >> 4;
-                uint32_t scA = 0x3f800000u;
-                {
-                    const uint8_t* w; const float* sc;
-                    qkv_row(lw, sp, 16 * r + rl, w, sc);
-                    scA = ldg_bits(sc);
-                }
-                double s8 = 0.0;
-                if (tid < 256 && bb < B) {
-                    double v8[kNSl];
-                    wt.get_packed<kNSl>(&qp[(size_t)bb * 512 + 16 * r + rl], kBMax * 512, pb, v8);
-                    s8 = sum_tree(v8);
-                }
-                // RMSNorm scale: thread t < 128: sequence t / 8, slice t % 8
-                const int b2 = tid >> 3, s2 = tid & 7;
-                double qv = 0.0;
-                if (tid < 128 && b2 < B) {
-                    double v1[1];
-                    wt.get_packed<1>(&qss[b2 * kNSl + s2], 1, pb, v1);
-                    qv = v1[0];
-                }
-                qv = group_sum64<kNSl>(qv);
-                if (tid < 128 && s2 == 0 && b2 < B) rs[b2] = rms_scale(qv, H, kEps);
-                __syncthreads();
-                if (tid < 256 && bb < B) {
-                    const float y = (float)(s8 * rs[bb] * (double)after_wait_f(scA));
-                    ll_put_xcd(&qkvx[bb * 512 + 16 * r + rl], __float_as_uint(y), tag(l, BS_QKV));
-                    if (l == last && a.dbg_qkv != nullptr) a.dbg_qkv[((int64_t)bb * 8 + x) * 512 + 16 * r + rl] = y;
-                }
-            }
+            // every wave has read the digit rows and es (stage B / C write them next)
+            __syncthreads();
         }
 
         trace(l, 2);
@@ -519,9 +487,29 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 nw1 = ldg_bits(nw + lane + 64);
             }
             {
-                float v1[1];
-                wt.get_strided<1>(qkvx + r * 512 + tid, 0, tag(l, BS_QKV), v1);
-                att_in[tid] = v1[0];
+                // this sequence's 512 q|k|v rows straight from stage A's partials: thread t sums
+                // row t over the 8 K slices (written by all 32 ranks of the XCD), times the
+                // RMSNorm scale from the slices' sums of squares (lanes 0..7 of every wave) and
+                // the row scale
+                uint32_t scA;
+                {
+                    const uint8_t* w; const float* sc;
+                    qkv_row(lw, sp, tid, w, sc);
+                    scA = ldg_bits(sc);
+                }
+                double qv = 0.0;
+                if (lane < kNSl) {
+                    double v1[1];
+                    wt.get_packed<1>(&qss[r * kNSl + lane], 1, pb, v1);
+                    qv = v1[0];
+                }
+                qv = group_sum64<kNSl>(qv);
+                const double rsb = rms_scale(__shfl(qv, 0, kWave), H, kEps);
+                double v8[kNSl];
+                wt.get_packed<kNSl>(&qp[(size_t)r * 512 + tid], kBMax * 512, pb, v8);
+                const float y = (float)(sum_tree(v8) * rsb * (double)after_wait_f(scA));
+                att_in[tid] = y;
+                if (l == last && a.dbg_qkv != nullptr) a.dbg_qkv[((int64_t)r * 8 + x) * 512 + tid] = y;
             }
 #pragma unroll
             for (int i = 0; i < kPreU4; ++i) {
