@@ -137,7 +137,7 @@ def run_decode(args, mq, torch):
         if not args.no_kernel_events:
             dec.set_timing_events(starts[i], ends[i])
         dec.launch_step(tok)
-        tok = int(dec.output_token.item())
+        tok = dec.wait_token()
         toks.append(tok)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -319,7 +319,7 @@ def run_longctx(args, mq, torch):
         for i in range(steps):
             dec.set_timing_events(starts[i], ends[i])
             dec.launch_step(tok)
-            tok = int(dec.output_token.item())
+            tok = dec.wait_token()
             toks.append(tok)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
@@ -396,7 +396,7 @@ def run_batched(args, mq, torch):
         for i in range(steps):
             dec.set_timing_events(starts[i], ends[i])
             dec.launch_step(out)
-            out = dec.output_tokens.tolist()
+            out = dec.wait_tokens()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         dec.set_timing_events(None, None)

@@ -384,6 +384,14 @@ __device__ __forceinline__ uint4 ldg16(const void* p) {
     const u32x4_t v = *(const __attribute__((address_space(1))) u32x4_t*)p;
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+// The same with the non-temporal hint, for the layer weights: every step streams
+// them once (440 MB at the 0.6B shape, more than the 256 MB last-level cache), so
+// they should not displace what is reused from one step to the next there (the
+// LM-head matrix, 156 MB, read after every step's layers).
+__device__ __forceinline__ uint4 ldg16_stream(const void* p) {
+    const u32x4_t v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x4_t*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
 // Raw 32-bit load of a float / bf16 value for after_wait().
 __device__ __forceinline__ uint32_t ldg_bits(const float* p) { return *gview(reinterpret_cast<const uint32_t*>(p)); }
 __device__ __forceinline__ uint32_t ldg_bits(const uint16_t* p) { return *gview(p); }

@@ -100,7 +100,7 @@ struct Stage_ {
         for (int j = 0; j < IPW; ++j) {
             const int it = (wave - W0) + NWV * j;
             w[j] = make_uint4(0, 0, 0, 0);
-            if (it < ITEMS) w[j] = ldg16(rowptr(it / CH) + (it % CH) * 1024 + lane * 16);
+            if (it < ITEMS) w[j] = ldg16_stream(rowptr(it / CH) + (it % CH) * 1024 + lane * 16);
         }
     }
     __device__ __forceinline__ void compute(const double2* xd, double* part, int wave, int lane) const {

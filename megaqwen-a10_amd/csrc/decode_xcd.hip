@@ -263,7 +263,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         for (int k = 0; k < PPL_O; ++k) {
             const int pc = clr + LPR * k;
             wo[k] = make_uint4(0, 0, 0, 0);
-            if (pc < PC_O) wo[k] = ldg16(ob + (int64_t)(R0 + crow) * (16 * D) * ES + (int64_t)AD * x * ES + pc * 16);
+            if (pc < PC_O) wo[k] = ldg16_stream(ob + (int64_t)(R0 + crow) * (16 * D) * ES + (int64_t)AD * x * ES + pc * 16);
         }
         if (kInt8 && tid < RPW) so = ldg_bits(s_sp[ll].o_scale + R0 + tid);
         if constexpr (!kLateInputs) load_gains(lw);
@@ -501,7 +501,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 for (int k = 0; k < PPL_D; ++k) {
                     const int pc = clr + LPR * k;
                     wd[k] = make_uint4(0, 0, 0, 0);
-                    if (pc < PC_D) wd[k] = ldg16(db + (int64_t)(R0 + crow) * I * ES + (int64_t)IX * x * ES + pc * 16);
+                    if (pc < PC_D) wd[k] = ldg16_stream(db + (int64_t)(R0 + crow) * I * ES + (int64_t)IX * x * ES + pc * 16);
                 }
                 if (kInt8 && tid < RPW) sd = ldg_bits(sp.down_scale + R0 + tid);
             }

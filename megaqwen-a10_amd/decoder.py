@@ -176,7 +176,9 @@ class _DecoderBase:
         self.g_normalized = torch.zeros(H, **f32)
         self.block_max_vals = torch.zeros(LM_PARTIALS, **f32)
         self.block_max_idxs = torch.zeros(LM_PARTIALS, dtype=torch.int32, device=dev)
-        self.output_token = torch.zeros(1, dtype=torch.int32, device=dev)
+        # the kernel writes the token straight into pinned host memory: reading it back
+        # costs a stream synchronisation, not a device-to-host copy
+        self.output_token = torch.zeros(1, dtype=torch.int32, pin_memory=True)
 
         self._lib = _lib.load()
         self._dims = _lib.ModelDims(H, I, 16, 8, D, V)
@@ -229,15 +231,20 @@ class _DecoderBase:
         _lib.check(st, "decode step")
         self._pos += 1
 
-    def decode_step(self, input_token_id: int) -> int:
-        self.launch_step(input_token_id)
-        tok = int(self.output_token.item())
+    def wait_token(self) -> int:
+        """Wait for the last enqueued step and return its token."""
+        torch.cuda.current_stream(self.device).synchronize()
+        tok = int(self.output_token[0])
         if tok < 0:
             status = self._lib.mq_decode_check(self.workspace.data_ptr(),
                                                ctypes.c_void_p(_lib.stream_handle(self.device)))
             self._init_workspace()
             _lib.check(status if status != _lib.MQ_OK else _lib.MQ_ERR_TIMEOUT, "decode step")
         return tok
+
+    def decode_step(self, input_token_id: int) -> int:
+        self.launch_step(input_token_id)
+        return self.wait_token()
 
     def reset(self) -> None:
         self._pos = 0
@@ -378,7 +385,7 @@ class A10Int8BatchDecoder(_DecoderBase):
         D = 128
         self.k_cache = torch.zeros((batch, num_layers, 8, max_seq_len, D), dtype=torch.bfloat16, device=dev)
         self.v_cache = torch.zeros_like(self.k_cache)
-        self.output_tokens = torch.zeros(batch, dtype=torch.int32, device=dev)
+        self.output_tokens = torch.zeros(batch, dtype=torch.int32, pin_memory=True)   # written by the kernel
         self.hidden_buffer = torch.zeros((batch, H), dtype=torch.bfloat16, device=dev)
         f32 = dict(dtype=torch.float32, device=dev)
         self.qkv_buffer = torch.zeros((batch, 8, 512), **f32)
@@ -431,8 +438,9 @@ class A10Int8BatchDecoder(_DecoderBase):
         _lib.check(st, "batched decode step")
         self._positions = [p + 1 for p in self._positions]
 
-    def decode_step(self, tokens) -> list:
-        self.launch_step(tokens)
+    def wait_tokens(self) -> list:
+        """Wait for the last enqueued step and return its tokens."""
+        torch.cuda.current_stream(self.device).synchronize()
         out = self.output_tokens.tolist()
         if min(out) < 0:
             status = self._lib.mq_decode_check(self.workspace.data_ptr(),
@@ -440,6 +448,10 @@ class A10Int8BatchDecoder(_DecoderBase):
             self._init_workspace()
             _lib.check(status if status != _lib.MQ_OK else _lib.MQ_ERR_TIMEOUT, "batched decode step")
         return out
+
+    def decode_step(self, tokens) -> list:
+        self.launch_step(tokens)
+        return self.wait_tokens()
 
     def reset(self) -> None:
         self._positions = [0] * self.batch
