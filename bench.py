@@ -52,7 +52,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-steps", type=int, default=32, help="greedy steps of the CPU baseline sample")
+    ap.add_argument("--cpu-steps", type=int, default=112,
+                    help="greedy steps of the CPU baseline sample (about 10 s on 16 host threads)")
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "matvec", "positions", "longctx", "batched", "traffic"])
     ap.add_argument("--depths", default="1024,4096,8192", help="longctx: KV depths")
@@ -95,11 +96,51 @@ def cpu_baseline(keep, cfg, prompt, steps):
             "seconds": round(dt, 3), "tokens": toks}
 
 
+def _events(torch, n):
+    """n start/end pairs of timing events, created before any timed region."""
+    ev = ([torch.cuda.Event(enable_timing=True) for _ in range(n)],
+          [torch.cuda.Event(enable_timing=True) for _ in range(n)])
+    for e in ev[0] + ev[1]:
+        e.record()
+    torch.cuda.synchronize()
+    return ev
+
+
+def _timed_pass(torch, dec, first, steps, wait, events=None):
+    """`steps` greedy steps from `first` through launch_step + wait: (tokens, wall s, kernel ms).
+
+    With `events` every dispatch records its own start/end pair (hipExtLaunchKernel on the
+    launch stream), which costs about 20 us of host time per launch. So the pass that sets
+    a workload's tok/s runs without them, and a second pass over the same steps (same
+    positions, same tokens) measures the kernel."""
+    toks, tok = [], first
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        if events is not None:
+            dec.set_timing_events(events[0][i], events[1][i])
+        dec.launch_step(tok)
+        tok = wait()
+        toks.append(tok)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_ms = None
+    if events is not None:
+        dec.set_timing_events(None, None)
+        kern_ms = [a.elapsed_time(b) for a, b in zip(*events)]
+    return toks, wall, kern_ms
+
+
+KERNEL_TIMING = ("a second pass over the same steps (same positions and tokens), each dispatch recording "
+                 "its own start/end HIP events (hipExtLaunchKernel, launch stream); the pass that sets tok/s "
+                 "runs without them, since they add about 20 us of host time per launch")
+
+
 def run_decode(args, mq, torch):
     dev = torch.device("cuda:0")
     cfg = mq.QWEN3_0_6B
     state, prompt = mq.random_init_state(cfg, seed=args.seed)
-    S = PROMPT_LEN + max(args.steps, args.warmup) + 8
+    S = PROMPT_LEN + max(args.steps, args.warmup, 0 if args.no_cpu else args.cpu_steps) + 8
     cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
     qstate = mq.quantize_state(state, cfg, dev)
     del state
@@ -118,35 +159,18 @@ def run_decode(args, mq, torch):
     tok = prefill()
     for _ in range(args.warmup):
         tok = dec.decode_step(tok)
-    first = prefill()
-    torch.cuda.synchronize()
+    events = None if args.no_kernel_events else _events(torch, args.steps)
 
     # timed region: K greedy steps through the drop-in API
-    starts, ends = [], []
-    if not args.no_kernel_events:
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-        for e in starts + ends:
-            e.record()                 # create the HIP events before the timed region
-    toks = []
-    tok = first
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        # the dispatch itself records the pair at the kernel's start and end (hipExtLaunchKernel)
-        if not args.no_kernel_events:
-            dec.set_timing_events(starts[i], ends[i])
-        dec.launch_step(tok)
-        tok = dec.wait_token()
-        toks.append(tok)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    if not args.no_kernel_events:
-        dec.set_timing_events(None, None)
+    first = prefill()
+    toks, wall, _ = _timed_pass(torch, dec, first, args.steps, dec.wait_token)
+    repeat_identical = None
     if args.no_kernel_events:
         kern_ms = [wall * 1e3 / args.steps] * args.steps
     else:
-        kern_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+        first2 = prefill()
+        toks2, _, kern_ms = _timed_pass(torch, dec, first2, args.steps, dec.wait_token, events)
+        repeat_identical = first2 == first and toks2 == toks
     if min(toks) < 0:
         status = dec._lib.mq_decode_check(dec.workspace.data_ptr(), None)
         raise RuntimeError(f"decode step {toks.index(min(toks))} of the timed region failed: "
@@ -192,8 +216,8 @@ def run_decode(args, mq, torch):
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(kernel),
                      "kernel": kernel,
                      "kernel_avg_us": round(sum(kern_ms) / len(kern_ms) * 1e3, 2),
-                     "timing": "wall per step" if args.no_kernel_events else
-                               "HIP events recorded by the dispatch itself (hipExtLaunchKernel), launch stream",
+                     "timing": "wall per step" if args.no_kernel_events else KERNEL_TIMING,
+                     "kernel_pass_tokens_identical": repeat_identical,
                      "bytes_per_launch_avg": int(bytes_total / args.steps)},
         "device_tok_s": round(args.steps / kern_s, 1),
         "parity": parity,
@@ -301,10 +325,7 @@ def run_longctx(args, mq, torch):
     dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
     dec.set_attn_split(args.split_min)
     first = int(prompt[-1])
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    for e in starts + ends:
-        e.record()
+    events = _events(torch, steps)
     per_depth = {}
     for depth in depths:
         dec.prefill_random_kv(depth, seed=args.seed)
@@ -312,21 +333,11 @@ def run_longctx(args, mq, torch):
         for _ in range(args.warmup):
             tok = dec.decode_step(tok)
         dec.prefill_random_kv(depth, seed=args.seed)
-        torch.cuda.synchronize()
-        tok = first
-        toks = []
-        t0 = time.perf_counter()
-        for i in range(steps):
-            dec.set_timing_events(starts[i], ends[i])
-            dec.launch_step(tok)
-            tok = dec.wait_token()
-            toks.append(tok)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        dec.set_timing_events(None, None)
+        toks, wall, _ = _timed_pass(torch, dec, first, steps, dec.wait_token)
         if min(toks) < 0:
             raise RuntimeError(f"a timed decode step at depth {depth} failed: {mq._lib.last_error()}")
-        kern_ms = [a.elapsed_time(b) for a, b in zip(starts, ends)]
+        dec.prefill_random_kv(depth, seed=args.seed)
+        toks2, _, kern_ms = _timed_pass(torch, dec, first, steps, dec.wait_token, events)
         bytes_total = sum(cfg.int8_step_bytes(cache_len=depth + i + 1) for i in range(steps))
         achieved = bytes_total / (sum(kern_ms) / 1e3) / 1e9
         roof_tok_s = steps / (bytes_total / (HBM_PEAK_GBS * 1e9))
@@ -334,7 +345,7 @@ def run_longctx(args, mq, torch):
             "tok_s": round(steps / wall, 1), "kernel_avg_us": round(sum(kern_ms) / steps * 1e3, 2),
             "device_tok_s": round(steps / (sum(kern_ms) / 1e3), 1), "achieved_GBs": round(achieved, 1),
             "frac": round(achieved / HBM_PEAK_GBS, 4), "roofline_tok_s": round(roof_tok_s, 1),
-            "bytes_per_launch_avg": int(bytes_total / steps)}
+            "bytes_per_launch_avg": int(bytes_total / steps), "kernel_pass_tokens_identical": toks2 == toks}
         print(f"depth {depth}: {per_depth[str(depth)]}", file=sys.stderr, flush=True)
     top = per_depth[str(max(depths))]
     variant = mq.decode_variant(cfg.hidden_size, cfg.intermediate_size, int8=True)
@@ -348,7 +359,7 @@ def run_longctx(args, mq, torch):
                        "attn_split_min": args.split_min or "library default", "per_depth": per_depth},
             "roofline": {"bound": "hbm", "achieved": top["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": top["frac"], "traffic": None, "kernel_avg_us": top["kernel_avg_us"],
-                         "timing": "HIP events recorded by the dispatch itself (hipExtLaunchKernel), launch stream"}}
+                         "timing": KERNEL_TIMING}}
 
 
 def run_batched(args, mq, torch):
@@ -371,10 +382,7 @@ def run_batched(args, mq, torch):
     # useful int8 multiply-adds per sequence and step: every projection and the LM head once
     H, I, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_layers
     macs = L * (H * (cfg.q_size + 2 * cfg.kv_size) + cfg.q_size * H + 3 * H * I) + V * H
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    for e in starts + ends:
-        e.record()
+    events = _events(torch, steps)
     per_batch = {}
     for B in batches:
         prompts = prompts_all[:B]
@@ -390,19 +398,14 @@ def run_batched(args, mq, torch):
         out = prefill()
         for _ in range(args.warmup):
             out = dec.decode_step(out)
-        out = prefill()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for i in range(steps):
-            dec.set_timing_events(starts[i], ends[i])
-            dec.launch_step(out)
-            out = dec.wait_tokens()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        dec.set_timing_events(None, None)
+        first = prefill()
+        toks, wall, _ = _timed_pass(torch, dec, first, steps, dec.wait_tokens)
+        out = toks[-1]
+        first2 = prefill()
+        toks2, _, kern_ms = _timed_pass(torch, dec, first2, steps, dec.wait_tokens, events)
         if min(out) < 0:
             raise RuntimeError(f"a timed batched step (B={B}) failed: {mq._lib.last_error()}")
-        kern_s = sum(a.elapsed_time(b) for a, b in zip(starts, ends)) / 1e3
+        kern_s = sum(kern_ms) / 1e3
         kv_bytes = sum(B * L * 2 * cfg.num_kv_heads * cfg.head_dim * 2 * (PROMPT_LEN + i + 1) for i in range(steps))
         achieved = (steps * weight_bytes + kv_bytes) / kern_s / 1e9
         mfma_tops = 2.0 * macs * B * steps / kern_s / 1e12
@@ -411,7 +414,8 @@ def run_batched(args, mq, torch):
             "device_tok_s": round(B * steps / kern_s, 1), "achieved_GBs": round(achieved, 1),
             "hbm_frac": round(achieved / HBM_PEAK_GBS, 4),
             "roofline_tok_s": round(B * HBM_PEAK_GBS * 1e9 / (weight_bytes + kv_bytes / steps / 1.0), 1),
-            "useful_int8_TOPs": round(mfma_tops, 2), "mfma_util": round(mfma_tops / INT8_PEAK_TOPS, 5)}
+            "useful_int8_TOPs": round(mfma_tops, 2), "mfma_util": round(mfma_tops / INT8_PEAK_TOPS, 5),
+            "kernel_pass_tokens_identical": first2 == first and toks2 == toks}
         print(f"batch {B}: {per_batch[str(B)]}", file=sys.stderr, flush=True)
         del dec
         torch.cuda.empty_cache()
@@ -427,7 +431,7 @@ def run_batched(args, mq, torch):
             "roofline": {"bound": "hbm", "achieved": top["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": top["hbm_frac"], "traffic": None, "kernel_avg_us": top["kernel_avg_us"],
                          "mfma_util": top["mfma_util"],
-                         "timing": "HIP events recorded by the dispatch itself (hipExtLaunchKernel), launch stream"}}
+                         "timing": KERNEL_TIMING}}
 
 
 def run_traffic(args, mq, torch):
