@@ -43,7 +43,7 @@ PROMPT_LEN = 8
 # Memory traffic per decode launch of this kernel, measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE runs of megaqwen-a10_amd/profile_decode.py, each scaled by the counter's reading for a
 # 256 MiB copy (the commands and numbers are in profiles/decode_xcd_kernel_int8_qwen3-0.6b_traffic.txt).
-MEASURED_TRAFFIC = {"mq::decode_xcd_kernel<1024, 3072, mq::Int8W, false>": 638_600_000}
+MEASURED_TRAFFIC = {"mq::decode_xcd_kernel<1024, 3072, mq::Int8W, false>": 639_234_240}
 
 
 def parse():
