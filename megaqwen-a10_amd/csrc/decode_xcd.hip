@@ -121,7 +121,13 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     __shared__ uint32_t mrg[kGS * 19];      // split attention: the 32 partials of this rank's 8 dims
     // split slices staged in LDS: up to 320 positions (context 10240) at H = 1024,
     // 256 (context 8192) at H = 2048, whose other buffers leave less LDS
-    constexpr int kSlice = H <= 1024 ? 320 : 256;
+    // Split-slice capacity of the register/DMA path (sdma below). The bf16 instantiation
+    // has no registers to spare for a slice's V words (they were spilled right after
+    // loading, turning the prefetch into a wait), so it has no such path: its slices come
+    // from the rows prefetched a layer ahead up to kKvLds positions, and from the cache
+    // inside the loop beyond that.
+    constexpr bool kSliceRegs = kInt8;
+    constexpr int kSlice = !kSliceRegs ? kKvLds : H <= 1024 ? 320 : 256;
     __shared__ __align__(16) AttnShared<kSlice> at;
     __shared__ float lm_v[kWaves];
     __shared__ int lm_i[kWaves];
@@ -202,7 +208,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     // K rows go straight to LDS and the V words to registers ahead of the QKV
     // wait (sdma); longer slices read the cache inside the loop
     const bool spre = split && cs <= kKvLds;
-    const bool sdma = split && !spre && cs <= kSlice;
+    const bool sdma = kSliceRegs && split && !spre && cs <= kSlice;
     // the range's first npre earlier positions prefetched into registers, staged
     // in LDS (the current one comes from the QKV words)
     const int npre = sdma ? 0 : max(0, min(kKvLds, min(sj1, a.pos) - sj0));

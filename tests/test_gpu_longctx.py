@@ -129,6 +129,39 @@ def _check_long(mq, dev, dec, ref, prompt, depth, split_min):
     torch.cuda.empty_cache()
 
 
+def test_bf16_split_tokens_match_fixture(xcd, mq, dev):
+    """bf16 weights with the split forced on every step (slices of at most two positions, taken
+    from the rows prefetched a layer ahead): the 32 tokens of the bf16 fixture."""
+    dec, d, prompt, cfg, keep = _build(mq, dev, "qwen3_0.6b_bf16")
+    dec.set_attn_split(1)
+    try:
+        print("qwen3_0.6b_bf16 32 steps, split from 1", flush=True)
+        assert _greedy(dec, prompt, 32) == d["tokens"]
+    finally:
+        dec.set_attn_split(0)
+    del dec, keep
+    torch.cuda.empty_cache()
+
+
+def test_bf16_long_context_matches_oracle(xcd, mq, dev):
+    """bf16 weights at depth 4100: split slices of 129 positions, more than the 64 rows prefetched a
+    layer ahead, so the bf16 kernel reads them from the cache inside the loop (it has no register
+    slice path); 6 greedy steps against the float64 oracle started from the same cache."""
+    depth = 4100
+    cfg = mq.QWEN3_0_6B.with_(num_layers=2, vocab_size=4096)
+    state, prompt = mq.random_init_state(cfg, seed=3, norm_jitter=0.1)
+    embed, layers, fnorm, lm = mq.pack_bf16(state, cfg, dev)
+    S = depth + 16
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    dec = mq.A10MegakernelDecoder(embed, layers, fnorm, lm, cos, sin, cfg.num_layers, S)
+    c = lambda t: t.cpu()
+    ref = RefDecoder(Dims(hidden_size=cfg.hidden_size, intermediate_size=cfg.intermediate_size,
+                          vocab_size=cfg.vocab_size), c(embed), [c(t) for t in layers], None, c(fnorm), c(lm), None,
+                     c(cos), c(sin), cfg.num_layers, S)
+    print(f"bf16 long context depth {depth}", flush=True)
+    _check_long(mq, dev, dec, ref, prompt.tolist(), depth, 0)
+
+
 def test_full_model_long_context_matches_oracle(xcd, mq, dev):
     """Qwen3-0.6B shape (28 layers, full vocabulary) at depth 4096: 4 greedy steps
     against the live float64 oracle from the same pre-filled cache."""
