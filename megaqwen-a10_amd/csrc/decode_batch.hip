@@ -561,8 +561,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 }
             }
             if (b < B && (tid & 31) == 0) es[b] = e;
-            // the next stages' inputs of the attention rank (its layer l + 1 rows)
-            if (l < last) prefetch_attn(l + 1);
             __syncthreads();
             const int nt = wave >> 1;
             i32x4_t cm[4];
@@ -770,10 +768,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                     }
                 }
             }
-            // the next layer's stage A weights, behind the stores
+            // the next layer's stage A weights and, on an attention rank, its first K/V rows,
+            // behind the stores
             if (l < last) {
                 issue_fence();
                 load_a(l + 1);
+                prefetch_attn(l + 1);
                 issue_fence();
             }
         }
