@@ -199,7 +199,7 @@ __device__ __forceinline__ void attn_finish(AS& at, double a00, double a01, doub
 // l = sum_j e^(s_j - m_h). An empty range gives acc = l = 0, m = -inf.
 // Returns without a barrier. mark(k) is called after sub-stage k (0 scores,
 // 1 and 2 softmax with P @ V) for timing instrumentation.
-template <class AS, class Emit, class Mark>
+template <bool kBatchTail = false, class AS, class Emit, class Mark>
 __device__ __forceinline__ void attn_partial(AS& at, const uint16_t* kh, const uint16_t* vh, int j0, int j1,
                                              int pos, double scale, int tid, int lane, int wave, Emit emit, Mark mark) {
     const int n = j1 - j0;
@@ -242,7 +242,23 @@ __device__ __forceinline__ void attn_partial(AS& at, const uint16_t* kh, const u
                 l0 += q0;
                 l1 += q1;
             };
-            for (int t = 0; t < T; ++t) accum(vword(t), t);
+            if constexpr (kBatchTail) {
+                // positions past the kKvLds prefetched rows read their V word from memory: that
+                // tail is loaded eight words at a time before use, one round trip per eight
+                // positions instead of one per position (same accumulation order)
+                const int T_lds = min(T, max(0, (kKvLds - c0 + kWaves - 1) / kWaves));
+                for (int t = 0; t < T_lds; ++t) accum(vword(t), t);
+                for (int t0 = T_lds; t0 < T; t0 += 8) {
+                    uint32_t vw[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) vw[u] = t0 + u < T ? vword(t0 + u) : 0u;
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        if (t0 + u < T) accum(vw[u], t0 + u);
+                }
+            } else {
+                for (int t = 0; t < T; ++t) accum(vword(t), t);
+            }
         }
         attn_finish(at, a00, a01, a10, a11, l0, l1, M0, M1, tid, lane, wave, emit, mark);
     }
@@ -424,10 +440,10 @@ __device__ __forceinline__ void attn_partial_lds(AS& at, int j0, int j1, int pos
 // Attention output of both query heads over positions [0, n) in one workgroup:
 // calls emit(i, value) with the fp32 output element i = h * 128 + dim on
 // threads tid < 256, then returns without a barrier.
-template <class AS, class Emit, class Mark>
+template <bool kBatchTail = false, class AS, class Emit, class Mark>
 __device__ __forceinline__ void attn_core(AS& at, const uint16_t* kh, const uint16_t* vh, int n, int pos,
                                           double scale, int tid, int lane, int wave, Emit emit, Mark mark) {
-    attn_partial(at, kh, vh, 0, n, pos, scale, tid, lane, wave,
+    attn_partial<kBatchTail>(at, kh, vh, 0, n, pos, scale, tid, lane, wave,
                  [&](int i, double acc, double l, double) { emit(i, (float)(acc * rcp_nr(l))); }, mark);
 }
 

@@ -525,7 +525,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             attn_qk_rope(at, att_in, nw0, nw1, rope_s[0][lane], rope_s[1][lane], rope_s[0][lane + 64],
                          rope_s[1][lane + 64], a.kc + cur, a.vc + cur, nullptr, nullptr, nullptr, wave, lane);
             __syncthreads();
-            attn_core(at, a.kc + cache_base, a.vc + cache_base, apos + 1, apos, (double)a.attn_scale, tid, lane,
+            // the batched path attends over up to 1024 positions, most of them read from memory
+            attn_core<true>(at, a.kc + cache_base, a.vc + cache_base, apos + 1, apos, (double)a.attn_scale, tid, lane,
                       wave, [&](int i, float v) {
                           ll_put_xcd(&atto[r * 256 + i], __float_as_uint(v), tag(l, BS_ATT));
                           if (l == last && a.dbg_attn != nullptr) a.dbg_attn[(int64_t)r * 2048 + 256 * x + i] = v;
