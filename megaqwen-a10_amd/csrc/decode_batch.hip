@@ -453,7 +453,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             const double ss = slice_digits(hv, win8);
             if (b < B && (tid & 31) == 0 && rg == 0) ll_put64(&qss[b * kNSl + sl], pack_tagged(ss, pb));
             __syncthreads();
-            // stage C's weights (consumed after the attention exchange)
+            // stage C's weights (consumed after the attention exchange; issued behind this
+            // stage's stores they arrive too late)
             load_c(l);
             issue_fence();
             {
@@ -666,10 +667,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                     }
                 }
             }
-            // stage F's weights, behind the stores
-            issue_fence();
-            load_f(l);
-            issue_fence();
             trace(l, 6);
             // reduce channels [24r, +24) (gate rows 24 r + c, up rows IX + 24 r + c) over the 8 slices
             const uint32_t gsc = ldg_bits(sp.gate_scale + IX * x + 24 * r + tid % 24);
@@ -705,6 +702,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 ll_put_xcd(&mlpx[bb * IX + 24 * r + c], __float_as_uint(m), tag(l, BS_MLP));
                 if (l == last && a.dbg_mlp != nullptr) a.dbg_mlp[(int64_t)bb * I + IX * x + 24 * r + c] = m;
             }
+            // stage F's weights, behind this stage's stores (its K-slice reduction polls
+            // must not queue behind them)
+            issue_fence();
+            load_f(l);
+            issue_fence();
         }
 
         trace(l, 7);
