@@ -216,6 +216,14 @@ int mq_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t strea
 int mq_int8_decode_step(const mq_decode_args* args, hipStream_t stream);
 /* Same with bf16 weights (scales and lm_head_scale ignored). Replaces launch_a10_decode. */
 int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream);
+/* Host-side wait for a token the kernel stores into host memory (pinned, e.g.
+ * hipHostMalloc): spins until *token differs from `sentinel`, which the
+ * caller wrote before the launch. MQ_OK, or MQ_ERR_TIMEOUT after timeout_us
+ * microseconds (then synchronise the stream and call mq_decode_check). The
+ * kernel stores the token last, so this returns as the step ends, without the
+ * stream synchronisation's wake-up. No counterpart in the reference, which
+ * copies the token back with .item(). */
+int mq_wait_host_token(const volatile int* token, int sentinel, unsigned int timeout_us);
 /* After a completed step: MQ_ERR_TIMEOUT if a bounded wait of that step expired, else MQ_OK.
  * Synchronises `stream`. */
 int mq_decode_check(void* workspace, hipStream_t stream);

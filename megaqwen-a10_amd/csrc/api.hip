@@ -3,6 +3,7 @@
 // workspaces behind the reference-signature launchers, and workspace reset.
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -156,6 +157,18 @@ int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream) {
     int st = validate_decode(args, false, &s);
     if (st != MQ_OK) return st;
     return launch_decode(*args, s, false, stream);
+}
+
+int mq_wait_host_token(const volatile int* token, int sentinel, unsigned int timeout_us) {
+    clear_error();
+    if (!token) return set_error(MQ_ERR_INVALID_ARGUMENT, "token is NULL");
+    const auto t0 = std::chrono::steady_clock::now();
+    for (unsigned int n = 0;; ++n) {
+        if (*token != sentinel) return MQ_OK;
+        if ((n & 1023u) == 1023u &&
+            std::chrono::steady_clock::now() - t0 > std::chrono::microseconds(timeout_us))
+            return set_error(MQ_ERR_TIMEOUT, "no token after %u us", timeout_us);
+    }
 }
 
 int mq_decode_check(void* workspace, hipStream_t stream) {

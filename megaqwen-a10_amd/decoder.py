@@ -29,6 +29,9 @@ from .config import QWEN3_0_6B, ModelConfig
 from .rope import precompute_rope_freqs
 from .weights import pack_bf16, pack_int8, quantize_state, random_init_state
 
+TOKEN_PENDING = -2          # written into the pinned token word before a launch; kernels store >= -1
+WAIT_US = 2_000_000         # host spin on the token before falling back to a stream synchronisation
+
 LM_PARTIALS = 256   # per-workgroup LM-head maxima written to block_max_vals/idxs
 
 VARIANTS = {"auto": 0, "flat": 1, "xcd": 2}
@@ -176,9 +179,10 @@ class _DecoderBase:
         self.g_normalized = torch.zeros(H, **f32)
         self.block_max_vals = torch.zeros(LM_PARTIALS, **f32)
         self.block_max_idxs = torch.zeros(LM_PARTIALS, dtype=torch.int32, device=dev)
-        # the kernel writes the token straight into pinned host memory: reading it back
-        # costs a stream synchronisation, not a device-to-host copy
+        # the kernel writes the token straight into pinned host memory: the host spins on
+        # it (no device-to-host copy, no stream-synchronisation wake-up)
         self.output_token = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self._tok_host = self.output_token.numpy()
 
         self._lib = _lib.load()
         self._dims = _lib.ModelDims(H, I, 16, 8, D, V)
@@ -227,15 +231,20 @@ class _DecoderBase:
         a.input_token_id = input_token_id
         a.position = self._pos
         a.cache_len = self._pos + 1
+        self._tok_host[0] = TOKEN_PENDING
         st = self._step_fn(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(self.device)))
         _lib.check(st, "decode step")
         self._pos += 1
 
     def wait_token(self) -> int:
-        """Wait for the last enqueued step and return its token."""
-        torch.cuda.current_stream(self.device).synchronize()
-        tok = int(self.output_token[0])
+        """Wait for the last enqueued step and return its token. Spins on the pinned word the
+        kernel stores last; falls back to a stream synchronisation (which reports errors) if
+        no token arrives within WAIT_US or the step reports a failure (-1)."""
+        if self._lib.mq_wait_host_token(self._tok_host.ctypes.data, TOKEN_PENDING, WAIT_US) != _lib.MQ_OK:
+            torch.cuda.current_stream(self.device).synchronize()
+        tok = int(self._tok_host[0])
         if tok < 0:
+            torch.cuda.current_stream(self.device).synchronize()
             status = self._lib.mq_decode_check(self.workspace.data_ptr(),
                                                ctypes.c_void_p(_lib.stream_handle(self.device)))
             self._init_workspace()
