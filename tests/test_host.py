@@ -186,3 +186,19 @@ def test_random_init_is_deterministic(mq):
     w = s1["model.layers.0.self_attn.q_proj.weight"]
     assert w.dtype == torch.bfloat16 and tuple(w.shape) == (2048, 1024)
     assert abs(float(w.float().std()) - 0.02) < 1e-3
+
+
+def test_wait_host_token(mq):
+    """mq_wait_host_token returns as soon as the word differs from the sentinel, and reports a
+    timeout (without touching the word) when it never does."""
+    import time
+    from megaqwen_a10_amd import _lib
+    lib = _lib.load()
+    word = ctypes.c_int(7)
+    assert lib.mq_wait_host_token(ctypes.byref(word), -2, 1000) == _lib.MQ_OK
+    word.value = -2
+    t0 = time.perf_counter()
+    assert lib.mq_wait_host_token(ctypes.byref(word), -2, 20_000) == _lib.MQ_ERR_TIMEOUT
+    assert time.perf_counter() - t0 >= 0.019
+    assert "no token" in _lib.last_error() and word.value == -2
+    assert lib.mq_wait_host_token(None, -2, 10) == _lib.MQ_ERR_INVALID_ARGUMENT
