@@ -281,18 +281,21 @@ struct SliceRegs {
 // K rows of positions [j0, jend) (jend <= the current position, whose row
 // comes from at.kv_cur) into at.kst[j - j0], the 16-byte chunks of row r
 // permuted (chunk g at g ^ (r % 16), see kst_chunk) so that 16 rows read at the
-// same head dims hit 16 different bank groups. Asynchronous: wait for the loads
-// (vmcnt) and barrier before reading them.
-template <class AS>
+// same head dims hit 16 different bank groups, issued by NW waves (wave < NW).
+// Asynchronous: wait for the loads (vmcnt) and barrier before reading them.
+template <int NW = kWaves, class AS>
 __device__ __forceinline__ void attn_slice_k(AS& at, const uint16_t* kh, int j0, int jend, int lane, int wave) {
-    constexpr int PW = AS::kNR / (4 * kWaves);     // instructions per wave
-    static_assert(AS::kNR % (4 * kWaves) == 0, "whole instructions per wave");
+    constexpr int PW = AS::kNR / (4 * NW);         // instructions per wave
+    static_assert(AS::kNR % (4 * NW) == 0, "whole instructions per wave");
     // wave w moves rows [4 PW w, 4 PW (w + 1)): 4 rows (1 KB) per instruction;
     // each lane's 16 bytes land at the instruction's base + 16 l, i.e. LDS chunk
-    // l % 16 of row 4c + l / 16, so lane l fetches the row's chunk (l % 16) ^ r
+    // l % 16 of row 4c + l / 16, so lane l fetches the row's chunk (l % 16) ^ r.
+    // z (zero, hidden from the optimiser) keeps the per-instruction addresses
+    // from being hoisted out of a caller's loop and held in (spilled) registers.
+    const int z = opaque(0);
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
-        const int c = wave * PW + i;
+        const int c = wave * PW + i + z;
         const int r = 4 * c + lane / 16;
         const int j = j0 + r;
         if (4 * c < jend - j0 && j < jend)
@@ -315,6 +318,28 @@ __device__ __forceinline__ void attn_slice_v(SliceRegs<NR>& sr, const uint16_t* 
         sr.v[t] = *gview(base + (int64_t)j * (kHD / 2));
     }
     issue_fence();      // all loads issued here, not sunk to their uses
+}
+
+// V rows of positions [j0, jend) (jend <= the current position) into vs[j - j0],
+// straight from HBM as attn_slice_k does for K, by NW waves (no chunk
+// permutation: the P @ V loop reads one 4-byte word per lane of a row).
+// Asynchronous, as attn_slice_k.
+template <int NR, int NW = kWaves>
+__device__ __forceinline__ void attn_slice_v_lds(uint32_t (*vs)[kHD / 2], const uint16_t* vh, int j0, int jend,
+                                                 int lane, int wave) {
+    constexpr int PW = NR / (4 * NW);
+    static_assert(NR % (4 * NW) == 0, "whole instructions per wave");
+    const int z = opaque(0);            // as in attn_slice_k
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+        const int c = wave * PW + i + z;
+        const int j = j0 + 4 * c + lane / 16;
+        if (4 * c < jend - j0 && j < jend)
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1)))*)(vh + (int64_t)j * kHD + (lane % 16) * 8),
+                (void __attribute__((address_space(3)))*)(&vs[4 * c][0]), 16, 0, 0);
+    }
+    issue_fence();
 }
 
 // Waits for this wave's outstanding vector memory operations (the LDS-direct
@@ -435,6 +460,20 @@ __device__ __forceinline__ void attn_partial_lds(AS& at, int j0, int j1, int pos
     mark(0);
     attn_softmax_pv<kKvLds / kWaves>(at, [&](int t) { return at.kv_pre[1][wave + kWaves * t][lane]; }, j0, j1 - j0,
                                      pos, tid, lane, wave, emit, mark);
+}
+
+// attn_partial for a range [j0, j1) of at most NR positions whose K rows are in
+// at.kst (attn_slice_k) and V rows in vs (attn_slice_v_lds), waited for with a
+// barrier: scores on the matrix cores, softmax and P @ V in fp64.
+template <class AS, int NR, class Emit, class Mark>
+__device__ __forceinline__ void attn_partial_lds_v(AS& at, const uint32_t (*vs)[kHD / 2], int j0, int j1, int pos,
+                                                   double scale, int tid, int lane, int wave, Emit emit, Mark mark) {
+    static_assert(NR <= AS::kNR && NR % 16 == 0, "slice capacity");
+    attn_scores_mfma(at, j0, j1, pos, scale, lane, wave);
+    __syncthreads();
+    mark(0);
+    attn_softmax_pv<NR / kWaves>(at, [&](int t) { return vs[wave + kWaves * t][lane]; }, j0, j1 - j0, pos, tid,
+                                 lane, wave, emit, mark);
 }
 
 // Attention output of both query heads over positions [0, n) in one workgroup:

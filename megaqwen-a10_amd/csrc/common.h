@@ -478,9 +478,15 @@ struct Waiter {
     // each equals `pbit` and returns the fp64 values with that bit cleared.
     template <int N>
     __device__ __forceinline__ void get_packed(const uint64_t* p, int stride, uint32_t pbit, double (&out)[N]) {
+        get_packed_at<N>([&](int i) { return p + i * stride; }, pbit, out);
+    }
+
+    // As get_packed, for the N packed words at addr(0) .. addr(N - 1).
+    template <int N, class Addr>
+    __device__ __forceinline__ void get_packed_at(Addr addr, uint32_t pbit, double (&out)[N]) {
         uint64_t w[N];
 #pragma unroll
-        for (int i = 0; i < N; ++i) w[i] = ll_load(p + i * stride);
+        for (int i = 0; i < N; ++i) w[i] = ll_load(addr(i));
         uint32_t pending = 0;
 #pragma unroll
         for (int i = 0; i < N; ++i)
@@ -490,7 +496,7 @@ struct Waiter {
             __builtin_amdgcn_s_sleep(1);
 #pragma unroll
             for (int i = 0; i < N; ++i)
-                if (pending & (1u << i)) w[i] = ll_load(p + i * stride);
+                if (pending & (1u << i)) w[i] = ll_load(addr(i));
 #pragma unroll
             for (int i = 0; i < N; ++i)
                 if ((pending & (1u << i)) && (uint32_t)(w[i] & 1u) == pbit) pending &= ~(1u << i);

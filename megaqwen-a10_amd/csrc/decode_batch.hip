@@ -49,6 +49,7 @@ constexpr int kBX = 8;                  // XCDs
 constexpr int kBG = kNWG / kBX;         // ranks per XCD
 constexpr int kSl = 64;                 // hidden elements per rank
 constexpr int kD = 128;                 // head dim
+constexpr int kSliceB = 128;            // longest sequence whose K/V rows stage B loads straight into LDS
 constexpr int kLmTiles = 5;             // LM-head 16-row tiles per wave
 constexpr int kLmRowsPerWG = 16 * kLmTiles * kWaves;
 
@@ -231,6 +232,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     __shared__ float lm_v[kWaves][kBMax];
     __shared__ int lm_i[kWaves][kBMax];
     __shared__ uint32_t rope_s[2][kD];        // attention rank: cos / sin row of its position (bf16 bits)
+    __shared__ __align__(16) uint32_t vsl[kSliceB][kD / 2];   // attention rank, short sequences: V rows
     constexpr size_t kBigF = (size_t)64 * KPF + (size_t)4 * 4 * 64 * 16;          // F digits + pair partials
     constexpr size_t kBigLM = (size_t)8 * 64 * 64;                                  // 8 k-steps of LM digits
     constexpr size_t kBig0 = sizeof(AttnShared<128>) > kBigF ? sizeof(AttnShared<128>) : kBigF;
@@ -306,13 +308,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     // in stage B with the query gather
     const bool attn = r < B;
     const int apos = attn ? a.pos[r] : 0;
+    // a sequence of at most kSliceB positions has all its earlier K and V rows loaded straight into
+    // LDS at the start of stage B (at.kst, vsl) and its scores taken on the matrix cores; a longer
+    // one uses the rows prefetched a layer ahead and reads the rest inside the attention loops
+    const bool sliced = attn && apos < kSliceB;
     if (attn && tid < 2 * kD) {
         const uint16_t* row = (tid < kD ? a.cos_t : a.sin_t) + (int64_t)apos * kD;
         rope_s[tid / kD][tid % kD] = ldg_bits(row + tid % kD);
     }
     constexpr int kPreU4 = 2 * kKvLds * (kD / 8) / kThreads;
     uint4 pre[kPreU4];
-    const int npre = attn ? min(apos, kKvLds) : 0;
+    const int npre = (attn && !sliced) ? min(apos, kKvLds) : 0;
     auto prefetch_attn = [&](int ll) {
         if (!attn) return;
         const int64_t cb = (int64_t)r * seq_stride + ((int64_t)ll * 8 + x) * head_stride;
@@ -481,22 +487,36 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
         trace(l, 2);
         // ---------------- B: attention of sequence r (ranks r < B) ----------------
         if (attn) {
+            const int64_t cache_base = (int64_t)r * seq_stride + ((int64_t)l * 8 + x) * head_stride;
+            // a short sequence: waves 4-7 load its earlier K and V rows straight into LDS
+            // while waves 0-3 gather the q|k|v rows (loads return in order per wave, so the
+            // gathering waves' polls do not wait for these loads; stage A's last barrier
+            // ordered every read of the LDS they overwrite)
+            const bool loader = sliced && __builtin_amdgcn_readfirstlane(wave) >= 4;   // wave-uniform branch
             uint32_t nw0 = 0, nw1 = 0;
-            if (wave < 3) {
-                const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
-                nw0 = ldg_bits(nw + lane);
-                nw1 = ldg_bits(nw + lane + 64);
-            }
-            {
-                // this sequence's 512 q|k|v rows straight from stage A's partials: thread t sums
-                // row t over the 8 K slices (written by all 32 ranks of the XCD), times the
+            if (loader) {
+                const int ln = opaque(lane);    // per-lane offsets are recomputed, not held across layers
+                attn_slice_k<4>(at, a.kc + cache_base, 0, apos, ln, wave - 4);
+                attn_slice_v_lds<kSliceB, 4>(vsl, a.vc + cache_base, 0, apos, ln, wave - 4);
+                wait_vmem();                    // the rows are in LDS after the barrier below
+            } else {
+                if (wave < 3) {
+                    const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
+                    nw0 = ldg_bits(nw + lane);
+                    nw1 = ldg_bits(nw + lane + 64);
+                }
+                // this sequence's 512 q|k|v rows straight from stage A's partials: a thread sums
+                // row m over the 8 K slices (written by all 32 ranks of the XCD), times the
                 // RMSNorm scale from the slices' sums of squares (lanes 0..7 of every wave) and
-                // the row scale
-                uint32_t scA;
-                {
+                // the row scale; rows tid and, with 4 gathering waves, tid + 256
+                const int nr = sliced ? 2 : 1;
+                uint32_t scA[2] = {0x3f800000u, 0x3f800000u};
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    if (k >= nr) break;
                     const uint8_t* w; const float* sc;
-                    qkv_row(lw, sp, tid, w, sc);
-                    scA = ldg_bits(sc);
+                    qkv_row(lw, sp, tid + 256 * k, w, sc);
+                    scA[k] = ldg_bits(sc);
                 }
                 double qv = 0.0;
                 if (lane < kNSl) {
@@ -506,11 +526,15 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 }
                 qv = group_sum64<kNSl>(qv);
                 const double rsb = rms_scale(__shfl(qv, 0, kWave), H, kEps);
-                double v8[kNSl];
-                wt.get_packed<kNSl>(&qp[(size_t)r * 512 + tid], kBMax * 512, pb, v8);
-                const float y = (float)(sum_tree(v8) * rsb * (double)after_wait_f(scA));
-                att_in[tid] = y;
-                if (l == last && a.dbg_qkv != nullptr) a.dbg_qkv[((int64_t)r * 8 + x) * 512 + tid] = y;
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    if (k >= nr) break;
+                    double v8[kNSl];
+                    wt.get_packed<kNSl>(&qp[(size_t)r * 512 + tid + 256 * k], kBMax * 512, pb, v8);
+                    const float y = (float)(sum_tree(v8) * rsb * (double)after_wait_f(scA[k]));
+                    att_in[tid + 256 * k] = y;
+                    if (l == last && a.dbg_qkv != nullptr) a.dbg_qkv[((int64_t)r * 8 + x) * 512 + tid + 256 * k] = y;
+                }
             }
 #pragma unroll
             for (int i = 0; i < kPreU4; ++i) {
@@ -521,18 +545,23 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 if (j < npre) *reinterpret_cast<uint4*>(&at.kv_pre[side][j][c * 4]) = pre[i];
             }
             __syncthreads();
-            const int64_t cache_base = (int64_t)r * seq_stride + ((int64_t)l * 8 + x) * head_stride;
             const int64_t cur = cache_base + (int64_t)apos * kD;
             attn_qk_rope(at, att_in, nw0, nw1, rope_s[0][lane], rope_s[1][lane], rope_s[0][lane + 64],
-                         rope_s[1][lane + 64], a.kc + cur, a.vc + cur, nullptr, nullptr, nullptr, wave, lane);
+                         rope_s[1][lane + 64], a.kc + cur, a.vc + cur, nullptr, nullptr, nullptr, wave, lane, sliced);
             __syncthreads();
-            // the batched path attends over up to 1024 positions, most of them read from memory
-            attn_core<true>(at, a.kc + cache_base, a.vc + cache_base, apos + 1, apos, (double)a.attn_scale, tid, lane,
-                      wave, [&](int i, float v) {
-                          ll_put_xcd(&atto[r * 256 + i], __float_as_uint(v), tag(l, BS_ATT));
-                          if (l == last && a.dbg_attn != nullptr) a.dbg_attn[(int64_t)r * 2048 + 256 * x + i] = v;
-                      },
-                      [](int) {});
+            auto emit = [&](int i, float v) {
+                ll_put_xcd(&atto[r * 256 + i], __float_as_uint(v), tag(l, BS_ATT));
+                if (l == last && a.dbg_attn != nullptr) a.dbg_attn[(int64_t)r * 2048 + 256 * x + i] = v;
+            };
+            if (sliced) {
+                attn_partial_lds_v<AttnShared<128>, kSliceB>(
+                    at, vsl, 0, apos + 1, apos, (double)a.attn_scale, tid, lane, wave,
+                    [&](int i, double acc, double l1, double) { emit(i, (float)(acc * rcp_nr(l1))); }, [](int) {});
+            } else {
+                // up to 1024 positions, most of them read from memory
+                attn_core<true>(at, a.kc + cache_base, a.vc + cache_base, apos + 1, apos, (double)a.attn_scale, tid,
+                                lane, wave, emit, [](int) {});
+            }
             __syncthreads();
         }
 
