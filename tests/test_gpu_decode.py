@@ -265,7 +265,29 @@ def test_full_bf16_32_tokens(variant, mq, dev):
     dec, d, prompt, cfg, keep = _build(mq, dev, "qwen3_0.6b_bf16")
     toks = _greedy(dec, prompt, 32)
     assert toks == d["tokens"], (toks, d["tokens"])
-    del dec, keep
+    del dec
+    # the chat program's free functions (a10_chat.py:84-189) on caller-owned KV cache and
+    # scratch, sized as that program sizes them, give the same tokens
+    embed, layers, fnorm, lm, cos, sin = keep
+    ck, L, S = mq.chat_kernel, cfg.num_layers, d["max_seq_len"]
+    ck.init_ldg_layer_weights(*[[layers[11 * l + f] for l in range(L)] for f in range(11)])
+    ck.init_ldg_embed_weight(embed)
+    kc = torch.zeros((L, 8, S, 128), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    f32 = lambda n: torch.zeros(n, dtype=torch.float32, device=dev)
+    H, I = cfg.hidden_size, cfg.intermediate_size
+    scratch = [torch.zeros(H, dtype=torch.bfloat16, device=dev), f32(H), f32(H), f32(2048), f32(1024), f32(1024),
+               f32(2048), f32(I), f32(H), f32(1184), torch.zeros(1184, dtype=torch.int32, device=dev)]
+    seq, pos = list(prompt), 0
+    out = []
+    while len(out) < 32:
+        tok = ck.decode_a10(int(seq[pos]), fnorm, lm, cos, sin, kc, vc, *scratch, L, pos, pos + 1, S)
+        pos += 1
+        if pos >= len(prompt):
+            out.append(tok)
+            seq.append(tok)
+    assert out == d["tokens"], (out, d["tokens"])
+    del keep, kc, vc, scratch
     torch.cuda.empty_cache()
 
 
