@@ -49,7 +49,7 @@ constexpr int kBX = 8;                  // XCDs
 constexpr int kBG = kNWG / kBX;         // ranks per XCD
 constexpr int kSl = 64;                 // hidden elements per rank
 constexpr int kD = 128;                 // head dim
-constexpr int kSliceB = 128;            // longest sequence whose K/V rows stage B loads straight into LDS
+constexpr int kSliceB = 192;            // longest sequence whose K/V rows stage B loads straight into LDS
 constexpr int kLmTiles = 5;             // LM-head 16-row tiles per wave
 constexpr int kLmRowsPerWG = 16 * kLmTiles * kWaves;
 
@@ -235,10 +235,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     __shared__ __align__(16) uint32_t vsl[kSliceB][kD / 2];   // attention rank, short sequences: V rows
     constexpr size_t kBigF = (size_t)64 * KPF + (size_t)4 * 4 * 64 * 16;          // F digits + pair partials
     constexpr size_t kBigLM = (size_t)8 * 64 * 64;                                  // 8 k-steps of LM digits
-    constexpr size_t kBig0 = sizeof(AttnShared<128>) > kBigF ? sizeof(AttnShared<128>) : kBigF;
+    constexpr size_t kBig0 = sizeof(AttnShared<kSliceB>) > kBigF ? sizeof(AttnShared<kSliceB>) : kBigF;
     constexpr size_t kBig = kBig0 > kBigLM ? kBig0 : kBigLM;
     __shared__ __align__(16) uint8_t big[kBig];
-    AttnShared<128>& at = *reinterpret_cast<AttnShared<128>*>(big);
+    AttnShared<kSliceB>& at = *reinterpret_cast<AttnShared<kSliceB>*>(big);
     uint8_t* const dg = big;                                      // digit rows
     i32x4_t* const cred = reinterpret_cast<i32x4_t*>(big + (size_t)64 * KPF);   // pair partials [nt][mg][lane]
     double* const gu = reinterpret_cast<double*>(big + 64 * KPA); // stage E reducer sums [48][16]
@@ -554,7 +554,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 if (l == last && a.dbg_attn != nullptr) a.dbg_attn[(int64_t)r * 2048 + 256 * x + i] = v;
             };
             if (sliced) {
-                attn_partial_lds_v<AttnShared<128>, kSliceB>(
+                attn_partial_lds_v<AttnShared<kSliceB>, kSliceB>(
                     at, vsl, 0, apos + 1, apos, (double)a.attn_scale, tid, lane, wave,
                     [&](int i, double acc, double l1, double) { emit(i, (float)(acc * rcp_nr(l1))); }, [](int) {});
             } else {

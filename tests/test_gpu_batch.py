@@ -81,12 +81,14 @@ def test_batch_matches_oracle_per_sequence(mq, dev, model, batch):
 
 
 def test_batch_long_positions_match_oracle(mq, dev):
-    """Past the positions the config-5 benchmark reaches (8 prompt tokens + 128 steps): three
-    sequences, 8 prompt tokens and 142 greedy steps, up to position 149."""
-    long_model = _model(mq, dev, 160, seed=6)
+    """Past the positions the config-5 benchmark reaches (8 prompt tokens + 128 steps) and past the
+    192 positions whose K/V rows the attention rank loads straight into LDS (longer sequences take
+    the path that reads the rows beyond the first 64 inside the attention loops): three sequences,
+    8 prompt tokens and 200 greedy steps, up to position 207."""
+    long_model = _model(mq, dev, 216, seed=6)
     prompts = _prompts(3, long_model[0].vocab_size, seed=29)
-    print("batch 3, 142 steps", flush=True)
-    _check_against_oracle(mq, long_model, prompts, 142)
+    print("batch 3, 200 steps", flush=True)
+    _check_against_oracle(mq, long_model, prompts, 200)
 
 
 def _check_against_oracle(mq, model, prompts, steps):
