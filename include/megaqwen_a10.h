@@ -117,11 +117,11 @@ typedef struct mq_decode_args {
     void* workspace;                  /* device memory of mq_decode_workspace_bytes(dims)     */
     size_t workspace_bytes;
     unsigned int spin_limit;          /* bound on each in-kernel wait (polls); 0 = default    */
-    /* Optional hipEvent_t pair. When both are set the step is dispatched with
-     * hipExtLaunchKernel, which records them at the kernel's own start and end
-     * (exact kernel time); otherwise it is a cooperative launch. Either way all
+    /* Optional hipEvent_t pair, recorded at the kernel's own start and end
+     * (exact kernel time). Steps are dispatched with hipExtLaunchKernel. All
      * 256 workgroups must be co-resident, which the library checks once per
-     * device from the kernel's occupancy. */
+     * device from the kernel's occupancy; if other work holds compute units when
+     * a step starts, its bounded waits end it with MQ_ERR_TIMEOUT. */
     void* timing_start;
     void* timing_stop;
     /* Optional per-stage timeline: uint64 [(num_layers + 1) * 10 * 256], written

@@ -523,7 +523,11 @@ int decode_variant_in_use(const DecodeShape& s, bool int8) {
 }
 
 // All kNWG workgroups wait on each other, so they must be resident at once;
-// checked once per (kernel, device) from the occupancy calculator.
+// checked once per (kernel, device) from the occupancy calculator. The kernels
+// need co-residency only (their exchanges are their own, no runtime grid
+// barrier), so they are launched plainly: on this runtime a cooperative launch
+// cost about 10 us more per step. If other work holds CUs when a step starts,
+// its bounded waits end the step with MQ_ERR_TIMEOUT instead of hanging.
 int check_residency(const void* fn) {
     static thread_local const void* checked_fn[64] = {nullptr};
     static thread_local int checked[64] = {0};
@@ -550,14 +554,9 @@ static int launch_t(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t 
     if (st != MQ_OK) return st;
     KArgs copy = ka;
     void* args[] = {&copy};
-    hipError_t e;
-    if (t0 != nullptr && t1 != nullptr) {
-        e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
-        if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode): %s", hipGetErrorString(e));
-    } else {
-        e = hipLaunchCooperativeKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream);
-        if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipLaunchCooperativeKernel(decode): %s", hipGetErrorString(e));
-    }
+    // a plain launch (start/stop events when given): see check_residency
+    const hipError_t e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode): %s", hipGetErrorString(e));
     return MQ_OK;
 }
 

@@ -1090,14 +1090,9 @@ int launch_decode_batch(const mq_batch_args& a, const DecodeShape& s, hipStream_
     if (st != MQ_OK) return st;
     void* args[] = {&k};
     hipEvent_t t0 = static_cast<hipEvent_t>(a.timing_start), t1 = static_cast<hipEvent_t>(a.timing_stop);
-    hipError_t e;
-    if (t0 != nullptr && t1 != nullptr) {
-        e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
-        if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode_batch): %s", hipGetErrorString(e));
-    } else {
-        e = hipLaunchCooperativeKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream);
-        if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipLaunchCooperativeKernel(decode_batch): %s", hipGetErrorString(e));
-    }
+    // a plain launch (start/stop events when given): see check_residency
+    const hipError_t e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode_batch): %s", hipGetErrorString(e));
     return MQ_OK;
 }
 

@@ -746,14 +746,9 @@ static int launch_xcd_t(const KArgs& ka, bool debug, hipStream_t stream, hipEven
     if (st != MQ_OK) return st;
     KArgs copy = ka;
     void* args[] = {&copy};
-    hipError_t e;
-    if (t0 != nullptr && t1 != nullptr) {
-        e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
-        if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode_xcd): %s", hipGetErrorString(e));
-    } else {
-        e = hipLaunchCooperativeKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream);
-        if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipLaunchCooperativeKernel(decode_xcd): %s", hipGetErrorString(e));
-    }
+    // a plain launch (start/stop events when given): see check_residency
+    const hipError_t e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode_xcd): %s", hipGetErrorString(e));
     return MQ_OK;
 }
 
