@@ -124,7 +124,10 @@ def test_c_api_rejects_bad_arguments_without_launching(mq):
 
 def test_step_byte_accounting(mq):
     cfg = mq.QWEN3_0_6B
-    assert cfg.int8_step_bytes(cache_len=0) - 114688 == 598_101_504    # BASELINE.md section 2
+    # weights, scales and gains of one step: 28 layers x (15,728,640 B int8 + 49,152 B fp32 scales
+    # + 4,608 B bf16 gains) + the 155,582,464 B int8 LM head, its 607,744 B of scales, the 2,048 B
+    # final gain and one 2,048 B embedding row
+    assert cfg.int8_step_bytes(cache_len=0) - 114688 == 598_101_504
     assert cfg.bf16_step_bytes(cache_len=0) - 114688 == 1_192_101_888
     assert cfg.int8_step_bytes(cache_len=10) - cfg.int8_step_bytes(cache_len=9) == 114_688
 
