@@ -488,35 +488,32 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
         // ---------------- B: attention of sequence r (ranks r < B) ----------------
         if (attn) {
             const int64_t cache_base = (int64_t)r * seq_stride + ((int64_t)l * 8 + x) * head_stride;
-            // a short sequence: waves 4-7 load its earlier K and V rows straight into LDS
-            // while waves 0-3 gather the q|k|v rows (loads return in order per wave, so the
-            // gathering waves' polls do not wait for these loads; stage A's last barrier
-            // ordered every read of the LDS they overwrite)
+            // a short sequence: waves 4-7 first load its earlier K and V rows straight into LDS.
+            // Loads return in order per wave, so only these waves' gather polls come back after
+            // them (about when stage A's partials are complete anyway); waves 0-3 poll at once.
+            // Stage A's last barrier ordered every read of the LDS they overwrite.
             const bool loader = sliced && __builtin_amdgcn_readfirstlane(wave) >= 4;   // wave-uniform branch
-            uint32_t nw0 = 0, nw1 = 0;
             if (loader) {
                 const int ln = opaque(lane);    // per-lane offsets are recomputed, not held across layers
                 attn_slice_k<4>(at, a.kc + cache_base, 0, apos, ln, wave - 4);
                 attn_slice_v_lds<kSliceB, 4>(vsl, a.vc + cache_base, 0, apos, ln, wave - 4);
-                wait_vmem();                    // the rows are in LDS after the barrier below
-            } else {
-                if (wave < 3) {
-                    const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
-                    nw0 = ldg_bits(nw + lane);
-                    nw1 = ldg_bits(nw + lane + 64);
-                }
-                // this sequence's 512 q|k|v rows straight from stage A's partials: a thread sums
-                // row m over the 8 K slices (written by all 32 ranks of the XCD), times the
+            }
+            uint32_t nw0 = 0, nw1 = 0;
+            if (wave < 3) {
+                const uint16_t* nw = (const uint16_t*)(wave < 2 ? lw.q_norm_weight : lw.k_norm_weight);
+                nw0 = ldg_bits(nw + lane);
+                nw1 = ldg_bits(nw + lane + 64);
+            }
+            {
+                // this sequence's 512 q|k|v rows straight from stage A's partials: thread t sums
+                // row t over the 8 K slices (written by all 32 ranks of the XCD), times the
                 // RMSNorm scale from the slices' sums of squares (lanes 0..7 of every wave) and
-                // the row scale; rows tid and, with 4 gathering waves, tid + 256
-                const int nr = sliced ? 2 : 1;
-                uint32_t scA[2] = {0x3f800000u, 0x3f800000u};
-#pragma unroll
-                for (int k = 0; k < 2; ++k) {
-                    if (k >= nr) break;
+                // the row scale
+                uint32_t scA;
+                {
                     const uint8_t* w; const float* sc;
-                    qkv_row(lw, sp, tid + 256 * k, w, sc);
-                    scA[k] = ldg_bits(sc);
+                    qkv_row(lw, sp, tid, w, sc);
+                    scA = ldg_bits(sc);
                 }
                 double qv = 0.0;
                 if (lane < kNSl) {
@@ -526,16 +523,13 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 }
                 qv = group_sum64<kNSl>(qv);
                 const double rsb = rms_scale(__shfl(qv, 0, kWave), H, kEps);
-#pragma unroll
-                for (int k = 0; k < 2; ++k) {
-                    if (k >= nr) break;
-                    double v8[kNSl];
-                    wt.get_packed<kNSl>(&qp[(size_t)r * 512 + tid + 256 * k], kBMax * 512, pb, v8);
-                    const float y = (float)(sum_tree(v8) * rsb * (double)after_wait_f(scA[k]));
-                    att_in[tid + 256 * k] = y;
-                    if (l == last && a.dbg_qkv != nullptr) a.dbg_qkv[((int64_t)r * 8 + x) * 512 + tid + 256 * k] = y;
-                }
+                double v8[kNSl];
+                wt.get_packed<kNSl>(&qp[(size_t)r * 512 + tid], kBMax * 512, pb, v8);
+                const float y = (float)(sum_tree(v8) * rsb * (double)after_wait_f(scA));
+                att_in[tid] = y;
+                if (l == last && a.dbg_qkv != nullptr) a.dbg_qkv[((int64_t)r * 8 + x) * 512 + tid] = y;
             }
+            if (loader) wait_vmem();            // the slice rows are in LDS after the barrier below
 #pragma unroll
             for (int i = 0; i < kPreU4; ++i) {
                 const int f = tid + i * kThreads;
