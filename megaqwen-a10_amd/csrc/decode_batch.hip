@@ -493,10 +493,14 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             // them (about when stage A's partials are complete anyway); waves 0-3 poll at once.
             // Stage A's last barrier ordered every read of the LDS they overwrite.
             const bool loader = sliced && __builtin_amdgcn_readfirstlane(wave) >= 4;   // wave-uniform branch
-            if (loader) {
-                const int ln = opaque(lane);    // per-lane offsets are recomputed, not held across layers
-                attn_slice_k<4>(at, a.kc + cache_base, 0, apos, ln, wave - 4);
-                attn_slice_v_lds<kSliceB, 4>(vsl, a.vc + cache_base, 0, apos, ln, wave - 4);
+            // (every LDS access of a wave after its LDS-direct loads waits for them, so the pointer
+            // tables are read and the row scale is requested first, and the RMSNorm scale is
+            // broadcast with a lane read)
+            uint32_t scA;
+            {
+                const uint8_t* w; const float* sc;
+                qkv_row(lw, sp, tid, w, sc);
+                scA = ldg_bits(sc);
             }
             uint32_t nw0 = 0, nw1 = 0;
             if (wave < 3) {
@@ -504,17 +508,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 nw0 = ldg_bits(nw + lane);
                 nw1 = ldg_bits(nw + lane + 64);
             }
+            issue_fence();
+            if (loader) {
+                const int ln = opaque(lane);    // per-lane offsets are recomputed, not held across layers
+                attn_slice_k<4>(at, a.kc + cache_base, 0, apos, ln, wave - 4);
+                attn_slice_v_lds<kSliceB, 4>(vsl, a.vc + cache_base, 0, apos, ln, wave - 4);
+            }
             {
                 // this sequence's 512 q|k|v rows straight from stage A's partials: thread t sums
                 // row t over the 8 K slices (written by all 32 ranks of the XCD), times the
                 // RMSNorm scale from the slices' sums of squares (lanes 0..7 of every wave) and
                 // the row scale
-                uint32_t scA;
-                {
-                    const uint8_t* w; const float* sc;
-                    qkv_row(lw, sp, tid, w, sc);
-                    scA = ldg_bits(sc);
-                }
                 double qv = 0.0;
                 if (lane < kNSl) {
                     double v1[1];
@@ -522,7 +526,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                     qv = v1[0];
                 }
                 qv = group_sum64<kNSl>(qv);
-                const double rsb = rms_scale(__shfl(qv, 0, kWave), H, kEps);
+                const double rsb = rms_scale(readlane64(qv, 0), H, kEps);
                 double v8[kNSl];
                 wt.get_packed<kNSl>(&qp[(size_t)r * 512 + tid], kBMax * 512, pb, v8);
                 const float y = (float)(sum_tree(v8) * rsb * (double)after_wait_f(scA));
