@@ -401,8 +401,10 @@ __device__ __forceinline__ void attn_scores_mfma(AS& at, int j0, int j1, int pos
 // computing exp(s - m) for its t and readlane handing it to every lane; vword(t)
 // is lane l's V word (dims 2l, 2l+1) of local position w + 8t, the current
 // position's coming from at.kv_cur. The probability sums are wave sums of the
-// lanes' own values. Then attn_finish.
-template <int TV, class AS, class VWord, class Emit, class Mark>
+// lanes' own values. Then attn_finish. With kFastExp the numerators are the
+// hardware fp32 2^x of (s - m) log2(e) (relative error about 2^-23, for paths
+// checked to a tolerance) instead of the fp64 exp.
+template <int TV, bool kFastExp = false, class AS, class VWord, class Emit, class Mark>
 __device__ __forceinline__ void attn_softmax_pv(AS& at, VWord vword, int j0, int n, int pos, int tid, int lane,
                                                 int wave, Emit emit, Mark mark) {
     static_assert(TV <= kWave, "one P @ V chunk");
@@ -412,8 +414,14 @@ __device__ __forceinline__ void attn_softmax_pv(AS& at, VWord vword, int j0, int
     const int jl = wave + kWaves * lane;
     double p0 = 0.0, p1 = 0.0;
     if (lane < TV && jl < n) {
-        p0 = exp(at.p[0][jl] - M0);
-        p1 = exp(at.p[1][jl] - M1);
+        if constexpr (kFastExp) {
+            constexpr double kLog2e = 1.4426950408889634;
+            p0 = (double)__builtin_amdgcn_exp2f((float)((at.p[0][jl] - M0) * kLog2e));
+            p1 = (double)__builtin_amdgcn_exp2f((float)((at.p[1][jl] - M1) * kLog2e));
+        } else {
+            p0 = exp(at.p[0][jl] - M0);
+            p1 = exp(at.p[1][jl] - M1);
+        }
     }
     // wave-uniform bounds (scalar branches below)
     const int wu = __builtin_amdgcn_readfirstlane(wave);
@@ -464,16 +472,17 @@ __device__ __forceinline__ void attn_partial_lds(AS& at, int j0, int j1, int pos
 
 // attn_partial for a range [j0, j1) of at most NR positions whose K rows are in
 // at.kst (attn_slice_k) and V rows in vs (attn_slice_v_lds), waited for with a
-// barrier: scores on the matrix cores, softmax and P @ V in fp64.
-template <class AS, int NR, class Emit, class Mark>
+// barrier: scores on the matrix cores, softmax and P @ V in fp64 (numerators as
+// attn_softmax_pv's kFastExp says).
+template <class AS, int NR, bool kFastExp = false, class Emit, class Mark>
 __device__ __forceinline__ void attn_partial_lds_v(AS& at, const uint32_t (*vs)[kHD / 2], int j0, int j1, int pos,
                                                    double scale, int tid, int lane, int wave, Emit emit, Mark mark) {
     static_assert(NR <= AS::kNR && NR % 16 == 0, "slice capacity");
     attn_scores_mfma(at, j0, j1, pos, scale, lane, wave);
     __syncthreads();
     mark(0);
-    attn_softmax_pv<NR / kWaves>(at, [&](int t) { return vs[wave + kWaves * t][lane]; }, j0, j1 - j0, pos, tid,
-                                 lane, wave, emit, mark);
+    attn_softmax_pv<NR / kWaves, kFastExp>(at, [&](int t) { return vs[wave + kWaves * t][lane]; }, j0, j1 - j0,
+                                           pos, tid, lane, wave, emit, mark);
 }
 
 // Attention output of both query heads over positions [0, n) in one workgroup:

@@ -552,7 +552,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 if (l == last && a.dbg_attn != nullptr) a.dbg_attn[(int64_t)r * 2048 + 256 * x + i] = v;
             };
             if (sliced) {
-                attn_partial_lds_v<AttnShared<kSliceB>, kSliceB>(
+                attn_partial_lds_v<AttnShared<kSliceB>, kSliceB, true>(
                     at, vsl, 0, apos + 1, apos, (double)a.attn_scale, tid, lane, wave,
                     [&](int i, double acc, double l1, double) { emit(i, (float)(acc * rcp_nr(l1))); }, [](int) {});
             } else {
