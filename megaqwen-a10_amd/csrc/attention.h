@@ -401,9 +401,10 @@ __device__ __forceinline__ void attn_scores_mfma(AS& at, int j0, int j1, int pos
 // computing exp(s - m) for its t and readlane handing it to every lane; vword(t)
 // is lane l's V word (dims 2l, 2l+1) of local position w + 8t, the current
 // position's coming from at.kv_cur. The probability sums are wave sums of the
-// lanes' own values. Then attn_finish. With kFastExp the numerators are the
-// hardware fp32 2^x of (s - m) log2(e) (relative error about 2^-23, for paths
-// checked to a tolerance) instead of the fp64 exp.
+// lanes' own values. Then attn_finish. With kFastExp (for paths checked to a
+// tolerance) the numerators are the hardware fp32 2^x of (s - m) log2(e)
+// (relative error about 2^-23) instead of the fp64 exp, and the products and
+// sums are fp32 (fixed order) instead of fp64.
 template <int TV, bool kFastExp = false, class AS, class VWord, class Emit, class Mark>
 __device__ __forceinline__ void attn_softmax_pv(AS& at, VWord vword, int j0, int n, int pos, int tid, int lane,
                                                 int wave, Emit emit, Mark mark) {
@@ -412,34 +413,53 @@ __device__ __forceinline__ void attn_softmax_pv(AS& at, VWord vword, int j0, int
 #pragma unroll
     for (int w = 1; w < kWaves; ++w) { M0 = fmax(M0, at.wred[0][w]); M1 = fmax(M1, at.wred[1][w]); }
     const int jl = wave + kWaves * lane;
-    double p0 = 0.0, p1 = 0.0;
-    if (lane < TV && jl < n) {
-        if constexpr (kFastExp) {
-            constexpr double kLog2e = 1.4426950408889634;
-            p0 = (double)__builtin_amdgcn_exp2f((float)((at.p[0][jl] - M0) * kLog2e));
-            p1 = (double)__builtin_amdgcn_exp2f((float)((at.p[1][jl] - M1) * kLog2e));
-        } else {
-            p0 = exp(at.p[0][jl] - M0);
-            p1 = exp(at.p[1][jl] - M1);
-        }
-    }
     // wave-uniform bounds (scalar branches below)
     const int wu = __builtin_amdgcn_readfirstlane(wave);
     const int T = __builtin_amdgcn_readfirstlane(n > wu ? (n - wu + kWaves - 1) / kWaves : 0);
     const int tc = __builtin_amdgcn_readfirstlane(pos - j0 - wu);   // t of the current position, if this wave has it
-    double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
-#pragma unroll
-    for (int t = 0; t < TV; ++t) {
-        if (t < T) {
-            const uint32_t vw = t * kWaves == tc ? at.kv_cur[1][lane] : vword(t);
-            const double r0 = readlane64(p0, t), r1 = readlane64(p1, t);
-            const double v0 = __uint_as_float(vw << 16);
-            const double v1 = __uint_as_float(vw & 0xffff0000u);
-            a00 = fma(r0, v0, a00); a01 = fma(r0, v1, a01);
-            a10 = fma(r1, v0, a10); a11 = fma(r1, v1, a11);
+    if constexpr (kFastExp) {
+        // fp32 numerators, products and sums (fixed order)
+        constexpr double kLog2e = 1.4426950408889634;
+        float p0 = 0.0f, p1 = 0.0f;
+        if (lane < TV && jl < n) {
+            p0 = __builtin_amdgcn_exp2f((float)((at.p[0][jl] - M0) * kLog2e));
+            p1 = __builtin_amdgcn_exp2f((float)((at.p[1][jl] - M1) * kLog2e));
         }
+        float a00 = 0.0f, a01 = 0.0f, a10 = 0.0f, a11 = 0.0f;
+#pragma unroll
+        for (int t = 0; t < TV; ++t) {
+            if (t < T) {
+                const uint32_t vw = t * kWaves == tc ? at.kv_cur[1][lane] : vword(t);
+                const float r0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(p0), t));
+                const float r1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(p1), t));
+                const float v0 = __uint_as_float(vw << 16);
+                const float v1 = __uint_as_float(vw & 0xffff0000u);
+                a00 = fmaf(r0, v0, a00); a01 = fmaf(r0, v1, a01);
+                a10 = fmaf(r1, v0, a10); a11 = fmaf(r1, v1, a11);
+            }
+        }
+        attn_finish(at, (double)a00, (double)a01, (double)a10, (double)a11, (double)wave_sum(p0),
+                    (double)wave_sum(p1), M0, M1, tid, lane, wave, emit, mark);
+    } else {
+        double p0 = 0.0, p1 = 0.0;
+        if (lane < TV && jl < n) {
+            p0 = exp(at.p[0][jl] - M0);
+            p1 = exp(at.p[1][jl] - M1);
+        }
+        double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
+#pragma unroll
+        for (int t = 0; t < TV; ++t) {
+            if (t < T) {
+                const uint32_t vw = t * kWaves == tc ? at.kv_cur[1][lane] : vword(t);
+                const double r0 = readlane64(p0, t), r1 = readlane64(p1, t);
+                const double v0 = __uint_as_float(vw << 16);
+                const double v1 = __uint_as_float(vw & 0xffff0000u);
+                a00 = fma(r0, v0, a00); a01 = fma(r0, v1, a01);
+                a10 = fma(r1, v0, a10); a11 = fma(r1, v1, a11);
+            }
+        }
+        attn_finish(at, a00, a01, a10, a11, wave_sum64(p0), wave_sum64(p1), M0, M1, tid, lane, wave, emit, mark);
     }
-    attn_finish(at, a00, a01, a10, a11, wave_sum64(p0), wave_sum64(p1), M0, M1, tid, lane, wave, emit, mark);
 }
 
 // attn_partial for a range [j0, j1) of at most NR positions whose K rows and
