@@ -32,7 +32,7 @@
 // (agent-scope stores and loads). Words carry a (step, layer, stage) tag as in
 // decode.hip. Every reduction sums in a fixed order, so all ranks see identical
 // values and results are bitwise reproducible. The LM head is split over all
-// 256 workgroups; its argmax is gathered per XCD and then by workgroup 0.
+// 256 workgroups; workgroup (0, 0) reads their 256 maxima in one round.
 //
 // Each stage's weights (and scales / norm gains) are loaded into registers
 // before the preceding wait, so their fetch overlaps the exchange latency.
@@ -52,7 +52,7 @@ constexpr uint32_t kXStages = 8;
 constexpr int kAttWords = 2 * 256 + 2 * 3;
 
 struct XLayout {
-    size_t qkvx, actx, mlpx, hidx, lmx, po, pd, lmc, attp, atto, total;
+    size_t qkvx, actx, mlpx, hidx, lmg, po, pd, attp, atto, total;
 };
 // The regions follow the single-level kernel's (layout_for), so neither kernel
 // writes words the other could take for its own: the packed words below carry
@@ -64,10 +64,9 @@ constexpr XLayout xlayout_for(int H, int I) {
     o.actx = off; off += round256((size_t)kNX * H * 8);
     o.mlpx = off; off += round256((size_t)kNX * (I / kNX) * 8);
     o.hidx = off; off += round256((size_t)kNX * H * 8);
-    o.lmx = off; off += round256((size_t)kNX * kGS * 2 * 8);
+    o.lmg = off; off += round256((size_t)kNWG * 2 * 8);        // LM-head maxima [workgroup][key, index]
     o.po = off; off += round256((size_t)kNX * H * 8);          // packed fp64 partials [xcd][row]
     o.pd = off; off += round256((size_t)kNX * H * 8);
-    o.lmc = off; off += round256((size_t)kNX * 2 * 8);
     o.attp = off; off += round256((size_t)kNX * kGS * kAttWords * 8);
     o.atto = off; off += round256((size_t)kNX * 256 * 8);
     o.total = off;
@@ -80,6 +79,22 @@ template <class W>
 __device__ __forceinline__ float dot_piece(uint4 w, const float* x) {
     const float4* x4 = reinterpret_cast<const float4*>(x);
     return W::dot(w, x4, 0.0f);
+}
+
+// One wave gathers the N tagged words at base (N a multiple of 128) into dst[0, N):
+// 16-byte agent-coherent loads of two words, consecutive lanes on consecutive chunks.
+template <int N>
+__device__ __forceinline__ void gather_xcd(Waiter& wt, const uint64_t* base, uint32_t tag, float* dst, int lane) {
+    static_assert(N % 128 == 0, "whole 128-word rounds");
+    constexpr int C = N / 128;
+    uint32_t w[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) w[i] = 2u * (uint32_t)(lane + 64 * i);
+    float v[2 * C];
+    wt.get_pairs<C>(XRegion(base, N), w, tag, v);
+#pragma unroll
+    for (int i = 0; i < C; ++i)
+        *reinterpret_cast<float2*>(&dst[2 * (lane + 64 * i)]) = make_float2(v[2 * i], v[2 * i + 1]);
 }
 
 template <int H, int I, class W, bool kDebug>
@@ -111,8 +126,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 
     __shared__ double2 xd[H / 2];           // fp64 matvec input in per-lane order (QKV, gate/up)
     __shared__ float4 xs[H / 4];            // fp32 LM-head input in per-lane order
-    __shared__ float hid[H];                // layer input (bf16 values)
-    __shared__ float act[H];                // post-attention residual stream (fp32 values)
+    __shared__ __align__(16) float hid[H];  // layer input (bf16 values)
+    __shared__ __align__(16) float act[H];                // post-attention residual stream (fp32 values)
     __shared__ double attn_d[AD];           // this XCD's attention outputs (fp32 values), piece-major
     __shared__ double mlp_d[IX];            // this XCD's SwiGLU outputs (fp32 values), piece-major
     __shared__ double part[256];
@@ -149,10 +164,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     uint64_t* const actx = reinterpret_cast<uint64_t*>(a.ws + kLay.actx) + (size_t)x * H;
     uint64_t* const mlpx = reinterpret_cast<uint64_t*>(a.ws + kLay.mlpx) + (size_t)x * IX;
     uint64_t* const hidx = reinterpret_cast<uint64_t*>(a.ws + kLay.hidx) + (size_t)x * H;
-    uint64_t* const lmx = reinterpret_cast<uint64_t*>(a.ws + kLay.lmx) + (size_t)x * kGS * 2;
+    uint64_t* const lmg = reinterpret_cast<uint64_t*>(a.ws + kLay.lmg);
     uint64_t* const po = reinterpret_cast<uint64_t*>(a.ws + kLay.po);    // packed [8][H]
     uint64_t* const pd = reinterpret_cast<uint64_t*>(a.ws + kLay.pd);    // packed [8][H]
-    uint64_t* const lmc = reinterpret_cast<uint64_t*>(a.ws + kLay.lmc);
     uint64_t* const attp = reinterpret_cast<uint64_t*>(a.ws + kLay.attp) + (size_t)x * kGS * kAttWords;
     uint64_t* const atto = reinterpret_cast<uint64_t*>(a.ws + kLay.atto) + (size_t)x * AD;
 
@@ -302,6 +316,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     }
     prefetch_b(0);
 
+    uint32_t wfn[PT];                       // final RMSNorm gains (raw bits, loaded in the last layer)
     const int tid_all = tid;
     for (int l = 0; l < a.L; ++l) {
         const LayerWeights& lw = s_lw[l];
@@ -493,10 +508,13 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 ll_put_xcd(&actx[R0 + tid], __float_as_uint(av), tag(l, XS_ACT));
             }
 
+            // wave 0 gathers every residual row: the other waves have stage E's weights in
+            // flight, and their polls would return only after those (loads return in order)
+            if (wave == 0) gather_xcd<H>(wt, actx, tag(l, XS_ACT), act, lane);
+            __syncthreads();
             float av[PT];
-            wt.get_strided<PT>(actx + tid, kThreads, tag(l, XS_ACT), av);
 #pragma unroll
-            for (int i = 0; i < PT; ++i) act[tid + i * kThreads] = av[i];
+            for (int i = 0; i < PT; ++i) av[i] = act[tid + i * kThreads];
             trace(l, 5);
             issue_fence();
             {
@@ -578,6 +596,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 #pragma unroll
                 for (int i = 0; i < PT; ++i) wln[i] = ldg_bits(lnw + tid + i * kThreads);
                 issue_fence();
+            } else {
+                // the final RMSNorm gains, so that the tail's norm does not wait behind
+                // the first LM-head weight batch
+#pragma unroll
+                for (int i = 0; i < PT; ++i) wfn[i] = ldg_bits(a.final_norm + tid + i * kThreads);
+                issue_fence();
             }
             if (tid < RPW) {
                 double v8[kNX];
@@ -588,19 +612,19 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 ll_put_xcd(&hidx[R0 + tid], __float_as_uint(round_bf16(hf)), tag(l, XS_HID));
             }
 
-            float hv[PT];
-            wt.get_strided<PT>(hidx + tid, kThreads, tag(l, XS_HID), hv);
+            // wave 0 gathers every hidden row (the other waves have the next layer's QKV
+            // weights in flight)
+            if (wave == 0) gather_xcd<H>(wt, hidx, tag(l, XS_HID), hid, lane);
+            __syncthreads();
+            if (kDebug && l == last && g == 0 && a.dbg_hidden) {
 #pragma unroll
-            for (int i = 0; i < PT; ++i) {
-                hid[tid + i * kThreads] = hv[i];
-                if (kDebug && l == last && g == 0 && a.dbg_hidden)
-                    a.dbg_hidden[tid + i * kThreads] = (uint16_t)f32_to_bf16_bits(hv[i]);
+                for (int i = 0; i < PT; ++i)
+                    a.dbg_hidden[tid + i * kThreads] = (uint16_t)f32_to_bf16_bits(hid[tid + i * kThreads]);
             }
             // the next layer's stage B inputs: after the hidden gather, so that
             // neither exchange waits for them; stage A covers their latency
             issue_fence();
             if (l < last) prefetch_b(l + 1);
-            __syncthreads();
             trace(l, 9);
         }
     }
@@ -631,10 +655,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         int b = wave;
         if (b < nb) fetch(b, cur, scur);
         double ss = 0.0;
-        uint32_t wfn[PT];
 #pragma unroll
         for (int i = 0; i < PT; ++i) {
-            wfn[i] = ldg_bits(a.final_norm + tid + i * kThreads);
             const double v = hid[tid + i * kThreads];
             ss = fma(v, v, ss);
         }
@@ -681,8 +703,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         if (lane == 0) { lm_v[wave] = best_v; lm_i[wave] = best_i; }
         __syncthreads();
         trace(a.L, 1);
-        // argmax over the 8 waves, then the XCD's 32 workgroups, then the 8 XCDs
-        const uint32_t tag_l1 = tag(a.L, 0), tag_l2 = tag(a.L, 1);
+        // argmax over the 8 waves; then workgroup (0, 0) reads the maxima of all 256
+        // workgroups in one cross-XCD round (4 per lane) and publishes the token
+        const uint32_t tag_lm = tag(a.L, 0);
         if (tid == 0) {
             float bv = lm_v[0];
             int bi = lm_i[0];
@@ -690,15 +713,21 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 if (lm_v[w] > bv || (lm_v[w] == bv && lm_i[w] < bi)) { bv = lm_v[w]; bi = lm_i[w]; }
             if (kDebug && a.dbg_bmax) a.dbg_bmax[g] = bv;
             if (kDebug && a.dbg_bidx) a.dbg_bidx[g] = bi;
-            ll_put_xcd(&lmx[2 * r], ordered_key(bv), tag_l1);
-            ll_put_xcd(&lmx[2 * r + 1], (uint32_t)bi, tag_l1);
+            ll_put(&lmg[2 * g], ordered_key(bv), tag_lm);
+            ll_put(&lmg[2 * g + 1], (uint32_t)bi, tag_lm);
         }
-        if (r == 0 && wave == 0) {
-            // XCD leader: one lane per rank
-            uint32_t kv = 0, iv = 0x7fffffffu;
-            if (lane < kGS) {
-                kv = wt.get(&lmx[2 * lane], tag_l1);
-                iv = wt.get(&lmx[2 * lane + 1], tag_l1);
+        if (x == 0 && r == 0 && wave == 0) {
+            constexpr int C = kNWG / kWave;
+            uint32_t w[C];
+#pragma unroll
+            for (int i = 0; i < C; ++i) w[i] = 2u * (uint32_t)(lane + kWave * i);
+            float v[2 * C];
+            wt.get_pairs<C>(XRegion(lmg, 2 * kNWG), w, tag_lm, v);
+            uint32_t kv = __float_as_uint(v[0]), iv = __float_as_uint(v[1]);
+#pragma unroll
+            for (int i = 1; i < C; ++i) {
+                const uint32_t ok = __float_as_uint(v[2 * i]), oi = __float_as_uint(v[2 * i + 1]);
+                if (ok > kv || (ok == kv && oi < iv)) { kv = ok; iv = oi; }
             }
 #define MQ_KEY_LEVEL(M)                                                                      \
             {                                                                                \
@@ -707,29 +736,15 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 if (ok > kv || (ok == kv && oi < iv)) { kv = ok; iv = oi; }                  \
             }
             MQ_KEY_LEVEL(1) MQ_KEY_LEVEL(2) MQ_KEY_LEVEL(4) MQ_KEY_LEVEL(8) MQ_KEY_LEVEL(16) MQ_KEY_LEVEL(32)
-            if (lane == 0) {
-                ll_put(&lmc[2 * x], kv, tag_l2);
-                ll_put(&lmc[2 * x + 1], iv, tag_l2);
-            }
-            if (x == 0) {
-                uint32_t k2 = 0, i2 = 0x7fffffffu;
-                if (lane < kNX) {
-                    k2 = wt.get(&lmc[2 * lane], tag_l2);
-                    i2 = wt.get(&lmc[2 * lane + 1], tag_l2);
-                }
-                kv = k2;
-                iv = i2;
-                MQ_KEY_LEVEL(1) MQ_KEY_LEVEL(2) MQ_KEY_LEVEL(4) MQ_KEY_LEVEL(8) MQ_KEY_LEVEL(16) MQ_KEY_LEVEL(32)
-                if (lane == 0) {
-                    const bool aborted = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
-                    *a.out_token = (aborted || wt.dead) ? -1 : (int)iv;
-                    __hip_atomic_store(&hdr->xsteps, XS + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(&hdr->epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if (kDebug && a.trace != nullptr)
-                        a.trace[((int64_t)a.L * kTracePoints + 2) * kNWG] = __builtin_amdgcn_s_memrealtime();
-                }
-            }
 #undef MQ_KEY_LEVEL
+            if (lane == 0) {
+                const bool aborted = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+                *a.out_token = (aborted || wt.dead) ? -1 : (int)iv;
+                __hip_atomic_store(&hdr->xsteps, XS + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&hdr->epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (kDebug && a.trace != nullptr)
+                    a.trace[((int64_t)a.L * kTracePoints + 2) * kNWG] = __builtin_amdgcn_s_memrealtime();
+            }
         }
     }
 }
