@@ -248,7 +248,14 @@ int mq_decode_variant(const mq_model_dims* dims, int int8);
 /* a10_int8_decode_kernel.cu:821-842. Uses a library-owned workspace per
  * device (allocated on first use): calls that overlap on one device race.
  * The block_max_* buffers need >= 256 entries. Errors are reported through
- * mq_last_error() since the reference signature returns void. */
+ * mq_last_error() since the reference signature returns void. A step that
+ * fails inside the kernel (expired bounded wait) stores token -1; the next
+ * call on that device then re-initialises the workspace before launching and
+ * reports the earlier failure through mq_last_error() (the reference's caller
+ * reads every token back, bench_int8.py:218, so the failure is known by then).
+ * The vocabulary and layer shapes are those of mq_reference_set_dims (default
+ * Qwen3-0.6B); the embedding, LM head, caches and tables are checked on the host
+ * against the device allocations that hold them, where the runtime can tell. */
 void launch_a10_int8_decode(
     int input_token_id, int* output_token_id,
     const void* embed_weight, const LayerWeights* layer_weights,
@@ -273,6 +280,16 @@ void launch_a10_decode(
     void* g_normalized, void* block_max_vals, void* block_max_idxs,
     int num_layers, int position, int cache_len, int max_seq_len, float attn_scale,
     hipStream_t stream);
+
+/* Bound on each in-kernel wait (polls) of the steps the two launchers above
+ * run; 0 = library default. No counterpart in the reference (for tests that
+ * force the failure path from the host). */
+void mq_reference_set_spin_limit(unsigned int polls);
+/* Model dims the two launchers above assume from now on (NULL = Qwen3-0.6B,
+ * vocab 151936). The reference compiles its dims in (config.cuh:15-43); its
+ * launchers' signature carries none, so another model (e.g. a smaller
+ * vocabulary) must be declared here first. Returns a status code. */
+int mq_reference_set_dims(const mq_model_dims* dims);
 
 /* ---- standalone kernels ------------------------------------------------- */
 /* int8_decoder.py:100-115: y[j] = scale[j] * sum_k x[k] * w[j,k].

@@ -110,6 +110,8 @@ _SIGNATURES = {
     "mq_int8_decode_batch_step": (c_int, [POINTER(BatchArgs), c_void_p]),
     "launch_a10_int8_decode": (None, [c_int, c_void_p] + [c_void_p] * 20 + [c_int] * 4 + [c_float, c_void_p, c_void_p]),
     "launch_a10_decode": (None, [c_int, c_void_p] + [c_void_p] * 19 + [c_int] * 4 + [c_float, c_void_p]),
+    "mq_reference_set_spin_limit": (None, [c_uint]),
+    "mq_reference_set_dims": (c_int, [c_void_p]),
     "mq_int8_gemv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "mq_quantize_per_channel_bf16": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
 }

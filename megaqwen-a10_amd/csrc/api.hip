@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 
 #include "internal.h"
@@ -57,6 +58,29 @@ __global__ void ws_init_kernel(uint64_t* ws, size_t words) {
     if (blockIdx.x == 0 && threadIdx.x == 0) reinterpret_cast<WsHeader*>(ws)->epoch = 1u;
 }
 
+// Whether [p, p + need) lies inside the device allocation that holds p. A best-effort
+// guard for arguments that arrive without sizes (the reference-signature launchers
+// pass bare pointers): a pointer the runtime cannot place is not rejected, and a
+// tensor carved out of a larger allocation is only checked against that allocation's
+// end. The last few results are kept per thread, so a decode loop that passes the
+// same buffers every step asks the runtime once.
+static bool in_allocation(const void* p, size_t need) {
+    struct Seen { const void* p; size_t need; bool ok; };
+    static thread_local Seen seen[16];
+    static thread_local unsigned next = 0;
+    for (const Seen& e : seen)
+        if (e.p == p && e.need == need) return e.ok;
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    bool ok = true;
+    if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) == hipSuccess && base != nullptr)
+        ok = reinterpret_cast<uintptr_t>(p) + need <= reinterpret_cast<uintptr_t>(base) + size;
+    else
+        (void)hipGetLastError();
+    seen[next++ % 16] = Seen{p, need, ok};
+    return ok;
+}
+
 static int validate_decode(const mq_decode_args* a, bool int8, DecodeShape* s) {
     if (a == nullptr) return set_error(MQ_ERR_INVALID_ARGUMENT, "args is NULL");
     int st = shape_of(a->dims, s);
@@ -80,40 +104,114 @@ static int validate_decode(const mq_decode_args* a, bool int8, DecodeShape* s) {
         return set_error(MQ_ERR_INVALID_ARGUMENT, "workspace of %zu bytes needed, %zu given",
                          decode_workspace_bytes(*s), a->workspace ? a->workspace_bytes : (size_t)0);
     if (!aligned16(a->workspace)) return set_error(MQ_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+    const size_t HV = (size_t)s->H * (size_t)s->V;
+    const size_t cache = (size_t)a->num_layers * s->NKV * a->max_seq_len * s->D * 2;
+    const size_t table = (size_t)a->max_seq_len * s->D * 2;
+    if (!in_allocation(a->embed_weight, HV * 2) || !in_allocation(a->lm_head_weight, HV * (int8 ? 1 : 2)) ||
+        (int8 && !in_allocation(a->lm_head_scale, (size_t)s->V * 4)))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "embed_weight / lm_head_weight hold fewer than vocab_size = %d rows "
+                         "of %d (set the model dims; the reference-signature launchers assume Qwen3-0.6B unless "
+                         "mq_reference_set_dims says otherwise)", s->V, s->H);
+    if (!in_allocation(a->k_cache, cache) || !in_allocation(a->v_cache, cache))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "the KV caches hold fewer than num_layers x %d x max_seq_len x %d "
+                         "bf16 values", s->NKV, s->D);
+    if (!in_allocation(a->cos_table, table) || !in_allocation(a->sin_table, table))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "the RoPE tables hold fewer than max_seq_len rows of %d", s->D);
     return MQ_OK;
 }
 
-// Library-owned workspace per device for the reference-signature launchers.
+// Library-owned workspace per device for the reference-signature launchers,
+// with a pinned host word into which every step's token publisher stores the
+// step's abort flag (0 = completed). The reference's caller reads each token
+// back (bench_int8.py:218), so by the next call the word holds the previous
+// step's outcome; a failed step is then reported through mq_last_error(), its
+// workspace re-initialised (and the single-level kernel selected if a
+// workgroup ran on an unexpected XCD) before the new step is launched.
 struct DeviceWorkspace {
     void* ptr = nullptr;
     size_t bytes = 0;
+    volatile uint32_t* status = nullptr;
 };
 static std::mutex g_ws_mu;
 static DeviceWorkspace g_ws[64];
+static std::atomic<unsigned int> g_ref_spin{0};   // spin limit of the reference-signature launchers (0 = default)
+// model dims of the reference-signature launchers (their signature has none); unset = Qwen3-0.6B
+static std::mutex g_ref_mu;
+static bool g_ref_has_dims = false;
+static mq_model_dims g_ref_dims;
 
-static int default_workspace(hipStream_t stream, void** out, size_t* bytes) {
+// The reference launchers' dims for this call (copied into *store; NULL when unset).
+static const mq_model_dims* reference_dims(mq_model_dims* store) {
+    std::lock_guard<std::mutex> lk(g_ref_mu);
+    if (!g_ref_has_dims) return nullptr;
+    *store = g_ref_dims;
+    return store;
+}
+
+static int default_workspace(const mq_model_dims* dims, hipStream_t stream, void** out, size_t* bytes,
+                             uint32_t** status) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
         return set_error(MQ_ERR_HIP, "hipGetDevice failed");
+    DecodeShape s;
+    int st0 = shape_of(dims, &s);
+    if (st0 != MQ_OK) return st0;
+    const size_t need = decode_workspace_bytes(s);
     std::lock_guard<std::mutex> lk(g_ws_mu);
     DeviceWorkspace& w = g_ws[dev];
+    if (w.ptr != nullptr && w.bytes < need) {
+        // larger dims than before: a new workspace (hipFree waits for the steps using the old one)
+        (void)hipFree(w.ptr);
+        w.ptr = nullptr;
+    }
     if (w.ptr == nullptr) {
-        DecodeShape s;
-        shape_of(nullptr, &s);
-        const size_t need = decode_workspace_bytes(s);
+        if (w.status == nullptr) {
+            void* st_word = nullptr;
+            if (hipHostMalloc(&st_word, sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
+                return set_error(MQ_ERR_OUT_OF_MEMORY, "hipHostMalloc of the step status word failed");
+            w.status = static_cast<volatile uint32_t*>(st_word);
+        }
         if (hipMalloc(&w.ptr, need) != hipSuccess) {
             w.ptr = nullptr;
             return set_error(MQ_ERR_OUT_OF_MEMORY, "hipMalloc(%zu) for the decode workspace failed", need);
         }
         w.bytes = need;
+        *w.status = 0u;
         hipLaunchKernelGGL(ws_init_kernel, dim3(64), dim3(256), 0, stream, static_cast<uint64_t*>(w.ptr),
                            need / 8);
         int st = check_launch("ws_init_kernel");
         if (st != MQ_OK) return st;
+    } else if (*w.status != 0u) {
+        // the previous step on this workspace failed: recover before this one
+        const uint32_t flag = *w.status;
+        *w.status = 0u;
+        if (flag == 2u) mark_xcd_unusable();
+        hipLaunchKernelGGL(ws_init_kernel, dim3(64), dim3(256), 0, stream, static_cast<uint64_t*>(w.ptr),
+                           w.bytes / 8);
+        int st = check_launch("ws_init_kernel");
+        if (st != MQ_OK) return st;
+        set_error(MQ_ERR_TIMEOUT, "the previous step failed (%s; its token is -1); the workspace was re-initialised "
+                                  "and this step launched",
+                  flag == 2u ? "a workgroup ran on an unexpected XCD, the single-level kernel is selected"
+                             : "a bounded wait in the decode kernel expired");
     }
     *out = w.ptr;
     *bytes = w.bytes;
+    *status = const_cast<uint32_t*>(w.status);
     return MQ_OK;
+}
+
+// One step of a reference-signature launcher: validation and launch with the
+// library-owned status word. A message left by default_workspace() (the
+// previous step's failure) stays visible unless this step's own validation or
+// launch fails.
+static void reference_step(const mq_decode_args* a, bool int8, uint32_t* status, hipStream_t stream) {
+    char pending[sizeof(g_err)];
+    memcpy(pending, g_err, sizeof(g_err));
+    DecodeShape s;
+    int st = validate_decode(a, int8, &s);
+    if (st == MQ_OK) st = launch_decode(*a, s, int8, stream, status);
+    if (st == MQ_OK) memcpy(g_err, pending, sizeof(g_err));
 }
 
 }  // namespace mq
@@ -122,7 +220,7 @@ using namespace mq;
 
 extern "C" {
 
-int mq_abi_version(void) { return 2; }
+int mq_abi_version(void) { return 3; }
 
 const char* mq_last_error(void) { return g_err; }
 
@@ -216,6 +314,24 @@ int mq_int8_decode_batch_step(const mq_batch_args* args, hipStream_t stream) {
     return launch_decode_batch(*args, s, stream);
 }
 
+void mq_reference_set_spin_limit(unsigned int polls) {
+    clear_error();
+    g_ref_spin = polls;
+}
+
+int mq_reference_set_dims(const mq_model_dims* dims) {
+    clear_error();
+    if (dims != nullptr) {
+        DecodeShape s;
+        const int st = shape_of(dims, &s);
+        if (st != MQ_OK) return st;
+    }
+    std::lock_guard<std::mutex> lk(g_ref_mu);
+    g_ref_has_dims = dims != nullptr;
+    if (dims != nullptr) g_ref_dims = *dims;
+    return MQ_OK;
+}
+
 int mq_decode_set_variant(int variant) {
     clear_error();
     return set_decode_variant(variant);
@@ -242,7 +358,10 @@ void launch_a10_int8_decode(int input_token_id, int* output_token_id, const void
     clear_error();
     mq_decode_args a;
     memset(&a, 0, sizeof(a));
-    if (default_workspace(stream, &a.workspace, &a.workspace_bytes) != MQ_OK) return;
+    uint32_t* status = nullptr;
+    mq_model_dims dims;
+    a.dims = reference_dims(&dims);
+    if (default_workspace(a.dims, stream, &a.workspace, &a.workspace_bytes, &status) != MQ_OK) return;
     a.input_token_id = input_token_id;
     a.output_token_id = output_token_id;
     a.embed_weight = embed_weight;
@@ -271,7 +390,8 @@ void launch_a10_int8_decode(int input_token_id, int* output_token_id, const void
     a.cache_len = cache_len;
     a.max_seq_len = max_seq_len;
     a.attn_scale = attn_scale;
-    mq_int8_decode_step(&a, stream);
+    a.spin_limit = g_ref_spin.load();
+    reference_step(&a, true, status, stream);
 }
 
 void launch_a10_decode(int input_token_id, int* output_token_id, const void* embed_weight,
@@ -284,7 +404,10 @@ void launch_a10_decode(int input_token_id, int* output_token_id, const void* emb
     clear_error();
     mq_decode_args a;
     memset(&a, 0, sizeof(a));
-    if (default_workspace(stream, &a.workspace, &a.workspace_bytes) != MQ_OK) return;
+    uint32_t* status = nullptr;
+    mq_model_dims dims;
+    a.dims = reference_dims(&dims);
+    if (default_workspace(a.dims, stream, &a.workspace, &a.workspace_bytes, &status) != MQ_OK) return;
     a.input_token_id = input_token_id;
     a.output_token_id = output_token_id;
     a.embed_weight = embed_weight;
@@ -311,7 +434,8 @@ void launch_a10_decode(int input_token_id, int* output_token_id, const void* emb
     a.cache_len = cache_len;
     a.max_seq_len = max_seq_len;
     a.attn_scale = attn_scale;
-    mq_bf16_decode_step(&a, stream);
+    a.spin_limit = g_ref_spin.load();
+    reference_step(&a, false, status, stream);
 }
 
 int mq_int8_gemv(const float* x, const int8_t* w, const float* scale, float* y, int M, int K, hipStream_t stream) {

@@ -445,8 +445,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             const uint32_t prev = __hip_atomic_fetch_add(&hdr->done[slot], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
             if (prev == gridDim.x - 1) {
                 const uint64_t k = __hip_atomic_load(&hdr->best[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const bool aborted = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
-                *a.out_token = aborted ? -1 : (int)(~(uint32_t)(k & 0xffffffffu));
+                const uint32_t flag = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *a.out_token = flag != 0u ? -1 : (int)(~(uint32_t)(k & 0xffffffffu));
+                if (a.status_out) *a.status_out = flag;
                 __hip_atomic_store(&hdr->epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if (kDebug && a.trace != nullptr) a.trace[((int64_t)a.L * kTracePoints + 2) * kNWG] = __builtin_amdgcn_s_memrealtime();
             }
@@ -462,6 +463,9 @@ size_t decode_workspace_bytes(const DecodeShape& s) {
 }
 
 // ---- kernel variant selection ----
+// XCD of each workgroup of the placement check (a device array: the check allocates nothing)
+static __device__ uint32_t g_xcc_map[kNWG];
+
 __global__ void xcc_map_kernel(uint32_t* out) {
     if (threadIdx.x == 0) {
         uint32_t v;
@@ -495,7 +499,7 @@ bool xcd_placement_ok() {
     if (st != 0) return st == 1;
     bool ok = false;
     uint32_t* d = nullptr;
-    if (hipMalloc(&d, kNWG * sizeof(uint32_t)) == hipSuccess) {
+    if (hipGetSymbolAddress(reinterpret_cast<void**>(&d), HIP_SYMBOL(g_xcc_map)) == hipSuccess && d != nullptr) {
         hipLaunchKernelGGL(xcc_map_kernel, dim3(kNWG), dim3(kThreads), 0, 0, d);
         uint32_t h[kNWG];
         if (hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
@@ -508,7 +512,6 @@ bool xcd_placement_ok() {
             }
             for (int i = 8; i < kNWG; ++i) ok = ok && (h[i] == h[i % 8]);
         }
-        (void)hipFree(d);
     }
     g_xcd_ok[dev] = ok ? 1 : 2;
     return ok;
@@ -560,7 +563,7 @@ static int launch_t(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t 
     return MQ_OK;
 }
 
-int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream) {
+int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream, uint32_t* status_out) {
     if (a.num_layers > kMaxLayers)
         return set_error(MQ_ERR_UNSUPPORTED, "num_layers %d exceeds %d", a.num_layers, kMaxLayers);
     const int variant = decode_variant_in_use(s, int8);
@@ -607,6 +610,7 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
     k.spin_limit = a.spin_limit ? a.spin_limit : (1u << 21);
     k.trace = static_cast<uint64_t*>(a.trace);
     k.ws = static_cast<uint8_t*>(a.workspace);
+    k.status_out = status_out;
     const bool debug = a.hidden_buffer || a.g_activations || a.g_residual || a.g_q || a.g_k || a.g_v ||
                        a.g_attn_out || a.g_mlp_intermediate || a.g_normalized || a.block_max_vals ||
                        a.block_max_idxs || a.trace;

@@ -52,6 +52,7 @@ struct KArgs {
     uint32_t spin_limit;
     uint64_t* trace;
     uint8_t* ws;
+    uint32_t* status_out;                  // optional: the step's abort flag (0 = completed), stored with the token
 };
 
 constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }

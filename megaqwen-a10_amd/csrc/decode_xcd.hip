@@ -738,8 +738,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             MQ_KEY_LEVEL(1) MQ_KEY_LEVEL(2) MQ_KEY_LEVEL(4) MQ_KEY_LEVEL(8) MQ_KEY_LEVEL(16) MQ_KEY_LEVEL(32)
 #undef MQ_KEY_LEVEL
             if (lane == 0) {
-                const bool aborted = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
-                *a.out_token = (aborted || wt.dead) ? -1 : (int)iv;
+                const uint32_t flag = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *a.out_token = (flag != 0u || wt.dead) ? -1 : (int)iv;
+                if (a.status_out) *a.status_out = flag != 0u ? flag : (wt.dead ? 1u : 0u);
                 __hip_atomic_store(&hdr->xsteps, XS + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 __hip_atomic_store(&hdr->epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if (kDebug && a.trace != nullptr)

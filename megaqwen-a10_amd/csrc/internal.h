@@ -42,8 +42,10 @@ int set_decode_variant(int variant);
 int decode_variant_in_use(const DecodeShape& s, bool int8);
 // After an in-kernel placement failure: use the single-level kernel from now on.
 void mark_xcd_unusable();
-// Launches one decode step; `int8` selects the weight format.
-int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream);
+// Launches one decode step; `int8` selects the weight format. When status_out is
+// non-null the step's token publisher also stores the abort flag there (0 = completed).
+int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream,
+                  uint32_t* status_out = nullptr);
 // True when the workgroups of each residue class g mod 8 run on one XCD (checked once per device).
 bool xcd_placement_ok();
 

@@ -29,8 +29,9 @@ from .config import QWEN3_0_6B, ModelConfig
 from .rope import precompute_rope_freqs
 from .weights import pack_bf16, pack_int8, quantize_state, random_init_state
 
-TOKEN_PENDING = -2          # written into the pinned token word before a launch; kernels store >= -1
+TOKEN_PENDING = -2          # written into a pinned token word before a launch; kernels store >= -1
 WAIT_US = 2_000_000         # host spin on the token before falling back to a stream synchronisation
+TOKEN_SLOTS = 256           # pinned token words, one per step in flight (launch_step without wait_token)
 
 LM_PARTIALS = 256   # per-workgroup LM-head maxima written to block_max_vals/idxs
 
@@ -180,9 +181,13 @@ class _DecoderBase:
         self.block_max_vals = torch.zeros(LM_PARTIALS, **f32)
         self.block_max_idxs = torch.zeros(LM_PARTIALS, dtype=torch.int32, device=dev)
         # the kernel writes the token straight into pinned host memory: the host spins on
-        # it (no device-to-host copy, no stream-synchronisation wake-up)
-        self.output_token = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        # it (no device-to-host copy, no stream-synchronisation wake-up). Each step in
+        # flight has its own word, so a step launched behind another (a prefill that does
+        # not read its tokens) cannot have its word overwritten by the earlier one's store.
+        self.output_token = torch.full((TOKEN_SLOTS,), TOKEN_PENDING, dtype=torch.int32, pin_memory=True)
         self._tok_host = self.output_token.numpy()
+        self._next_slot = 0
+        self._inflight = []          # (slot, position) of every launched step not yet collected
 
         self._lib = _lib.load()
         self._dims = _lib.ModelDims(H, I, 16, 8, D, V)
@@ -194,7 +199,7 @@ class _DecoderBase:
         self._init_workspace()
 
         a = _lib.DecodeArgs()
-        a.output_token_id = self.output_token.data_ptr()
+        a.output_token_id = self.output_token.data_ptr()      # slot 0; launch_step picks the slot
         a.embed_weight = embed.data_ptr()
         a.layer_weights = self.d_layer_weights.data_ptr()
         a.scales = self.d_layer_scales.data_ptr() if self._int8 else None
@@ -221,34 +226,57 @@ class _DecoderBase:
 
     # -- reference surface ---------------------------------------------------------------
     def launch_step(self, input_token_id: int) -> None:
-        """Enqueue one decode step on the current stream without waiting for the token."""
+        """Enqueue one decode step on the current stream without waiting for the token.
+        Several steps may be launched before ``wait_token`` (for example a prefill whose
+        tokens are not needed); ``wait_token`` then returns the last one's token."""
         V = self.dims[2]
         if not isinstance(input_token_id, int) or not 0 <= input_token_id < V:
             raise ValueError(f"input_token_id {input_token_id!r} outside [0, {V})")
         if self._pos >= self.max_seq_len:
             raise ValueError(f"KV cache full: position {self._pos} == max_seq_len {self.max_seq_len}")
+        slot = self._next_slot
+        if any(sl == slot for sl, _ in self._inflight):
+            # TOKEN_SLOTS steps already in flight: let them finish before this word is reused
+            torch.cuda.current_stream(self.device).synchronize()
         a = self._args
         a.input_token_id = input_token_id
         a.position = self._pos
         a.cache_len = self._pos + 1
-        self._tok_host[0] = TOKEN_PENDING
+        a.output_token_id = self.output_token.data_ptr() + 4 * slot
+        self._tok_host[slot] = TOKEN_PENDING
         st = self._step_fn(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(self.device)))
         _lib.check(st, "decode step")
+        self._inflight.append((slot, self._pos))
+        self._next_slot = (slot + 1) % TOKEN_SLOTS
         self._pos += 1
 
     def wait_token(self) -> int:
         """Wait for the last enqueued step and return its token. Spins on the pinned word the
         kernel stores last; falls back to a stream synchronisation (which reports errors) if
-        no token arrives within WAIT_US or the step reports a failure (-1)."""
-        if self._lib.mq_wait_host_token(self._tok_host.ctypes.data, TOKEN_PENDING, WAIT_US) != _lib.MQ_OK:
+        no token arrives within WAIT_US or the step reports a failure (-1).
+
+        A failed step (its in-kernel wait expired, MQTimeoutError) leaves the decoder at that
+        step's position with a re-initialised workspace: the steps from there on are undone,
+        and decoding continues by feeding the same token again (the cache rows the failed
+        steps wrote are rewritten when those positions are recomputed)."""
+        if not self._inflight:
+            raise RuntimeError("no decode step in flight (call launch_step first)")
+        slot = self._inflight[-1][0]
+        word = self._tok_host[slot:].ctypes.data
+        if self._lib.mq_wait_host_token(word, TOKEN_PENDING, WAIT_US) != _lib.MQ_OK:
             torch.cuda.current_stream(self.device).synchronize()
-        tok = int(self._tok_host[0])
+        tok = int(self._tok_host[slot])
         if tok < 0:
             torch.cuda.current_stream(self.device).synchronize()
+            # a failed step makes every later step on the workspace fail too: resume at the first
+            failed = [pos for sl, pos in self._inflight if int(self._tok_host[sl]) < 0]
+            self._pos = failed[0] if failed else self._inflight[-1][1]
+            self._inflight.clear()
             status = self._lib.mq_decode_check(self.workspace.data_ptr(),
                                                ctypes.c_void_p(_lib.stream_handle(self.device)))
             self._init_workspace()
             _lib.check(status if status != _lib.MQ_OK else _lib.MQ_ERR_TIMEOUT, "decode step")
+        self._inflight.clear()
         return tok
 
     def decode_step(self, input_token_id: int) -> int:
@@ -256,6 +284,10 @@ class _DecoderBase:
         return self.wait_token()
 
     def reset(self) -> None:
+        if self._inflight:
+            # steps still in flight store into their token words: let them land first
+            torch.cuda.current_stream(self.device).synchronize()
+            self._inflight.clear()
         self._pos = 0
         self.k_cache.zero_()
         self.v_cache.zero_()
@@ -427,9 +459,13 @@ class A10Int8BatchDecoder(_DecoderBase):
         a.workspace_bytes = ws_bytes
         self._args = a
         self._positions = [0] * batch
+        self._inflight = None        # positions before the launched, not yet collected step
 
     def launch_step(self, tokens) -> None:
-        """Enqueue one step (one token per sequence) on the current stream."""
+        """Enqueue one step (one token per sequence) on the current stream. A step still
+        in flight is collected first (its tokens are dropped): the token words are reused."""
+        if self._inflight is not None:
+            self.wait_tokens()
         tokens = [int(t) for t in tokens]
         if len(tokens) != self.batch:
             raise ValueError(f"expected {self.batch} tokens, got {len(tokens)}")
@@ -443,15 +479,25 @@ class A10Int8BatchDecoder(_DecoderBase):
         for b in range(self.batch):
             a.input_token_ids[b] = tokens[b]
             a.positions[b] = self._positions[b]
+        # a step that returns before its token stores (an early exit of the kernel) leaves the
+        # sentinel in place, which wait_tokens reports as a failure
+        self.output_tokens.fill_(TOKEN_PENDING)
         st = self._lib.mq_int8_decode_batch_step(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(self.device)))
         _lib.check(st, "batched decode step")
+        self._inflight = list(self._positions)
         self._positions = [p + 1 for p in self._positions]
 
     def wait_tokens(self) -> list:
-        """Wait for the last enqueued step and return its tokens."""
+        """Wait for the last enqueued step and return its tokens. A failed step (MQTimeoutError)
+        is undone: positions go back to the step's own and the workspace is re-initialised, so
+        the same tokens can be fed again."""
+        if self._inflight is None:
+            raise RuntimeError("no batched step in flight (call launch_step first)")
         torch.cuda.current_stream(self.device).synchronize()
         out = self.output_tokens.tolist()
+        before, self._inflight = self._inflight, None
         if min(out) < 0:
+            self._positions = before
             status = self._lib.mq_decode_check(self.workspace.data_ptr(),
                                                ctypes.c_void_p(_lib.stream_handle(self.device)))
             self._init_workspace()
@@ -463,6 +509,9 @@ class A10Int8BatchDecoder(_DecoderBase):
         return self.wait_tokens()
 
     def reset(self) -> None:
+        if self._inflight is not None:
+            torch.cuda.current_stream(self.device).synchronize()
+            self._inflight = None
         self._positions = [0] * self.batch
         self.k_cache.zero_()
         self.v_cache.zero_()

@@ -91,14 +91,16 @@ def test_batch_long_positions_match_oracle(mq, dev):
     _check_against_oracle(mq, long_model, prompts, 200)
 
 
-def _check_against_oracle(mq, model, prompts, steps):
-    """Teacher-forced parity of every sequence (module docstring)."""
+def _check_against_oracle(mq, model, prompts, steps, shared_ref=None):
+    """Teacher-forced parity of every sequence (module docstring). With `shared_ref` one
+    oracle instance is reset per sequence instead of built per sequence."""
     dec, toks = _run_batch(mq, model, prompts, steps, debug=True)
     assert dec.positions() == [8 + steps - 1] * len(prompts)
     hidden = dec.get_hidden().float().cpu().double()
     bad, worst, differ = [], 0.0, 0
     for b, p in enumerate(prompts):
-        ref = _ref(model)
+        ref = shared_ref if shared_ref is not None else _ref(model)
+        ref.reset()
         for i, t in enumerate(list(p) + toks[b][:-1]):
             logits = ref.step_logits(int(t))
             j = i - (len(p) - 1)
@@ -117,6 +119,32 @@ def _check_against_oracle(mq, model, prompts, steps):
     print(f"{len(prompts)} sequences x {steps} steps: {differ} tokens differ from the oracle's argmax, "
           f"largest logit deficit {worst:.2e} std", flush=True)
     assert not bad, bad
+
+
+@pytest.fixture(scope="module")
+def full_vocab(mq, dev):
+    """One Qwen3-1.7B-shape layer with the real 151,936-row vocabulary, and one oracle for it."""
+    cfg = mq.QWEN3_1_7B.with_(num_layers=1)
+    state, _ = mq.random_init_state(cfg, seed=8, norm_jitter=0.1)
+    qstate = mq.quantize_state(state, cfg, dev)
+    del state
+    packed = mq.pack_int8(qstate, cfg)
+    S = 32
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    model = (cfg, packed, cos, sin, S)
+    return model, _ref(model)
+
+
+@pytest.mark.parametrize("batch", [1, 16])
+def test_batch_full_vocabulary_matches_oracle(mq, dev, full_vocab, batch):
+    """At the real vocabulary each workgroup owns 593-594 LM-head rows: 38 tiles of 16 rows over
+    the 8 waves (5 per wave), a ragged last tile, the two-deep weight ring and the argmax merged
+    across waves and workgroups all run, which the 4,096-row models above never reach. Every
+    sequence is checked teacher-forced against the oracle as in the other batched tests."""
+    model, ref = full_vocab
+    prompts = _prompts(batch, model[0].vocab_size, seed=51)
+    print(f"full vocabulary, batch {batch}", flush=True)
+    _check_against_oracle(mq, model, prompts, STEPS, shared_ref=ref)
 
 
 def test_batch_hidden_state_matches_oracle(mq, dev, model):

@@ -307,3 +307,212 @@ def test_1p7b_int8_matches_oracle(variant, mq, dev):
                      cfg.num_layers, S)
     want, margins = greedy_generate(ref, prompt.tolist(), 12)
     assert toks == want, (toks, want, margins)
+
+
+def test_failed_step_resumes_without_reset(mq, small):
+    """A step whose in-kernel waits expire (spin limit of one poll; every kernel still exits)
+    raises MQTimeoutError and leaves the decoder at that step's position: feeding the same
+    token again continues the sequence, with no reset, to the fixture's tokens
+    (bench_int8.py:193-219 semantics for position and cache)."""
+    dec, d, prompt, cfg, _ = small
+    dec.reset()
+    for t in prompt[:3]:
+        dec.decode_step(int(t))
+    dec.set_spin_limit(1)
+    with pytest.raises(mq._lib.MQTimeoutError):
+        for t in prompt[3:]:
+            dec.decode_step(int(t))
+    dec.set_spin_limit(0)
+    resume = dec.position()
+    assert 3 <= resume < len(prompt), resume
+    tok = None
+    for t in prompt[resume:]:
+        tok = dec.decode_step(int(t))
+    out = [tok]
+    while len(out) < 12:
+        tok = dec.decode_step(tok)
+        out.append(tok)
+    assert out == d["tokens"][:12], (out, d["tokens"][:12])
+
+
+def test_pipelined_steps_keep_their_own_tokens(small):
+    """Steps launched back to back without reading their tokens (each has its own token word):
+    the last one's token is the fixture's, however many are in flight."""
+    dec, d, prompt, cfg, _ = small
+    dec.reset()
+    for t in prompt:
+        dec.launch_step(int(t))
+    assert dec.wait_token() == d["tokens"][0]
+    with pytest.raises(RuntimeError):
+        dec.wait_token()                        # nothing in flight any more
+
+
+def _reference_scratch(dev, H, I, n_partials=1184):
+    """The scratch buffers the reference's INT8 class allocates (bench_int8.py:176-188)."""
+    f32 = lambda n: torch.zeros(n, dtype=torch.float32, device=dev)
+    return {"hidden_buffer": torch.zeros(H, dtype=torch.bfloat16, device=dev), "g_activations": f32(H),
+            "g_residual": f32(H), "g_q": f32(2048), "g_k": f32(1024), "g_v": f32(1024), "g_attn_out": f32(2048),
+            "g_mlp_intermediate": f32(I), "g_normalized": f32(H), "block_max_vals": f32(n_partials),
+            "block_max_idxs": torch.zeros(n_partials, dtype=torch.int32, device=dev)}
+
+
+_SCRATCH_ORDER = ("hidden_buffer", "g_activations", "g_residual", "g_q", "g_k", "g_v", "g_attn_out",
+                  "g_mlp_intermediate", "g_normalized", "block_max_vals", "block_max_idxs")
+
+
+class _reference_dims:
+    """The reference-signature launchers assume Qwen3-0.6B unless told otherwise
+    (mq_reference_set_dims): declare a test model's dims for the duration of a block."""
+
+    def __init__(self, mq, cfg):
+        self.lib = mq._lib.load()
+        self.dims = mq._lib.ModelDims(cfg.hidden_size, cfg.intermediate_size, 16, 8, 128, cfg.vocab_size)
+
+    def __enter__(self):
+        assert self.lib.mq_reference_set_dims(ctypes.byref(self.dims)) == 0
+
+    def __exit__(self, *exc):
+        self.lib.mq_reference_set_dims(None)
+
+
+def _reference_drive(mq, dev, d, prompt, n, launch, scr):
+    """Prefill + greedy decode through a reference-signature launcher, the way
+    bench_int8.py:193-219 drives it (token buffer on the device, .item() per step)."""
+    out_tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    toks, seq, pos = [], list(prompt), 0
+    while len(toks) < n:
+        launch(int(seq[pos]), out_tok, pos, [scr[k].data_ptr() for k in _SCRATCH_ORDER])
+        assert mq._lib.last_error() == "", mq._lib.last_error()
+        tok = int(out_tok.item())
+        pos += 1
+        if pos >= len(prompt):
+            toks.append(tok)
+            seq.append(tok)
+    return toks
+
+
+def test_reference_int8_launcher_with_scratch_buffers(mq, dev, small):
+    """launch_a10_int8_decode called exactly as the reference's class calls it, every scratch
+    buffer set (sized as bench_int8.py allocates them): 32 fixture tokens, and the debug
+    buffers hold the last layer's values of the last step (run_benchmark.py:174-183)."""
+    dec, d, prompt, cfg, keep = small
+    embed, layers, scales, lm_q, lm_s, fnorm, cos, sin = keep
+    lib, S = mq._lib.load(), d["max_seq_len"]
+    kc = torch.zeros((cfg.num_layers, 8, S, 128), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    scr = _reference_scratch(dev, cfg.hidden_size, cfg.intermediate_size)
+    stream = ctypes.c_void_p(mq._lib.stream_handle(dev))
+
+    def launch(tok, out_tok, pos, ptrs):
+        lib.launch_a10_int8_decode(tok, out_tok.data_ptr(), embed.data_ptr(), dec.d_layer_weights.data_ptr(),
+                                   fnorm.data_ptr(), lm_q.data_ptr(), lm_s.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                   kc.data_ptr(), vc.data_ptr(), *ptrs, cfg.num_layers, pos, pos + 1, S,
+                                   dec.attn_scale, dec.d_layer_scales.data_ptr(), stream)
+
+    with _reference_dims(mq, cfg):
+        toks = _reference_drive(mq, dev, d, prompt, 32, launch, scr)
+    assert toks == d["tokens"], (toks, d["tokens"])
+    # the debug buffers of the last step against the oracle run over the same tokens
+    ref = _ref_for(small)
+    ref.reset()
+    for t in (list(prompt) + toks)[: len(prompt) + 31]:
+        ref.step_logits(int(t))
+    last = ref.last
+    for name, key in (("q", "g_q"), ("k", "g_k"), ("v", "g_v"), ("attn_out", "g_attn_out"),
+                      ("residual", "g_residual"), ("activations", "g_activations"),
+                      ("mlp_intermediate", "g_mlp_intermediate"), ("normalized", "g_normalized")):
+        a, b = scr[key].cpu().double(), last[name].double()
+        e = float(torch.linalg.norm(a - b) / torch.linalg.norm(b))
+        assert e < 1e-3, (name, e)
+    h = scr["hidden_buffer"].cpu().float().double()
+    assert float(torch.linalg.norm(h - last["hidden"]) / torch.linalg.norm(last["hidden"])) < 1e-3
+    # per-workgroup maxima: the largest is the step's token
+    bv, bi = scr["block_max_vals"][:256].cpu(), scr["block_max_idxs"][:256].cpu()
+    assert int(bi[int(torch.argmax(bv))]) == toks[-1]
+
+
+def test_reference_bf16_launcher(mq, dev):
+    """launch_a10_decode (a10_decode_kernel.cu:761-780) driven through ctypes for 8 prompt and 32
+    greedy steps, scratch buffers as a10_decode.py allocates them: the bf16 fixture's tokens."""
+    print("building qwen3_0.6b_bf16", flush=True)
+    dec, d, prompt, cfg, keep = _build(mq, dev, "qwen3_0.6b_bf16")
+    embed, layers, fnorm, lm, cos, sin = keep
+    lib, S = mq._lib.load(), d["max_seq_len"]
+    kc = torch.zeros((cfg.num_layers, 8, S, 128), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    scr = _reference_scratch(dev, cfg.hidden_size, cfg.intermediate_size)
+    stream = ctypes.c_void_p(mq._lib.stream_handle(dev))
+
+    def launch(tok, out_tok, pos, ptrs):
+        lib.launch_a10_decode(tok, out_tok.data_ptr(), embed.data_ptr(), dec.d_layer_weights.data_ptr(),
+                              fnorm.data_ptr(), lm.data_ptr(), cos.data_ptr(), sin.data_ptr(), kc.data_ptr(),
+                              vc.data_ptr(), *ptrs, cfg.num_layers, pos, pos + 1, S, dec.attn_scale, stream)
+
+    toks = _reference_drive(mq, dev, d, prompt, 32, launch, scr)
+    assert toks == d["tokens"], (toks, d["tokens"])
+    del dec, keep, kc, vc
+    torch.cuda.empty_cache()
+
+
+def test_reference_launcher_recovers_after_failed_step(mq, dev, small):
+    """A step of launch_a10_int8_decode whose waits expire stores token -1; the next call
+    reports that failure through mq_last_error(), re-initialises the library-owned workspace
+    and launches, so the sequence continues (the failed position is fed again)."""
+    dec, d, prompt, cfg, keep = small
+    embed, layers, scales, lm_q, lm_s, fnorm, cos, sin = keep
+    lib, S = mq._lib.load(), d["max_seq_len"]
+    kc = torch.zeros((cfg.num_layers, 8, S, 128), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    stream = ctypes.c_void_p(mq._lib.stream_handle(dev))
+    out_tok = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def step(tok, pos):
+        lib.launch_a10_int8_decode(tok, out_tok.data_ptr(), embed.data_ptr(), dec.d_layer_weights.data_ptr(),
+                                   fnorm.data_ptr(), lm_q.data_ptr(), lm_s.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                                   kc.data_ptr(), vc.data_ptr(), *([None] * 11), cfg.num_layers, pos, pos + 1, S,
+                                   dec.attn_scale, dec.d_layer_scales.data_ptr(), stream)
+        msg = mq._lib.last_error()
+        return int(out_tok.item()), msg
+
+    with _reference_dims(mq, cfg):
+        _recover_after_failed_step(lib, step, prompt, d)
+
+
+def _recover_after_failed_step(lib, step, prompt, d):
+    for pos in range(3):
+        _, msg = step(int(prompt[pos]), pos)
+        assert msg == "", msg
+    lib.mq_reference_set_spin_limit(1)
+    try:
+        tok, _ = step(int(prompt[3]), 3)
+    finally:
+        lib.mq_reference_set_spin_limit(0)
+    assert tok == -1
+    tok, msg = step(int(prompt[3]), 3)          # the failed position again
+    assert "previous step failed" in msg, msg
+    for pos in range(4, len(prompt)):
+        tok, msg = step(int(prompt[pos]), pos)
+        assert msg == "", msg
+    toks, pos = [tok], len(prompt)
+    while len(toks) < 8:
+        tok, msg = step(tok, pos)
+        assert msg == "", msg
+        toks.append(tok)
+        pos += 1
+    assert toks == d["tokens"][:8], (toks, d["tokens"][:8])
+
+
+@pytest.mark.parametrize("int8", [True, False])
+def test_a10decoder_generate(mq, dev, int8):
+    """A10Decoder (a10_decode.py:35-393) with seeded random weights: generate() prefills one
+    decode_step per prompt token and takes the last prefill output as the first generated token
+    (verify_correctness_a10.py:323-339), giving the config-1 / config-3 fixtures' 32 tokens."""
+    d = _fixture("qwen3_0.6b_int8" if int8 else "qwen3_0.6b_bf16")
+    print(f"A10Decoder int8={int8}", flush=True)
+    dec = mq.A10Decoder(seed=d["seed"], int8=int8, max_seq_len=d["max_seq_len"], device=dev)
+    ids, tok_s, times = dec.generate(d["prompt"], 32)
+    assert ids[:8] == d["prompt"]
+    assert ids[8:] == d["tokens"], (ids[8:], d["tokens"])
+    assert tok_s > 0 and len(times) == 31
+    del dec
+    torch.cuda.empty_cache()

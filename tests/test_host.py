@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol(mq):
     assert sorted(_lib.EXPORTED) == declared
     for name in declared:
         assert hasattr(lib, name), name
-    assert lib.mq_abi_version() == 2
+    assert lib.mq_abi_version() == 3
 
 
 def test_struct_layout_matches_c(tmp_path, mq):
