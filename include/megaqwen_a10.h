@@ -216,6 +216,16 @@ int mq_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t strea
 int mq_int8_decode_step(const mq_decode_args* args, hipStream_t stream);
 /* Same with bf16 weights (scales and lm_head_scale ignored). Replaces launch_a10_decode. */
 int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream);
+/* Allocation-free variant of mq_int8_decode_step. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * args->workspace is ignored: the step uses a library-held static device array
+ * of 4 MiB per device (every compiled dims fits: at most 1.8 MB), cleared by a
+ * fill kernel on `stream` at the start of every call, so no state carries over
+ * from one call to the next. The call allocates nothing (no hipMalloc, no
+ * library allocation). Every call on a device shares that device's array:
+ * calls that overlap on one device (other streams, other threads) race. */
+int mq_int8_decode_step_noalloc(const mq_decode_args* args, hipStream_t stream);
 /* Host-side wait for a token the kernel stores into host memory (pinned, e.g.
  * hipHostMalloc): spins until *token differs from `sentinel`, which the
  * caller wrote before the launch. MQ_OK, or MQ_ERR_TIMEOUT after timeout_us

@@ -102,6 +102,7 @@ _SIGNATURES = {
     "mq_workspace_init": (c_int, [c_void_p, c_size_t, c_void_p]),
     "mq_int8_decode_step": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mq_bf16_decode_step": (c_int, [POINTER(DecodeArgs), c_void_p]),
+    "mq_int8_decode_step_noalloc": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mq_decode_check": (c_int, [c_void_p, c_void_p]),
     "mq_wait_host_token": (c_int, [c_void_p, c_int, c_uint]),
     "mq_decode_set_variant": (c_int, [c_int]),

@@ -201,6 +201,32 @@ static int default_workspace(const mq_model_dims* dims, hipStream_t stream, void
     return MQ_OK;
 }
 
+// ---- allocation-free decode step --------------------------------------------------------
+// A file-scope device array serves as the workspace of mq_int8_decode_step_noalloc,
+// one copy per device. Host code uses the per-device address from
+// hipGetSymbolAddress (taken once per device on the first call there), never the
+// array's name, which on the host is only a stand-in for the symbol.
+constexpr size_t kStaticScratchBytes = 4u << 20;   // 4 MiB per device
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+static void* g_scratch_ptr[64];
+static std::mutex g_scratch_mu;
+
+static int static_scratch(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return set_error(MQ_ERR_HIP, "hipGetDevice failed");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr)
+            return set_error(MQ_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return MQ_OK;
+}
+
 // One step of a reference-signature launcher: validation and launch with the
 // library-owned status word. A message left by default_workspace() (the
 // previous step's failure) stays visible unless this step's own validation or
@@ -255,6 +281,32 @@ int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream) {
     int st = validate_decode(args, false, &s);
     if (st != MQ_OK) return st;
     return launch_decode(*args, s, false, stream);
+}
+
+int mq_int8_decode_step_noalloc(const mq_decode_args* args, hipStream_t stream) {
+    clear_error();
+    if (args == nullptr) return set_error(MQ_ERR_INVALID_ARGUMENT, "args is NULL");
+    DecodeShape s;
+    int st = shape_of(args->dims, &s);
+    if (st != MQ_OK) return st;
+    const size_t need = decode_workspace_bytes(s);
+    if (need > kStaticScratchBytes)
+        return set_error(MQ_ERR_UNSUPPORTED, "these dims need a %zu-byte workspace; the static scratch holds %zu", need,
+                         kStaticScratchBytes);
+    void* ws = nullptr;
+    st = static_scratch(&ws);
+    if (st != MQ_OK) return st;
+    mq_decode_args a = *args;
+    a.workspace = ws;
+    a.workspace_bytes = need;
+    st = validate_decode(&a, true, &s);
+    if (st != MQ_OK) return st;
+    // every call starts from a cleared scratch (a fill kernel on the caller's stream), so
+    // nothing a previous call left there, a failed step's state included, carries over
+    hipLaunchKernelGGL(ws_init_kernel, dim3(64), dim3(256), 0, stream, static_cast<uint64_t*>(ws), need / 8);
+    st = check_launch("ws_init_kernel");
+    if (st != MQ_OK) return st;
+    return launch_decode(a, s, true, stream);
 }
 
 int mq_wait_host_token(const volatile int* token, int sentinel, unsigned int timeout_us) {
