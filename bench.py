@@ -176,8 +176,13 @@ def run_decode(args, mq, torch):
         raise RuntimeError(f"decode step {toks.index(min(toks))} of the timed region failed: "
                            f"status {status}: {mq._lib.last_error()}")
     variant = mq.decode_variant(cfg.hidden_size, cfg.intermediate_size, int8=True)
-    kernel = {"xcd": "mq::decode_xcd_kernel<1024, 3072, mq::Int8W, false>",
+    kernel = {"async": "mq::decode_async_kernel<false>",
+              "xcd": "mq::decode_xcd_kernel<1024, 3072, mq::Int8W, false>",
               "flat": "mq::decode_kernel<1024, 3072, mq::Int8W, false>"}[variant]
+    arithmetic = ("matrix products as exact sums of int8 digits of a 55-bit fixed-point activation on the int8 "
+                  "matrix cores, recombined in fp64; other layer stages fp64; values rounded to fp32/bf16 where "
+                  "the reference stores them; LM head fp32") if variant == "async" else (
+                  "layer stages fp64 (rounded to fp32/bf16 where the reference stores), LM head fp32")
 
     # algorithmic bytes of each timed launch: positions PROMPT_LEN .. PROMPT_LEN+K-1
     bytes_total = sum(cfg.int8_step_bytes(cache_len=PROMPT_LEN + i + 1) for i in range(args.steps))
@@ -209,7 +214,7 @@ def run_decode(args, mq, torch):
         "config": {"workload": "config 1: INT8 greedy decode, Qwen3-0.6B architecture random-init (seed 0), "
                                "bs=1, 8-token random prompt prefilled untimed, K greedy steps timed",
                    "weights": "int8 per-output-channel (scale=bf16(absmax/127)); embed/norms/RoPE/KV bf16",
-                   "arithmetic": "layer stages fp64 (rounded to fp32/bf16 where the reference stores), LM head fp32",
+                   "arithmetic": arithmetic, "kernel_variant": variant,
                    "layers": cfg.num_layers, "hidden": cfg.hidden_size, "vocab": cfg.vocab_size,
                    "batch": 1, "prompt_len": PROMPT_LEN, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

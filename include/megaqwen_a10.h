@@ -247,11 +247,14 @@ size_t mq_batch_workspace_bytes(const mq_model_dims* dims);
 int mq_int8_decode_batch_step(const mq_batch_args* args, hipStream_t stream);
 
 /* Kernel variant for all following steps in this process: 0 = automatic
- * (default: the XCD-aware kernel when the workgroups of each residue class
- * g mod 8 share one XCD and the 8 classes cover the 8 XCDs, checked once per
- * device), 1 = single-level exchange kernel, 2 = XCD-aware. */
+ * (default: the async-wave kernel for INT8 steps of the Qwen3-0.6B shape up to
+ * 64 cached positions, otherwise the XCD-aware kernel, when the workgroups of
+ * each residue class g mod 8 share one XCD and the 8 classes cover the 8 XCDs,
+ * checked once per device), 1 = single-level exchange kernel, 2 = XCD-aware,
+ * 3 = async-wave (INT8 Qwen3-0.6B shape, cache_len <= 64 only). */
 int mq_decode_set_variant(int variant);
-/* The variant a step with these dims would use now (1 or 2), or -status. */
+/* The variant a short-context step (cache_len 1) with these dims would use now
+ * (1, 2 or 3), or -status. */
 int mq_decode_variant(const mq_model_dims* dims, int int8);
 
 /* ---- reference-signature entry points (drop-in for the CUDA launchers) --- */

@@ -395,7 +395,7 @@ int mq_decode_variant(const mq_model_dims* dims, int int8) {
     int st = shape_of(dims, &s);
     if (st != MQ_OK) return -st;
     const int v = decode_variant_in_use(s, int8 != 0);
-    return v == 1 || v == 2 ? v : -v;
+    return v >= 1 && v <= 3 ? v : -v;
 }
 
 void launch_a10_int8_decode(int input_token_id, int* output_token_id, const void* embed_weight,

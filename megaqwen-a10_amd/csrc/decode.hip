@@ -459,7 +459,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
 
 size_t decode_workspace_bytes(const DecodeShape& s) {
     const size_t a = layout_for(s.H, s.I, s.NQ, s.NKV, s.D).total, b = decode_xcd_workspace_bytes(s);
-    return a > b ? a : b;
+    const size_t c = decode_async_workspace_bytes(s);      // follows the other two regions (0 if unsupported)
+    return std::max(std::max(a, b), c);
 }
 
 // ---- kernel variant selection ----
@@ -478,7 +479,7 @@ static std::atomic<int> g_variant{0};
 static std::atomic<int> g_xcd_ok[64];     // 0 unknown, 1 placement verified, 2 not usable
 
 int set_decode_variant(int variant) {
-    if (variant < 0 || variant > 2) return set_error(MQ_ERR_INVALID_ARGUMENT, "variant %d not in {0,1,2}", variant);
+    if (variant < 0 || variant > 3) return set_error(MQ_ERR_INVALID_ARGUMENT, "variant %d not in {0,1,2,3}", variant);
     g_variant = variant;
     return MQ_OK;
 }
@@ -517,13 +518,24 @@ bool xcd_placement_ok() {
     return ok;
 }
 
-int decode_variant_in_use(const DecodeShape& s, bool int8) {
+// The kernel a step of these dims with `cache_len` cached positions uses: the async-wave
+// kernel (3) for the INT8 Qwen3-0.6B shape up to 64 positions, the XCD-aware kernel (2)
+// otherwise when the workgroup placement allows, else the single-level kernel (1).
+int decode_variant_for(const DecodeShape& s, bool int8, int cache_len) {
     const int v = g_variant.load();
     const bool have_xcd = decode_xcd_kernel_ptr(s, int8, false) != nullptr;
     if (v == 1) return 1;
     if (v == 2) return have_xcd ? 2 : set_error(MQ_ERR_UNSUPPORTED, "no XCD-aware kernel for these dims");
-    return (have_xcd && xcd_placement_ok()) ? 2 : 1;
+    if (v == 3)
+        return decode_async_supports(s, int8, cache_len)
+                   ? 3
+                   : set_error(MQ_ERR_UNSUPPORTED, "the async-wave kernel covers INT8 hidden 1024 / intermediate 3072 "
+                                                   "up to 64 cached positions (cache_len %d)", cache_len);
+    if (!(have_xcd && xcd_placement_ok())) return 1;
+    return decode_async_supports(s, int8, cache_len) ? 3 : 2;
 }
+
+int decode_variant_in_use(const DecodeShape& s, bool int8) { return decode_variant_for(s, int8, 1); }
 
 // All kNWG workgroups wait on each other, so they must be resident at once;
 // checked once per (kernel, device) from the occupancy calculator. The kernels
@@ -566,8 +578,8 @@ static int launch_t(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t 
 int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream, uint32_t* status_out) {
     if (a.num_layers > kMaxLayers)
         return set_error(MQ_ERR_UNSUPPORTED, "num_layers %d exceeds %d", a.num_layers, kMaxLayers);
-    const int variant = decode_variant_in_use(s, int8);
-    if (variant != 1 && variant != 2) return variant;
+    const int variant = decode_variant_for(s, int8, a.cache_len);
+    if (variant < 1 || variant > 3) return variant;
     // split attention (XCD kernel only): a slice of at most kMaxAttnLen positions per workgroup
     int split_min = a.attn_split_min == 0 ? kDefaultSplitMin : a.attn_split_min;
     split_min = split_min > 0 ? std::min(split_min, kMaxAttnLen + 1) : INT_MAX;
@@ -616,6 +628,7 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
                        a.block_max_idxs || a.trace;
 
     hipEvent_t t0 = static_cast<hipEvent_t>(a.timing_start), t1 = static_cast<hipEvent_t>(a.timing_stop);
+    if (variant == 3) return launch_decode_async(k, debug, stream, t0, t1);
     if (variant == 2) return launch_decode_xcd(k, s, int8, debug, stream, t0, t1);
     if (s.H == 1024 && s.I == 3072) {
         return int8 ? launch_t<1024, 3072, Int8W>(k, debug, stream, t0, t1) : launch_t<1024, 3072, Bf16W>(k, debug, stream, t0, t1);

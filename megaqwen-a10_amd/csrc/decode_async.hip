@@ -1,0 +1,969 @@
+// Asynchronous-wave persistent decode step: the INT8 Qwen3-0.6B shape (hidden
+// 1024, intermediate 3072, 16 / 8 heads of 128) up to 64 cached positions.
+//
+// Same computation (a10_int8_decode_kernel.cu:21-815) and the same work split
+// over workgroups as decode_xcd.hip: workgroup g runs on XCD x = HW_REG_XCC_ID
+// with rank r = g / 8; XCD x owns KV head x and its two query heads; rank r owns
+// 16 of the XCD's 512 q|k|v rows, O and down rows [32r, +32) and gate/up
+// channels [384x + 12r, +12). What differs is how a workgroup runs a layer.
+// Measured on MI355X, a workgroup barrier costs about 135 ns, an LDS
+// store-then-load round trip 57 ns, an fp64 wave sum 106 ns and a workgroup
+// fp64 sum 300 ns, so a layer built from barrier-separated stages spends most
+// of its time synchronising. Here:
+//
+//  * Waves 0-3 (compute waves) run the layer's critical path. They issue no
+//    weight loads (a wave's loads return in order, so a poll behind a weight
+//    batch would wait for the whole batch) and never meet at an s_barrier:
+//    they synchronise through LDS counters, and a sum over the four waves is
+//    finished by whichever arrives last.
+//  * Waves 4-7 (loader waves) copy each layer's weights, scales, norm gains and
+//    cached K/V rows straight into LDS (global_load_lds), a slot as soon as the
+//    compute waves are done with the previous layer's contents of it, and raise
+//    that slot's ready counter once their copies have landed.
+//  * The products run on the int8 matrix cores (v_mfma_i32_16x16x64_i8). A
+//    compute wave writes its slice of the activation vector as a 55-bit fixed
+//    point number (scale from the slice's largest exponent) in eight 7-bit
+//    digits, the top one signed; the digit sums are exact integers, recombined
+//    in fp64, so every stored value is the correctly rounded value of the
+//    reference's expression, as in the fp64 kernels.
+//  * Attention runs on the four compute waves: wave c takes query head c & 1
+//    over half c >> 1 of the positions (scores, softmax numerators and P V in
+//    fp64), and the halves are merged with their log-sum-exp weights.
+//
+// Per layer, compute wave c:
+//   A  hidden slice [256c, +256) (polled) and the sum of squares from the 32
+//      partial sums the hidden rows' producers published; RMSNorm, digits, 4
+//      MFMA steps over the rank's 16 q|k|v rows       -> last arriver: XCD-local words
+//   B  attention of head c & 1 over half c >> 1 of the positions; the four
+//      waves meet in LDS, and wave c merges attention dims [64c, +64)
+//   C  those dims x O rows [32r, +32), 2 MFMAs         -> last arriver: cross-XCD packed partials
+//   D  wave 0: the 8-XCD sum of its 32 rows, scale, residual
+//                                                      -> XCD-local act words + sum of squares
+//   E  act slice [256c, +256), RMSNorm, digits, 8 MFMAs over the 24 gate|up rows
+//                                                      -> last arriver: SwiGLU, XCD-local words
+//   F  c < 3: SwiGLU outputs [384x + 128c, +128) x down rows [32r, +32)
+//                                                      -> last arriver: cross-XCD packed partials
+//   G  wave 0: the 8-XCD sum, scale, residual, bf16    -> XCD-local hidden words + sum of squares
+// Then all eight waves run the final RMSNorm, the LM head and the argmax as in
+// decode_xcd.hip.
+#include "attention.h"
+
+#include <hip/hip_ext.h>
+
+namespace mq {
+
+namespace {
+
+constexpr int kAH = 1024, kAI = 3072, kAD = 128;
+constexpr int kAX = 8;                     // XCDs
+constexpr int kAIX = kAI / kAX;            // intermediate channels per XCD
+constexpr int kAMaxLen = 64;               // cache_len this kernel attends over
+constexpr int kCW = 4;                     // compute waves
+// digit plane pitch in words: 68, not 64, so that the 8 planes one A-operand read
+// touches start in different LDS banks
+constexpr int kPlane = 68;
+
+enum AStage { AS_QKV = 0, AS_ACT = 2, AS_MLP = 4, AS_HID = 5 };
+constexpr uint32_t kAStages = 8;
+
+// LDS counters (sync[]): ready and consumed per loader slot, arrival per combine
+enum ASlot { SL_A = 0, SL_B = 1, SL_C = 2, SL_E = 3, SL_F = 4, kSlots = 5 };
+constexpr int kReady = 0, kConsumed = 5, kArrive = 10;   // + slot / stage
+constexpr int kWindow = 15;          // layers whose attention compute wave 0 has begun
+enum AArr { AR_A = 0, AR_B = 1, AR_C = 2, AR_E = 3, AR_F = 4 };
+
+// An XCD's hidden (or act) block: the 1024 row words, then the 32 ranks' partial sums
+// of squares (low and high word each), so that one buffer load reaches both.
+constexpr int kVecWords = kAH + 64;
+struct ALayout {
+    size_t qkvx, hidx, actx, mlpx, po, pd, lmg, total;
+};
+// After the other two kernels' regions, so that the three can alternate on one workspace.
+constexpr ALayout alayout_for(size_t base) {
+    ALayout o{};
+    size_t off = base;
+    o.qkvx = off; off += round256((size_t)kAX * 512 * 8);
+    o.hidx = off; off += round256((size_t)kAX * kVecWords * 8);
+    o.actx = off; off += round256((size_t)kAX * kVecWords * 8);
+    o.mlpx = off; off += round256((size_t)kAX * kAIX * 8);
+    o.po = off; off += round256((size_t)kAX * kAH * 8);        // packed fp64 partials [xcd][row]
+    o.pd = off; off += round256((size_t)kAX * kAH * 8);
+    o.lmg = off; off += round256((size_t)kNWG * 2 * 8);
+    o.total = off;
+    return o;
+}
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+struct __align__(16) AsyncLds {
+    // loader slots: layer l's data, written while the compute waves run layer l - 1
+    uint4 wA[kCW][4][kWave];               // QKV: [wave][K step][lane] of the MFMA B operand
+    uint4 wC[kCW][2][kWave];               // O: [wave][row tile][lane]
+    uint4 wE[kCW][4][2][kWave];            // gate|up: [wave][K step][row tile][lane]
+    uint4 wF[3][2][2][kWave];              // down: [wave][K step][row tile][lane]
+    __align__(16) uint16_t kvk[kAMaxLen][kAD];           // cached K rows of positions [0, pos) (bf16)
+    __align__(16) uint16_t kvv[kAMaxLen][kAD];           // cached V rows
+    __align__(16) uint16_t lnA[kAH];                     // input RMSNorm gains
+    __align__(16) uint16_t lnE[kAH];                     // post-attention RMSNorm gains
+    uint16_t qkn[2][kAD];                  // q / k norm gains
+    float scA[16], scC[32], scE[24], scF[32];
+    uint16_t rope[2][kAD];                 // cos / sin at this position (once per step)
+    uint16_t fnorm[kAH];                   // final RMSNorm gains (once per step)
+    // compute waves
+    __align__(16) uint32_t dig[kCW][8][kPlane];          // digit planes of each wave's slice (byte k of plane d)
+    double qw[kCW][kAD];                   // each wave's rotated query
+    double pw[kCW][kAMaxLen / 2];          // scores, then softmax numerators, of each wave's positions
+    double acc[kCW][kAD];                  // P V partials
+    double ml[kCW][2];                     // (max score, numerator sum) of each wave
+    __align__(16) float hs[kAH];                         // the layer's input (bf16 values): stage D's residual
+    double part[4][kCW][32];               // per-wave row partials of the combines A, C, E, F
+    uint32_t sync[16];
+    // tail
+    __align__(16) float4 xs[kAH / 4];                    // final normalized vector, per-lane layout
+    double fss;                            // final sum of squares
+    float lm_v[kWaves];
+    int lm_i[kWaves];
+};
+
+// ---- LDS synchronisation --------------------------------------------------------------
+__device__ __forceinline__ uint32_t lds_load(const uint32_t* p) {
+    return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Compiler-level ordering only: LDS operations of one wave complete in order, so data
+// written before a counter update is in LDS when another wave sees the update.
+__device__ __forceinline__ void lds_order() { asm volatile("" ::: "memory"); }
+
+// Spins until *p >= target. Bounded: after `limit` polls it raises the abort flag and
+// returns (the step then reports MQ_ERR_TIMEOUT, as the exchange waits do).
+__device__ __forceinline__ void lds_wait(const uint32_t* p, uint32_t target, uint32_t limit, uint32_t* abort_flag) {
+    uint32_t n = 0;
+    while (lds_load(p) < target) {
+        __builtin_amdgcn_s_sleep(1);
+        if (++n >= limit) {
+            __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return;
+        }
+    }
+    lds_order();
+}
+__device__ __forceinline__ void lds_add(uint32_t* p, int lane) {
+    lds_order();
+    if (lane == 0) __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Arrival of one of the kCW compute waves at a combine; true for the last of the four.
+__device__ __forceinline__ bool last_arrival(uint32_t* p, int lane) {
+    lds_order();
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    old = __builtin_amdgcn_readfirstlane(old);
+    lds_order();
+    return (old % kCW) == kCW - 1;
+}
+
+// ---- digits ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, __float_as_uint(partner<1>(__uint_as_float(v))));
+    v = max(v, __float_as_uint(partner<2>(__uint_as_float(v))));
+    v = max(v, __float_as_uint(partner<4>(__uint_as_float(v))));
+    v = max(v, __float_as_uint(partner<8>(__uint_as_float(v))));
+    v = max(v, __float_as_uint(partner<16>(__uint_as_float(v))));
+    v = max(v, __float_as_uint(partner<32>(__uint_as_float(v))));
+    return v;
+}
+__device__ __forceinline__ uint32_t exp_field(float v) { return (__float_as_uint(v) >> 23) & 0xffu; }
+
+// X = trunc(v * 2^(181 - emax)) for fp32 v whose biased exponent is at most emax
+// (|X| < 2^55), as its eight digits: X = sum_d dig[d] 2^(49 - 7d), dig[0] in
+// [-64, 63], the others in [0, 127]. Zeros and denormals give X = 0.
+__device__ __forceinline__ void digits55(float v, uint32_t emax, int (&dig)[8]) {
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t e = (b >> 23) & 0xffu;
+    const uint64_t m = (uint64_t)((b & 0x7fffffu) | 0x800000u) << 31;
+    const uint32_t sh = emax - e;
+    uint64_t X = (e != 0u && sh < 56u) ? (m >> sh) : 0ull;
+    if (b >> 31) X = (uint64_t)(-(int64_t)X);
+    const uint32_t lo = (uint32_t)X, hi = (uint32_t)(X >> 32);
+    dig[0] = ((int)(hi << 8)) >> 25;                     // bits 49..55, sign-extended
+    dig[1] = (int)((hi >> 10) & 127u);
+    dig[2] = (int)((hi >> 3) & 127u);
+    dig[3] = (int)(__builtin_amdgcn_alignbit(hi, lo, 28) & 127u);
+    dig[4] = (int)((lo >> 21) & 127u);
+    dig[5] = (int)((lo >> 14) & 127u);
+    dig[6] = (int)((lo >> 7) & 127u);
+    dig[7] = (int)(lo & 127u);
+}
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+    const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+
+// Digit planes of a wave's slice, four consecutive elements per lane (element 4 lane + i).
+__device__ __forceinline__ void put_digits4(uint32_t (*planes)[kPlane], const float (&v)[4], uint32_t emax, int lane) {
+    int d[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) digits55(v[i], emax, d[i]);
+#pragma unroll
+    for (int p = 0; p < 8; ++p) planes[p][lane] = pack4(d[0][p], d[1][p], d[2][p], d[3][p]);
+}
+// Two consecutive elements per lane (element 2 lane + i).
+__device__ __forceinline__ void put_digits2(uint32_t (*planes)[kPlane], const float (&v)[2], uint32_t emax, int lane) {
+    int d[2][8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) digits55(v[i], emax, d[i]);
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+        reinterpret_cast<uint16_t*>(planes[p])[lane] = (uint16_t)(pack4(d[0][p], d[1][p], 0, 0) & 0xffffu);
+}
+// One element per lane (element lane).
+__device__ __forceinline__ void put_digits1(uint32_t (*planes)[kPlane], float v, uint32_t emax, int lane) {
+    int d[8];
+    digits55(v, emax, d);
+#pragma unroll
+    for (int p = 0; p < 8; ++p) reinterpret_cast<uint8_t*>(planes[p])[lane] = (uint8_t)(d[p] & 0xff);
+}
+// MFMA A operand of K step s: lane l holds digit plane l % 16 (zero past plane 7) at
+// elements [64 s + 16 (l / 16), +16).
+__device__ __forceinline__ i32x4_t a_frag(const uint32_t (*planes)[kPlane], int s, int lane) {
+    const int p = lane % 16;
+    if (p >= 8) return i32x4_t{0, 0, 0, 0};
+    const uint4 w = *reinterpret_cast<const uint4*>(&planes[p][16 * s + 4 * (lane / 16)]);
+    return i32x4_t{(int)w.x, (int)w.y, (int)w.z, (int)w.w};
+}
+__device__ __forceinline__ i32x4_t b_frag(const uint4& w) { return i32x4_t{(int)w.x, (int)w.y, (int)w.z, (int)w.w}; }
+__device__ __forceinline__ i32x4_t mfma_i8(i32x4_t a, i32x4_t b, i32x4_t c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+// Row value of an MFMA output tile: lane n (< 16) holds digit sums 0-3 of row n and lane
+// n + 16 sums 4-7; the exact integer sum_d S_d 2^(49 - 7d) is formed from the two 4-digit
+// halves (each exact in fp64) with one rounding, then scaled by 2^(emax - 181).
+__device__ __forceinline__ double tile_value(i32x4_t c, uint32_t emax) {
+    const double half = (double)(((int64_t)c[0] << 21) + ((int64_t)c[1] << 14) + ((int64_t)c[2] << 7) + (int64_t)c[3]);
+    const double lo = partner64<16>(half);
+    return ldexp(fma(half, 268435456.0, lo), (int)emax - 181);
+}
+
+// ---- polls ----------------------------------------------------------------------------
+// One round of polls over an XCD's vector block (kVecWords words at `block`, one tag):
+// elements [256 slice + 4 lane, +4) into v, and the 32 fp64 partial sums of squares
+// (lanes < 32 one each), returned summed in a fixed order (the same value in every lane).
+__device__ __forceinline__ double poll_slice(Waiter& wt, const uint64_t* block, uint32_t tag, int slice, int lane,
+                                             float (&v)[4]) {
+    uint32_t w[3] = {2u * (uint32_t)(128 * slice + 2 * lane), 2u * (uint32_t)(128 * slice + 2 * lane) + 2u,
+                     (uint32_t)kAH + 2u * (uint32_t)(lane & 31)};
+    float o[6];
+    wt.get_pairs<3>(XRegion(block, kVecWords), w, tag, o, lane < 32 ? 3 : 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = o[i];
+    double s = lane < 32 ? __longlong_as_double((long long)(((uint64_t)__float_as_uint(o[5]) << 32) |
+                                                            __float_as_uint(o[4])))
+                         : 0.0;
+    s += partner64<1>(s);
+    s += partner64<2>(s);
+    s += partner64<4>(s);
+    s += partner64<8>(s);
+    s += partner64<16>(s);
+    s += partner64<32>(s);             // lanes 32-63 hold 0: every lane gets the total
+    return s;
+}
+
+}  // namespace
+
+template <bool kDebug>
+__global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
+    constexpr int H = kAH, D = kAD;
+    constexpr ALayout kLay = alayout_for(xlayout_total(kAH, kAI));
+    __shared__ AsyncLds S;
+
+    const int g = blockIdx.x;
+    const int x = (int)hw_xcc_id();
+    const int r = g / kAX;
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave;
+    const int wave = tid / kWave;
+
+    WsHeader* hdr = reinterpret_cast<WsHeader*>(a.ws);
+    uint64_t* const qkvx = reinterpret_cast<uint64_t*>(a.ws + kLay.qkvx) + (size_t)x * 512;
+    uint64_t* const hidx = reinterpret_cast<uint64_t*>(a.ws + kLay.hidx) + (size_t)x * kVecWords;
+    uint64_t* const hss = hidx + H;
+    uint64_t* const actx = reinterpret_cast<uint64_t*>(a.ws + kLay.actx) + (size_t)x * kVecWords;
+    uint64_t* const ass = actx + H;
+    uint64_t* const mlpx = reinterpret_cast<uint64_t*>(a.ws + kLay.mlpx) + (size_t)x * kAIX;
+    uint64_t* const po = reinterpret_cast<uint64_t*>(a.ws + kLay.po);     // packed [8][H]
+    uint64_t* const pd = reinterpret_cast<uint64_t*>(a.ws + kLay.pd);
+    uint64_t* const lmg = reinterpret_cast<uint64_t*>(a.ws + kLay.lmg);
+
+    const uint32_t E = __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t AS = __hip_atomic_load(&hdr->asteps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t tps = kAStages * (uint32_t)a.L + 4u;
+    // tags end in binary 10 (the other kernels' in 01 and 11)
+    auto tag = [&](int l, int st) -> uint32_t { return ((E * tps + kAStages * (uint32_t)l + (uint32_t)st) << 2) | 2u; };
+    // one-bit tag of the packed cross-XCD words (po and pd are each written once per layer)
+    auto pbit = [&](int l) -> uint32_t { return (AS * (uint32_t)a.L + (uint32_t)l + 1u) & 1u; };
+    Waiter wt(&hdr->abort_flag, a.spin_limit);
+    const uint32_t lds_limit = a.spin_limit * 8u;
+    auto trace = [&](int l, int point) {
+        if (kDebug && a.trace != nullptr && tid == 0)
+            a.trace[((int64_t)l * kTracePoints + point) * kNWG + g] = __builtin_amdgcn_s_memrealtime();
+    };
+    if (x >= kAX) {
+        if (tid == 0) __hip_atomic_store(&hdr->abort_flag, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (tid < 16) S.sync[tid] = 0u;
+    __syncthreads();
+
+    const int pos = a.pos;                  // cache_len = pos + 1 <= kAMaxLen (checked by the host)
+    const int last = a.L - 1;
+    const int64_t kv_head_stride = (int64_t)a.S * D;
+
+    if (wave >= kCW) {
+        // ================================ loader waves ================================
+        // Loader d loads its share of layer l into registers once compute wave 0 has begun
+        // layer l - 1's attention (the compute waves then have no exchange poll in flight
+        // for a while, and a poll queued behind these loads would wait for them), writes
+        // each slot into LDS when the compute waves have released the previous layer's
+        // contents of it, and raises the slot's ready counter:
+        //   d = 0: slot A (the rank's q|k|v rows, input norm gains, row scales)
+        //   d = 1: slots C and F (O and down rows, their scales)
+        //   d = 2: slot E (gate|up rows, post-attention norm gains, scales)
+        //   d = 3: slot B (cached K and V rows of positions [0, pos), QK-norm gains), and
+        //          once per step this position's RoPE row and the final norm gains
+        const int d = wave - kCW;
+        auto await_free = [&](int slot, int l) {
+            lds_wait(&S.sync[kConsumed + slot], (uint32_t)(kCW * l), lds_limit, &hdr->abort_flag);
+        };
+        auto raise = [&](int slot, int l) {
+            lds_order();
+            if (lane == 0)
+                __hip_atomic_store(&S.sync[kReady + slot], (uint32_t)(l + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        };
+        auto ld32 = [&](const void* q) -> uint32_t { return *gview(static_cast<const uint32_t*>(q)); };
+        auto put32 = [&](void* base, int word, uint32_t v) { static_cast<uint32_t*>(base)[word] = v; };
+        if (d == 3) {
+            const uint32_t cw = ld32(a.cos_t + (int64_t)pos * D + 2 * lane);
+            const uint32_t sw = ld32(a.sin_t + (int64_t)pos * D + 2 * lane);
+            uint32_t fw[H / 128];
+#pragma unroll
+            for (int i = 0; i < H / 128; ++i) fw[i] = ld32(reinterpret_cast<const uint8_t*>(a.final_norm) + 256 * i + 4 * lane);
+            put32(S.rope[0], lane, cw);
+            put32(S.rope[1], lane, sw);
+#pragma unroll
+            for (int i = 0; i < H / 128; ++i) put32(S.fnorm, 64 * i + lane, fw[i]);
+        }
+        for (int l = 0; l < a.L; ++l) {
+            if (l > 0) lds_wait(&S.sync[kWindow], (uint32_t)l, lds_limit, &hdr->abort_flag);
+            const LayerWeights lw = a.lw[l];
+            const ScalePointers sp = a.sp[l];
+            if (d == 0) {
+                const uint8_t* base;
+                const float* sc;
+                int mrow0;
+                if (r < 16) { base = (const uint8_t*)lw.q_proj_weight; sc = sp.q_scale; mrow0 = 2 * x * D + 16 * r; }
+                else if (r < 24) { base = (const uint8_t*)lw.k_proj_weight; sc = sp.k_scale; mrow0 = x * D + 16 * (r - 16); }
+                else { base = (const uint8_t*)lw.v_proj_weight; sc = sp.v_scale; mrow0 = x * D + 16 * (r - 24); }
+                const uint8_t* rowp = base + (int64_t)(mrow0 + lane % 16) * H + 16 * (lane / 16);
+                uint4 w[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) w[i] = ldg16_stream(rowp + 256 * (i / 4) + 64 * (i % 4));
+                uint32_t gw[H / 128];
+#pragma unroll
+                for (int i = 0; i < H / 128; ++i) gw[i] = ld32(static_cast<const uint8_t*>(lw.input_layernorm_weight) + 256 * i + 4 * lane);
+                const uint32_t scv = lane < 16 ? ld32(sc + mrow0 + lane) : 0u;
+                await_free(SL_A, l);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) S.wA[i / 4][i % 4][lane] = w[i];
+#pragma unroll
+                for (int i = 0; i < H / 128; ++i) put32(S.lnA, 64 * i + lane, gw[i]);
+                if (lane < 16) put32(S.scA, lane, scv);
+                raise(SL_A, l);
+            } else if (d == 1) {
+                const uint8_t* ob = (const uint8_t*)lw.o_proj_weight + (int64_t)(32 * r + lane % 16) * 2048 + 256 * x +
+                                    16 * (lane / 16);
+                uint4 wc[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) wc[i] = ldg16_stream(ob + (int64_t)16 * (i % 2) * 2048 + 64 * (i / 2));
+                const uint32_t so = lane < 32 ? ld32(sp.o_scale + 32 * r + lane) : 0u;
+                const uint8_t* db = (const uint8_t*)lw.down_proj_weight + (int64_t)(32 * r + lane % 16) * kAI + kAIX * x +
+                                    16 * (lane / 16);
+                uint4 wf[12];
+#pragma unroll
+                for (int i = 0; i < 12; ++i)                 // i = (2 c + s) * 2 + t
+                    wf[i] = ldg16_stream(db + (int64_t)16 * (i % 2) * kAI + 64 * (i / 2));
+                const uint32_t sdv = lane < 32 ? ld32(sp.down_scale + 32 * r + lane) : 0u;
+                await_free(SL_C, l);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) S.wC[i / 2][i % 2][lane] = wc[i];
+                if (lane < 32) put32(S.scC, lane, so);
+                raise(SL_C, l);
+                await_free(SL_F, l);
+#pragma unroll
+                for (int i = 0; i < 12; ++i) S.wF[i / 4][(i / 2) % 2][i % 2][lane] = wf[i];
+                if (lane < 32) put32(S.scF, lane, sdv);
+                raise(SL_F, l);
+            } else if (d == 2) {
+                const int c0 = kAIX * x + 12 * r;
+                uint4 we[32];                                  // i = (4 c + s) * 2 + t; tile rows 24-31 zero
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int j = 16 * t + lane % 16;
+                    const uint8_t* rowp = (j < 12 ? (const uint8_t*)lw.gate_proj_weight + (int64_t)(c0 + j) * H
+                                                  : (const uint8_t*)lw.up_proj_weight + (int64_t)(c0 + min(j, 23) - 12) * H) +
+                                          16 * (lane / 16);
+#pragma unroll
+                    for (int k = 0; k < 16; ++k) {
+                        we[2 * k + t] = make_uint4(0, 0, 0, 0);
+                        if (j < 24) we[2 * k + t] = ldg16_stream(rowp + 64 * k);
+                    }
+                }
+                uint32_t gw[H / 128];
+#pragma unroll
+                for (int i = 0; i < H / 128; ++i)
+                    gw[i] = ld32(static_cast<const uint8_t*>(lw.post_attn_layernorm_weight) + 256 * i + 4 * lane);
+                const uint32_t scv = lane < 12 ? ld32(sp.gate_scale + c0 + lane)
+                                   : lane < 24 ? ld32(sp.up_scale + c0 + lane - 12) : 0u;
+                await_free(SL_E, l);
+#pragma unroll
+                for (int k = 0; k < 16; ++k)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) S.wE[k / 4][k % 4][t][lane] = we[2 * k + t];
+#pragma unroll
+                for (int i = 0; i < H / 128; ++i) put32(S.lnE, 64 * i + lane, gw[i]);
+                if (lane < 24) put32(S.scE, lane, scv);
+                raise(SL_E, l);
+            } else {
+                // K rows keep their 16-byte chunks XOR-permuted by row (chunk g of row j at
+                // g ^ (j % 16)), so the 8 rows the score loop reads at once hit different banks
+                const int64_t cb = ((int64_t)l * kAX + x) * kv_head_stride;
+                uint4 rk[kAMaxLen / 4], rv[kAMaxLen / 4];
+#pragma unroll
+                for (int i = 0; i < kAMaxLen / 4; ++i) {
+                    const int j = 4 * i + lane / 16;
+                    rk[i] = make_uint4(0, 0, 0, 0);
+                    rv[i] = make_uint4(0, 0, 0, 0);
+                    if (j < pos) {
+                        rk[i] = ldg16(a.kc + cb + (int64_t)j * D + 8 * (lane % 16));
+                        rv[i] = ldg16(a.vc + cb + (int64_t)j * D + 8 * (lane % 16));
+                    }
+                }
+                const uint32_t qn = ld32(static_cast<const uint8_t*>(lw.q_norm_weight) + 4 * lane);
+                const uint32_t kn = ld32(static_cast<const uint8_t*>(lw.k_norm_weight) + 4 * lane);
+                await_free(SL_B, l);
+#pragma unroll
+                for (int i = 0; i < kAMaxLen / 4; ++i) {
+                    const int j = 4 * i + lane / 16;
+                    if (j < pos) {
+                        reinterpret_cast<uint4*>(S.kvk[j])[(lane % 16) ^ (j % 16)] = rk[i];
+                        reinterpret_cast<uint4*>(S.kvv[j])[lane % 16] = rv[i];
+                    }
+                }
+                put32(S.qkn[0], lane, qn);
+                put32(S.qkn[1], lane, kn);
+                raise(SL_B, l);
+            }
+        }
+    } else {
+        // =============================== compute waves ================================
+        const int c = wave;
+        float act_reg = 0.0f;                   // wave 0: this rank's residual row (lane % 32) from stage D
+        for (int l = 0; l < a.L; ++l) {
+            // ---------------- A: RMSNorm + QKV ----------------
+            float hv[4];
+            double ssq;
+            if (l == 0) {
+                typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+                const u32x2_t e4 = *(const __attribute__((address_space(1))) u32x2_t*)(a.embed + (int64_t)a.token * H +
+                                                                                        256 * c + 4 * lane);
+                hv[0] = bf16_bits_to_f32(e4.x & 0xffffu); hv[1] = bf16_bits_to_f32(e4.x >> 16);
+                hv[2] = bf16_bits_to_f32(e4.y & 0xffffu); hv[3] = bf16_bits_to_f32(e4.y >> 16);
+                const uint4* er = reinterpret_cast<const uint4*>(a.embed + (int64_t)a.token * H);
+                const uint4 u0 = ldg16(er + 2 * lane), u1 = ldg16(er + 2 * lane + 1);
+                const uint32_t wv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+                double s = 0.0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const double lo = bf16_bits_to_f32(wv[i] & 0xffffu), hi = bf16_bits_to_f32(wv[i] >> 16);
+                    s = fma(lo, lo, s);
+                    s = fma(hi, hi, s);
+                }
+                ssq = wave_sum64(s);
+            } else {
+                ssq = poll_slice(wt, hidx, tag(l - 1, AS_HID), c, lane, hv);
+            }
+            *reinterpret_cast<float4*>(&S.hs[256 * c + 4 * lane]) = make_float4(hv[0], hv[1], hv[2], hv[3]);
+            trace(l, 0);
+            const double rstd = rms_scale(ssq, H, kEps);
+            lds_wait(&S.sync[kReady + SL_A], (uint32_t)(l + 1), lds_limit, &hdr->abort_flag);
+            float nv[4];
+            {
+                const uint2 gw = *reinterpret_cast<const uint2*>(&S.lnA[256 * c + 4 * lane]);
+                const float gl[4] = {bf16_bits_to_f32(gw.x & 0xffffu), bf16_bits_to_f32(gw.x >> 16),
+                                     bf16_bits_to_f32(gw.y & 0xffffu), bf16_bits_to_f32(gw.y >> 16)};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) nv[i] = (float)((double)hv[i] * rstd * (double)gl[i]);
+            }
+            {
+                uint32_t em = max(max(exp_field(nv[0]), exp_field(nv[1])), max(exp_field(nv[2]), exp_field(nv[3])));
+                em = wave_max_u32(em);
+                put_digits4(S.dig[c], nv, em, lane);
+                lds_order();
+                i32x4_t acc = {0, 0, 0, 0};
+#pragma unroll
+                for (int s = 0; s < 4; ++s) acc = mfma_i8(a_frag(S.dig[c], s, lane), b_frag(S.wA[c][s][lane]), acc);
+                const double v = tile_value(acc, em);
+                if (lane < 16) S.part[0][c][lane] = v;
+            }
+            if (last_arrival(&S.sync[kArrive + AR_A], lane)) {
+                if (lane < 16) {
+                    const double* P = &S.part[0][0][lane];
+                    const double v = ((P[0] + P[32]) + (P[64] + P[96])) *
+                                     (double)S.scA[lane];
+                    ll_put_xcd(&qkvx[16 * r + lane], __float_as_uint((float)v), tag(l, AS_QKV));
+                }
+            }
+            lds_add(&S.sync[kConsumed + SL_A], lane);
+            trace(l, 1);
+
+            // ---------------- B: attention ----------------
+            {
+                const int h = c & 1, half = c >> 1;
+                const int n = pos + 1;
+                const int hn = (n + 1) / 2;
+                const int j0 = half ? hn : 0, j1 = half ? n : hn;
+                const int np = j1 - j0;
+                const bool owner = j0 <= pos && pos < j1;
+                float qv[2], kv2[2] = {0.0f, 0.0f}, vv[2] = {0.0f, 0.0f};
+                {
+                    // q of head h, and k and v for the wave whose half holds this position
+                    uint32_t w[3] = {2u * (uint32_t)(64 * h + lane), 2u * (uint32_t)(128 + lane), 2u * (uint32_t)(192 + lane)};
+                    float o[6];
+                    wt.get_pairs<3>(XRegion(qkvx, 512), w, tag(l, AS_QKV), o, owner ? 3 : 1);
+                    qv[0] = o[0]; qv[1] = o[1];
+                    kv2[0] = o[2]; kv2[1] = o[3];
+                    vv[0] = o[4]; vv[1] = o[5];
+                }
+                if (c == 0) {
+                    trace(l, 2);
+                    if (lane == 0)
+                        __hip_atomic_store(&S.sync[kWindow], (uint32_t)(l + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+                lds_wait(&S.sync[kReady + SL_B], (uint32_t)(l + 1), lds_limit, &hdr->abort_flag);
+                // QK-norm and RoPE (lane holds dims 2 lane, 2 lane + 1; the rotation partner
+                // dims i -+ 64 sit in lane -+ 32)
+                const int i0 = 2 * lane;
+                const double c0r = bf16_bits_to_f32(S.rope[0][i0]), c1r = bf16_bits_to_f32(S.rope[0][i0 + 1]);
+                const double s0r = bf16_bits_to_f32(S.rope[1][i0]), s1r = bf16_bits_to_f32(S.rope[1][i0 + 1]);
+                auto norm_rope = [&](const float (&in)[2], const uint16_t* gain, float (&out)[2]) {
+                    const double x0 = in[0], x1 = in[1];
+                    const double ss = wave_sum64(fma(x0, x0, x1 * x1));
+                    const double sc = rms_scale(ss, D, kEps);
+                    const double y0 = x0 * sc * (double)bf16_bits_to_f32(gain[i0]);
+                    const double y1 = x1 * sc * (double)bf16_bits_to_f32(gain[i0 + 1]);
+                    const double p0 = partner64<32>(y0), p1 = partner64<32>(y1);
+                    if (lane < 32) {
+                        out[0] = (float)(y0 * c0r - p0 * s0r);
+                        out[1] = (float)(y1 * c1r - p1 * s1r);
+                    } else {
+                        out[0] = (float)(p0 * s0r + y0 * c0r);
+                        out[1] = (float)(p1 * s1r + y1 * c1r);
+                    }
+                };
+                float qr[2];
+                norm_rope(qv, S.qkn[0], qr);
+                S.qw[c][i0] = qr[0];
+                S.qw[c][i0 + 1] = qr[1];
+                const bool dbg = kDebug && r == 0 && l == last;
+                if (dbg && half == 0 && a.dbg_q) {
+                    a.dbg_q[(2 * x + h) * D + i0] = qr[0];
+                    a.dbg_q[(2 * x + h) * D + i0 + 1] = qr[1];
+                }
+                if (owner) {
+                    float kr[2];
+                    norm_rope(kv2, S.qkn[1], kr);
+                    const uint32_t kw = f32_to_bf16_bits(kr[0]) | (f32_to_bf16_bits(kr[1]) << 16);
+                    const uint32_t vw = f32_to_bf16_bits(vv[0]) | (f32_to_bf16_bits(vv[1]) << 16);
+                    reinterpret_cast<uint32_t*>(S.kvk[pos])[4 * ((lane / 4) ^ (pos % 16)) + lane % 4] = kw;
+                    reinterpret_cast<uint32_t*>(S.kvv[pos])[lane] = vw;
+                    if (r == 0 && h == 0) {
+                        const int64_t cur = ((int64_t)l * kAX + x) * kv_head_stride + (int64_t)pos * D;
+                        reinterpret_cast<uint32_t*>(a.kc + cur)[lane] = kw;
+                        reinterpret_cast<uint32_t*>(a.vc + cur)[lane] = vw;
+                        if (dbg && a.dbg_k) { a.dbg_k[x * D + i0] = kr[0]; a.dbg_k[x * D + i0 + 1] = kr[1]; }
+                        if (dbg && a.dbg_v) { a.dbg_v[x * D + i0] = vv[0]; a.dbg_v[x * D + i0 + 1] = vv[1]; }
+                    }
+                }
+                lds_order();
+                // scores: 8 lanes per position, each over dims [16 (lane % 8), +16)
+                double mloc = -INFINITY;
+                {
+                    double qd[16];
+                    const int db = 16 * (lane % 8);
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) qd[e] = S.qw[c][db + e];
+                    for (int t = 0; 8 * t < np; ++t) {
+                        const int jl = 8 * t + lane / 8;
+                        double d0 = 0.0, d1 = 0.0;
+                        if (jl < np) {
+                            const int row = j0 + jl;
+                            const uint4* kp = reinterpret_cast<const uint4*>(S.kvk[row]);
+                            const uint4 k0 = kp[(2 * (lane % 8)) ^ (row % 16)], k1 = kp[(2 * (lane % 8) + 1) ^ (row % 16)];
+                            const uint32_t kw8[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) {
+                                d0 = fma(qd[2 * e], (double)bf16_bits_to_f32(kw8[e] & 0xffffu), d0);
+                                d1 = fma(qd[2 * e + 1], (double)__uint_as_float(kw8[e] & 0xffff0000u), d1);
+                            }
+                        }
+                        const double sv = group_sum64<8>(d0 + d1) * (double)a.attn_scale;
+                        if (jl < np) {
+                            if ((lane % 8) == 0) S.pw[c][jl] = sv;
+                            mloc = fmax(mloc, sv);
+                        }
+                    }
+                }
+                mloc = wave_max64(mloc);
+                lds_order();
+                // softmax numerators of the wave's positions (lane jl), then P V: lane l
+                // accumulates dims 2l, 2l+1 with the numerators read back from LDS
+                if (lane < np) S.pw[c][lane] = exp(S.pw[c][lane] - mloc);
+                lds_order();
+                double a0 = 0.0, a1 = 0.0, ls = 0.0;
+                for (int jb = 0; jb < np; jb += 4) {
+                    double pp[4];
+                    uint32_t vw[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int jl = min(jb + u, np - 1);
+                        pp[u] = S.pw[c][jl];
+                        vw[u] = reinterpret_cast<const uint32_t*>(S.kvv[j0 + jl])[lane];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        if (jb + u < np) {
+                            a0 = fma(pp[u], (double)bf16_bits_to_f32(vw[u] & 0xffffu), a0);
+                            a1 = fma(pp[u], (double)__uint_as_float(vw[u] & 0xffff0000u), a1);
+                            ls += pp[u];
+                        }
+                    }
+                }
+                S.acc[c][i0] = a0;
+                S.acc[c][i0 + 1] = a1;
+                if (lane == 0) { S.ml[c][0] = np > 0 ? mloc : -INFINITY; S.ml[c][1] = ls; }
+                // all four waves' partials in LDS
+                lds_add(&S.sync[kArrive + AR_B], lane);
+                lds_wait(&S.sync[kArrive + AR_B], (uint32_t)(kCW * (l + 1)), lds_limit, &hdr->abort_flag);
+                lds_add(&S.sync[kConsumed + SL_B], lane);
+            }
+            // merge: wave c takes attention dims [64c, +64) (head c / 2), from the partials of
+            // waves c / 2 (first half of the positions) and c / 2 + 2 (second half)
+            float ao;
+            {
+                const int hh = c >> 1, dim = 64 * (c & 1) + lane;
+                const double ma = S.ml[hh][0], mb = S.ml[hh + 2][0];
+                const double M = fmax(ma, mb);
+                const double wa = ma == -INFINITY ? 0.0 : exp(ma - M);
+                const double wb = mb == -INFINITY ? 0.0 : exp(mb - M);
+                const double num = fma(wa, S.acc[hh][dim], wb * S.acc[hh + 2][dim]);
+                const double den = fma(wa, S.ml[hh][1], wb * S.ml[hh + 2][1]);
+                ao = (float)(num * rcp_nr(den));
+                if (kDebug && r == 0 && l == last && a.dbg_attn) a.dbg_attn[2 * D * x + 64 * c + lane] = ao;
+            }
+            if (c == 0) trace(l, 3);
+
+            // ---------------- C: O partial over this XCD's attention dims ----------------
+            lds_wait(&S.sync[kReady + SL_C], (uint32_t)(l + 1), lds_limit, &hdr->abort_flag);
+            {
+                const uint32_t em = wave_max_u32(exp_field(ao));
+                put_digits1(S.dig[c], ao, em, lane);
+                lds_order();
+                const i32x4_t af = a_frag(S.dig[c], 0, lane);
+                const i32x4_t t0 = mfma_i8(af, b_frag(S.wC[c][0][lane]), i32x4_t{0, 0, 0, 0});
+                const i32x4_t t1 = mfma_i8(af, b_frag(S.wC[c][1][lane]), i32x4_t{0, 0, 0, 0});
+                const double v0 = tile_value(t0, em), v1 = tile_value(t1, em);
+                if (lane < 16) { S.part[1][c][lane] = v0; S.part[1][c][16 + lane] = v1; }
+            }
+            if (last_arrival(&S.sync[kArrive + AR_C], lane)) {
+                if (lane < 32) {
+                    const double* P = &S.part[1][0][lane];
+                    const double v = (P[0] + P[32]) + (P[64] + P[96]);
+                    ll_put64(&po[(size_t)x * H + 32 * r + lane], pack_tagged(v, pbit(l)));
+                }
+            }
+            if (c != 0) lds_add(&S.sync[kConsumed + SL_C], lane);
+            if (c == 0) trace(l, 4);
+
+            // ---------------- D (wave 0): reduce the O partials -> residual rows ----------------
+            if (c == 0) {
+                const int rr = lane % 32, q = lane / 32;
+                double v4[4];
+                wt.get_packed<4>(po + (size_t)(4 * q) * H + 32 * r + rr, H, pbit(l), v4);
+                const double s4 = (v4[0] + v4[1]) + (v4[2] + v4[3]);
+                const double tot = s4 + partner64<32>(s4);
+                act_reg = (float)(tot * (double)S.scC[rr] + (double)S.hs[32 * r + rr]);
+                lds_add(&S.sync[kConsumed + SL_C], lane);
+                if (lane < 32) ll_put_xcd(&actx[32 * r + lane], __float_as_uint(act_reg), tag(l, AS_ACT));
+                double ss = lane < 32 ? (double)act_reg * (double)act_reg : 0.0;
+                ss += partner64<1>(ss);
+                ss += partner64<2>(ss);
+                ss += partner64<4>(ss);
+                ss += partner64<8>(ss);
+                ss += partner64<16>(ss);
+                if (lane == 0) {
+                    const uint64_t u = (uint64_t)__double_as_longlong(ss);
+                    ll_put_xcd(&ass[2 * r], (uint32_t)u, tag(l, AS_ACT));
+                    ll_put_xcd(&ass[2 * r + 1], (uint32_t)(u >> 32), tag(l, AS_ACT));
+                }
+                trace(l, 5);
+            }
+
+            // ---------------- E: RMSNorm + gate/up + SwiGLU ----------------
+            {
+                float av[4];
+                const double ss = poll_slice(wt, actx, tag(l, AS_ACT), c, lane, av);
+                const double rstd2 = rms_scale(ss, H, kEps);
+                lds_wait(&S.sync[kReady + SL_E], (uint32_t)(l + 1), lds_limit, &hdr->abort_flag);
+                const uint2 gw = *reinterpret_cast<const uint2*>(&S.lnE[256 * c + 4 * lane]);
+                const float gl[4] = {bf16_bits_to_f32(gw.x & 0xffffu), bf16_bits_to_f32(gw.x >> 16),
+                                     bf16_bits_to_f32(gw.y & 0xffffu), bf16_bits_to_f32(gw.y >> 16)};
+                float nv2[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) nv2[i] = (float)((double)av[i] * rstd2 * (double)gl[i]);
+                if (kDebug && g == 0 && l == last) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (a.dbg_act) a.dbg_act[256 * c + 4 * lane + i] = nv2[i];
+                        if (a.dbg_resid) a.dbg_resid[256 * c + 4 * lane + i] = av[i];
+                    }
+                }
+                uint32_t em = max(max(exp_field(nv2[0]), exp_field(nv2[1])), max(exp_field(nv2[2]), exp_field(nv2[3])));
+                em = wave_max_u32(em);
+                put_digits4(S.dig[c], nv2, em, lane);
+                lds_order();
+                i32x4_t t0 = {0, 0, 0, 0}, t1 = {0, 0, 0, 0};
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const i32x4_t af = a_frag(S.dig[c], s, lane);
+                    t0 = mfma_i8(af, b_frag(S.wE[c][s][0][lane]), t0);
+                    t1 = mfma_i8(af, b_frag(S.wE[c][s][1][lane]), t1);
+                }
+                const double v0 = tile_value(t0, em), v1 = tile_value(t1, em);
+                if (lane < 16) { S.part[2][c][lane] = v0; S.part[2][c][16 + lane] = v1; }
+            }
+            if (last_arrival(&S.sync[kArrive + AR_E], lane)) {
+                if (lane < 12) {
+                    const double* P = &S.part[2][0][lane];
+                    const double gs = ((P[0] + P[32]) + (P[64] + P[96])) * (double)S.scE[lane];
+                    const double us = ((P[12] + P[44]) + (P[76] + P[108])) * (double)S.scE[12 + lane];
+                    const float m = (float)silu_mul(gs, us);
+                    ll_put_xcd(&mlpx[12 * r + lane], __float_as_uint(m), tag(l, AS_MLP));
+                    if (kDebug && l == last && a.dbg_mlp) a.dbg_mlp[kAIX * x + 12 * r + lane] = m;
+                }
+            }
+            lds_add(&S.sync[kConsumed + SL_E], lane);
+            if (c == 0) trace(l, 6);
+
+            // ---------------- F: down partial over this XCD's channels ----------------
+            if (c < 3) {
+                float mv[2];
+                uint32_t w[1] = {2u * (uint32_t)(64 * c + lane)};
+                wt.get_pairs<1>(XRegion(mlpx, kAIX), w, tag(l, AS_MLP), mv);
+                if (c == 0) trace(l, 7);
+                lds_wait(&S.sync[kReady + SL_F], (uint32_t)(l + 1), lds_limit, &hdr->abort_flag);
+                const uint32_t em = wave_max_u32(max(exp_field(mv[0]), exp_field(mv[1])));
+                put_digits2(S.dig[c], mv, em, lane);
+                lds_order();
+                i32x4_t t0 = {0, 0, 0, 0}, t1 = {0, 0, 0, 0};
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const i32x4_t af = a_frag(S.dig[c], s, lane);
+                    t0 = mfma_i8(af, b_frag(S.wF[c][s][0][lane]), t0);
+                    t1 = mfma_i8(af, b_frag(S.wF[c][s][1][lane]), t1);
+                }
+                const double v0 = tile_value(t0, em), v1 = tile_value(t1, em);
+                if (lane < 16) { S.part[3][c][lane] = v0; S.part[3][c][16 + lane] = v1; }
+            }
+            if (last_arrival(&S.sync[kArrive + AR_F], lane)) {      // wave 3 has no F slice: waves 0-2 sum
+                if (lane < 32) {
+                    const double* P = &S.part[3][0][lane];
+                    const double v = (P[0] + P[32]) + P[64];
+                    ll_put64(&pd[(size_t)x * H + 32 * r + lane], pack_tagged(v, pbit(l)));
+                }
+            }
+            if (c != 0) lds_add(&S.sync[kConsumed + SL_F], lane);
+            if (c == 0) trace(l, 8);
+
+            // ---------------- G (wave 0): reduce the down partials -> hidden rows ----------------
+            if (c == 0) {
+                const int rr = lane % 32, q = lane / 32;
+                double v4[4];
+                wt.get_packed<4>(pd + (size_t)(4 * q) * H + 32 * r + rr, H, pbit(l), v4);
+                const double s4 = (v4[0] + v4[1]) + (v4[2] + v4[3]);
+                const double tot = s4 + partner64<32>(s4);
+                const float hb = round_bf16((float)(tot * (double)S.scF[rr] + (double)act_reg));
+                lds_add(&S.sync[kConsumed + SL_F], lane);
+                if (lane < 32) ll_put_xcd(&hidx[32 * r + lane], __float_as_uint(hb), tag(l, AS_HID));
+                double ss = lane < 32 ? (double)hb * (double)hb : 0.0;
+                ss += partner64<1>(ss);
+                ss += partner64<2>(ss);
+                ss += partner64<4>(ss);
+                ss += partner64<8>(ss);
+                ss += partner64<16>(ss);
+                if (lane == 0) {
+                    const uint64_t u = (uint64_t)__double_as_longlong(ss);
+                    ll_put_xcd(&hss[2 * r], (uint32_t)u, tag(l, AS_HID));
+                    ll_put_xcd(&hss[2 * r + 1], (uint32_t)(u >> 32), tag(l, AS_HID));
+                }
+                trace(l, 9);
+            }
+        }
+        // the final hidden vector and its sum of squares
+        {
+            float hv[4];
+            const double ssq = poll_slice(wt, hidx, tag(last, AS_HID), c, lane, hv);
+            *reinterpret_cast<float4*>(&S.hs[256 * c + 4 * lane]) = make_float4(hv[0], hv[1], hv[2], hv[3]);
+            if (c == 0 && lane == 0) S.fss = ssq;
+            if (kDebug && g == 0 && a.dbg_hidden) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) a.dbg_hidden[256 * c + 4 * lane + i] = (uint16_t)f32_to_bf16_bits(hv[i]);
+            }
+        }
+    }
+
+    // ================= final RMSNorm + LM head + greedy argmax (all waves) =================
+    {
+        constexpr int CH = H / (64 * 16);   // 1 KB chunks per row
+        constexpr int RB = 8 / CH;
+        constexpr int R = RB * CH;
+        constexpr int span = kWave / RB;
+        const int r0 = (int)((int64_t)a.V * g / kNWG);
+        const int r1 = (int)((int64_t)a.V * (g + 1) / kNWG);
+        const int nb = (r1 - r0 + RB - 1) / RB;
+        const int64_t rowbytes = H;
+        uint4 cur[R], nxt[R];
+        float scur = 0.0f, snxt = 0.0f;
+        auto fetch = [&](int b, uint4* dst, float& s) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int row = r0 + b * RB + i / CH;
+                dst[i] = make_uint4(0, 0, 0, 0);
+                if (row < r1) dst[i] = ldg16(a.lm_w + row * rowbytes + (i % CH) * 1024 + lane * 16);
+            }
+            const int myrow = r0 + b * RB + lane / span;
+            s = 1.0f;
+            if (myrow < r1) s = gview(a.lm_s)[myrow];
+        };
+        int b = wave;
+        if (b < nb) fetch(b, cur, scur);
+        __syncthreads();                    // final hidden vector and sum of squares in LDS; loaders done
+        const double rstd = rms_scale(S.fss, H, kEps);
+        float* xsf = reinterpret_cast<float*>(S.xs);
+#pragma unroll
+        for (int i = 0; i < H / kThreads; ++i) {
+            const int k = tid + i * kThreads;
+            const float nv = (float)((double)S.hs[k] * rstd * (double)bf16_bits_to_f32(S.fnorm[k]));
+            xsf[xs_index<Int8W>(k)] = nv;
+            if (kDebug && g == 0 && a.dbg_norm) a.dbg_norm[k] = nv;
+        }
+        __syncthreads();
+        trace(a.L, 0);
+
+        float best_v = -INFINITY;
+        int best_i = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < R; ++i) nxt[i] = make_uint4(0, 0, 0, 0);
+        for (; b < nb; b += kWaves) {
+            if (b + kWaves < nb) fetch(b + kWaves, nxt, snxt);
+            float accv[R];
+#pragma unroll
+            for (int i = 0; i < R; ++i) accv[i] = dot_frag<Int8W>(cur[i], xs_frag<Int8W>(S.xs, i % CH, lane), 0.0f);
+            const float s = transpose_reduce<R, CH>(accv, lane);
+            const int row = r0 + b * RB + lane / span;
+            if ((lane % span) == 0 && row < r1) {
+                const float v = s * scur;
+                if (v > best_v) { best_v = v; best_i = row; }
+            }
+#pragma unroll
+            for (int i = 0; i < R; ++i) cur[i] = nxt[i];
+            scur = snxt;
+        }
+#define MQ_ARGMAX_LEVEL(M)                                                                   \
+        {                                                                                    \
+            const float ov = partner<M>(best_v);                                             \
+            const int oi = __float_as_int(partner<M>(__int_as_float(best_i)));               \
+            if (ov > best_v || (ov == best_v && oi < best_i)) { best_v = ov; best_i = oi; }  \
+        }
+        MQ_ARGMAX_LEVEL(1) MQ_ARGMAX_LEVEL(2) MQ_ARGMAX_LEVEL(4) MQ_ARGMAX_LEVEL(8)
+        MQ_ARGMAX_LEVEL(16) MQ_ARGMAX_LEVEL(32)
+#undef MQ_ARGMAX_LEVEL
+        if (lane == 0) { S.lm_v[wave] = best_v; S.lm_i[wave] = best_i; }
+        __syncthreads();
+        trace(a.L, 1);
+        const uint32_t tag_lm = tag(a.L, 0);
+        if (tid == 0) {
+            float bv = S.lm_v[0];
+            int bi = S.lm_i[0];
+            for (int w = 1; w < kWaves; ++w)
+                if (S.lm_v[w] > bv || (S.lm_v[w] == bv && S.lm_i[w] < bi)) { bv = S.lm_v[w]; bi = S.lm_i[w]; }
+            if (kDebug && a.dbg_bmax) a.dbg_bmax[g] = bv;
+            if (kDebug && a.dbg_bidx) a.dbg_bidx[g] = bi;
+            ll_put(&lmg[2 * g], ordered_key(bv), tag_lm);
+            ll_put(&lmg[2 * g + 1], (uint32_t)bi, tag_lm);
+        }
+        if (x == 0 && r == 0 && wave == 0) {
+            constexpr int C = kNWG / kWave;
+            uint32_t w[C];
+#pragma unroll
+            for (int i = 0; i < C; ++i) w[i] = 2u * (uint32_t)(lane + kWave * i);
+            float v[2 * C];
+            wt.get_pairs<C>(XRegion(lmg, 2 * kNWG), w, tag_lm, v);
+            uint32_t kv = __float_as_uint(v[0]), iv = __float_as_uint(v[1]);
+#pragma unroll
+            for (int i = 1; i < C; ++i) {
+                const uint32_t ok = __float_as_uint(v[2 * i]), oi = __float_as_uint(v[2 * i + 1]);
+                if (ok > kv || (ok == kv && oi < iv)) { kv = ok; iv = oi; }
+            }
+#define MQ_KEY_LEVEL(M)                                                                      \
+            {                                                                                \
+                const uint32_t ok = __float_as_uint(partner<M>(__uint_as_float(kv)));        \
+                const uint32_t oi = __float_as_uint(partner<M>(__uint_as_float(iv)));        \
+                if (ok > kv || (ok == kv && oi < iv)) { kv = ok; iv = oi; }                  \
+            }
+            MQ_KEY_LEVEL(1) MQ_KEY_LEVEL(2) MQ_KEY_LEVEL(4) MQ_KEY_LEVEL(8) MQ_KEY_LEVEL(16) MQ_KEY_LEVEL(32)
+#undef MQ_KEY_LEVEL
+            if (lane == 0) {
+                const uint32_t flag = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *a.out_token = (flag != 0u || wt.dead) ? -1 : (int)iv;
+                if (a.status_out) *a.status_out = flag != 0u ? flag : (wt.dead ? 1u : 0u);
+                __hip_atomic_store(&hdr->asteps, AS + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&hdr->epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (kDebug && a.trace != nullptr)
+                    a.trace[((int64_t)a.L * kTracePoints + 2) * kNWG] = __builtin_amdgcn_s_memrealtime();
+            }
+        }
+    }
+}
+
+// ---------------- host side ----------------
+
+size_t decode_async_workspace_bytes(const DecodeShape& s) {
+    if (s.H != kAH || s.I != kAI) return 0;
+    return alayout_for(xlayout_total(kAH, kAI)).total;
+}
+
+bool decode_async_supports(const DecodeShape& s, bool int8, int cache_len) {
+    return int8 && s.H == kAH && s.I == kAI && s.NQ == 16 && s.NKV == 8 && s.D == kAD && cache_len <= kAMaxLen;
+}
+
+int launch_decode_async(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
+    auto fn = debug ? reinterpret_cast<const void*>(&decode_async_kernel<true>)
+                    : reinterpret_cast<const void*>(&decode_async_kernel<false>);
+    int st = check_residency(fn);
+    if (st != MQ_OK) return st;
+    KArgs copy = ka;
+    void* args[] = {&copy};
+    const hipError_t e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode_async): %s", hipGetErrorString(e));
+    return MQ_OK;
+}
+
+}  // namespace mq

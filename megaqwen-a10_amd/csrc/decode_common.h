@@ -73,6 +73,40 @@ constexpr Layout layout_for(int H, int I, int NQ, int NKV, int D) {
     return o;
 }
 
+// ---- XCD-aware kernel (decode_xcd.hip): roles and workspace regions ----
+constexpr int kNX = 8;                 // XCDs, one KV head each (the 8-term reductions below assume 8)
+constexpr int kGS = kNWG / kNX;        // workgroups per XCD
+
+enum XStage { XS_QKV = 0, XS_PO = 1, XS_ACT = 2, XS_MLP = 3, XS_PD = 4, XS_HID = 5, XS_ATP = 6, XS_ATO = 7 };
+constexpr uint32_t kXStages = 8;
+// split attention partial of one rank: 256 fp64 weighted sums (low word, high
+// word), then per head the fp32 maximum and the fp64 probability sum (3 words)
+constexpr int kAttWords = 2 * 256 + 2 * 3;
+
+struct XLayout {
+    size_t qkvx, actx, mlpx, hidx, lmg, po, pd, attp, atto, total;
+};
+// The regions follow the single-level kernel's (layout_for), so neither kernel
+// writes words the other could take for its own: the packed words below carry
+// a one-bit tag only.
+constexpr XLayout xlayout_for(int H, int I) {
+    XLayout o{};
+    size_t off = layout_for(H, I, 16, 8, 128).total;
+    o.qkvx = off; off += round256((size_t)kNX * 512 * 8);
+    o.actx = off; off += round256((size_t)kNX * H * 8);
+    o.mlpx = off; off += round256((size_t)kNX * (I / kNX) * 8);
+    o.hidx = off; off += round256((size_t)kNX * H * 8);
+    o.lmg = off; off += round256((size_t)kNWG * 2 * 8);        // LM-head maxima [workgroup][key, index]
+    o.po = off; off += round256((size_t)kNX * H * 8);          // packed fp64 partials [xcd][row]
+    o.pd = off; off += round256((size_t)kNX * H * 8);
+    o.attp = off; off += round256((size_t)kNX * kGS * kAttWords * 8);
+    o.atto = off; off += round256((size_t)kNX * 256 * 8);
+    o.total = off;
+    return o;
+}
+
+constexpr size_t xlayout_total(int H, int I) { return xlayout_for(H, I).total; }
+
 constexpr int pow2ceil(int x) { return x <= 1 ? 1 : 2 * pow2ceil((x + 1) / 2); }
 
 // One matvec stage of a workgroup: ROWS rows of K inputs, split into (row,
@@ -206,6 +240,11 @@ __device__ __forceinline__ double rms_scale(double sumsq, int n, double eps) {
 // All kNWG workgroups wait on each other, so they must be resident at once:
 // checked once per (kernel, device) with the occupancy calculator.
 int check_residency(const void* fn);
+
+// Async-wave kernel (decode_async.hip): INT8 Qwen3-0.6B shape, cache_len <= 64.
+size_t decode_async_workspace_bytes(const DecodeShape& s);
+bool decode_async_supports(const DecodeShape& s, bool int8, int cache_len);
+int launch_decode_async(const KArgs& k, bool debug, hipStream_t stream, hipEvent_t t0, hipEvent_t t1);
 
 // XCD-aware kernel (decode_xcd.hip).
 size_t decode_xcd_workspace_bytes(const DecodeShape& s);

@@ -42,37 +42,6 @@
 
 namespace mq {
 
-constexpr int kNX = 8;                 // XCDs, one KV head each (the 8-term reductions below assume 8)
-constexpr int kGS = kNWG / kNX;        // workgroups per XCD
-
-enum XStage { XS_QKV = 0, XS_PO = 1, XS_ACT = 2, XS_MLP = 3, XS_PD = 4, XS_HID = 5, XS_ATP = 6, XS_ATO = 7 };
-constexpr uint32_t kXStages = 8;
-// split attention partial of one rank: 256 fp64 weighted sums (low word, high
-// word), then per head the fp32 maximum and the fp64 probability sum (3 words)
-constexpr int kAttWords = 2 * 256 + 2 * 3;
-
-struct XLayout {
-    size_t qkvx, actx, mlpx, hidx, lmg, po, pd, attp, atto, total;
-};
-// The regions follow the single-level kernel's (layout_for), so neither kernel
-// writes words the other could take for its own: the packed words below carry
-// a one-bit tag only.
-constexpr XLayout xlayout_for(int H, int I) {
-    XLayout o{};
-    size_t off = layout_for(H, I, 16, 8, 128).total;
-    o.qkvx = off; off += round256((size_t)kNX * 512 * 8);
-    o.actx = off; off += round256((size_t)kNX * H * 8);
-    o.mlpx = off; off += round256((size_t)kNX * (I / kNX) * 8);
-    o.hidx = off; off += round256((size_t)kNX * H * 8);
-    o.lmg = off; off += round256((size_t)kNWG * 2 * 8);        // LM-head maxima [workgroup][key, index]
-    o.po = off; off += round256((size_t)kNX * H * 8);          // packed fp64 partials [xcd][row]
-    o.pd = off; off += round256((size_t)kNX * H * 8);
-    o.attp = off; off += round256((size_t)kNX * kGS * kAttWords * 8);
-    o.atto = off; off += round256((size_t)kNX * 256 * 8);
-    o.total = off;
-    return o;
-}
-
 // Partial-row matvec piece: 16 bytes of weights against the matching fp32
 // activations held contiguously in LDS.
 template <class W>

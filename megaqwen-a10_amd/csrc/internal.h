@@ -27,7 +27,8 @@ struct WsHeader {
     uint32_t xsteps;       // steps run by the XCD-aware kernel (parity tags of its packed words)
     uint32_t bsteps;       // steps run by the batched kernel (parity tags of its packed words)
     uint32_t batch;        // sequences per step of the batched kernel (0 until its first step)
-    uint32_t pad[53];
+    uint32_t asteps;       // steps run by the async-wave kernel (parity tags of its packed words)
+    uint32_t pad[52];
 };
 static_assert(sizeof(WsHeader) == 256, "workspace header is 256 bytes");
 

@@ -35,14 +35,15 @@ TOKEN_SLOTS = 256           # pinned token words, one per step in flight (launch
 
 LM_PARTIALS = 256   # per-workgroup LM-head maxima written to block_max_vals/idxs
 
-VARIANTS = {"auto": 0, "flat": 1, "xcd": 2}
+VARIANTS = {"auto": 0, "flat": 1, "xcd": 2, "async": 3}
 
 
 def set_decode_variant(name: str) -> None:
     """Select the decode kernel for all following steps in this process:
-    ``"auto"`` (default; the XCD-aware kernel when the workgroups of each
-    residue class g mod 8 share one XCD, checked once per device), ``"flat"``
-    (single-level exchanges) or ``"xcd"``."""
+    ``"auto"`` (default: the async-wave kernel for INT8 Qwen3-0.6B-shape steps
+    up to 64 cached positions, else the XCD-aware kernel when the workgroups of
+    each residue class g mod 8 share one XCD, checked once per device),
+    ``"flat"`` (single-level exchanges), ``"xcd"`` or ``"async"``."""
     lib = _lib.load()
     _lib.check(lib.mq_decode_set_variant(VARIANTS[name]), "mq_decode_set_variant")
 
@@ -54,7 +55,7 @@ def decode_variant(hidden_size: int = 1024, intermediate_size: int = 3072, int8:
     v = lib.mq_decode_variant(ctypes.byref(dims), int(int8))
     if v < 0:
         _lib.check(-v, "mq_decode_variant")
-    return {1: "flat", 2: "xcd"}[v]
+    return {1: "flat", 2: "xcd", 3: "async"}[v]
 
 
 def _check_tensor(t, name, dtype, shape=None, device=None):

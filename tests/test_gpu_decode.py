@@ -57,13 +57,24 @@ def _greedy(dec, prompt, n):
     return out
 
 
-@pytest.fixture(params=["flat", "xcd"])
-def variant(request, mq, dev):
-    """Runs a test once per decode kernel (single-level exchanges / XCD-aware)."""
-    mq.set_decode_variant(request.param)
-    assert mq.decode_variant() == request.param
-    yield request.param
+def _use_variant(mq, name):
+    mq.set_decode_variant(name)
+    assert mq.decode_variant() == name
+    yield name
     mq.set_decode_variant("auto")
+
+
+@pytest.fixture(params=["flat", "xcd", "async"])
+def variant(request, mq, dev):
+    """Runs a test once per decode kernel (single-level exchanges / XCD-aware / async-wave;
+    the async-wave kernel covers the INT8 Qwen3-0.6B shape up to 64 cached positions)."""
+    yield from _use_variant(mq, request.param)
+
+
+@pytest.fixture(params=["flat", "xcd"])
+def variant_any_shape(request, mq, dev):
+    """The kernels that run every compiled shape and weight format."""
+    yield from _use_variant(mq, request.param)
 
 
 @pytest.fixture(scope="module")
@@ -259,7 +270,7 @@ def test_full_int8_32_tokens(variant, mq, dev):
     torch.cuda.empty_cache()
 
 
-def test_full_bf16_32_tokens(variant, mq, dev):
+def test_full_bf16_32_tokens(variant_any_shape, mq, dev):
     """BASELINE config 3 gate: Qwen3-0.6B shape, bf16 weights, 32 greedy tokens identical to the oracle."""
     print("building qwen3_0.6b_bf16", flush=True)
     dec, d, prompt, cfg, keep = _build(mq, dev, "qwen3_0.6b_bf16")
@@ -291,7 +302,7 @@ def test_full_bf16_32_tokens(variant, mq, dev):
     torch.cuda.empty_cache()
 
 
-def test_1p7b_int8_matches_oracle(variant, mq, dev):
+def test_1p7b_int8_matches_oracle(variant_any_shape, mq, dev):
     """Qwen3-1.7B layer shapes (H=2048, I=6144), 2 layers, small vocabulary, live oracle."""
     cfg = mq.QWEN3_1_7B.with_(num_layers=2, vocab_size=2048)
     state, prompt = mq.random_init_state(cfg, seed=5, norm_jitter=0.1)
