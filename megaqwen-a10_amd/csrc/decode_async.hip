@@ -111,10 +111,10 @@ struct __align__(16) AsyncLds {
     uint16_t fnorm[kAH];                   // final RMSNorm gains (once per step)
     // compute waves
     __align__(16) uint32_t dig[kCW][8][kPlane];          // digit planes of each wave's slice (byte k of plane d)
-    double qw[kCW][kAD];                   // each wave's rotated query
-    double pw[kCW][kAMaxLen / 2];          // scores, then softmax numerators, of each wave's positions
-    double acc[kCW][kAD];                  // P V partials
-    double ml[kCW][2];                     // (max score, numerator sum) of each wave
+    double qa[kCW][2][kAD];                // each wave's copy of the two rotated queries
+    double pacc[kCW][2][kAD];              // P V partials of each wave's block, both heads
+    double pml[kCW][2][2];                 // (max score, numerator sum) per wave and head
+    __align__(16) double pw[kCW][16][2];   // softmax numerators of each wave's block [position][head]
     __align__(16) float hs[kAH];                         // the layer's input (bf16 values): stage D's residual
     double part[4][kCW][32];               // per-wave row partials of the combines A, C, E, F
     uint32_t sync[16];
@@ -158,6 +158,88 @@ __device__ __forceinline__ bool last_arrival(uint32_t* p, int lane) {
     old = __builtin_amdgcn_readfirstlane(old);
     lds_order();
     return (old % kCW) == kCW - 1;
+}
+
+// ---- exchange layout of the q|k|v rows ------------------------------------------------
+// Word of q|k|v row m (q heads 2x, 2x + 1: rows 0-255, k: 256-383, v: 384-511). Within
+// each 128-row q or k block, dims i and i + 64 (a RoPE rotation pair) share one 16-byte
+// chunk, so lane l of a consumer reads both with one load; v rows stay in order (lane l
+// reads dims 2l, 2l + 1, the word layout of a cache row).
+__device__ __forceinline__ int qkv_word(int m) {
+    if (m >= 384) return m;
+    const int i = m & 127;
+    return (m & ~127) + 2 * (i & 63) + (i >> 6);
+}
+
+// ---- cross-lane fp64 ------------------------------------------------------------------
+// Value of lane l ^ 8 (DPP row rotation by 8) and of lane l ^ 4 (half-row mirror, l ^ 7,
+// then the quad reversal, l ^ 3), for fp64 values.
+template <int CTRL>
+__device__ __forceinline__ double dpp64(double v) {
+    const uint64_t u = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double xor8_64(double v) { return dpp64<0x128>(v); }
+__device__ __forceinline__ double xor4_64(double v) { return dpp64<0x1B>(dpp64<0x141>(v)); }
+// Transposed pair sums across lane bit 5 (bit 4): lanes with the bit clear get
+// lo(self) + lo(partner), lanes with it set hi(self) + hi(partner). One
+// v_permlane32_swap (v_permlane16_swap) per 32-bit word exchanges the halves the
+// partner keeps, so no lane selects are needed; with lo == hi this is a plain
+// butterfly sum.
+__device__ __forceinline__ double tsum32(double lo, double hi) {
+    const uint64_t a = (uint64_t)__double_as_longlong(lo), b = (uint64_t)__double_as_longlong(hi);
+    const auto w0 = __builtin_amdgcn_permlane32_swap((uint32_t)a, (uint32_t)b, false, false);
+    const auto w1 = __builtin_amdgcn_permlane32_swap((uint32_t)(a >> 32), (uint32_t)(b >> 32), false, false);
+    const double x = __longlong_as_double((long long)(((uint64_t)w1[0] << 32) | w0[0]));
+    const double y = __longlong_as_double((long long)(((uint64_t)w1[1] << 32) | w0[1]));
+    return x + y;
+}
+__device__ __forceinline__ double tsum16(double lo, double hi) {
+    const uint64_t a = (uint64_t)__double_as_longlong(lo), b = (uint64_t)__double_as_longlong(hi);
+    const auto w0 = __builtin_amdgcn_permlane16_swap((uint32_t)a, (uint32_t)b, false, false);
+    const auto w1 = __builtin_amdgcn_permlane16_swap((uint32_t)(a >> 32), (uint32_t)(b >> 32), false, false);
+    const double x = __longlong_as_double((long long)(((uint64_t)w1[0] << 32) | w0[0]));
+    const double y = __longlong_as_double((long long)(((uint64_t)w1[1] << 32) | w0[1]));
+    return x + y;
+}
+// max(self, lane ^ 32) and max(self, lane ^ 16), the same way
+__device__ __forceinline__ double xmax32(double v) {
+    const uint64_t a = (uint64_t)__double_as_longlong(v);
+    const auto w0 = __builtin_amdgcn_permlane32_swap((uint32_t)a, (uint32_t)a, false, false);
+    const auto w1 = __builtin_amdgcn_permlane32_swap((uint32_t)(a >> 32), (uint32_t)(a >> 32), false, false);
+    return fmax(__longlong_as_double((long long)(((uint64_t)w1[0] << 32) | w0[0])),
+                __longlong_as_double((long long)(((uint64_t)w1[1] << 32) | w0[1])));
+}
+__device__ __forceinline__ double xmax16(double v) {
+    const uint64_t a = (uint64_t)__double_as_longlong(v);
+    const auto w0 = __builtin_amdgcn_permlane16_swap((uint32_t)a, (uint32_t)a, false, false);
+    const auto w1 = __builtin_amdgcn_permlane16_swap((uint32_t)(a >> 32), (uint32_t)(a >> 32), false, false);
+    return fmax(__longlong_as_double((long long)(((uint64_t)w1[0] << 32) | w0[0])),
+                __longlong_as_double((long long)(((uint64_t)w1[1] << 32) | w0[1])));
+}
+// Sum over each 16-lane row (every lane of the row receives it): four DPP levels.
+__device__ __forceinline__ double row_sum64(double v) {
+    v += partner64<1>(v);
+    v += partner64<2>(v);
+    v += partner64<4>(v);
+    v += partner64<8>(v);
+    return v;
+}
+__device__ __forceinline__ double row_max64(double v) {
+    v = fmax(v, partner64<1>(v));
+    v = fmax(v, partner64<2>(v));
+    v = fmax(v, partner64<4>(v));
+    v = fmax(v, partner64<8>(v));
+    return v;
+}
+// Sum over the wave, the same value in every lane: row sums by DPP, then the four
+// row sums read out and added in a fixed order (the cross-row permlane levels of a
+// full butterfly cost twice a DPP level).
+__device__ __forceinline__ double wave_sum64_u(double v) {
+    v = row_sum64(v);
+    return (readlane64(v, 0) + readlane64(v, 16)) + (readlane64(v, 32) + readlane64(v, 48));
 }
 
 // ---- digits ---------------------------------------------------------------------------
@@ -280,7 +362,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     const int r = g / kAX;
     const int tid = threadIdx.x;
     const int lane = tid % kWave;
-    const int wave = tid / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);    // uniform: scalar registers
 
     WsHeader* hdr = reinterpret_cast<WsHeader*>(a.ws);
     uint64_t* const qkvx = reinterpret_cast<uint64_t*>(a.ws + kLay.qkvx) + (size_t)x * 512;
@@ -432,8 +514,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 if (lane < 24) put32(S.scE, lane, scv);
                 raise(SL_E, l);
             } else {
-                // K rows keep their 16-byte chunks XOR-permuted by row (chunk g of row j at
-                // g ^ (j % 16)), so the 8 rows the score loop reads at once hit different banks
+                // K and V rows keep their 16-byte chunks XOR-permuted by row (chunk g of row j
+                // at g ^ (j % 16)), so that lanes reading the same chunk of different rows hit
+                // different banks
                 const int64_t cb = ((int64_t)l * kAX + x) * kv_head_stride;
                 uint4 rk[kAMaxLen / 4], rv[kAMaxLen / 4];
 #pragma unroll
@@ -454,7 +537,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     const int j = 4 * i + lane / 16;
                     if (j < pos) {
                         reinterpret_cast<uint4*>(S.kvk[j])[(lane % 16) ^ (j % 16)] = rk[i];
-                        reinterpret_cast<uint4*>(S.kvv[j])[lane % 16] = rv[i];
+                        reinterpret_cast<uint4*>(S.kvv[j])[(lane % 16) ^ (j % 16)] = rv[i];
                     }
                 }
                 put32(S.qkn[0], lane, qn);
@@ -518,29 +601,34 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     const double* P = &S.part[0][0][lane];
                     const double v = ((P[0] + P[32]) + (P[64] + P[96])) *
                                      (double)S.scA[lane];
-                    ll_put_xcd(&qkvx[16 * r + lane], __float_as_uint((float)v), tag(l, AS_QKV));
+                    ll_put_xcd(&qkvx[qkv_word(16 * r + lane)], __float_as_uint((float)v), tag(l, AS_QKV));
                 }
             }
             lds_add(&S.sync[kConsumed + SL_A], lane);
             trace(l, 1);
 
             // ---------------- B: attention ----------------
+            // Every compute wave takes both query heads over its block of q0 = ceil(n / 4)
+            // consecutive positions, so each cached K and V word is converted once for the
+            // two heads. Lane l holds dims l and l + 64 of the queries (and of k), the
+            // rotation pairs of RoPE; v dims 2l, 2l + 1 (the word layout of a cache row).
+            float ao;
             {
-                const int h = c & 1, half = c >> 1;
                 const int n = pos + 1;
-                const int hn = (n + 1) / 2;
-                const int j0 = half ? hn : 0, j1 = half ? n : hn;
+                const int q0 = (n + kCW - 1) / kCW;                  // <= 16
+                const int j0 = min(n, c * q0), j1 = min(n, j0 + q0);
                 const int np = j1 - j0;
                 const bool owner = j0 <= pos && pos < j1;
-                float qv[2], kv2[2] = {0.0f, 0.0f}, vv[2] = {0.0f, 0.0f};
+                float qv[2][2], kv2[2], vv[2];
                 {
-                    // q of head h, and k and v for the wave whose half holds this position
-                    uint32_t w[3] = {2u * (uint32_t)(64 * h + lane), 2u * (uint32_t)(128 + lane), 2u * (uint32_t)(192 + lane)};
-                    float o[6];
-                    wt.get_pairs<3>(XRegion(qkvx, 512), w, tag(l, AS_QKV), o, owner ? 3 : 1);
-                    qv[0] = o[0]; qv[1] = o[1];
-                    kv2[0] = o[2]; kv2[1] = o[3];
-                    vv[0] = o[4]; vv[1] = o[5];
+                    const uint32_t w[4] = {2u * (uint32_t)lane, 128u + 2u * (uint32_t)lane, 256u + 2u * (uint32_t)lane,
+                                           384u + 2u * (uint32_t)lane};
+                    float o[8];
+                    wt.get_pairs<4>(XRegion(qkvx, 512), w, tag(l, AS_QKV), o, owner ? 4 : 2);
+                    qv[0][0] = o[0]; qv[0][1] = o[1];
+                    qv[1][0] = o[2]; qv[1][1] = o[3];
+                    kv2[0] = o[4]; kv2[1] = o[5];
+                    vv[0] = o[6]; vv[1] = o[7];
                 }
                 if (c == 0) {
                     trace(l, 2);
@@ -548,123 +636,176 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                         __hip_atomic_store(&S.sync[kWindow], (uint32_t)(l + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
                 lds_wait(&S.sync[kReady + SL_B], (uint32_t)(l + 1), lds_limit, &hdr->abort_flag);
-                // QK-norm and RoPE (lane holds dims 2 lane, 2 lane + 1; the rotation partner
-                // dims i -+ 64 sit in lane -+ 32)
-                const int i0 = 2 * lane;
-                const double c0r = bf16_bits_to_f32(S.rope[0][i0]), c1r = bf16_bits_to_f32(S.rope[0][i0 + 1]);
-                const double s0r = bf16_bits_to_f32(S.rope[1][i0]), s1r = bf16_bits_to_f32(S.rope[1][i0 + 1]);
-                auto norm_rope = [&](const float (&in)[2], const uint16_t* gain, float (&out)[2]) {
-                    const double x0 = in[0], x1 = in[1];
-                    const double ss = wave_sum64(fma(x0, x0, x1 * x1));
-                    const double sc = rms_scale(ss, D, kEps);
-                    const double y0 = x0 * sc * (double)bf16_bits_to_f32(gain[i0]);
-                    const double y1 = x1 * sc * (double)bf16_bits_to_f32(gain[i0 + 1]);
-                    const double p0 = partner64<32>(y0), p1 = partner64<32>(y1);
-                    if (lane < 32) {
-                        out[0] = (float)(y0 * c0r - p0 * s0r);
-                        out[1] = (float)(y1 * c1r - p1 * s1r);
-                    } else {
-                        out[0] = (float)(p0 * s0r + y0 * c0r);
-                        out[1] = (float)(p1 * s1r + y1 * c1r);
-                    }
+                // QK-norm and RoPE: out[i] = y[i] cos[i] - y[i+64] sin[i],
+                // out[i+64] = y[i] sin[i+64] + y[i+64] cos[i+64] (i = lane)
+                const double cl = bf16_bits_to_f32(S.rope[0][lane]), ch = bf16_bits_to_f32(S.rope[0][lane + 64]);
+                const double sl = bf16_bits_to_f32(S.rope[1][lane]), sh = bf16_bits_to_f32(S.rope[1][lane + 64]);
+                const double gq0 = bf16_bits_to_f32(S.qkn[0][lane]), gq1 = bf16_bits_to_f32(S.qkn[0][lane + 64]);
+                const double ssq0 = wave_sum64_u(fma((double)qv[0][0], (double)qv[0][0], (double)qv[0][1] * (double)qv[0][1]));
+                const double ssq1 = wave_sum64_u(fma((double)qv[1][0], (double)qv[1][0], (double)qv[1][1] * (double)qv[1][1]));
+                const double ssk = owner ? wave_sum64_u(fma((double)kv2[0], (double)kv2[0], (double)kv2[1] * (double)kv2[1]))
+                                         : 1.0;
+                auto rope = [&](double sc, const float (&in)[2], double g0, double g1, float (&out)[2]) {
+                    const double y0 = (double)in[0] * sc * g0, y1 = (double)in[1] * sc * g1;
+                    out[0] = (float)(y0 * cl - y1 * sl);
+                    out[1] = (float)(y0 * sh + y1 * ch);
                 };
-                float qr[2];
-                norm_rope(qv, S.qkn[0], qr);
-                S.qw[c][i0] = qr[0];
-                S.qw[c][i0 + 1] = qr[1];
+                float qr[2][2];
+                rope(rms_scale(ssq0, D, kEps), qv[0], gq0, gq1, qr[0]);
+                rope(rms_scale(ssq1, D, kEps), qv[1], gq0, gq1, qr[1]);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    S.qa[c][h][lane] = qr[h][0];
+                    S.qa[c][h][lane + 64] = qr[h][1];
+                }
                 const bool dbg = kDebug && r == 0 && l == last;
-                if (dbg && half == 0 && a.dbg_q) {
-                    a.dbg_q[(2 * x + h) * D + i0] = qr[0];
-                    a.dbg_q[(2 * x + h) * D + i0 + 1] = qr[1];
+                if (dbg && c == 0 && a.dbg_q) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        a.dbg_q[(2 * x + h) * D + lane] = qr[h][0];
+                        a.dbg_q[(2 * x + h) * D + lane + 64] = qr[h][1];
+                    }
                 }
                 if (owner) {
+                    // this position's K and V rows, into the LDS copies the loops below read
+                    // (K chunks permuted as the loader stores them) and, once per XCD, the cache
                     float kr[2];
-                    norm_rope(kv2, S.qkn[1], kr);
-                    const uint32_t kw = f32_to_bf16_bits(kr[0]) | (f32_to_bf16_bits(kr[1]) << 16);
+                    rope(rms_scale(ssk, D, kEps), kv2, bf16_bits_to_f32(S.qkn[1][lane]),
+                         bf16_bits_to_f32(S.qkn[1][lane + 64]), kr);
+                    const uint32_t k0 = f32_to_bf16_bits(kr[0]), k1 = f32_to_bf16_bits(kr[1]);
                     const uint32_t vw = f32_to_bf16_bits(vv[0]) | (f32_to_bf16_bits(vv[1]) << 16);
-                    reinterpret_cast<uint32_t*>(S.kvk[pos])[4 * ((lane / 4) ^ (pos % 16)) + lane % 4] = kw;
-                    reinterpret_cast<uint32_t*>(S.kvv[pos])[lane] = vw;
-                    if (r == 0 && h == 0) {
+                    const int p16 = pos % 16;
+                    S.kvk[pos][8 * ((lane >> 3) ^ p16) + (lane & 7)] = (uint16_t)k0;
+                    S.kvk[pos][8 * (((lane + 64) >> 3) ^ p16) + (lane & 7)] = (uint16_t)k1;
+                    reinterpret_cast<uint32_t*>(S.kvv[pos])[4 * ((lane >> 2) ^ p16) + (lane & 3)] = vw;
+                    if (r == 0) {
                         const int64_t cur = ((int64_t)l * kAX + x) * kv_head_stride + (int64_t)pos * D;
-                        reinterpret_cast<uint32_t*>(a.kc + cur)[lane] = kw;
+                        a.kc[cur + lane] = (uint16_t)k0;
+                        a.kc[cur + lane + 64] = (uint16_t)k1;
                         reinterpret_cast<uint32_t*>(a.vc + cur)[lane] = vw;
-                        if (dbg && a.dbg_k) { a.dbg_k[x * D + i0] = kr[0]; a.dbg_k[x * D + i0 + 1] = kr[1]; }
-                        if (dbg && a.dbg_v) { a.dbg_v[x * D + i0] = vv[0]; a.dbg_v[x * D + i0 + 1] = vv[1]; }
+                        if (dbg && a.dbg_k) { a.dbg_k[x * D + lane] = kr[0]; a.dbg_k[x * D + lane + 64] = kr[1]; }
+                        if (dbg && a.dbg_v) { a.dbg_v[x * D + 2 * lane] = vv[0]; a.dbg_v[x * D + 2 * lane + 1] = vv[1]; }
                     }
                 }
                 lds_order();
-                // scores: 8 lanes per position, each over dims [16 (lane % 8), +16)
-                double mloc = -INFINITY;
-                {
-                    double qd[16];
-                    const int db = 16 * (lane % 8);
+                // Scores. Lane = jj + 4 d16: jj (bits 0-1) takes the positions j0 + 4p + jj of
+                // passes p < ceil(np / 4), d16 (bits 2-5) the dims [8 d16, +8), both heads.
+                double mh = -INFINITY, lh = 0.0;         // block max and numerator sum of head (lane >> 3) & 1
+                const int jj = lane & 3, d16 = lane >> 2;
+                if (np > 0) {
+                    const int passes = (np + 3) >> 2;    // <= 4
+                    double2 qd[2][4];
+                    uint4 kc[4];
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) qd[e] = S.qw[c][db + e];
-                    for (int t = 0; 8 * t < np; ++t) {
-                        const int jl = 8 * t + lane / 8;
-                        double d0 = 0.0, d1 = 0.0;
-                        if (jl < np) {
-                            const int row = j0 + jl;
-                            const uint4* kp = reinterpret_cast<const uint4*>(S.kvk[row]);
-                            const uint4 k0 = kp[(2 * (lane % 8)) ^ (row % 16)], k1 = kp[(2 * (lane % 8) + 1) ^ (row % 16)];
-                            const uint32_t kw8[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+                    for (int h = 0; h < 2; ++h)
 #pragma unroll
-                            for (int e = 0; e < 8; ++e) {
-                                d0 = fma(qd[2 * e], (double)bf16_bits_to_f32(kw8[e] & 0xffffu), d0);
-                                d1 = fma(qd[2 * e + 1], (double)__uint_as_float(kw8[e] & 0xffff0000u), d1);
+                        for (int t = 0; t < 4; ++t) qd[h][t] = reinterpret_cast<const double2*>(&S.qa[c][h][8 * d16])[t];
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        const int row = j0 + min(4 * p + jj, np - 1);
+                        kc[p] = reinterpret_cast<const uint4*>(S.kvk[row])[d16 ^ (row & 15)];
+                    }
+                    double E[8];                         // entry 2p + h: partial score over the 8 dims
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        double s0 = 0.0, s1 = 0.0;
+                        if (p < passes) {
+                            const uint32_t k4[4] = {kc[p].x, kc[p].y, kc[p].z, kc[p].w};
+#pragma unroll
+                            for (int t = 0; t < 4; ++t) {
+                                const double klo = bf16_bits_to_f32(k4[t] & 0xffffu);
+                                const double khi = __uint_as_float(k4[t] & 0xffff0000u);
+                                s0 = fma(qd[0][t].x, klo, s0);
+                                s0 = fma(qd[0][t].y, khi, s0);
+                                s1 = fma(qd[1][t].x, klo, s1);
+                                s1 = fma(qd[1][t].y, khi, s1);
                             }
                         }
-                        const double sv = group_sum64<8>(d0 + d1) * (double)a.attn_scale;
-                        if (jl < np) {
-                            if ((lane % 8) == 0) S.pw[c][jl] = sv;
-                            mloc = fmax(mloc, sv);
+                        E[2 * p] = s0;
+                        E[2 * p + 1] = s1;
+                    }
+                    // sum over d16 (lane bits 5, 4, 3, 2), transposed: the lane keeps entry
+                    // 4 b5 + 2 b4 + b3, i.e. pass pe = 2 b5 + b4, head he = b3
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) E[k] = tsum32(E[k], E[k + 4]);
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) E[k] = tsum16(E[k], E[k + 2]);
+                    {
+                        const bool u3 = (lane & 8) != 0;
+                        const double keep = u3 ? E[1] : E[0], send = u3 ? E[0] : E[1];
+                        E[0] = keep + xor8_64(send);
+                        E[0] += xor4_64(E[0]);
+                    }
+                    const int pe = 2 * ((lane >> 5) & 1) + ((lane >> 4) & 1);
+                    const bool valid = 4 * pe + jj < np;
+                    const double sc = valid ? E[0] * (double)a.attn_scale : -INFINITY;
+                    // max and numerator sum over the lanes of the same head (bits 0, 1, 4, 5)
+                    double m = sc;
+                    m = fmax(m, partner64<1>(m));
+                    m = fmax(m, partner64<2>(m));
+                    m = fmax(m, xmax16(m));
+                    m = fmax(m, xmax32(m));
+                    const double pv = valid ? exp(sc - m) : 0.0;
+                    double ls = pv + partner64<1>(pv);
+                    ls += partner64<2>(ls);
+                    ls = tsum16(ls, ls);
+                    ls = tsum32(ls, ls);
+                    mh = m;
+                    lh = ls;
+                    // numerators to LDS: position 4 pe + jj, head he (one lane of each pair)
+                    if ((lane & 4) == 0 && valid) S.pw[c][4 * pe + jj][(lane >> 3) & 1] = pv;
+                }
+                // P V: lane l accumulates dims 2l, 2l + 1 of both heads over the wave's block;
+                // the numerators come back from LDS as same-address (broadcast) reads
+                double pa[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
+                lds_order();
+                for (int t0 = 0; t0 < np; t0 += 8) {
+                    double2 pp[8];
+                    uint32_t vw[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int t = min(t0 + u, np - 1);
+                        const int row = j0 + t;
+                        pp[u] = *reinterpret_cast<const double2*>(S.pw[c][t]);
+                        vw[u] = reinterpret_cast<const uint32_t*>(S.kvv[row])[4 * ((lane >> 2) ^ (row & 15)) + (lane & 3)];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        if (t0 + u < np) {
+                            const double vlo = bf16_bits_to_f32(vw[u] & 0xffffu), vhi = __uint_as_float(vw[u] & 0xffff0000u);
+                            pa[0][0] = fma(pp[u].x, vlo, pa[0][0]);
+                            pa[0][1] = fma(pp[u].x, vhi, pa[0][1]);
+                            pa[1][0] = fma(pp[u].y, vlo, pa[1][0]);
+                            pa[1][1] = fma(pp[u].y, vhi, pa[1][1]);
                         }
                     }
                 }
-                mloc = wave_max64(mloc);
-                lds_order();
-                // softmax numerators of the wave's positions (lane jl), then P V: lane l
-                // accumulates dims 2l, 2l+1 with the numerators read back from LDS
-                if (lane < np) S.pw[c][lane] = exp(S.pw[c][lane] - mloc);
-                lds_order();
-                double a0 = 0.0, a1 = 0.0, ls = 0.0;
-                for (int jb = 0; jb < np; jb += 4) {
-                    double pp[4];
-                    uint32_t vw[4];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const int jl = min(jb + u, np - 1);
-                        pp[u] = S.pw[c][jl];
-                        vw[u] = reinterpret_cast<const uint32_t*>(S.kvv[j0 + jl])[lane];
-                    }
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        if (jb + u < np) {
-                            a0 = fma(pp[u], (double)bf16_bits_to_f32(vw[u] & 0xffffu), a0);
-                            a1 = fma(pp[u], (double)__uint_as_float(vw[u] & 0xffff0000u), a1);
-                            ls += pp[u];
-                        }
-                    }
+                for (int h = 0; h < 2; ++h)
+                    *reinterpret_cast<double2*>(&S.pacc[c][h][2 * lane]) = make_double2(pa[h][0], pa[h][1]);
+                if ((lane & ~8) == 0) {
+                    S.pml[c][lane >> 3][0] = mh;
+                    S.pml[c][lane >> 3][1] = lh;
                 }
-                S.acc[c][i0] = a0;
-                S.acc[c][i0 + 1] = a1;
-                if (lane == 0) { S.ml[c][0] = np > 0 ? mloc : -INFINITY; S.ml[c][1] = ls; }
+                lds_add(&S.sync[kConsumed + SL_B], lane);
                 // all four waves' partials in LDS
                 lds_add(&S.sync[kArrive + AR_B], lane);
                 lds_wait(&S.sync[kArrive + AR_B], (uint32_t)(kCW * (l + 1)), lds_limit, &hdr->abort_flag);
-                lds_add(&S.sync[kConsumed + SL_B], lane);
-            }
-            // merge: wave c takes attention dims [64c, +64) (head c / 2), from the partials of
-            // waves c / 2 (first half of the positions) and c / 2 + 2 (second half)
-            float ao;
-            {
+                // merge: wave c takes attention dims [64c, +64) (head c / 2) from the four blocks;
+                // lane w < 4 computes block w's weight e^(m_w - M), the others read it
                 const int hh = c >> 1, dim = 64 * (c & 1) + lane;
-                const double ma = S.ml[hh][0], mb = S.ml[hh + 2][0];
-                const double M = fmax(ma, mb);
-                const double wa = ma == -INFINITY ? 0.0 : exp(ma - M);
-                const double wb = mb == -INFINITY ? 0.0 : exp(mb - M);
-                const double num = fma(wa, S.acc[hh][dim], wb * S.acc[hh + 2][dim]);
-                const double den = fma(wa, S.ml[hh][1], wb * S.ml[hh + 2][1]);
+                double M = -INFINITY;
+#pragma unroll
+                for (int w = 0; w < kCW; ++w) M = fmax(M, S.pml[w][hh][0]);
+                const double mine = S.pml[lane & 3][hh][0];
+                const double ew = mine == -INFINITY ? 0.0 : exp(mine - M);
+                double num = 0.0, den = 0.0;
+#pragma unroll
+                for (int w = 0; w < kCW; ++w) {
+                    const double e = readlane64(ew, w);
+                    num = fma(e, S.pacc[w][hh][dim], num);
+                    den = fma(e, S.pml[w][hh][1], den);
+                }
                 ao = (float)(num * rcp_nr(den));
                 if (kDebug && r == 0 && l == last && a.dbg_attn) a.dbg_attn[2 * D * x + 64 * c + lane] = ao;
             }

@@ -6,7 +6,7 @@ greedy steps through ``A10Int8MegakernelDecoder.decode_step``. With
 ``--copy-mib N`` it first runs four uint8 adds over an N MiB buffer (each reads
 and writes exactly N MiB), the calibration for FETCH_SIZE / WRITE_SIZE.
 
-    python megaqwen-a10_amd/profile_decode.py [--steps 32] [--variant auto|flat|xcd] [--copy-mib 256]
+    python megaqwen-a10_amd/profile_decode.py [--steps 32] [--variant auto|flat|xcd|async] [--copy-mib 256]
 """
 from __future__ import annotations
 
@@ -21,7 +21,7 @@ sys.path.insert(0, str(ROOT))
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--steps", type=int, default=32)
-    ap.add_argument("--variant", default="auto", choices=["auto", "flat", "xcd"])
+    ap.add_argument("--variant", default="auto", choices=["auto", "flat", "xcd", "async"])
     ap.add_argument("--copy-mib", type=int, default=0)
     args = ap.parse_args()
 
