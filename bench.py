@@ -176,7 +176,7 @@ def run_decode(args, mq, torch):
         raise RuntimeError(f"decode step {toks.index(min(toks))} of the timed region failed: "
                            f"status {status}: {mq._lib.last_error()}")
     variant = mq.decode_variant(cfg.hidden_size, cfg.intermediate_size, int8=True)
-    kernel = {"async": "mq::decode_async_kernel<false>",
+    kernel = {"async": "mq::decode_async_kernel<false, false>",
               "xcd": "mq::decode_xcd_kernel<1024, 3072, mq::Int8W, false>",
               "flat": "mq::decode_kernel<1024, 3072, mq::Int8W, false>"}[variant]
     arithmetic = ("matrix products as exact sums of int8 digits of a 55-bit fixed-point activation on the int8 "
@@ -188,6 +188,25 @@ def run_decode(args, mq, torch):
     bytes_total = sum(cfg.int8_step_bytes(cache_len=PROMPT_LEN + i + 1) for i in range(args.steps))
     kern_s = sum(kern_ms) / 1e3
     achieved = bytes_total / kern_s / 1e9
+
+    device_loop = None
+    if variant == "async":
+        # the same K steps as ONE launch (mq_int8_decode_generate): each step's token goes to
+        # the next on the device, so no host round trip per token; wall time of the call.
+        # None from the one-launch path: the steps reach past the kernel's position range.
+        first3 = prefill()
+        warm = dec._generate_one_launch([first3], 1)
+        if warm is not None:
+            prefill()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            toks3 = dec._generate_one_launch([first3], args.steps)
+            wall3 = time.perf_counter() - t0
+            if toks3 is not None:
+                device_loop = {"tok_s": round(args.steps / wall3, 1),
+                               "ms_per_step": round(wall3 / args.steps * 1e3, 4),
+                               "entry_point": "mq_int8_decode_generate: one launch for all K steps",
+                               "tokens_match_per_step_launches": first3 == first and toks3 == toks}
 
     parity = None
     fx = ROOT / "tests" / "golden" / "tokens_qwen3_0.6b_int8.json"
@@ -225,6 +244,7 @@ def run_decode(args, mq, torch):
                      "kernel_pass_tokens_identical": repeat_identical,
                      "bytes_per_launch_avg": int(bytes_total / args.steps)},
         "device_tok_s": round(args.steps / kern_s, 1),
+        "device_loop": device_loop,
         "parity": parity,
     }
     if not args.no_cpu:

@@ -143,7 +143,36 @@ typedef struct mq_decode_args {
      * (48), > 1025 is taken as 1025, < 0 = never split. The single-level
      * kernel never splits (cache_len <= 1024). */
     int attn_split_min;
+    /* Sampling (no counterpart in the reference, whose generate() accepts a
+     * temperature and ignores it, a10_decode.py:358): 0 = greedy argmax; > 0 =
+     * the token is drawn from softmax(logits / temperature) by the Gumbel-max
+     * rule, argmax over rows of logit / temperature + g, with the noise g keyed
+     * by (seed, position, vocabulary row): a given seed gives the same tokens
+     * one launch per step and in mq_int8_decode_generate. */
+    float temperature;
+    unsigned long long seed;
 } mq_decode_args;
+
+/* ---- device-side generation loop (no counterpart in the reference) --------
+ * Runs n_forced + n_generate - 1 decode steps in ONE launch, each step handing
+ * its token to the next on the device (a10_decode.py:358-393 and
+ * bench_int8.py:218 launch one step per token and read each token back).
+ * Step i, at position args->position + i, takes prompt_tokens[i] for
+ * i < n_forced (the prefill) and the previous step's output after that;
+ * output_tokens[j] receives the output of step n_forced - 1 + j (the last
+ * prefill step's output is the first generated token, the convention of
+ * verify_correctness_a10.py:323-339) and args->output_token_id the last one.
+ * args->input_token_id must equal prompt_tokens[0] and cache_len position + 1.
+ * Runs on the async-wave kernel: INT8 Qwen3-0.6B layer shapes and
+ * position + n_forced + n_generate - 1 <= 64; otherwise MQ_ERR_UNSUPPORTED
+ * (nothing launched), and a loop over mq_int8_decode_step gives the same
+ * tokens, sampled ones included. */
+typedef struct mq_generate_args {
+    const int* prompt_tokens;         /* HOST int32[n_forced], each in [0, vocab_size)        */
+    int n_forced;                     /* >= 1                                                 */
+    int n_generate;                   /* >= 1                                                 */
+    int* output_tokens;               /* device or pinned host int32[n_generate]              */
+} mq_generate_args;
 
 /* ---- batched INT8 decode (no counterpart in the reference) ---------------
  * B <= MQ_MAX_BATCH independent sequences share one pass over the weights per
@@ -226,6 +255,8 @@ int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream);
  * library allocation). Every call on a device shares that device's array:
  * calls that overlap on one device (other streams, other threads) race. */
 int mq_int8_decode_step_noalloc(const mq_decode_args* args, hipStream_t stream);
+/* Several steps per launch (see mq_generate_args). */
+int mq_int8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream);
 /* Host-side wait for a token the kernel stores into host memory (pinned, e.g.
  * hipHostMalloc): spins until *token differs from `sentinel`, which the
  * caller wrote before the launch. MQ_OK, or MQ_ERR_TIMEOUT after timeout_us

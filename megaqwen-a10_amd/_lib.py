@@ -60,7 +60,13 @@ class DecodeArgs(Structure):
         ("workspace_bytes", c_size_t), ("spin_limit", c_uint),
         ("timing_start", c_void_p), ("timing_stop", c_void_p), ("trace", c_void_p),
         ("attn_split_min", c_int),
+        ("temperature", c_float), ("seed", ctypes.c_ulonglong),
     ]
+
+
+class GenerateArgs(Structure):
+    """mq_generate_args: several decode steps in one launch."""
+    _fields_ = [("prompt_tokens", c_void_p), ("n_forced", c_int), ("n_generate", c_int), ("output_tokens", c_void_p)]
 
 
 MAX_BATCH = 16
@@ -103,6 +109,7 @@ _SIGNATURES = {
     "mq_int8_decode_step": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mq_bf16_decode_step": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mq_int8_decode_step_noalloc": (c_int, [POINTER(DecodeArgs), c_void_p]),
+    "mq_int8_decode_generate": (c_int, [POINTER(DecodeArgs), POINTER(GenerateArgs), c_void_p]),
     "mq_decode_check": (c_int, [c_void_p, c_void_p]),
     "mq_wait_host_token": (c_int, [c_void_p, c_int, c_uint]),
     "mq_decode_set_variant": (c_int, [c_int]),

@@ -93,6 +93,8 @@ static int validate_decode(const mq_decode_args* a, bool int8, DecodeShape* s) {
         return set_error(MQ_ERR_INVALID_ARGUMENT, "position %d outside [0, max_seq_len=%d)", a->position, a->max_seq_len);
     if (a->cache_len != a->position + 1)
         return set_error(MQ_ERR_INVALID_ARGUMENT, "cache_len %d != position + 1 (%d)", a->cache_len, a->position + 1);
+    if (!(a->temperature >= 0.0f) || a->temperature == INFINITY)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "temperature %g is not a finite value >= 0", (double)a->temperature);
     if (!a->output_token_id || !a->embed_weight || !a->layer_weights || !a->final_norm_weight ||
         !a->lm_head_weight || !a->cos_table || !a->sin_table || !a->k_cache || !a->v_cache)
         return set_error(MQ_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
@@ -307,6 +309,40 @@ int mq_int8_decode_step_noalloc(const mq_decode_args* args, hipStream_t stream) 
     st = check_launch("ws_init_kernel");
     if (st != MQ_OK) return st;
     return launch_decode(a, s, true, stream);
+}
+
+int mq_int8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream) {
+    clear_error();
+    if (args == nullptr || gen == nullptr) return set_error(MQ_ERR_INVALID_ARGUMENT, "args is NULL");
+    if (gen->prompt_tokens == nullptr || gen->output_tokens == nullptr)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "prompt_tokens and output_tokens must be non-NULL");
+    if (gen->n_forced < 1 || gen->n_generate < 1)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "n_forced %d and n_generate %d must be >= 1", gen->n_forced,
+                         gen->n_generate);
+    DecodeShape s;
+    int st = validate_decode(args, true, &s);
+    if (st != MQ_OK) return st;
+    if (args->input_token_id != gen->prompt_tokens[0])
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "input_token_id %d != prompt_tokens[0] %d", args->input_token_id,
+                         gen->prompt_tokens[0]);
+    for (int i = 0; i < gen->n_forced; ++i)
+        if (gen->prompt_tokens[i] < 0 || gen->prompt_tokens[i] >= s.V)
+            return set_error(MQ_ERR_INVALID_ARGUMENT, "prompt_tokens[%d] = %d outside [0, %d)", i, gen->prompt_tokens[i], s.V);
+    const int64_t n_steps = (int64_t)gen->n_forced + gen->n_generate - 1;
+    if (args->position + n_steps > args->max_seq_len)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "position %d + %lld steps exceed max_seq_len %d", args->position,
+                         (long long)n_steps, args->max_seq_len);
+    const size_t off = decode_async_token_offset(s);
+    if (off == 0 || args->position + n_steps > decode_async_max_len())
+        return set_error(MQ_ERR_UNSUPPORTED, "several steps per launch run on the async-wave kernel only (INT8, hidden "
+                         "1024 / intermediate 3072, up to %d positions; here %lld)", decode_async_max_len(),
+                         (long long)(args->position + n_steps));
+    int* dev_tokens = reinterpret_cast<int*>(static_cast<uint8_t*>(args->workspace) + off);
+    const hipError_t e = hipMemcpyAsync(dev_tokens, gen->prompt_tokens, (size_t)gen->n_forced * sizeof(int),
+                                        hipMemcpyHostToDevice, stream);
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipMemcpyAsync(prompt tokens): %s", hipGetErrorString(e));
+    const GenPlan plan{dev_tokens, gen->n_forced, (int)n_steps, gen->output_tokens};
+    return launch_decode(*args, s, true, stream, nullptr, &plan);
 }
 
 int mq_wait_host_token(const volatile int* token, int sentinel, unsigned int timeout_us) {

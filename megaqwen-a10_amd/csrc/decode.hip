@@ -411,7 +411,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_kernel(KArgs a) {
             const float s = transpose_reduce<R, CH>(acc, lane);
             const int row = r0 + b * RB + lane / span;
             if ((lane % span) == 0 && row < r1) {
-                const float v = kInt8 ? s * scur : s;
+                float v = kInt8 ? s * scur : s;
+                // sampling: the Gumbel-max rule (see gumbel_noise)
+                if (a.inv_temp > 0.0f) v = v * a.inv_temp + gumbel_noise(a.seed, a.pos, row);
                 if (v > best_v) { best_v = v; best_i = row; }
             }
 #pragma unroll
@@ -543,7 +545,7 @@ int decode_variant_in_use(const DecodeShape& s, bool int8) { return decode_varia
 // barrier), so they are launched plainly: on this runtime a cooperative launch
 // cost about 10 us more per step. If other work holds CUs when a step starts,
 // its bounded waits end the step with MQ_ERR_TIMEOUT instead of hanging.
-int check_residency(const void* fn) {
+int check_residency(const void* fn, int threads) {
     static thread_local const void* checked_fn[64] = {nullptr};
     static thread_local int checked[64] = {0};
     int dev = 0;
@@ -551,7 +553,7 @@ int check_residency(const void* fn) {
     if (checked[dev] && checked_fn[dev] == fn) return MQ_OK;
     int ncu = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kThreads, 0) != hipSuccess)
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0) != hipSuccess)
         return set_error(MQ_ERR_HIP, "occupancy query failed");
     if ((int64_t)ncu * per_cu < kNWG)
         return set_error(MQ_ERR_UNSUPPORTED, "device holds %d x %d resident workgroups, the decode kernel needs %d",
@@ -575,11 +577,17 @@ static int launch_t(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t 
     return MQ_OK;
 }
 
-int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream, uint32_t* status_out) {
+int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream, uint32_t* status_out,
+                  const GenPlan* plan) {
     if (a.num_layers > kMaxLayers)
         return set_error(MQ_ERR_UNSUPPORTED, "num_layers %d exceeds %d", a.num_layers, kMaxLayers);
-    const int variant = decode_variant_for(s, int8, a.cache_len);
+    // several steps per launch: the async-wave kernel, over every position the launch covers
+    const int variant = decode_variant_for(s, int8, plan ? a.position + plan->n_steps : a.cache_len);
     if (variant < 1 || variant > 3) return variant;
+    if (plan && variant != 3)
+        return set_error(MQ_ERR_UNSUPPORTED, "several steps per launch run on the async-wave kernel only (INT8, hidden "
+                         "1024 / intermediate 3072, up to %d positions; here %d)", decode_async_max_len(),
+                         a.position + plan->n_steps);
     // split attention (XCD kernel only): a slice of at most kMaxAttnLen positions per workgroup
     int split_min = a.attn_split_min == 0 ? kDefaultSplitMin : a.attn_split_min;
     split_min = split_min > 0 ? std::min(split_min, kMaxAttnLen + 1) : INT_MAX;
@@ -623,6 +631,12 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
     k.trace = static_cast<uint64_t*>(a.trace);
     k.ws = static_cast<uint8_t*>(a.workspace);
     k.status_out = status_out;
+    k.n_steps = plan ? plan->n_steps : 1;
+    k.n_forced = plan ? plan->n_forced : 1;
+    k.step_tokens = plan ? plan->tokens : nullptr;
+    k.tokens_out = plan ? plan->tokens_out : nullptr;
+    k.inv_temp = a.temperature > 0.0f ? 1.0f / a.temperature : 0.0f;
+    k.seed = a.seed;
     const bool debug = a.hidden_buffer || a.g_activations || a.g_residual || a.g_q || a.g_k || a.g_v ||
                        a.g_attn_out || a.g_mlp_intermediate || a.g_normalized || a.block_max_vals ||
                        a.block_max_idxs || a.trace;

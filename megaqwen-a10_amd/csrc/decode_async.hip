@@ -76,7 +76,7 @@ enum AArr { AR_A = 0, AR_B = 1, AR_C = 2, AR_E = 3, AR_F = 4 };
 // of squares (low and high word each), so that one buffer load reaches both.
 constexpr int kVecWords = kAH + 64;
 struct ALayout {
-    size_t qkvx, hidx, actx, mlpx, po, pd, lmg, total;
+    size_t qkvx, hidx, actx, mlpx, po, pd, lmg, tok, total;
 };
 // After the other two kernels' regions, so that the three can alternate on one workspace.
 constexpr ALayout alayout_for(size_t base) {
@@ -89,6 +89,7 @@ constexpr ALayout alayout_for(size_t base) {
     o.po = off; off += round256((size_t)kAX * kAH * 8);        // packed fp64 partials [xcd][row]
     o.pd = off; off += round256((size_t)kAX * kAH * 8);
     o.lmg = off; off += round256((size_t)kNWG * 2 * 8);
+    o.tok = off; off += round256((size_t)kAMaxLen * 4);        // a launch's forced input tokens
     o.total = off;
     return o;
 }
@@ -123,6 +124,7 @@ struct __align__(16) AsyncLds {
     double fss;                            // final sum of squares
     float lm_v[kWaves];
     int lm_i[kWaves];
+    int next_tok;                          // the step's token (every workgroup reduces it)
 };
 
 // ---- LDS synchronisation --------------------------------------------------------------
@@ -351,7 +353,15 @@ __device__ __forceinline__ double poll_slice(Waiter& wt, const uint64_t* block, 
 
 }  // namespace
 
-template <bool kDebug>
+// A kernel argument read afresh (volatile): used for what only the LM head needs, so
+// that with several steps per launch it is not held in registers through every layer.
+template <class T>
+__device__ __forceinline__ T karg(const T& v) { return *(const volatile T*)&v; }
+
+// kMulti: several steps per launch (a.n_steps); otherwise one, and the step loop
+// disappears (held across a loop back-edge, the kernel's long-lived values would
+// cost register spills in the one-step kernel too).
+template <bool kDebug, bool kMulti>
 __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     constexpr int H = kAH, D = kAD;
     constexpr ALayout kLay = alayout_for(xlayout_total(kAH, kAI));
@@ -360,9 +370,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     const int g = blockIdx.x;
     const int x = (int)hw_xcc_id();
     const int r = g / kAX;
-    const int tid = threadIdx.x;
-    const int lane = tid % kWave;
-    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);    // uniform: scalar registers
+    const int tid0 = threadIdx.x;
+    const int lane0 = tid0 % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid0 / kWave);   // uniform: scalar registers
 
     WsHeader* hdr = reinterpret_cast<WsHeader*>(a.ws);
     uint64_t* const qkvx = reinterpret_cast<uint64_t*>(a.ws + kLay.qkvx) + (size_t)x * 512;
@@ -375,8 +385,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     uint64_t* const pd = reinterpret_cast<uint64_t*>(a.ws + kLay.pd);
     uint64_t* const lmg = reinterpret_cast<uint64_t*>(a.ws + kLay.lmg);
 
-    const uint32_t E = __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t AS = __hip_atomic_load(&hdr->asteps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t E0 = __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t AS0 = __hip_atomic_load(&hdr->asteps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t E = E0, AS = AS0;              // the step's epoch (tags) and packed-word step count
     const uint32_t tps = kAStages * (uint32_t)a.L + 4u;
     // tags end in binary 10 (the other kernels' in 01 and 11)
     auto tag = [&](int l, int st) -> uint32_t { return ((E * tps + kAStages * (uint32_t)l + (uint32_t)st) << 2) | 2u; };
@@ -385,19 +396,42 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     Waiter wt(&hdr->abort_flag, a.spin_limit);
     const uint32_t lds_limit = a.spin_limit * 8u;
     auto trace = [&](int l, int point) {
-        if (kDebug && a.trace != nullptr && tid == 0)
+        if (kDebug && a.trace != nullptr && tid0 == 0)
             a.trace[((int64_t)l * kTracePoints + point) * kNWG + g] = __builtin_amdgcn_s_memrealtime();
     };
     if (x >= kAX) {
-        if (tid == 0) __hip_atomic_store(&hdr->abort_flag, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid0 == 0) __hip_atomic_store(&hdr->abort_flag, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    if (tid < 16) S.sync[tid] = 0u;
-    __syncthreads();
-
-    const int pos = a.pos;                  // cache_len = pos + 1 <= kAMaxLen (checked by the host)
+    if (tid0 < 16) S.sync[tid0] = 0u;
     const int last = a.L - 1;
     const int64_t kv_head_stride = (int64_t)a.S * D;
+    if (wave == kCW + 3) {
+        // the final norm gains, once per launch
+        uint32_t fw[H / 128];
+#pragma unroll
+        for (int i = 0; i < H / 128; ++i) fw[i] = *gview(reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(a.final_norm) + 256 * i + 4 * lane0));
+#pragma unroll
+        for (int i = 0; i < H / 128; ++i) reinterpret_cast<uint32_t*>(S.fnorm)[64 * i + lane0] = fw[i];
+    }
+    __syncthreads();
+
+    // Steps: step s decodes at position a.pos + s (cache_len = position + 1 <= kAMaxLen,
+    // checked by the host); its input token is a.step_tokens[s] for the first n_forced
+    // steps (a.token when there is no list) and the previous step's output after them.
+    // The LDS counters count layers over the whole launch (gl = s L + l).
+    int pos = a.pos;
+    int token = a.step_tokens ? (int)__builtin_amdgcn_readfirstlane(*gview(a.step_tokens)) : a.token;
+    const int n_steps = kMulti ? karg(a.n_steps) : 1;
+    for (int step = 0; step < n_steps; ++step) {
+    // lane-derived addresses are rederived every step (hidden from the optimiser): held
+    // across the step loop they would be live in the LM head too and be spilled
+    issue_fence();                          // loads (kernel arguments among them) are redone per step
+    const int tid = opaque(tid0);
+    const int lane = opaque(lane0);
+    E = E0 + (uint32_t)step;
+    AS = AS0 + (uint32_t)step;
+    pos = a.pos + step;
 
     if (wave >= kCW) {
         // ================================ loader waves ================================
@@ -422,19 +456,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         };
         auto ld32 = [&](const void* q) -> uint32_t { return *gview(static_cast<const uint32_t*>(q)); };
         auto put32 = [&](void* base, int word, uint32_t v) { static_cast<uint32_t*>(base)[word] = v; };
-        if (d == 3) {
-            const uint32_t cw = ld32(a.cos_t + (int64_t)pos * D + 2 * lane);
-            const uint32_t sw = ld32(a.sin_t + (int64_t)pos * D + 2 * lane);
-            uint32_t fw[H / 128];
-#pragma unroll
-            for (int i = 0; i < H / 128; ++i) fw[i] = ld32(reinterpret_cast<const uint8_t*>(a.final_norm) + 256 * i + 4 * lane);
-            put32(S.rope[0], lane, cw);
-            put32(S.rope[1], lane, sw);
-#pragma unroll
-            for (int i = 0; i < H / 128; ++i) put32(S.fnorm, 64 * i + lane, fw[i]);
-        }
         for (int l = 0; l < a.L; ++l) {
-            if (l > 0) lds_wait(&S.sync[kWindow], (uint32_t)l, lds_limit, &hdr->abort_flag);
+            const int gl = step * a.L + l;
+            if (gl > 0) lds_wait(&S.sync[kWindow], (uint32_t)gl, lds_limit, &hdr->abort_flag);
             const LayerWeights lw = a.lw[l];
             const ScalePointers sp = a.sp[l];
             if (d == 0) {
@@ -452,13 +476,13 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
 #pragma unroll
                 for (int i = 0; i < H / 128; ++i) gw[i] = ld32(static_cast<const uint8_t*>(lw.input_layernorm_weight) + 256 * i + 4 * lane);
                 const uint32_t scv = lane < 16 ? ld32(sc + mrow0 + lane) : 0u;
-                await_free(SL_A, l);
+                await_free(SL_A, gl);
 #pragma unroll
                 for (int i = 0; i < 16; ++i) S.wA[i / 4][i % 4][lane] = w[i];
 #pragma unroll
                 for (int i = 0; i < H / 128; ++i) put32(S.lnA, 64 * i + lane, gw[i]);
                 if (lane < 16) put32(S.scA, lane, scv);
-                raise(SL_A, l);
+                raise(SL_A, gl);
             } else if (d == 1) {
                 const uint8_t* ob = (const uint8_t*)lw.o_proj_weight + (int64_t)(32 * r + lane % 16) * 2048 + 256 * x +
                                     16 * (lane / 16);
@@ -473,16 +497,16 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 for (int i = 0; i < 12; ++i)                 // i = (2 c + s) * 2 + t
                     wf[i] = ldg16_stream(db + (int64_t)16 * (i % 2) * kAI + 64 * (i / 2));
                 const uint32_t sdv = lane < 32 ? ld32(sp.down_scale + 32 * r + lane) : 0u;
-                await_free(SL_C, l);
+                await_free(SL_C, gl);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) S.wC[i / 2][i % 2][lane] = wc[i];
                 if (lane < 32) put32(S.scC, lane, so);
-                raise(SL_C, l);
-                await_free(SL_F, l);
+                raise(SL_C, gl);
+                await_free(SL_F, gl);
 #pragma unroll
                 for (int i = 0; i < 12; ++i) S.wF[i / 4][(i / 2) % 2][i % 2][lane] = wf[i];
                 if (lane < 32) put32(S.scF, lane, sdv);
-                raise(SL_F, l);
+                raise(SL_F, gl);
             } else if (d == 2) {
                 const int c0 = kAIX * x + 12 * r;
                 uint4 we[32];                                  // i = (4 c + s) * 2 + t; tile rows 24-31 zero
@@ -504,7 +528,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     gw[i] = ld32(static_cast<const uint8_t*>(lw.post_attn_layernorm_weight) + 256 * i + 4 * lane);
                 const uint32_t scv = lane < 12 ? ld32(sp.gate_scale + c0 + lane)
                                    : lane < 24 ? ld32(sp.up_scale + c0 + lane - 12) : 0u;
-                await_free(SL_E, l);
+                await_free(SL_E, gl);
 #pragma unroll
                 for (int k = 0; k < 16; ++k)
 #pragma unroll
@@ -512,7 +536,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
 #pragma unroll
                 for (int i = 0; i < H / 128; ++i) put32(S.lnE, 64 * i + lane, gw[i]);
                 if (lane < 24) put32(S.scE, lane, scv);
-                raise(SL_E, l);
+                raise(SL_E, gl);
             } else {
                 // K and V rows keep their 16-byte chunks XOR-permuted by row (chunk g of row j
                 // at g ^ (j % 16)), so that lanes reading the same chunk of different rows hit
@@ -531,7 +555,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 }
                 const uint32_t qn = ld32(static_cast<const uint8_t*>(lw.q_norm_weight) + 4 * lane);
                 const uint32_t kn = ld32(static_cast<const uint8_t*>(lw.k_norm_weight) + 4 * lane);
-                await_free(SL_B, l);
+                // this step's RoPE row rides with layer 0's slot B (free once the previous
+                // step's last attention is done)
+                const uint32_t cw = l == 0 ? ld32(a.cos_t + (int64_t)pos * D + 2 * lane) : 0u;
+                const uint32_t sw = l == 0 ? ld32(a.sin_t + (int64_t)pos * D + 2 * lane) : 0u;
+                await_free(SL_B, gl);
 #pragma unroll
                 for (int i = 0; i < kAMaxLen / 4; ++i) {
                     const int j = 4 * i + lane / 16;
@@ -542,7 +570,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 }
                 put32(S.qkn[0], lane, qn);
                 put32(S.qkn[1], lane, kn);
-                raise(SL_B, l);
+                if (l == 0) {
+                    put32(S.rope[0], lane, cw);
+                    put32(S.rope[1], lane, sw);
+                }
+                raise(SL_B, gl);
             }
         }
     } else {
@@ -550,16 +582,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         const int c = wave;
         float act_reg = 0.0f;                   // wave 0: this rank's residual row (lane % 32) from stage D
         for (int l = 0; l < a.L; ++l) {
+            const int gl = step * a.L + l;
             // ---------------- A: RMSNorm + QKV ----------------
             float hv[4];
             double ssq;
             if (l == 0) {
                 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-                const u32x2_t e4 = *(const __attribute__((address_space(1))) u32x2_t*)(a.embed + (int64_t)a.token * H +
+                const u32x2_t e4 = *(const __attribute__((address_space(1))) u32x2_t*)(a.embed + (int64_t)token * H +
                                                                                         256 * c + 4 * lane);
                 hv[0] = bf16_bits_to_f32(e4.x & 0xffffu); hv[1] = bf16_bits_to_f32(e4.x >> 16);
                 hv[2] = bf16_bits_to_f32(e4.y & 0xffffu); hv[3] = bf16_bits_to_f32(e4.y >> 16);
-                const uint4* er = reinterpret_cast<const uint4*>(a.embed + (int64_t)a.token * H);
+                const uint4* er = reinterpret_cast<const uint4*>(a.embed + (int64_t)token * H);
                 const uint4 u0 = ldg16(er + 2 * lane), u1 = ldg16(er + 2 * lane + 1);
                 const uint32_t wv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
                 double s = 0.0;
@@ -576,7 +609,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
             *reinterpret_cast<float4*>(&S.hs[256 * c + 4 * lane]) = make_float4(hv[0], hv[1], hv[2], hv[3]);
             trace(l, 0);
             const double rstd = rms_scale(ssq, H, kEps);
-            lds_wait(&S.sync[kReady + SL_A], (uint32_t)(l + 1), lds_limit, &hdr->abort_flag);
+            lds_wait(&S.sync[kReady + SL_A], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
             float nv[4];
             {
                 const uint2 gw = *reinterpret_cast<const uint2*>(&S.lnA[256 * c + 4 * lane]);
@@ -633,9 +666,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 if (c == 0) {
                     trace(l, 2);
                     if (lane == 0)
-                        __hip_atomic_store(&S.sync[kWindow], (uint32_t)(l + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                        __hip_atomic_store(&S.sync[kWindow], (uint32_t)(gl + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
-                lds_wait(&S.sync[kReady + SL_B], (uint32_t)(l + 1), lds_limit, &hdr->abort_flag);
+                lds_wait(&S.sync[kReady + SL_B], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
                 // QK-norm and RoPE: out[i] = y[i] cos[i] - y[i+64] sin[i],
                 // out[i+64] = y[i] sin[i+64] + y[i+64] cos[i+64] (i = lane)
                 const double cl = bf16_bits_to_f32(S.rope[0][lane]), ch = bf16_bits_to_f32(S.rope[0][lane + 64]);
@@ -790,7 +823,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 lds_add(&S.sync[kConsumed + SL_B], lane);
                 // all four waves' partials in LDS
                 lds_add(&S.sync[kArrive + AR_B], lane);
-                lds_wait(&S.sync[kArrive + AR_B], (uint32_t)(kCW * (l + 1)), lds_limit, &hdr->abort_flag);
+                lds_wait(&S.sync[kArrive + AR_B], (uint32_t)(kCW * (gl + 1)), lds_limit, &hdr->abort_flag);
                 // merge: wave c takes attention dims [64c, +64) (head c / 2) from the four blocks;
                 // lane w < 4 computes block w's weight e^(m_w - M), the others read it
                 const int hh = c >> 1, dim = 64 * (c & 1) + lane;
@@ -812,7 +845,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
             if (c == 0) trace(l, 3);
 
             // ---------------- C: O partial over this XCD's attention dims ----------------
-            lds_wait(&S.sync[kReady + SL_C], (uint32_t)(l + 1), lds_limit, &hdr->abort_flag);
+            lds_wait(&S.sync[kReady + SL_C], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
             {
                 const uint32_t em = wave_max_u32(exp_field(ao));
                 put_digits1(S.dig[c], ao, em, lane);
@@ -862,7 +895,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 float av[4];
                 const double ss = poll_slice(wt, actx, tag(l, AS_ACT), c, lane, av);
                 const double rstd2 = rms_scale(ss, H, kEps);
-                lds_wait(&S.sync[kReady + SL_E], (uint32_t)(l + 1), lds_limit, &hdr->abort_flag);
+                lds_wait(&S.sync[kReady + SL_E], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
                 const uint2 gw = *reinterpret_cast<const uint2*>(&S.lnE[256 * c + 4 * lane]);
                 const float gl[4] = {bf16_bits_to_f32(gw.x & 0xffffu), bf16_bits_to_f32(gw.x >> 16),
                                      bf16_bits_to_f32(gw.y & 0xffffu), bf16_bits_to_f32(gw.y >> 16)};
@@ -909,7 +942,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 uint32_t w[1] = {2u * (uint32_t)(64 * c + lane)};
                 wt.get_pairs<1>(XRegion(mlpx, kAIX), w, tag(l, AS_MLP), mv);
                 if (c == 0) trace(l, 7);
-                lds_wait(&S.sync[kReady + SL_F], (uint32_t)(l + 1), lds_limit, &hdr->abort_flag);
+                lds_wait(&S.sync[kReady + SL_F], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
                 const uint32_t em = wave_max_u32(max(exp_field(mv[0]), exp_field(mv[1])));
                 put_digits2(S.dig[c], mv, em, lane);
                 lds_order();
@@ -976,8 +1009,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         constexpr int RB = 8 / CH;
         constexpr int R = RB * CH;
         constexpr int span = kWave / RB;
-        const int r0 = (int)((int64_t)a.V * g / kNWG);
-        const int r1 = (int)((int64_t)a.V * (g + 1) / kNWG);
+        const int V = karg(a.V);
+        const uint8_t* const lm_w = karg(a.lm_w);
+        const float* const lm_s = karg(a.lm_s);
+        const int r0 = (int)((int64_t)V * g / kNWG);
+        const int r1 = (int)((int64_t)V * (g + 1) / kNWG);
         const int nb = (r1 - r0 + RB - 1) / RB;
         const int64_t rowbytes = H;
         uint4 cur[R], nxt[R];
@@ -987,11 +1023,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
             for (int i = 0; i < R; ++i) {
                 const int row = r0 + b * RB + i / CH;
                 dst[i] = make_uint4(0, 0, 0, 0);
-                if (row < r1) dst[i] = ldg16(a.lm_w + row * rowbytes + (i % CH) * 1024 + lane * 16);
+                if (row < r1) dst[i] = ldg16(lm_w + row * rowbytes + (i % CH) * 1024 + lane * 16);
             }
             const int myrow = r0 + b * RB + lane / span;
             s = 1.0f;
-            if (myrow < r1) s = gview(a.lm_s)[myrow];
+            if (myrow < r1) s = gview(lm_s)[myrow];
         };
         int b = wave;
         if (b < nb) fetch(b, cur, scur);
@@ -1008,6 +1044,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         __syncthreads();
         trace(a.L, 0);
 
+        const float inv_temp = karg(a.inv_temp);
+        const uint64_t seed = karg(a.seed);
         float best_v = -INFINITY;
         int best_i = 0x7fffffff;
 #pragma unroll
@@ -1020,7 +1058,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
             const float s = transpose_reduce<R, CH>(accv, lane);
             const int row = r0 + b * RB + lane / span;
             if ((lane % span) == 0 && row < r1) {
-                const float v = s * scur;
+                float v = s * scur;
+                // sampling (temperature T > 0): argmax of logit / T + Gumbel noise draws the
+                // token with probability softmax(logits / T) (the Gumbel-max identity)
+                if (inv_temp > 0.0f) v = v * inv_temp + gumbel_noise(seed, pos, row);
                 if (v > best_v) { best_v = v; best_i = row; }
             }
 #pragma unroll
@@ -1050,7 +1091,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
             ll_put(&lmg[2 * g], ordered_key(bv), tag_lm);
             ll_put(&lmg[2 * g + 1], (uint32_t)bi, tag_lm);
         }
-        if (x == 0 && r == 0 && wave == 0) {
+        // every workgroup reduces the 256 partial maxima itself: the step's token is then in
+        // every workgroup for the next step's embedding, with no broadcast exchange
+        if (wave == 0) {
             constexpr int C = kNWG / kWave;
             uint32_t w[C];
 #pragma unroll
@@ -1073,14 +1116,30 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
 #undef MQ_KEY_LEVEL
             if (lane == 0) {
                 const uint32_t flag = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                *a.out_token = (flag != 0u || wt.dead) ? -1 : (int)iv;
-                if (a.status_out) *a.status_out = flag != 0u ? flag : (wt.dead ? 1u : 0u);
-                __hip_atomic_store(&hdr->asteps, AS + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(&hdr->epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (kDebug && a.trace != nullptr)
-                    a.trace[((int64_t)a.L * kTracePoints + 2) * kNWG] = __builtin_amdgcn_s_memrealtime();
+                const int chosen = (flag != 0u || wt.dead) ? -1 : (int)iv;
+                S.next_tok = chosen;
+                if (g == 0) {
+                    const int n_forced = karg(a.n_forced);
+                    int* const tokens_out = karg(a.tokens_out);
+                    if (tokens_out != nullptr && step >= n_forced - 1) tokens_out[step - (n_forced - 1)] = chosen;
+                    if (step == n_steps - 1) {
+                        *karg(a.out_token) = chosen;
+                        uint32_t* const status_out = karg(a.status_out);
+                        if (status_out) *status_out = flag != 0u ? flag : (wt.dead ? 1u : 0u);
+                        __hip_atomic_store(&hdr->asteps, AS0 + (uint32_t)n_steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(&hdr->epoch, E0 + (uint32_t)n_steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (kDebug && a.trace != nullptr)
+                            a.trace[((int64_t)a.L * kTracePoints + 2) * kNWG] = __builtin_amdgcn_s_memrealtime();
+                    }
+                }
             }
         }
+        __syncthreads();
+        // the next step's input: a forced token, else this step's output (a failed step's
+        // -1 becomes 0, which keeps the remaining steps' reads in bounds; they report -1)
+        if (step + 1 < karg(a.n_forced)) token = (int)__builtin_amdgcn_readfirstlane(*gview(karg(a.step_tokens) + step + 1));
+        else token = max(S.next_tok, 0);
+    }
     }
 }
 
@@ -1096,8 +1155,10 @@ bool decode_async_supports(const DecodeShape& s, bool int8, int cache_len) {
 }
 
 int launch_decode_async(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
-    auto fn = debug ? reinterpret_cast<const void*>(&decode_async_kernel<true>)
-                    : reinterpret_cast<const void*>(&decode_async_kernel<false>);
+    const void* fn;
+    if (ka.n_steps > 1) fn = reinterpret_cast<const void*>(&decode_async_kernel<false, true>);
+    else if (debug) fn = reinterpret_cast<const void*>(&decode_async_kernel<true, false>);
+    else fn = reinterpret_cast<const void*>(&decode_async_kernel<false, false>);
     int st = check_residency(fn);
     if (st != MQ_OK) return st;
     KArgs copy = ka;
@@ -1106,5 +1167,12 @@ int launch_decode_async(const KArgs& ka, bool debug, hipStream_t stream, hipEven
     if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode_async): %s", hipGetErrorString(e));
     return MQ_OK;
 }
+
+size_t decode_async_token_offset(const DecodeShape& s) {
+    if (s.H != kAH || s.I != kAI) return 0;
+    return alayout_for(xlayout_total(kAH, kAI)).tok;
+}
+
+int decode_async_max_len() { return kAMaxLen; }
 
 }  // namespace mq

@@ -53,7 +53,32 @@ struct KArgs {
     uint64_t* trace;
     uint8_t* ws;
     uint32_t* status_out;                  // optional: the step's abort flag (0 = completed), stored with the token
+    // Steps per launch (async kernel; the others run one): step s decodes at position pos + s,
+    // its input token is step_tokens[s] for s < n_forced (token when step_tokens is NULL) and
+    // the previous step's output after that; tokens_out[s - (n_forced - 1)] receives the
+    // output of every step from the last forced one on, out_token the last step's.
+    int n_steps;
+    int n_forced;
+    const int* step_tokens;
+    int* tokens_out;
+    float inv_temp;                        // 0: greedy argmax; > 0: sample at temperature 1 / inv_temp
+    uint64_t seed;                         // sampling seed
 };
+
+// Gumbel noise for sampling at position pos, vocabulary row `row`: 23 bits of
+// SplitMix64 (Steele, Lea, Flood 2014) of seed ^ ((pos << 32 | row) * golden ratio)
+// give u = (m + 0.5) 2^-23 in (0, 1), exact in fp32, and g = -log(-log(u)). The
+// argmax over rows of logit / T + g is a sample of softmax(logits / T) (the
+// Gumbel-max identity), and the noise depends only on (seed, position, row), so a
+// device-side loop and one launch per step draw the same tokens.
+__device__ __forceinline__ float gumbel_noise(uint64_t seed, int pos, int row) {
+    uint64_t z = seed ^ ((((uint64_t)(uint32_t)pos << 32) | (uint64_t)(uint32_t)row) * 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    const float u = ((float)(uint32_t)(z >> 41) + 0.5f) * 0x1p-23f;
+    return -logf(-logf(u));
+}
 
 constexpr size_t round256(size_t b) { return (b + 255) / 256 * 256; }
 
@@ -239,7 +264,7 @@ __device__ __forceinline__ double rms_scale(double sumsq, int n, double eps) {
 
 // All kNWG workgroups wait on each other, so they must be resident at once:
 // checked once per (kernel, device) with the occupancy calculator.
-int check_residency(const void* fn);
+int check_residency(const void* fn, int threads = kThreads);
 
 // Async-wave kernel (decode_async.hip): INT8 Qwen3-0.6B shape, cache_len <= 64.
 size_t decode_async_workspace_bytes(const DecodeShape& s);

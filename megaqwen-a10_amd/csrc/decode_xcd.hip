@@ -653,7 +653,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             const float s = transpose_reduce<R, CH>(acc, lane);
             const int row = r0 + b * RB + lane / span;
             if ((lane % span) == 0 && row < r1) {
-                const float v = kInt8 ? s * scur : s;
+                float v = kInt8 ? s * scur : s;
+                // sampling: the Gumbel-max rule (see gumbel_noise)
+                if (a.inv_temp > 0.0f) v = v * a.inv_temp + gumbel_noise(a.seed, a.pos, row);
                 if (v > best_v) { best_v = v; best_i = row; }
             }
 #pragma unroll

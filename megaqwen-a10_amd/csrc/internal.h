@@ -43,10 +43,24 @@ int set_decode_variant(int variant);
 int decode_variant_in_use(const DecodeShape& s, bool int8);
 // After an in-kernel placement failure: use the single-level kernel from now on.
 void mark_xcd_unusable();
-// Launches one decode step; `int8` selects the weight format. When status_out is
-// non-null the step's token publisher also stores the abort flag there (0 = completed).
+// Several decode steps in one launch: step i's input is tokens[i] (device memory) for
+// i < n_forced and the previous step's output after that; tokens_out[i - (n_forced - 1)]
+// receives the output of every step from the last forced one on.
+struct GenPlan {
+    const int* tokens;
+    int n_forced;
+    int n_steps;
+    int* tokens_out;
+};
+// Launches one decode step (several with a plan); `int8` selects the weight format. When
+// status_out is non-null the last step's token publisher also stores the abort flag there
+// (0 = completed).
 int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream,
-                  uint32_t* status_out = nullptr);
+                  uint32_t* status_out = nullptr, const GenPlan* plan = nullptr);
+// Byte offset of the async-wave kernel's forced-token region in the workspace (0 when the
+// kernel does not cover these dims), and the longest cache it attends over.
+size_t decode_async_token_offset(const DecodeShape& s);
+int decode_async_max_len();
 // True when the workgroups of each residue class g mod 8 run on one XCD (checked once per device).
 bool xcd_placement_ok();
 

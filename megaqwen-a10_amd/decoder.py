@@ -336,6 +336,82 @@ class _DecoderBase:
         """Bound on every in-kernel wait (0 = library default)."""
         self._args.spin_limit = int(polls)
 
+    def set_sampling(self, temperature: float = 0.0, seed: int = 0) -> None:
+        """Token choice of every following step: ``temperature`` 0 (default) is the greedy
+        argmax; above 0 the token is drawn from softmax(logits / temperature) by the
+        Gumbel-max rule with noise keyed by (seed, position, vocabulary row), so a given
+        seed gives the same tokens whether steps run one per launch or in one launch
+        (``generate``). The reference accepts a temperature and ignores it
+        (a10_decode.py:358)."""
+        t = float(temperature)
+        if not (t >= 0.0) or t == float("inf"):
+            raise ValueError(f"temperature must be a finite value >= 0, got {temperature!r}")
+        if not isinstance(seed, int) or not 0 <= seed < 2 ** 64:
+            raise ValueError(f"seed must be an int in [0, 2**64), got {seed!r}")
+        self._args.temperature = t
+        self._args.seed = seed
+
+    def generate(self, prompt_ids, n_tokens: int, device_loop: bool = True) -> list:
+        """Feed ``prompt_ids`` from the current position and return ``n_tokens`` generated
+        tokens, the first being the last prompt step's output (verify_correctness_a10.py:
+        323-339). The tokens follow ``set_sampling``. Within the async-wave kernel's range
+        (INT8, hidden 1024, up to 64 positions) every step runs in ONE launch and hands its
+        token to the next on the device (mq_int8_decode_generate); otherwise, or with
+        ``device_loop=False``, one launch per step. Both give the same tokens. A failed
+        launch leaves the decoder at the position it started from."""
+        ids = [int(t) for t in prompt_ids]
+        V = self.dims[2]
+        if not ids:
+            raise ValueError("empty prompt")
+        if any(not 0 <= t < V for t in ids):
+            raise ValueError(f"prompt token outside [0, {V})")
+        if not isinstance(n_tokens, int) or n_tokens < 1:
+            raise ValueError(f"n_tokens must be a positive int, got {n_tokens!r}")
+        if self._pos + len(ids) + n_tokens - 1 > self.max_seq_len:
+            raise ValueError(f"position {self._pos} + {len(ids) + n_tokens - 1} steps exceed max_seq_len "
+                             f"{self.max_seq_len}")
+        if device_loop and self._int8:
+            out = self._generate_one_launch(ids, n_tokens)
+            if out is not None:
+                return out
+        tok = None
+        for t in ids:
+            tok = self.decode_step(t)
+        out = [tok]
+        while len(out) < n_tokens:
+            tok = self.decode_step(tok)
+            out.append(tok)
+        return out
+
+    def _generate_one_launch(self, ids, n_tokens):
+        """mq_int8_decode_generate; None when the kernel's range does not cover the request."""
+        if self._inflight:
+            torch.cuda.current_stream(self.device).synchronize()
+            self._inflight.clear()
+        out = torch.full((n_tokens,), TOKEN_PENDING, dtype=torch.int32, pin_memory=True)
+        prompt = (ctypes.c_int * len(ids))(*ids)
+        a = self._args
+        a.input_token_id = ids[0]
+        a.position = self._pos
+        a.cache_len = self._pos + 1
+        a.output_token_id = self.output_token.data_ptr()
+        self._tok_host[0] = TOKEN_PENDING
+        g = _lib.GenerateArgs(ctypes.cast(prompt, ctypes.c_void_p), len(ids), n_tokens, out.data_ptr())
+        st = self._lib.mq_int8_decode_generate(ctypes.byref(a), ctypes.byref(g),
+                                               ctypes.c_void_p(_lib.stream_handle(self.device)))
+        if st == _lib.MQ_ERR_UNSUPPORTED:
+            return None
+        _lib.check(st, "mq_int8_decode_generate")
+        torch.cuda.current_stream(self.device).synchronize()
+        toks = out.tolist()
+        if min(toks) < 0:
+            status = self._lib.mq_decode_check(self.workspace.data_ptr(),
+                                               ctypes.c_void_p(_lib.stream_handle(self.device)))
+            self._init_workspace()
+            _lib.check(status if status != _lib.MQ_OK else _lib.MQ_ERR_TIMEOUT, "mq_int8_decode_generate")
+        self._pos += len(ids) + n_tokens - 1
+        return toks
+
     def set_attn_split(self, min_len: int) -> None:
         """Context length from which the XCD-aware kernel splits each KV head's attention
         over its 32 workgroups (0 = library default, negative = never; the unsplit
@@ -626,13 +702,18 @@ class A10Decoder:
     def reset(self):
         self.decoder.reset()
 
-    def generate(self, prompt, max_new_tokens: int = 128, temperature: float = 0.0):
-        """Greedy generation. ``prompt`` is a string (needs a tokenizer) or a list of ids.
-        The prompt is prefilled one ``decode_step`` per token and the last prefill
-        output is the first generated token (verify_correctness_a10.py:323-339;
-        a10_decode.py:375 re-feeds the last prompt token instead, which decodes it
-        twice). ``temperature`` is accepted for signature compatibility; decoding is greedy.
-        Returns ``(text_or_ids, tok_per_s, per_token_ms)``."""
+    def generate(self, prompt, max_new_tokens: int = 128, temperature: float = 0.0, seed: int = 0,
+                 device_loop: bool = True):
+        """Generation from a string (needs a tokenizer) or a list of ids. The prompt is
+        prefilled one step per token and the last prefill output is the first generated
+        token (verify_correctness_a10.py:323-339; a10_decode.py:375 re-feeds the last prompt
+        token instead, which decodes it twice). ``temperature`` 0 is greedy; above 0 tokens
+        are sampled from softmax(logits / temperature) with ``seed`` (the reference accepts
+        a temperature and ignores it, a10_decode.py:358). Within the INT8 async-wave
+        kernel's range every step runs in one launch (``device_loop``), else one launch per
+        step; the tokens are the same. Generation stops after an EOS token when the
+        tokenizer has one. Returns ``(text_or_ids, tok_per_s, per_token_ms)``: with one
+        launch, per_token_ms holds the launch's average time per step."""
         if isinstance(prompt, str):
             if self.tokenizer is None:
                 raise ValueError("a string prompt needs a checkpoint with a tokenizer; pass token ids")
@@ -641,18 +722,21 @@ class A10Decoder:
             ids = [int(t) for t in prompt]
         if not ids:
             raise ValueError("empty prompt")
+        if not isinstance(max_new_tokens, int) or max_new_tokens < 1:
+            raise ValueError(f"max_new_tokens must be a positive int, got {max_new_tokens!r}")
         self.reset()
-        tok = None
-        for t in ids:
-            tok = self.decoder.decode_step(t)
-        generated = list(ids) + [tok]
-        times = []
+        self.decoder.set_sampling(temperature, seed)
         eos = getattr(self.tokenizer, "eos_token_id", None)
-        while len(generated) - len(ids) < max_new_tokens and tok != eos:
-            t0 = time.perf_counter()
-            tok = self.decoder.decode_step(tok)
-            times.append((time.perf_counter() - t0) * 1e3)
-            generated.append(tok)
-        tok_s = 1e3 / (sum(times) / len(times)) if times else 0.0
+        torch.cuda.synchronize(self.device)
+        t0 = time.perf_counter()
+        toks = self.decoder.generate(ids, max_new_tokens, device_loop=device_loop)
+        torch.cuda.synchronize(self.device)
+        ms = (time.perf_counter() - t0) * 1e3
+        if eos is not None and eos in toks:
+            toks = toks[:toks.index(eos) + 1]
+        steps = len(ids) + max_new_tokens - 1
+        times = [ms / steps] * (len(toks) - 1)          # the steps after the first generated token
+        tok_s = 1e3 * steps / ms if ms > 0 else 0.0
+        generated = list(ids) + toks
         out = self.tokenizer.decode(generated) if self.tokenizer is not None else generated
         return out, tok_s, times

@@ -217,3 +217,46 @@ def greedy_generate(dec: RefDecoder, prompt, num_tokens: int):
         toks.append(nxt)
         margins.append(top2_margin(logits))
     return toks, margins
+
+
+# ---- sampling (no counterpart in the reference: its generate() accepts a temperature
+# and ignores it, a10_decode.py:358) -------------------------------------------------
+_GOLDEN = 0x9E3779B97F4A7C15
+_M64 = (1 << 64) - 1
+
+
+def splitmix64_mix(z):
+    """The SplitMix64 output function (Steele, Lea, Flood, OOPSLA 2014), on Python ints or
+    numpy uint64 arrays (wrapping arithmetic)."""
+    import numpy as np
+    if isinstance(z, np.ndarray):
+        z = z.astype(np.uint64)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+    z &= _M64
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _M64
+    return z ^ (z >> 31)
+
+
+def gumbel_noise(seed: int, pos: int, rows):
+    """Gumbel noise of vocabulary rows ``rows`` at position ``pos``: u = (m + 0.5) 2^-23
+    from the top 23 bits m of splitmix64_mix(seed ^ ((pos << 32 | row) * golden)), then
+    g = -log(-log(u)) in float64. The kernels compute the same u exactly and g in fp32."""
+    import numpy as np
+    rows = np.asarray(rows, dtype=np.uint64)
+    key = (np.uint64(pos) << np.uint64(32)) | rows
+    with np.errstate(over="ignore"):
+        z = splitmix64_mix(np.uint64(seed) ^ (key * np.uint64(_GOLDEN)))
+    u = ((z >> np.uint64(41)).astype(np.float64) + 0.5) * 2.0 ** -23
+    return -np.log(-np.log(u))
+
+
+def sampled_choice(logits, temperature: float, seed: int, pos: int):
+    """Gumbel-max sample of softmax(logits / temperature) at position ``pos``: returns
+    (token, margin), margin being the gap between the two largest perturbed values."""
+    import numpy as np
+    v = np.asarray(logits, dtype=np.float64) / temperature + gumbel_noise(seed, pos, np.arange(len(logits)))
+    top2 = np.partition(v, -2)[-2:]
+    return int(np.argmax(v)), float(top2[1] - top2[0])

@@ -1,0 +1,146 @@
+"""GPU tests of the device-side generation loop and of sampling (run with -m gpu).
+
+mq_int8_decode_generate runs the prefill and every generated step in one launch
+(the reference launches one step per token and reads each back,
+bench_int8.py:218, a10_decode.py:358-393). Gates: the config-1 fixture's 32
+greedy tokens from one launch; one launch and one launch per step agreeing
+bitwise (tokens and KV caches), greedy and sampled; sampled tokens against the
+float64 oracle's Gumbel-max choice wherever its top-2 margin exceeds fp32
+logit error; the fallback beyond the async-wave kernel's 64 positions;
+argument validation; a forced in-kernel wait expiry that leaves the decoder
+where it started.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle.ref_cpu import sampled_choice
+
+from .test_gpu_decode import _build, _greedy, _ref_for
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def small(mq, dev):
+    return _build(mq, dev, "small_int8")
+
+
+@pytest.fixture(scope="module")
+def full(mq, dev):
+    return _build(mq, dev, "qwen3_0.6b_int8")
+
+
+def _caches(dec):
+    torch.cuda.synchronize()
+    return dec.k_cache.clone(), dec.v_cache.clone()
+
+
+def test_one_launch_reproduces_fixture(full):
+    dec, d, prompt, cfg, _ = full
+    dec.set_sampling(0.0)
+    dec.reset()
+    print("config 1: 8 prompt + 31 generated steps in one launch", flush=True)
+    got = dec._generate_one_launch(prompt, 32)
+    assert got is not None, "the request is within the async-wave kernel's range"
+    assert got == d["tokens"]
+    assert dec.position() == len(prompt) + 31
+    k1, v1 = _caches(dec)
+    assert _greedy(dec, prompt, 32) == d["tokens"]             # one launch per step
+    k2, v2 = _caches(dec)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+
+
+@pytest.mark.parametrize("temperature,seed", [(0.0, 0), (0.8, 1234), (1.5, 2 ** 63 + 5)])
+def test_one_launch_equals_per_step(small, temperature, seed):
+    dec, d, prompt, cfg, _ = small
+    dec.set_sampling(temperature, seed)
+    dec.reset()
+    a = dec.generate(prompt, 24)
+    ka, va = _caches(dec)
+    dec.reset()
+    b = dec.generate(prompt, 24, device_loop=False)
+    kb, vb = _caches(dec)
+    dec.set_sampling(0.0)
+    print(f"T={temperature} seed={seed}: {a[:8]}", flush=True)
+    assert a == b
+    assert torch.equal(ka, kb) and torch.equal(va, vb)
+    if temperature == 0.0:
+        assert a == d["tokens"][:24]
+
+
+def test_sampled_tokens_match_oracle(small):
+    """Teacher-forced with the GPU's own tokens: at every step whose perturbed top-2 margin
+    (float64 oracle) exceeds 1e-3 (fp32 logit error is ~1e-6 here), the sampled token must be
+    the oracle's Gumbel-max choice."""
+    dec, d, prompt, cfg, _ = small
+    T, seed = 0.8, 99
+    dec.set_sampling(T, seed)
+    dec.reset()
+    toks = dec.generate(prompt, 32)
+    dec.set_sampling(0.0)
+    ref = _ref_for(small)
+    ref.reset()
+    logits = None
+    for t in prompt:
+        logits = ref.step_logits(int(t))
+    checked = 0
+    for i, got in enumerate(toks):
+        pos = len(prompt) - 1 + i
+        want, margin = sampled_choice(logits.numpy(), T, seed, pos)
+        if margin > 1e-3:
+            assert got == want, (i, got, want, margin)
+            checked += 1
+        logits = ref.step_logits(int(got))
+    print(f"sampled steps checked: {checked}/32", flush=True)
+    assert checked >= 28
+    assert len(set(toks)) > 1
+
+
+def test_beyond_kernel_range_falls_back(mq, dev, small):
+    """Past 64 positions generate() loops over single steps (the XCD-aware kernel) and gives
+    the per-step tokens."""
+    dec0, d, prompt, cfg, keep = small
+    embed, layers, scales, lm_q, lm_s, fnorm, _, _ = keep
+    S = 96
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+    n = S - len(prompt) + 1
+    assert dec._generate_one_launch(prompt, n) is None           # nothing launched
+    assert dec.position() == 0
+    got = dec.generate(prompt, n)
+    assert dec.position() == S
+    assert got == _greedy(dec, prompt, n)
+
+
+def test_generate_validation(small):
+    dec, d, prompt, cfg, _ = small
+    dec.reset()
+    with pytest.raises(ValueError):
+        dec.generate([cfg.vocab_size], 4)
+    with pytest.raises(ValueError):
+        dec.generate([], 4)
+    with pytest.raises(ValueError):
+        dec.generate(prompt, 0)
+    with pytest.raises(ValueError):
+        dec.generate(prompt, d["max_seq_len"])               # runs past the KV cache
+    with pytest.raises(ValueError):
+        dec.set_sampling(-1.0)
+    with pytest.raises(ValueError):
+        dec.set_sampling(float("nan"))
+    assert dec.position() == 0
+
+
+def test_expired_wait_leaves_position(mq, small):
+    dec, d, prompt, cfg, _ = small
+    dec.set_sampling(0.0)
+    dec.reset()
+    dec.set_spin_limit(1)
+    try:
+        with pytest.raises(mq._lib.MQTimeoutError):
+            dec.generate(prompt, 16)
+    finally:
+        dec.set_spin_limit(0)
+    assert dec.position() == 0
+    assert dec.generate(prompt, 16) == d["tokens"][:16]

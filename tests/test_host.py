@@ -72,6 +72,38 @@ def test_batch_struct_layout_matches_c(tmp_path, mq):
     assert out[2:] == [getattr(_lib.BatchArgs, f).offset for f in fields]
 
 
+def test_generate_struct_layout_matches_c(tmp_path, mq):
+    """offsetof() of every mq_generate_args field from a C program compiled against the header."""
+    from megaqwen_a10_amd import _lib
+    fields = [f for f, _ in _lib.GenerateArgs._fields_]
+    src = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){"]
+    src.append('printf("%zu\\n", sizeof(mq_generate_args));')
+    for f in fields:
+        src.append(f'printf("%zu\\n", offsetof(mq_generate_args, {f}));')
+    src.append("return 0;}")
+    c = tmp_path / "glayout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "glayout"
+    subprocess.run(["gcc", "-std=c11", "-o", str(exe), str(c)], check=True)
+    out = list(map(int, subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()))
+    assert out[0] == ctypes.sizeof(_lib.GenerateArgs)
+    assert out[1:] == [getattr(_lib.GenerateArgs, f).offset for f in fields]
+
+
+def test_generate_api_rejects_bad_arguments_without_launching(mq):
+    """Host validation of mq_int8_decode_generate: NULLs, counts and prompt ids (no device needed)."""
+    from megaqwen_a10_amd import _lib
+    lib = _lib.load()
+    a = _lib.DecodeArgs()
+    g = _lib.GenerateArgs()
+    assert lib.mq_int8_decode_generate(None, ctypes.byref(g), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert lib.mq_int8_decode_generate(ctypes.byref(a), ctypes.byref(g), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    prompt = (ctypes.c_int * 2)(1, 2)
+    g = _lib.GenerateArgs(ctypes.cast(prompt, ctypes.c_void_p), 0, 4, 1234)
+    assert lib.mq_int8_decode_generate(ctypes.byref(a), ctypes.byref(g), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert "n_forced" in _lib.last_error()
+
+
 def test_batch_api_rejects_bad_arguments_without_launching(mq):
     from megaqwen_a10_amd import _lib
     lib = _lib.load()

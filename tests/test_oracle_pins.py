@@ -245,3 +245,69 @@ def test_small_fixture_fp32_port_agrees():
 def test_full_int8_fixture_reproduced():
     margins = _check_tokens("qwen3_0.6b_int8")
     assert min(margins) > 1e-3
+
+
+# ---- sampling restatement (oracle.ref_cpu.gumbel_noise / sampled_choice) ----------------
+
+def test_splitmix64_known_answers():
+    """splitmix64_mix(k * golden) is the k-th output of SplitMix64 started from state 0; the
+    first three are the published values of the generator's reference implementation."""
+    from oracle.ref_cpu import _GOLDEN, splitmix64_mix
+    want = [0xE220A8397B1DCDAF, 0x6E789E6AA1B965F4, 0x06C45D188009454F]
+    assert [splitmix64_mix((k * _GOLDEN) % 2 ** 64) for k in (1, 2, 3)] == want
+    import numpy as np
+    keys = np.array([(k * _GOLDEN) % 2 ** 64 for k in (1, 2, 3)], dtype=np.uint64)
+    assert [int(v) for v in splitmix64_mix(keys)] == want       # the numpy path wraps the same way
+
+
+def test_gumbel_noise_matches_integer_restatement():
+    """The vectorised noise against a big-integer restatement, u exactly in (0, 1)."""
+    import math
+    import numpy as np
+    from oracle.ref_cpu import _GOLDEN, gumbel_noise, splitmix64_mix
+    rng = np.random.default_rng(5)
+    for _ in range(20):
+        seed = int(rng.integers(0, 2 ** 63)) * 2 + int(rng.integers(0, 2))
+        pos = int(rng.integers(0, 40000))
+        rows = rng.integers(0, 151936, size=16)
+        got = gumbel_noise(seed, pos, rows)
+        for r, gv in zip(rows.tolist(), got.tolist()):
+            z = splitmix64_mix(seed ^ ((((pos << 32) | r) * _GOLDEN) % 2 ** 64))
+            u = ((z >> 41) + 0.5) * 2.0 ** -23
+            assert 0.0 < u < 1.0
+            assert math.isclose(gv, -math.log(-math.log(u)), rel_tol=1e-14)   # numpy's log vs libm's: an ulp
+
+
+def test_gumbel_max_samples_softmax():
+    """argmax(logits / T + g) over independent noise (one position per draw) follows
+    softmax(logits / T): frequencies within 5 standard errors over 40,000 draws."""
+    import numpy as np
+    from oracle.ref_cpu import sampled_choice
+    logits = np.array([1.0, 0.5, -0.3, 2.0, 1.7])
+    T = 0.7
+    p = np.exp(logits / T - np.max(logits / T))
+    p /= p.sum()
+    n = 40000
+    counts = np.zeros(len(logits))
+    for pos in range(n):
+        tok, _ = sampled_choice(logits, T, seed=12345, pos=pos)
+        counts[tok] += 1
+    se = np.sqrt(p * (1 - p) / n)
+    assert np.all(np.abs(counts / n - p) < 5 * se), (counts / n, p)
+
+
+def test_gumbel_max_detects_wrong_temperature():
+    """The frequency check above fails for a sampler at the wrong temperature (T^2)."""
+    import numpy as np
+    from oracle.ref_cpu import sampled_choice
+    logits = np.array([1.0, 0.5, -0.3, 2.0, 1.7])
+    T = 0.7
+    p = np.exp(logits / T - np.max(logits / T))
+    p /= p.sum()
+    n = 20000
+    counts = np.zeros(len(logits))
+    for pos in range(n):
+        tok, _ = sampled_choice(logits, T * T, seed=7, pos=pos)
+        counts[tok] += 1
+    se = np.sqrt(p * (1 - p) / n)
+    assert not np.all(np.abs(counts / n - p) < 5 * se)
