@@ -353,10 +353,13 @@ __device__ __forceinline__ double poll_slice(Waiter& wt, const uint64_t* block, 
 
 }  // namespace
 
-// A kernel argument read afresh (volatile): used for what only the LM head needs, so
-// that with several steps per launch it is not held in registers through every layer.
-template <class T>
-__device__ __forceinline__ T karg(const T& v) { return *(const volatile T*)&v; }
+// The launch's arguments read afresh from the kernel-argument segment (a volatile
+// view): used for what only the LM head needs, so that with several steps per launch
+// it is not held in registers through every layer. (Reading the by-value parameter
+// through its address instead would copy the arguments to scratch memory.)
+__device__ __forceinline__ const volatile KArgs* kargs() {
+    return (const volatile KArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+}
 
 // kMulti: several steps per launch (a.n_steps); otherwise one, and the step loop
 // disappears (held across a loop back-edge, the kernel's long-lived values would
@@ -422,7 +425,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     // The LDS counters count layers over the whole launch (gl = s L + l).
     int pos = a.pos;
     int token = a.step_tokens ? (int)__builtin_amdgcn_readfirstlane(*gview(a.step_tokens)) : a.token;
-    const int n_steps = kMulti ? karg(a.n_steps) : 1;
+    const int n_steps = kMulti ? kargs()->n_steps : 1;
     for (int step = 0; step < n_steps; ++step) {
     // lane-derived addresses are rederived every step (hidden from the optimiser): held
     // across the step loop they would be live in the LM head too and be spilled
@@ -541,38 +544,42 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 // K and V rows keep their 16-byte chunks XOR-permuted by row (chunk g of row j
                 // at g ^ (j % 16)), so that lanes reading the same chunk of different rows hit
                 // different banks
+                // (the lane is rederived per layer, so that its row addresses are not held
+                // through the layer loop alongside the 128 registers of rows)
+                const int ln = opaque(lane);
                 const int64_t cb = ((int64_t)l * kAX + x) * kv_head_stride;
                 uint4 rk[kAMaxLen / 4], rv[kAMaxLen / 4];
 #pragma unroll
                 for (int i = 0; i < kAMaxLen / 4; ++i) {
-                    const int j = 4 * i + lane / 16;
+                    const int j = 4 * i + ln / 16;
                     rk[i] = make_uint4(0, 0, 0, 0);
                     rv[i] = make_uint4(0, 0, 0, 0);
                     if (j < pos) {
-                        rk[i] = ldg16(a.kc + cb + (int64_t)j * D + 8 * (lane % 16));
-                        rv[i] = ldg16(a.vc + cb + (int64_t)j * D + 8 * (lane % 16));
+                        rk[i] = ldg16(a.kc + cb + (int64_t)j * D + 8 * (ln % 16));
+                        rv[i] = ldg16(a.vc + cb + (int64_t)j * D + 8 * (ln % 16));
                     }
                 }
-                const uint32_t qn = ld32(static_cast<const uint8_t*>(lw.q_norm_weight) + 4 * lane);
-                const uint32_t kn = ld32(static_cast<const uint8_t*>(lw.k_norm_weight) + 4 * lane);
+                const uint32_t qn = ld32(static_cast<const uint8_t*>(lw.q_norm_weight) + 4 * ln);
+                const uint32_t kn = ld32(static_cast<const uint8_t*>(lw.k_norm_weight) + 4 * ln);
                 // this step's RoPE row rides with layer 0's slot B (free once the previous
                 // step's last attention is done)
-                const uint32_t cw = l == 0 ? ld32(a.cos_t + (int64_t)pos * D + 2 * lane) : 0u;
-                const uint32_t sw = l == 0 ? ld32(a.sin_t + (int64_t)pos * D + 2 * lane) : 0u;
+                const uint32_t cw = l == 0 ? ld32(a.cos_t + (int64_t)pos * D + 2 * ln) : 0u;
+                const uint32_t sw = l == 0 ? ld32(a.sin_t + (int64_t)pos * D + 2 * ln) : 0u;
                 await_free(SL_B, gl);
+                const int ls = opaque(ln);
 #pragma unroll
                 for (int i = 0; i < kAMaxLen / 4; ++i) {
-                    const int j = 4 * i + lane / 16;
+                    const int j = 4 * i + ls / 16;
                     if (j < pos) {
-                        reinterpret_cast<uint4*>(S.kvk[j])[(lane % 16) ^ (j % 16)] = rk[i];
-                        reinterpret_cast<uint4*>(S.kvv[j])[(lane % 16) ^ (j % 16)] = rv[i];
+                        reinterpret_cast<uint4*>(S.kvk[j])[(ls % 16) ^ (j % 16)] = rk[i];
+                        reinterpret_cast<uint4*>(S.kvv[j])[(ls % 16) ^ (j % 16)] = rv[i];
                     }
                 }
-                put32(S.qkn[0], lane, qn);
-                put32(S.qkn[1], lane, kn);
+                put32(S.qkn[0], ls, qn);
+                put32(S.qkn[1], ls, kn);
                 if (l == 0) {
-                    put32(S.rope[0], lane, cw);
-                    put32(S.rope[1], lane, sw);
+                    put32(S.rope[0], ls, cw);
+                    put32(S.rope[1], ls, sw);
                 }
                 raise(SL_B, gl);
             }
@@ -1009,9 +1016,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         constexpr int RB = 8 / CH;
         constexpr int R = RB * CH;
         constexpr int span = kWave / RB;
-        const int V = karg(a.V);
-        const uint8_t* const lm_w = karg(a.lm_w);
-        const float* const lm_s = karg(a.lm_s);
+        const int V = kargs()->V;
+        const uint8_t* const lm_w = kargs()->lm_w;
+        const float* const lm_s = kargs()->lm_s;
         const int r0 = (int)((int64_t)V * g / kNWG);
         const int r1 = (int)((int64_t)V * (g + 1) / kNWG);
         const int nb = (r1 - r0 + RB - 1) / RB;
@@ -1044,8 +1051,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         __syncthreads();
         trace(a.L, 0);
 
-        const float inv_temp = karg(a.inv_temp);
-        const uint64_t seed = karg(a.seed);
+        const float inv_temp = kargs()->inv_temp;
+        const uint64_t seed = kargs()->seed;
         float best_v = -INFINITY;
         int best_i = 0x7fffffff;
 #pragma unroll
@@ -1119,12 +1126,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 const int chosen = (flag != 0u || wt.dead) ? -1 : (int)iv;
                 S.next_tok = chosen;
                 if (g == 0) {
-                    const int n_forced = karg(a.n_forced);
-                    int* const tokens_out = karg(a.tokens_out);
+                    const int n_forced = kargs()->n_forced;
+                    int* const tokens_out = kargs()->tokens_out;
                     if (tokens_out != nullptr && step >= n_forced - 1) tokens_out[step - (n_forced - 1)] = chosen;
                     if (step == n_steps - 1) {
-                        *karg(a.out_token) = chosen;
-                        uint32_t* const status_out = karg(a.status_out);
+                        *kargs()->out_token = chosen;
+                        uint32_t* const status_out = kargs()->status_out;
                         if (status_out) *status_out = flag != 0u ? flag : (wt.dead ? 1u : 0u);
                         __hip_atomic_store(&hdr->asteps, AS0 + (uint32_t)n_steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         __hip_atomic_store(&hdr->epoch, E0 + (uint32_t)n_steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1137,7 +1144,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         __syncthreads();
         // the next step's input: a forced token, else this step's output (a failed step's
         // -1 becomes 0, which keeps the remaining steps' reads in bounds; they report -1)
-        if (step + 1 < karg(a.n_forced)) token = (int)__builtin_amdgcn_readfirstlane(*gview(karg(a.step_tokens) + step + 1));
+        if (step + 1 < kargs()->n_forced) token = (int)__builtin_amdgcn_readfirstlane(*gview(kargs()->step_tokens + step + 1));
         else token = max(S.next_tok, 0);
     }
     }
