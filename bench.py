@@ -20,7 +20,9 @@ The JSON line also carries:
 Other workloads (parity-case shapes, one JSON line each): ``matvec``
 ``positions`` (config 3 positions, bf16 weights),
 ``longctx`` (config 4: KV pre-filled to 1024 / 4096 / 8192, ``--steps 64``),
-``batched`` (config 5: Qwen3-1.7B shape, B = 1 / 4 / 8 / 16, ``--steps 128``), and
+``batched`` (config 5: Qwen3-1.7B shape, B = 1 / 4 / 8 / 16, ``--steps 128``; one
+sequence per batch size teacher-force checked against the float64 oracle for
+``--check-steps`` tokens, reported as ``per_batch[B].parity``), and
 ``traffic``: a uint8 add over a 256 MiB buffer (reads and writes exactly
 256 MiB, the calibration for the FETCH_SIZE / WRITE_SIZE counters) followed
 by 8 decode steps, for ``rocprofv3 --pmc`` runs.
@@ -61,6 +63,9 @@ def parse():
     ap.add_argument("--split-min", type=int, default=0,
                     help="longctx: attention split threshold (0 = library default, -1 = never)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--check-steps", type=int, default=8,
+                    help="batched: generated tokens of one sequence per batch size teacher-force checked "
+                         "against the float64 CPU oracle (0 = no check)")
     ap.add_argument("--no-kernel-events", action="store_true",
                     help="do not attach timing events to the decode launches (for runs under rocprofv3 "
                          "--kernel-trace, which supplies the kernel durations itself); roofline.achieved then "
@@ -431,6 +436,13 @@ def run_batched(args, mq, torch):
     H, I, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_layers
     macs = L * (H * (cfg.q_size + 2 * cfg.kv_size) + cfg.q_size * H + 3 * H * I) + V * H
     events = _events(torch, steps)
+    oracle = None
+    if args.check_steps > 0:
+        from oracle.ref_cpu import Dims, RefDecoder
+        embed, layers, scales, lm_q, lm_s, fnorm = packed
+        c = lambda t: t.cpu()
+        oracle = RefDecoder(Dims(hidden_size=H, intermediate_size=I, vocab_size=V), c(embed), [c(t) for t in layers],
+                            [c(t) for t in scales], c(fnorm), c(lm_q), c(lm_s), c(cos), c(sin), L, S)
     per_batch = {}
     for B in batches:
         prompts = prompts_all[:B]
@@ -464,6 +476,10 @@ def run_batched(args, mq, torch):
             "roofline_tok_s": round(B * HBM_PEAK_GBS * 1e9 / (weight_bytes + kv_bytes / steps / 1.0), 1),
             "useful_int8_TOPs": round(mfma_tops, 2), "mfma_util": round(mfma_tops / INT8_PEAK_TOPS, 5),
             "kernel_pass_tokens_identical": first2 == first and toks2 == toks}
+        if oracle is not None:
+            s_ = B - 1                           # a different prompt slot for every batch size
+            gen = [first[s_]] + [t[s_] for t in toks]
+            per_batch[str(B)]["parity"] = _teacher_force(oracle, prompts[s_], gen[:args.check_steps], s_)
         print(f"batch {B}: {per_batch[str(B)]}", file=sys.stderr, flush=True)
         del dec
         torch.cuda.empty_cache()
@@ -475,11 +491,38 @@ def run_batched(args, mq, torch):
             "config": {"workload": "config 5: Qwen3-1.7B architecture random-init (seed 0), independent seeded 8-token "
                                    "prompts per sequence prefilled untimed, K greedy steps timed per batch size",
                        "batches": batches, "per_batch": per_batch,
+                       "parity_all_match": None if oracle is None else all(
+                           v["parity"]["match"] for v in per_batch.values()),
                        "weight_bytes_per_step": weight_bytes, "useful_int8_macs_per_token": macs},
             "roofline": {"bound": "hbm", "achieved": top["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": top["hbm_frac"], "traffic": None, "kernel_avg_us": top["kernel_avg_us"],
                          "mfma_util": top["mfma_util"],
                          "timing": KERNEL_TIMING}}
+
+
+def _teacher_force(oracle, prompt, gen, seq, min_margin=1e-3):
+    """Feed `prompt` and then the GPU's own tokens `gen` to the float64 oracle; each GPU token
+    must be the oracle's argmax wherever the oracle's top-2 margin exceeds `min_margin`
+    (fp32 logit rounding is far below it)."""
+    import torch
+    from oracle.ref_cpu import top2_margin
+
+    oracle.reset()
+    logits = None
+    for t in prompt:
+        logits = oracle.step_logits(int(t))
+    checked = mismatched = skipped = 0
+    for i, tok in enumerate(gen):
+        if top2_margin(logits) > min_margin:
+            checked += 1
+            mismatched += int(tok != int(torch.argmax(logits)))
+        else:
+            skipped += 1
+        if i + 1 < len(gen):
+            logits = oracle.step_logits(int(tok))
+    return {"sequence": seq, "tokens": len(gen), "checked": checked, "skipped_small_margin": skipped,
+            "match": checked > 0 and mismatched == 0,
+            "oracle": "oracle.ref_cpu float64, prompt then the GPU's tokens teacher-forced"}
 
 
 def run_traffic(args, mq, torch):

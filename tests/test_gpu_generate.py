@@ -8,7 +8,9 @@ bitwise (tokens and KV caches), greedy and sampled; sampled tokens against the
 float64 oracle's Gumbel-max choice wherever its top-2 margin exceeds fp32
 logit error; the fallback beyond the async-wave kernel's 64 positions;
 argument validation; a forced in-kernel wait expiry that leaves the decoder
-where it started.
+where it started; a P-token prefill in one launch (P = 8 and 64) whose whole KV
+cache and first generated token match the oracle's per-token prefill
+(a10_decode.py:367-368).
 """
 from __future__ import annotations
 
@@ -144,3 +146,39 @@ def test_expired_wait_leaves_position(mq, small):
         dec.set_spin_limit(0)
     assert dec.position() == 0
     assert dec.generate(prompt, 16) == d["tokens"][:16]
+
+
+@pytest.mark.parametrize("P", [8, 64])
+def test_prefill_one_launch_matches_oracle(small, P):
+    """P prompt tokens and the first generated token from one launch: every cached K and V
+    row of every layer within one bf16 ulp of the float64 oracle's per-token prefill, most
+    of them bit-identical, and the generated token the oracle's argmax (its top-2 margin
+    checked to exceed fp32 logit error)."""
+    dec, d, prompt, cfg, _ = small
+    g = torch.Generator().manual_seed(4242 + P)
+    ids = torch.randint(0, cfg.vocab_size, (P,), generator=g).tolist()
+    dec.set_sampling(0.0)
+    dec.reset()
+    print(f"prefill P={P} in one launch", flush=True)
+    got = dec._generate_one_launch(ids, 1)
+    assert got is not None, "P <= 64 positions is within the async-wave kernel's range"
+    assert dec.position() == P
+    kc, vc = _caches(dec)
+    ref = _ref_for(small)
+    ref.reset()
+    logits = None
+    for t in ids:
+        logits = ref.step_logits(int(t))
+    top2 = torch.topk(logits.double(), 2).values
+    assert float(top2[0] - top2[1]) > 1e-4
+    assert got == [int(torch.argmax(logits))]
+    for name, gpu, want in (("K", kc, ref.k_cache), ("V", vc, ref.v_cache)):
+        a = gpu[:, :, :P].cpu().float()
+        b = want[:, :, :P].float()
+        err = (a - b).abs()
+        ulp = b.abs().clamp_min(2.0 ** -126) * 2.0 ** -7
+        print(f"{name}: max |err|/ulp {float((err / ulp).max()):.3f}, "
+              f"bit-identical {float((err == 0).double().mean()):.4f}", flush=True)
+        assert bool((err <= ulp).all()), name
+        assert float((err == 0).double().mean()) > 0.95, name
+        assert int(gpu[:, :, P:].abs().sum()) == 0            # nothing written past the prompt
