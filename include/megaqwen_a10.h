@@ -341,6 +341,16 @@ int mq_reference_set_dims(const mq_model_dims* dims);
  * scale fp32 [M], y fp32 [M]. 1 <= K <= 16384. */
 int mq_int8_gemv(const float* x, const int8_t* w, const float* scale, float* y,
                  int M, int K, hipStream_t stream);
+/* Steady-state form of mq_int8_gemv (no counterpart in the reference, whose
+ * microbenchmark int8_decoder.py:351-434 times isolated calls): one launch
+ * computes `reps` matvecs, rep i against weight copy i % n_copies at
+ * w + (i % n_copies) * copy_stride bytes, into y + (i % n_copies) * M. The
+ * matvecs are independent, so the launch streams weights without a launch gap
+ * or ramp between them; per-matvec time = launch time / reps. y fp32
+ * [n_copies, M]; copy_stride a multiple of 16 and >= M * K when n_copies > 1;
+ * reps * M < 2^31. reps = n_copies = 1 is mq_int8_gemv. */
+int mq_int8_gemv_repeat(const float* x, const int8_t* w, int64_t copy_stride, int n_copies,
+                        const float* scale, float* y, int M, int K, int reps, hipStream_t stream);
 
 /* bench_int8.py:19-24: per-row symmetric int8.
  *   amax = max_k |w[j,k]|               (bf16, exact)

@@ -8,7 +8,7 @@ fallback: if the library is missing, every entry point raises.
 from __future__ import annotations
 
 import ctypes
-from ctypes import POINTER, Structure, c_float, c_int, c_size_t, c_uint, c_void_p
+from ctypes import POINTER, Structure, c_float, c_int, c_int64, c_size_t, c_uint, c_void_p
 from pathlib import Path
 
 import torch  # noqa: F401  (must be loaded before the HIP library)
@@ -121,6 +121,8 @@ _SIGNATURES = {
     "mq_reference_set_spin_limit": (None, [c_uint]),
     "mq_reference_set_dims": (c_int, [c_void_p]),
     "mq_int8_gemv": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "mq_int8_gemv_repeat": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_int, c_int, c_int,
+                                    c_void_p]),
     "mq_quantize_per_channel_bf16": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
 }
 EXPORTED = tuple(_SIGNATURES)

@@ -535,6 +535,22 @@ int mq_int8_gemv(const float* x, const int8_t* w, const float* scale, float* y, 
     return launch_int8_gemv(x, w, scale, y, M, K, stream);
 }
 
+int mq_int8_gemv_repeat(const float* x, const int8_t* w, int64_t copy_stride, int n_copies, const float* scale,
+                        float* y, int M, int K, int reps, hipStream_t stream) {
+    clear_error();
+    if (!x || !w || !scale || !y) return set_error(MQ_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (M < 1 || K < 1 || K > 16384 || (K % 16) != 0)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "need M >= 1 and 16 <= K <= 16384 with K %% 16 == 0 (M=%d K=%d)", M, K);
+    if (n_copies < 1 || reps < 1 || (int64_t)reps * M >= ((int64_t)1 << 31))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "need n_copies >= 1, reps >= 1 and reps * M < 2^31 (n_copies=%d reps=%d)",
+                         n_copies, reps);
+    if (n_copies > 1 && (copy_stride < (int64_t)M * K || (copy_stride % 16) != 0))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "copy_stride %lld must be a multiple of 16 and >= M * K",
+                         (long long)copy_stride);
+    if (!aligned16(w) || !aligned16(x)) return set_error(MQ_ERR_INVALID_ARGUMENT, "x and w must be 16-byte aligned");
+    return launch_int8_gemv_repeat(x, w, n_copies > 1 ? copy_stride : 0, n_copies, scale, y, M, K, reps, stream);
+}
+
 int mq_quantize_per_channel_bf16(const void* w_bf16, int M, int K, int8_t* q, float* scale, hipStream_t stream) {
     clear_error();
     if (!w_bf16 || !q || !scale) return set_error(MQ_ERR_INVALID_ARGUMENT, "NULL pointer");

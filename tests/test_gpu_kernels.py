@@ -3,7 +3,8 @@
 * quantize_per_channel (csrc/quant.hip) must equal the oracle bit for bit;
 * int8_gemv (csrc/gemv.hip) must be within 1e-3 relative L2 of the fp64
   dequantized product (oracle/c/oracle.c) at the BASELINE config-2 shapes and
-  at ragged shapes.
+  at ragged shapes; so must every copy's output of its steady-state form
+  (int8_gemv_repeat, several distinct weight copies in one launch).
 """
 from __future__ import annotations
 
@@ -85,3 +86,26 @@ def test_int8_gemv_repeatable(mq, dev):
     a = mq.int8_gemv(x, q, s).cpu()
     b = mq.int8_gemv(x, q, s).cpu()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("shape,n,reps", [((1024, 2048), 3, 7), ((4096, 1024), 2, 5), ((37, 48), 2, 9),
+                                          ((1000, 8192), 3, 3)], ids=lambda v: str(v))
+def test_int8_gemv_repeat_parity(mq, dev, shape, n, reps):
+    M, K = shape
+    print(f"gemv repeat {M}x{K} copies={n} reps={reps}", flush=True)
+    g = torch.Generator().manual_seed(M + 3 * K + n)
+    qs, ss = [], []
+    for _ in range(n):
+        w = (torch.randn(M, K, generator=g) * 0.02).to(torch.bfloat16)
+        q, s = oquant.quantize_per_channel(w)
+        qs.append(q)
+        ss.append(s)
+    s = ss[0]                                         # one scale vector for every copy
+    x = torch.randn(K, generator=g, dtype=torch.float32)
+    y = mq.int8_gemv_repeat(x.to(dev), torch.stack(qs).to(dev), s.to(dev), reps)
+    torch.cuda.synchronize()
+    got = y.cpu().double().numpy()
+    for c in range(n):
+        ref = _matvec_f64(qs[c], s, x)
+        rel = np.linalg.norm(got[c] - ref) / np.linalg.norm(ref)
+        assert rel <= 1e-5, (c, rel)

@@ -135,6 +135,12 @@ def test_c_api_rejects_bad_arguments_without_launching(mq):
     assert "NULL" in _lib.last_error()
     fake = ctypes.c_void_p(0x1000)
     assert lib.mq_int8_gemv(fake, fake, fake, fake, 4, 17, None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    # the steady-state form: copies, repetitions and the copy stride are checked before any launch
+    bad = [(None, 0, 1, 4, 16, 1), (fake, 64, 0, 4, 16, 1), (fake, 64, 1, 4, 16, 0), (fake, 48, 2, 4, 16, 1),
+           (fake, 72, 2, 4, 16, 1), (fake, 64, 1, 4, 17, 1), (fake, 64, 1, 2 ** 20, 16, 2 ** 12)]
+    for w, stride, n, M, K, reps in bad:
+        assert lib.mq_int8_gemv_repeat(fake, w, stride, n, fake, fake, M, K, reps, None) == \
+            _lib.MQ_ERR_INVALID_ARGUMENT, (w, stride, n, M, K, reps)
     assert lib.mq_quantize_per_channel_bf16(fake, 0, 16, fake, fake, None) == _lib.MQ_ERR_INVALID_ARGUMENT
     a = _lib.DecodeArgs()
     a.num_layers, a.max_seq_len, a.position, a.cache_len = 2, 16, 0, 1
