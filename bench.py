@@ -42,10 +42,11 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0          # dense int8 MFMA, MI355X
 PROMPT_LEN = 8
-# Memory traffic per decode launch of this kernel, measured with rocprofv3 --pmc FETCH_SIZE and
+# Memory traffic per decode launch of each kernel, measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE runs of megaqwen-a10_amd/profile_decode.py, each scaled by the counter's reading for a
-# 256 MiB copy (the commands and numbers are in profiles/decode_xcd_kernel_int8_qwen3-0.6b_traffic.txt).
-MEASURED_TRAFFIC = {"mq::decode_xcd_kernel<1024, 3072, mq::Int8W, false>": 639_234_240}
+# 256 MiB copy (the commands and numbers are in profiles/decode_*_kernel_int8_qwen3-0.6b_traffic.txt).
+MEASURED_TRAFFIC = {"mq::decode_async_kernel<false, false>": 641_659_290,
+                    "mq::decode_xcd_kernel<1024, 3072, mq::Int8W, false>": 639_234_240}
 
 
 def parse():

@@ -4,9 +4,12 @@ Builds the config-1 model (Qwen3-0.6B shape, random-init seed 0, per-row INT8),
 prefills the 8-token prompt one decode_step per token and runs ``--steps``
 greedy steps through ``A10Int8MegakernelDecoder.decode_step``. With
 ``--copy-mib N`` it first runs four uint8 adds over an N MiB buffer (each reads
-and writes exactly N MiB), the calibration for FETCH_SIZE / WRITE_SIZE.
+and writes exactly N MiB), the calibration for FETCH_SIZE / WRITE_SIZE. With
+``--generate`` it then runs the same prompt and steps again as one launch
+(``generate``: prefill and greedy steps handed on on the device).
 
     python megaqwen-a10_amd/profile_decode.py [--steps 32] [--variant auto|flat|xcd|async] [--copy-mib 256]
+                                              [--generate]
 """
 from __future__ import annotations
 
@@ -23,6 +26,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=32)
     ap.add_argument("--variant", default="auto", choices=["auto", "flat", "xcd", "async"])
     ap.add_argument("--copy-mib", type=int, default=0)
+    ap.add_argument("--generate", action="store_true")
     args = ap.parse_args()
 
     import torch
@@ -54,6 +58,12 @@ def main() -> int:
     torch.cuda.synchronize()
     print(f"decoded {len(prompt) + args.steps} steps with the {mq.decode_variant()} kernel, last token {tok}",
           flush=True)
+    if args.generate:
+        dec.reset()
+        toks = dec.generate(prompt.tolist(), args.steps + 1)
+        torch.cuda.synchronize()
+        print(f"generate: {len(prompt) + args.steps} steps, last token {toks[-1]} "
+              f"({'same' if toks[-1] == tok else 'DIFFERENT'})", flush=True)
     # release device memory before interpreter shutdown (profilers finalise at exit)
     del dec, embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, qstate
     torch.cuda.synchronize()
