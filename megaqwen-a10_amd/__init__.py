@@ -15,7 +15,6 @@ library (``lib/libmegaqwen_a10.so``, declared in include/megaqwen_a10.h):
   seeded weights and the reference's tensor packing.
 """
 from .config import QWEN3_0_6B, QWEN3_1_7B, ModelConfig
-from . import chat_kernel
 from .decoder import (A10Decoder, A10Int8BatchDecoder, A10Int8MegakernelDecoder, A10MegakernelDecoder, decode_variant,
                       set_decode_variant)
 from .gemv import int8_gemv, int8_gemv_repeat
@@ -27,6 +26,6 @@ __all__ = [
     "ModelConfig", "QWEN3_0_6B", "QWEN3_1_7B",
     "A10Decoder", "A10Int8BatchDecoder", "A10Int8MegakernelDecoder", "A10MegakernelDecoder", "set_decode_variant",
     "decode_variant",
-    "chat_kernel", "int8_gemv", "int8_gemv_repeat", "quantize_per_channel", "make_rope", "precompute_rope_freqs",
+    "int8_gemv", "int8_gemv_repeat", "quantize_per_channel", "make_rope", "precompute_rope_freqs",
     "pack_bf16", "pack_int8", "quantize_state", "random_init_state", "state_digest",
 ]

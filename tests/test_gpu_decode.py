@@ -64,16 +64,17 @@ def _use_variant(mq, name):
     mq.set_decode_variant("auto")
 
 
-@pytest.fixture(params=["flat", "xcd", "async"])
+@pytest.fixture(params=["xcd", "async"])
 def variant(request, mq, dev):
-    """Runs a test once per decode kernel (single-level exchanges / XCD-aware / async-wave;
-    the async-wave kernel covers the INT8 Qwen3-0.6B shape up to 64 cached positions)."""
+    """Runs a test once per decode kernel the library selects on MI355X (XCD-aware /
+    async-wave; the async-wave kernel covers the INT8 Qwen3-0.6B shape up to 64 cached
+    positions). The single-level fallback has its own fixture test below."""
     yield from _use_variant(mq, request.param)
 
 
-@pytest.fixture(params=["flat", "xcd"])
+@pytest.fixture(params=["xcd"])
 def variant_any_shape(request, mq, dev):
-    """The kernels that run every compiled shape and weight format."""
+    """The kernel that runs every compiled shape and weight format."""
     yield from _use_variant(mq, request.param)
 
 
@@ -276,29 +277,23 @@ def test_full_bf16_32_tokens(variant_any_shape, mq, dev):
     dec, d, prompt, cfg, keep = _build(mq, dev, "qwen3_0.6b_bf16")
     toks = _greedy(dec, prompt, 32)
     assert toks == d["tokens"], (toks, d["tokens"])
-    del dec
-    # the chat program's free functions (a10_chat.py:84-189) on caller-owned KV cache and
-    # scratch, sized as that program sizes them, give the same tokens
-    embed, layers, fnorm, lm, cos, sin = keep
-    ck, L, S = mq.chat_kernel, cfg.num_layers, d["max_seq_len"]
-    ck.init_ldg_layer_weights(*[[layers[11 * l + f] for l in range(L)] for f in range(11)])
-    ck.init_ldg_embed_weight(embed)
-    kc = torch.zeros((L, 8, S, 128), dtype=torch.bfloat16, device=dev)
-    vc = torch.zeros_like(kc)
-    f32 = lambda n: torch.zeros(n, dtype=torch.float32, device=dev)
-    H, I = cfg.hidden_size, cfg.intermediate_size
-    scratch = [torch.zeros(H, dtype=torch.bfloat16, device=dev), f32(H), f32(H), f32(2048), f32(1024), f32(1024),
-               f32(2048), f32(I), f32(H), f32(1184), torch.zeros(1184, dtype=torch.int32, device=dev)]
-    seq, pos = list(prompt), 0
-    out = []
-    while len(out) < 32:
-        tok = ck.decode_a10(int(seq[pos]), fnorm, lm, cos, sin, kc, vc, *scratch, L, pos, pos + 1, S)
-        pos += 1
-        if pos >= len(prompt):
-            out.append(tok)
-            seq.append(tok)
-    assert out == d["tokens"], (out, d["tokens"])
-    del keep, kc, vc, scratch
+    del dec, keep
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("name", ["small_int8", "qwen3_0.6b_int8", "qwen3_0.6b_bf16"])
+def test_single_level_fallback_fixtures(mq, dev, name):
+    """The single-level kernel (the fallback for devices whose workgroup placement does not
+    fit the XCD-aware kernel; never selected on MI355X) against the 32-token fixtures."""
+    print(f"single-level kernel, {name}", flush=True)
+    dec, d, prompt, cfg, keep = _build(mq, dev, name)
+    mq.set_decode_variant("flat")
+    try:
+        assert mq.decode_variant(cfg.hidden_size, cfg.intermediate_size, int8=d["int8"]) == "flat"
+        assert _greedy(dec, prompt, 32) == d["tokens"]
+    finally:
+        mq.set_decode_variant("auto")
+    del dec, keep
     torch.cuda.empty_cache()
 
 

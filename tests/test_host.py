@@ -216,29 +216,6 @@ def test_decoder_validation_before_any_launch(mq):
         mq.quantize_per_channel(torch.zeros(4, 16))
 
 
-def test_chat_functions_validate_before_any_launch(mq):
-    """The chat program's free functions (a10_chat.py:84-189) refuse to step an
-    uninitialised model and reject bad weight lists, all before touching a device."""
-    ck = mq.chat_kernel
-    saved = (ck._state.layers, ck._state.embed)
-    ck._state.layers, ck._state.embed = None, None
-    try:
-        with pytest.raises(RuntimeError, match="init_ldg"):
-            ck.decode_a10(0, *([None] * 17), 1, 0, 1, 8)
-        w = torch.zeros(1024, dtype=torch.bfloat16)                      # CPU tensor
-        with pytest.raises(ValueError, match="q_proj_weights has 0"):
-            ck.init_ldg_layer_weights([w], [], [w], [w], [w], [w], [w], [w], [w], [w], [w])
-        with pytest.raises(ValueError, match="no layers"):
-            ck.init_ldg_layer_weights(*([[]] * 11))
-        with pytest.raises(ValueError, match="HIP device"):
-            ck.init_ldg_layer_weights(*([[w]] * 11))
-        with pytest.raises(ValueError, match="HIP device"):
-            ck.init_ldg_embed_weight(torch.zeros(16, 1024, dtype=torch.bfloat16))
-        assert ck._state.layers is None and ck._state.embed is None
-    finally:
-        ck._state.layers, ck._state.embed = saved
-
-
 def test_random_init_is_deterministic(mq):
     cfg = mq.QWEN3_0_6B.with_(num_layers=1, vocab_size=512)
     s1, p1 = mq.random_init_state(cfg, seed=3)
