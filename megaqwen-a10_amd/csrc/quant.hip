@@ -4,7 +4,8 @@
 //   scale = bf16_rne(amax / 127.0f)       the reference divides in bf16
 //           widened to fp32, clamped to >= 1e-12f
 //   q     = clamp(rint(fp32(w) / scale), -128, 127)   IEEE division, ties to even
-// One workgroup per row; rows are read with 16-byte loads when K % 8 == 0.
+// One workgroup per row; each thread reads the row's bf16 elements k = tid, tid + 256, ...
+// (2-byte loads; the quantizer runs once at load time, off the decode path).
 #include "common.h"
 #include "internal.h"
 
