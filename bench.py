@@ -18,7 +18,8 @@ The JSON line also carries:
 * ``parity`` — the timed tokens against the committed oracle fixture.
 
 Other workloads (parity-case shapes, one JSON line each): ``matvec``
-``positions`` (config 3 positions, bf16 weights),
+``formats`` (the config-2 shapes in INT8, INT4 per group and
+FP8 E4M3, steady state), ``positions`` (config 3 positions, bf16 weights),
 ``longctx`` (config 4: KV pre-filled to 1024 / 4096 / 8192, ``--steps 64``),
 ``batched`` (config 5: Qwen3-1.7B shape, B = 1 / 4 / 8 / 16, ``--steps 128``; one
 sequence per batch size teacher-force checked against the float64 oracle for
@@ -58,7 +59,7 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=112,
                     help="greedy steps of the CPU baseline sample (about 10 s on 16 host threads)")
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "matvec", "positions", "longctx", "batched", "traffic"])
+                    choices=["decode", "matvec", "formats", "positions", "longctx", "batched", "traffic"])
     ap.add_argument("--depths", default="1024,4096,8192", help="longctx: KV depths")
     ap.add_argument("--batches", default="1,4,8,16", help="batched: batch sizes")
     ap.add_argument("--split-min", type=int, default=0,
@@ -349,6 +350,67 @@ def run_matvec(args, mq, torch):
                        "steady_frac_min_small_shapes": min(res[k]["steady_frac"] for k in ("qkv", "o", "gate_up", "down"))}}
 
 
+def run_formats(args, mq, torch):
+    """Other weight formats: INT8 per row, INT4 per group of 128, FP8 E4M3 per row, at the config-2
+    shapes: steady-state time per matvec (one launch over rotating copies past the 256 MB MALL),
+    bytes read, and each format's error against the bf16 weights' product."""
+    dev = torch.device("cuda:0")
+    shapes = {"qkv": (4096, 1024), "o": (1024, 2048), "gate_up": (6144, 1024), "down": (1024, 3072),
+              "lm_head": (151936, 1024)}
+    g = torch.Generator().manual_seed(args.seed)
+    res = {}
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for name, (M, K) in shapes.items():
+        w = (torch.randn(M, K, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+        x = torch.randn(K, generator=g).to(dev)
+        exact = (w.double() @ x.double())
+        per = {}
+        for fmt in ("int8", "int4", "fp8"):
+            if fmt == "int8":
+                q, s = mq.quantize_per_channel(w)
+                rep = lambda xc, wc, n: mq.int8_gemv_repeat(xc, wc, s, n)
+            elif fmt == "int4":
+                q, s = mq.quantize_int4(w)
+                rep = lambda xc, wc, n: mq.int4_gemv_repeat(xc, wc, s, n)
+            else:
+                q, s = mq.quantize_fp8(w)
+                rep = lambda xc, wc, n: mq.fp8_gemv_repeat(xc, wc, s, n)
+            wbytes = q.numel() * q.element_size()
+            nbytes = wbytes + s.numel() * 4 + 4 * K + 4 * M
+            copies = max(1, -(-512 * 2 ** 20 // wbytes))
+            wc = q.unsqueeze(0).expand(copies, *q.shape).contiguous()
+            n_rep = max(copies, -(-2 * 2 ** 30 // wbytes))
+            y = rep(x, wc, n_rep)
+            torch.cuda.synchronize()
+            err = float(torch.linalg.norm(y[0].double() - exact) / torch.linalg.norm(exact))
+            ev0.record()
+            rep(x, wc, n_rep)
+            ev1.record()
+            torch.cuda.synchronize()
+            us = ev0.elapsed_time(ev1) / n_rep * 1e3
+            per[fmt] = {"us": round(us, 4), "bytes": nbytes, "GBs": round(nbytes / us / 1e3, 1),
+                        "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "rel_err_vs_bf16": float(f"{err:.3e}"),
+                        "reps": n_rep, "copies": copies}
+            del wc, q, s, y
+            torch.cuda.empty_cache()
+        res[name] = per
+        print(f"{name}: {per}", file=sys.stderr, flush=True)
+        del w
+    L = mq.QWEN3_0_6B.num_layers
+    step = {f: round(L * sum(res[k][f]["us"] for k in ("qkv", "o", "gate_up", "down")) + res["lm_head"][f]["us"], 2)
+            for f in ("int8", "int4", "fp8")}
+    return {"metric": "matvec-only decode step time at the Qwen3-0.6B shapes, INT4 per-group weights "
+                      "(steady state; INT8 and FP8 E4M3 beside it)",
+            "value": step["int4"], "unit": "us", "n_gpus": 1, "steps": 1, "warmup": 1,
+            "ms_per_step": round(step["int4"] / 1e3, 5), "higher_is_better": False, "scaling": "weak",
+            "vs_baseline": None, "dtype": "int4 / fp8 / int8 weights, fp32 activations and sums", "data": "synthetic",
+            "config": {"workload": "other weight formats: N(0, 0.02) bf16 weights per config-2 shape quantized to INT8 "
+                                   "per row, INT4 per group of 128, FP8 E4M3 per row; one launch of the format's "
+                                   "steady-state matvec over rotating copies (about 2 GB), time / reps; error = rel. "
+                                   "L2 of the format's product against the bf16 weights' float64 product",
+                       "step_us_28_layers_plus_lm_head": step, "shapes": res}}
+
+
 def run_positions(args, mq, torch):
     """bf16 weights, tok/s at positions 1, 25, 50, 100, 200 (n / wall(reset + n steps))."""
     dev = torch.device("cuda:0")
@@ -588,7 +650,8 @@ def main():
     if not torch.cuda.is_available():
         print("no HIP device visible", file=sys.stderr)
         return 1
-    fn = {"decode": run_decode, "matvec": run_matvec, "positions": run_positions, "longctx": run_longctx,
+    fn = {"decode": run_decode, "matvec": run_matvec, "formats": run_formats, "positions": run_positions,
+          "longctx": run_longctx,
           "batched": run_batched, "traffic": run_traffic}[args.workload]
     out = fn(args, mq, torch)
     print(json.dumps(out), flush=True)

@@ -352,6 +352,31 @@ int mq_int8_gemv(const float* x, const int8_t* w, const float* scale, float* y,
 int mq_int8_gemv_repeat(const float* x, const int8_t* w, int64_t copy_stride, int n_copies,
                         const float* scale, float* y, int M, int K, int reps, hipStream_t stream);
 
+/* ---- other weight formats (no counterpart in the reference, which has INT8
+ * and BF16 weights only; its one other-format figure is llama.cpp Q4_K_M,
+ * README.md:19). The quantizers follow mq_quantize_per_channel_bf16's pattern:
+ *   FP8 E4M3 (OCP E4M3FN: bias 7, subnormals m * 2^-9, 0x7F / 0xFF NaN, max 448),
+ *     per row:   s = fp32(amax) / 448 (IEEE), floored at 1e-12;
+ *                q = nearest code of fp32(w) / s, ties to the even code, |.| >= 448 -> +-448.
+ *     q uint8 [M,K], scale fp32 [M].
+ *   INT4 per group of 128 consecutive elements of a row:
+ *                s = bf16(amax / 7) (fp32 division rounded to bf16), floored at 1e-12;
+ *                q = clamp(round_half_even(fp32(w) / s), -8, 7);
+ *     q uint8 [M,K/2], byte i = (q[2i] & 15) | (q[2i+1] & 15) << 4; scale fp32 [M,K/128].
+ * Matvecs: y[j] = sum_k dequant(w)[j,k] * x[k], x fp32 [K], y fp32 [M], fp32
+ * accumulation; 16-byte aligned x and w; K <= 16384 and K % 16 == 0 (FP8) or
+ * K % 128 == 0 (INT4). The _repeat forms are the steady-state form of
+ * mq_int8_gemv_repeat (reps matvecs over n_copies copies copy_stride bytes
+ * apart, y [n_copies, M]). */
+int mq_quantize_fp8_rows_bf16(const void* w_bf16, int M, int K, uint8_t* q, float* scale, hipStream_t stream);
+int mq_quantize_int4_groups_bf16(const void* w_bf16, int M, int K, uint8_t* q, float* scale, hipStream_t stream);
+int mq_fp8_gemv(const float* x, const uint8_t* w, const float* scale, float* y, int M, int K, hipStream_t stream);
+int mq_int4_gemv(const float* x, const uint8_t* w, const float* scale, float* y, int M, int K, hipStream_t stream);
+int mq_fp8_gemv_repeat(const float* x, const uint8_t* w, int64_t copy_stride, int n_copies,
+                       const float* scale, float* y, int M, int K, int reps, hipStream_t stream);
+int mq_int4_gemv_repeat(const float* x, const uint8_t* w, int64_t copy_stride, int n_copies,
+                        const float* scale, float* y, int M, int K, int reps, hipStream_t stream);
+
 /* bench_int8.py:19-24: per-row symmetric int8.
  *   amax = max_k |w[j,k]|               (bf16, exact)
  *   s    = bf16(amax / 127)             (bf16 division), widened to fp32, clamped to >= 1e-12

@@ -4,7 +4,10 @@ Python host code on PyTorch-ROCm (device memory, streams) over a C-ABI HIP
 library (``lib/libmegaqwen_a10.so``, declared in include/megaqwen_a10.h):
 
 * ``quantize_per_channel`` — per-row symmetric INT8 (bench_int8.py:19-24), HIP kernel.
-* ``int8_gemv`` — INT8 weight-only matvec (int8_decoder.py:100-115), HIP kernel.
+* ``int8_gemv`` — INT8 weight-only matvec (int8_decoder.py:100-115), HIP kernel;
+  ``int8_gemv_repeat`` its steady-state form.
+* ``quantize_fp8`` / ``quantize_int4`` / ``fp8_gemv`` / ``int4_gemv`` (+ ``_repeat``) —
+  FP8 E4M3 per-row and INT4 per-group weights (no counterpart in the reference).
 * ``A10Int8MegakernelDecoder`` / ``A10MegakernelDecoder`` / ``A10Decoder`` —
   the reference's decoder classes (bench_int8.py:119-255, a10_decode.py:35-393),
   one persistent-kernel launch per token.
@@ -17,6 +20,7 @@ library (``lib/libmegaqwen_a10.so``, declared in include/megaqwen_a10.h):
 from .config import QWEN3_0_6B, QWEN3_1_7B, ModelConfig
 from .decoder import (A10Decoder, A10Int8BatchDecoder, A10Int8MegakernelDecoder, A10MegakernelDecoder, decode_variant,
                       set_decode_variant)
+from .formats import fp8_gemv, fp8_gemv_repeat, int4_gemv, int4_gemv_repeat, quantize_fp8, quantize_int4
 from .gemv import int8_gemv, int8_gemv_repeat
 from .quant import quantize_per_channel
 from .rope import make_rope, precompute_rope_freqs
@@ -26,6 +30,7 @@ __all__ = [
     "ModelConfig", "QWEN3_0_6B", "QWEN3_1_7B",
     "A10Decoder", "A10Int8BatchDecoder", "A10Int8MegakernelDecoder", "A10MegakernelDecoder", "set_decode_variant",
     "decode_variant",
-    "int8_gemv", "int8_gemv_repeat", "quantize_per_channel", "make_rope", "precompute_rope_freqs",
+    "int8_gemv", "int8_gemv_repeat", "quantize_per_channel",
+    "quantize_fp8", "quantize_int4", "fp8_gemv", "int4_gemv", "fp8_gemv_repeat", "int4_gemv_repeat", "make_rope", "precompute_rope_freqs",
     "pack_bf16", "pack_int8", "quantize_state", "random_init_state", "state_digest",
 ]

@@ -558,4 +558,62 @@ int mq_quantize_per_channel_bf16(const void* w_bf16, int M, int K, int8_t* q, fl
     return launch_quantize(w_bf16, M, K, q, scale, stream);
 }
 
+// ---- other weight formats ----------------------------------------------------------------
+int mq_quantize_fp8_rows_bf16(const void* w_bf16, int M, int K, uint8_t* q, float* scale, hipStream_t stream) {
+    clear_error();
+    if (!w_bf16 || !q || !scale) return set_error(MQ_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (M < 1 || K < 1) return set_error(MQ_ERR_INVALID_ARGUMENT, "need M >= 1 and K >= 1 (M=%d K=%d)", M, K);
+    return launch_quantize_fp8(w_bf16, M, K, q, scale, stream);
+}
+
+int mq_quantize_int4_groups_bf16(const void* w_bf16, int M, int K, uint8_t* q, float* scale, hipStream_t stream) {
+    clear_error();
+    if (!w_bf16 || !q || !scale) return set_error(MQ_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (M < 1 || K < 128 || (K % 128) != 0)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "need M >= 1 and K a positive multiple of 128 (M=%d K=%d)", M, K);
+    return launch_quantize_int4(w_bf16, M, K, q, scale, stream);
+}
+
+// Shared checks of the FP8 / INT4 matvecs; `kmul` is the row-length multiple (16 / 128),
+// `row_bytes` the bytes of one weight row.
+static int check_fmt_gemv(const float* x, const uint8_t* w, int64_t copy_stride, int n_copies, const float* scale,
+                          const float* y, int M, int K, int reps, int kmul, int64_t row_bytes) {
+    if (!x || !w || !scale || !y) return set_error(MQ_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (M < 1 || K < kmul || K > 16384 || (K % kmul) != 0)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "need M >= 1 and %d <= K <= 16384 with K %% %d == 0 (M=%d K=%d)",
+                         kmul, kmul, M, K);
+    if (n_copies < 1 || reps < 1 || (int64_t)reps * M >= ((int64_t)1 << 31))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "need n_copies >= 1, reps >= 1 and reps * M < 2^31 (n_copies=%d reps=%d)",
+                         n_copies, reps);
+    if (n_copies > 1 && (copy_stride < (int64_t)M * row_bytes || (copy_stride % 16) != 0))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "copy_stride %lld must be a multiple of 16 and >= M * row bytes",
+                         (long long)copy_stride);
+    if (!aligned16(w) || !aligned16(x)) return set_error(MQ_ERR_INVALID_ARGUMENT, "x and w must be 16-byte aligned");
+    return MQ_OK;
+}
+
+int mq_fp8_gemv_repeat(const float* x, const uint8_t* w, int64_t copy_stride, int n_copies, const float* scale,
+                       float* y, int M, int K, int reps, hipStream_t stream) {
+    clear_error();
+    const int st = check_fmt_gemv(x, w, copy_stride, n_copies, scale, y, M, K, reps, 16, K);
+    if (st != MQ_OK) return st;
+    return launch_fp8_gemv(x, w, n_copies > 1 ? copy_stride : 0, n_copies, scale, y, M, K, reps, stream);
+}
+
+int mq_fp8_gemv(const float* x, const uint8_t* w, const float* scale, float* y, int M, int K, hipStream_t stream) {
+    return mq_fp8_gemv_repeat(x, w, 0, 1, scale, y, M, K, 1, stream);
+}
+
+int mq_int4_gemv_repeat(const float* x, const uint8_t* w, int64_t copy_stride, int n_copies, const float* scale,
+                        float* y, int M, int K, int reps, hipStream_t stream) {
+    clear_error();
+    const int st = check_fmt_gemv(x, w, copy_stride, n_copies, scale, y, M, K, reps, 128, K / 2);
+    if (st != MQ_OK) return st;
+    return launch_int4_gemv(x, w, n_copies > 1 ? copy_stride : 0, n_copies, scale, y, M, K, reps, stream);
+}
+
+int mq_int4_gemv(const float* x, const uint8_t* w, const float* scale, float* y, int M, int K, hipStream_t stream) {
+    return mq_int4_gemv_repeat(x, w, 0, 1, scale, y, M, K, 1, stream);
+}
+
 }  // extern "C"

@@ -58,13 +58,19 @@ int8_gemv_kernel(const float* __restrict__ x, const int8_t* __restrict__ w, int6
                     wv[r][c] = *reinterpret_cast<const uint4*>(wc + (int64_t)(row0 + r) * rowbytes + col);
             }
         }
+        // chunk outer, rows inner: the lane's 16 activations of a chunk are read from LDS
+        // once and used for all R rows
         float acc[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            acc[r] = 0.0f;
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 #pragma unroll
-            for (int c = 0; c < CHMAX; ++c)
-                if (c < CH) acc[r] = dot_frag<Int8W>(wv[r][c], xs_frag<Int8W>(xs, c, lane), acc[r]);
+        for (int c = 0; c < CHMAX; ++c) {
+            if (c < CH) {
+                const float4* frag = xs_frag<Int8W>(xs, c, lane);
+                float4 xv[4] = {frag[0], frag[64], frag[128], frag[192]};
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r] = Int8W::dot(wv[r][c], xv, acc[r]);
+            }
         }
         const float s = transpose_reduce<R>(acc, lane);
         constexpr int span = kWave / R;

@@ -15,6 +15,12 @@ int set_error(int status, const char* fmt, ...);
 int check_launch(const char* what);
 
 int launch_quantize(const void* w_bf16, int M, int K, int8_t* q, float* scale, hipStream_t stream);
+int launch_quantize_fp8(const void* w_bf16, int M, int K, uint8_t* q, float* scale, hipStream_t stream);
+int launch_quantize_int4(const void* w_bf16, int M, int K, uint8_t* q, float* scale, hipStream_t stream);
+int launch_fp8_gemv(const float* x, const uint8_t* w, int64_t copy_stride, int n_copies, const float* scale, float* y,
+                    int M, int K, int reps, hipStream_t stream);
+int launch_int4_gemv(const float* x, const uint8_t* w, int64_t copy_stride, int n_copies, const float* scale, float* y,
+                     int M, int K, int reps, hipStream_t stream);
 int launch_int8_gemv(const float* x, const int8_t* w, const float* scale, float* y, int M, int K,
                      hipStream_t stream);
 int launch_int8_gemv_repeat(const float* x, const int8_t* w, int64_t copy_stride, int n_copies, const float* scale,

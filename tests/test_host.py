@@ -142,6 +142,15 @@ def test_c_api_rejects_bad_arguments_without_launching(mq):
         assert lib.mq_int8_gemv_repeat(fake, w, stride, n, fake, fake, M, K, reps, None) == \
             _lib.MQ_ERR_INVALID_ARGUMENT, (w, stride, n, M, K, reps)
     assert lib.mq_quantize_per_channel_bf16(fake, 0, 16, fake, fake, None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    # other weight formats: shapes, strides and group multiples are checked before any launch
+    assert lib.mq_quantize_fp8_rows_bf16(None, 4, 16, fake, fake, None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert lib.mq_quantize_int4_groups_bf16(fake, 4, 100, fake, fake, None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert lib.mq_fp8_gemv(fake, fake, fake, fake, 4, 24, None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert lib.mq_int4_gemv(fake, fake, fake, fake, 4, 64, None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert lib.mq_int4_gemv(fake, fake, fake, fake, 4, 16384 + 128, None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert lib.mq_int4_gemv_repeat(fake, fake, 4 * 64 - 16, 2, fake, fake, 4, 128, 1, None) == \
+        _lib.MQ_ERR_INVALID_ARGUMENT                                    # stride below one copy (M * K / 2)
+    assert lib.mq_fp8_gemv_repeat(fake, fake, 64, 2, fake, fake, 4, 16, 0, None) == _lib.MQ_ERR_INVALID_ARGUMENT
     a = _lib.DecodeArgs()
     a.num_layers, a.max_seq_len, a.position, a.cache_len = 2, 16, 0, 1
     a.input_token_id = 151936                                  # == vocab: out of range

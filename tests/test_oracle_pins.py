@@ -311,3 +311,97 @@ def test_gumbel_max_detects_wrong_temperature():
         counts[tok] += 1
     se = np.sqrt(p * (1 - p) / n)
     assert not np.all(np.abs(counts / n - p) < 5 * se)
+
+
+# ---- other weight formats (oracle/formats.py) -----------------------------------------
+def test_fp8_decode_known_answers():
+    """OCP E4M3FN values of landmark codes (exponent bias 7, subnormals m * 2^-9, 0x7F NaN)."""
+    import math
+    from oracle.formats import fp8_decode_table
+    t = fp8_decode_table()
+    want = {0x00: 0.0, 0x01: 2.0 ** -9, 0x07: 7 * 2.0 ** -9, 0x08: 2.0 ** -6, 0x38: 1.0, 0x3F: 1.875,
+            0x40: 2.0, 0x7E: 448.0, 0xB8: -1.0, 0xFE: -448.0, 0x80: 0.0}
+    for c, v in want.items():
+        assert t[c] == v, (hex(c), t[c], v)
+    assert math.copysign(1.0, t[0x80]) == -1.0
+    assert np.isnan(t[0x7F]) and np.isnan(t[0xFF])
+    assert np.sum(np.isnan(t)) == 2
+    finite = t[:0x7F]
+    assert np.all(np.diff(finite) > 0)                       # codes 0..0x7E increase strictly
+
+
+def _fp8_brute(x: float) -> int:
+    """Nearest finite code by exhaustive search; ties to the even code; saturation at 448."""
+    from oracle.formats import fp8_decode_table
+    t = fp8_decode_table()[:0x7F]
+    a = abs(x)
+    sign = 0x80 if np.signbit(np.float32(x)) else 0
+    if a >= 448.0:
+        return sign | 0x7E
+    d = np.abs(t - a)
+    best = np.flatnonzero(d == d.min())
+    c = int(best[0]) if len(best) == 1 else int([b for b in best if b % 2 == 0][0])
+    return sign | c
+
+
+def test_fp8_encode_brute_force():
+    from oracle.formats import fp8_decode_table, fp8_encode
+    t = fp8_decode_table()[:0x7F]
+    rng = np.random.default_rng(3)
+    xs = list(rng.choice([-1.0, 1.0], 3000) * 2.0 ** rng.uniform(-13, 10, 3000))
+    xs += [float((t[i] + t[i + 1]) / 2) for i in range(0x7E)]          # every midpoint: ties
+    xs += [float(-(t[i] + t[i + 1]) / 2) for i in range(0x7E)]
+    xs += [0.0, -0.0, 447.9, 448.0, 455.0, 464.0, 470.0, 480.0, 1e9, 2.0 ** -10, 2.0 ** -11, 3 * 2.0 ** -11]
+    xs32 = np.array(xs, dtype=np.float32)
+    got = fp8_encode(xs32)
+    for x, g in zip(xs32, got):
+        assert int(g) == _fp8_brute(float(x)), (float(x), hex(int(g)), hex(_fp8_brute(float(x))))
+
+
+def test_fp8_quantizer_round_trip():
+    """Every element's dequantized value is the nearest representable one: within half a step."""
+    from oracle.formats import dequant_fp8, quantize_fp8_rows
+    g = torch.Generator().manual_seed(11)
+    w = (torch.randn(37, 96, generator=g) * 0.02).to(torch.bfloat16)
+    w[3] = 0
+    q, s = quantize_fp8_rows(w)
+    d = dequant_fp8(q, s)
+    wf = w.double().numpy()
+    assert np.all(d[3] == 0) and s[3].item() == np.float32(1e-12)
+    rel = np.abs(d - wf) / np.maximum(np.abs(wf), 1e-30)
+    big = np.abs(wf) >= s.numpy()[:, None] * 2.0 ** -6                 # normal range of the codes
+    assert np.all(rel[big] <= 2.0 ** -4 + 1e-7)
+    assert np.all(np.abs(q.numpy().astype(np.int64) & 0x7F) <= 0x7E)
+    amax_code = (q.numpy()[np.arange(37) != 3] & 0x7F).max(axis=1)
+    assert np.all(amax_code == 0x7E)                                   # each row's largest maps to 448
+
+
+def test_int4_quantizer_matches_torch_expression():
+    """The numpy restatement against the INT8 quantizer's torch expression with 7 and a group axis."""
+    from oracle.formats import quantize_int4_groups, unpack_int4
+    g = torch.Generator().manual_seed(12)
+    M, K, G = 19, 512, 128
+    w = (torch.randn(M, K, generator=g) * 0.02).to(torch.bfloat16)
+    w[1] = 0
+    w[2, :128] = 0.5                                                   # a group of equal values
+    w[4, 5] = -3.0
+    packed, s = quantize_int4_groups(w)
+    wg = w.view(M, K // G, G)
+    amax = wg.abs().amax(dim=-1)                                       # bf16
+    s_t = (amax / 7.0).to(torch.float32).clamp(min=1e-12)              # bf16 division, widened
+    q_t = (wg.to(torch.float32) / s_t[..., None]).round().clamp(-8, 7).to(torch.int64).view(M, K)
+    assert torch.equal(torch.from_numpy(s.numpy()), s_t)
+    assert np.array_equal(unpack_int4(packed), q_t.numpy())
+
+
+def test_int4_packing_known_answer():
+    """Low nibble = even element, two's complement: [1, -1, 7, -8, 0, 3] -> 0xF1, 0x87, 0x30."""
+    from oracle.formats import unpack_int4
+    packed = torch.tensor([[0xF1, 0x87, 0x30]], dtype=torch.uint8)
+    assert unpack_int4(packed).tolist() == [[1, -1, 7, -8, 0, 3]]
+    from oracle.formats import quantize_int4_groups
+    w = torch.zeros(1, 128, dtype=torch.bfloat16)
+    w[0, :6] = torch.tensor([1.0, -1.0, 7.0, -7.0, 0.0, 3.0])
+    p, s = quantize_int4_groups(w)
+    assert s.tolist() == [[1.0]]
+    assert p[0, :3].tolist() == [0xF1, 0x97, 0x30]                     # -7 -> 0x9
