@@ -245,6 +245,14 @@ int mq_workspace_init(void* workspace, size_t workspace_bytes, hipStream_t strea
 int mq_int8_decode_step(const mq_decode_args* args, hipStream_t stream);
 /* Same with bf16 weights (scales and lm_head_scale ignored). Replaces launch_a10_decode. */
 int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream);
+/* Same with FP8 E4M3 weights: every linear and the LM head as codes from
+ * mq_quantize_fp8_rows_bf16 (uint8 [out, in]) with their per-row fp32 scales,
+ * in the INT8 layout and packing order. No counterpart in the reference (INT8
+ * and BF16 only). Hidden 1024 / intermediate 3072, on the XCD-aware kernel
+ * (MQ_ERR_UNSUPPORTED for other dims or when its workgroup placement does not
+ * hold). Every stored intermediate is the correctly rounded value of the
+ * dequantized weights' expression, as for INT8. */
+int mq_fp8_decode_step(const mq_decode_args* args, hipStream_t stream);
 /* Allocation-free variant of mq_int8_decode_step. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

@@ -277,6 +277,15 @@ int mq_int8_decode_step(const mq_decode_args* args, hipStream_t stream) {
     return launch_decode(*args, s, true, stream);
 }
 
+int mq_fp8_decode_step(const mq_decode_args* args, hipStream_t stream) {
+    clear_error();
+    DecodeShape s;
+    int st = validate_decode(args, true, &s);
+    if (st != MQ_OK) return st;
+    s.fp8 = true;
+    return launch_decode(*args, s, true, stream);
+}
+
 int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream) {
     clear_error();
     DecodeShape s;
@@ -430,8 +439,7 @@ int mq_decode_variant(const mq_model_dims* dims, int int8) {
     DecodeShape s;
     int st = shape_of(dims, &s);
     if (st != MQ_OK) return -st;
-    const int v = decode_variant_in_use(s, int8 != 0);
-    return v >= 1 && v <= 3 ? v : -v;
+    return decode_variant_in_use(s, int8 != 0);            // the variant, or minus the refusal's status
 }
 
 void launch_a10_int8_decode(int input_token_id, int* output_token_id, const void* embed_weight,

@@ -251,6 +251,49 @@ struct Int8W {
     template <int S = 1>
     __device__ static double dotd(uint4 w, const double2* x, double acc) { return dot_i8x16_d<S>(w, x, acc); }
 };
+// 16 FP8 E4M3 codes (OCP E4M3FN, decoded exactly by v_cvt_pk_f32_fp8) against 16 fp32
+// activations (x[0..3] hold elements 0-3, 4-7, 8-11, 12-15).
+__device__ __forceinline__ float dot_fp8x16(uint4 w, const float4* x, float acc) {
+    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 xv = x[i];
+        const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)wv[i], false);   // bytes 0, 1
+        const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)wv[i], true);    // bytes 2, 3
+        acc = fmaf(lo[0], xv.x, acc);
+        acc = fmaf(lo[1], xv.y, acc);
+        acc = fmaf(hi[0], xv.z, acc);
+        acc = fmaf(hi[1], xv.w, acc);
+    }
+    return acc;
+}
+// The same against 16 fp64 activations (8 double2 at x[0], x[S], ...): the decoded codes
+// and their products are exact in fp64, as the int8 ones are.
+template <int S = 1>
+__device__ __forceinline__ double dot_fp8x16_d(uint4 w, const double2* x, double acc) {
+    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+    double s[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)wv[i], false);
+        const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)wv[i], true);
+        const double2 x0 = x[(2 * i) * S], x1 = x[(2 * i + 1) * S];
+        s[0] = fma((double)lo[0], x0.x, s[0]);
+        s[1] = fma((double)lo[1], x0.y, s[1]);
+        s[2] = fma((double)hi[0], x1.x, s[2]);
+        s[3] = fma((double)hi[1], x1.y, s[3]);
+    }
+    return acc + ((s[0] + s[1]) + (s[2] + s[3]));
+}
+// FP8 E4M3 weights with per-row scales (the INT8 layout: one byte per element, so every
+// path that applies INT8 row scales applies these).
+struct Fp8W {
+    static constexpr int kBytes = 1;
+    static constexpr int kPerLane = 16;
+    __device__ static float dot(uint4 w, const float4* x, float acc) { return dot_fp8x16(w, x, acc); }
+    template <int S = 1>
+    __device__ static double dotd(uint4 w, const double2* x, double acc) { return dot_fp8x16_d<S>(w, x, acc); }
+};
 struct Bf16W {
     static constexpr int kBytes = 2;
     static constexpr int kPerLane = 8;

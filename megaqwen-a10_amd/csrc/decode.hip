@@ -523,15 +523,25 @@ bool xcd_placement_ok() {
 // The kernel a step of these dims with `cache_len` cached positions uses: the async-wave
 // kernel (3) for the INT8 Qwen3-0.6B shape up to 64 positions, the XCD-aware kernel (2)
 // otherwise when the workgroup placement allows, else the single-level kernel (1).
+// A refusal returns its status negated (MQ_ERR_UNSUPPORTED is 2, the XCD-aware kernel's
+// number, so it must not share the positive range).
 int decode_variant_for(const DecodeShape& s, bool int8, int cache_len) {
     const int v = g_variant.load();
     const bool have_xcd = decode_xcd_kernel_ptr(s, int8, false) != nullptr;
+    // FP8 weights run on the XCD-aware kernel only
+    if (s.fp8) {
+        if (!have_xcd) return -set_error(MQ_ERR_UNSUPPORTED, "no FP8 decode kernel for H=%d I=%d", s.H, s.I);
+        if (v == 1 || v == 3 || !xcd_placement_ok())
+            return -set_error(MQ_ERR_UNSUPPORTED, "FP8 weights run on the XCD-aware kernel only (variant %d%s)", v,
+                             xcd_placement_ok() ? "" : ", workgroup placement unsupported");
+        return 2;
+    }
     if (v == 1) return 1;
-    if (v == 2) return have_xcd ? 2 : set_error(MQ_ERR_UNSUPPORTED, "no XCD-aware kernel for these dims");
+    if (v == 2) return have_xcd ? 2 : -set_error(MQ_ERR_UNSUPPORTED, "no XCD-aware kernel for these dims");
     if (v == 3)
         return decode_async_supports(s, int8, cache_len)
                    ? 3
-                   : set_error(MQ_ERR_UNSUPPORTED, "the async-wave kernel covers INT8 hidden 1024 / intermediate 3072 "
+                   : -set_error(MQ_ERR_UNSUPPORTED, "the async-wave kernel covers INT8 hidden 1024 / intermediate 3072 "
                                                    "up to 64 cached positions (cache_len %d)", cache_len);
     if (!(have_xcd && xcd_placement_ok())) return 1;
     return decode_async_supports(s, int8, cache_len) ? 3 : 2;
@@ -583,7 +593,7 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
         return set_error(MQ_ERR_UNSUPPORTED, "num_layers %d exceeds %d", a.num_layers, kMaxLayers);
     // several steps per launch: the async-wave kernel, over every position the launch covers
     const int variant = decode_variant_for(s, int8, plan ? a.position + plan->n_steps : a.cache_len);
-    if (variant < 1 || variant > 3) return variant;
+    if (variant < 0) return -variant;
     if (plan && variant != 3)
         return set_error(MQ_ERR_UNSUPPORTED, "several steps per launch run on the async-wave kernel only (INT8, hidden "
                          "1024 / intermediate 3072, up to %d positions; here %d)", decode_async_max_len(),

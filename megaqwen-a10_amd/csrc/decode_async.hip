@@ -1158,7 +1158,8 @@ size_t decode_async_workspace_bytes(const DecodeShape& s) {
 }
 
 bool decode_async_supports(const DecodeShape& s, bool int8, int cache_len) {
-    return int8 && s.H == kAH && s.I == kAI && s.NQ == 16 && s.NKV == 8 && s.D == kAD && cache_len <= kAMaxLen;
+    return int8 && !s.fp8 && s.H == kAH && s.I == kAI && s.NQ == 16 && s.NKV == 8 && s.D == kAD &&
+           cache_len <= kAMaxLen;
 }
 
 int launch_decode_async(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {

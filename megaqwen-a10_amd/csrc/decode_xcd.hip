@@ -740,6 +740,10 @@ static int launch_xcd_t(const KArgs& ka, bool debug, hipStream_t stream, hipEven
 }
 
 const void* decode_xcd_kernel_ptr(const DecodeShape& s, bool int8, bool debug) {
+    if (s.fp8) {
+        if (!(int8 && s.H == 1024 && s.I == 3072)) return nullptr;
+        return debug ? (const void*)&decode_xcd_kernel<1024, 3072, Fp8W, true> : (const void*)&decode_xcd_kernel<1024, 3072, Fp8W, false>;
+    }
     if (s.H == 1024 && s.I == 3072) {
         if (int8) return debug ? (const void*)&decode_xcd_kernel<1024, 3072, Int8W, true> : (const void*)&decode_xcd_kernel<1024, 3072, Int8W, false>;
         return debug ? (const void*)&decode_xcd_kernel<1024, 3072, Bf16W, true> : (const void*)&decode_xcd_kernel<1024, 3072, Bf16W, false>;
@@ -751,6 +755,11 @@ const void* decode_xcd_kernel_ptr(const DecodeShape& s, bool int8, bool debug) {
 
 int launch_decode_xcd(const KArgs& k, const DecodeShape& s, bool int8, bool debug, hipStream_t stream,
                       hipEvent_t t0, hipEvent_t t1) {
+    if (s.fp8) {
+        if (int8 && s.H == 1024 && s.I == 3072) return launch_xcd_t<1024, 3072, Fp8W>(k, debug, stream, t0, t1);
+        return set_error(MQ_ERR_UNSUPPORTED, "FP8 weights are compiled for hidden 1024 / intermediate 3072 only "
+                         "(H=%d I=%d)", s.H, s.I);
+    }
     if (s.H == 1024 && s.I == 3072)
         return int8 ? launch_xcd_t<1024, 3072, Int8W>(k, debug, stream, t0, t1)
                     : launch_xcd_t<1024, 3072, Bf16W>(k, debug, stream, t0, t1);

@@ -98,7 +98,7 @@ __device__ __forceinline__ int fmt_xs_index(int k) {              // float index
 }
 
 // 16 FP8 codes against 16 activations (x[i] holds elements 4i .. 4i + 3)
-__device__ __forceinline__ float dot_fp8x16(uint4 w, const float4 (&x)[4], float acc) {
+__device__ __forceinline__ float dot_fp8x16_regs(uint4 w, const float4 (&x)[4], float acc) {
     const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -211,7 +211,7 @@ fmt_gemv_kernel(const float* __restrict__ x, const uint8_t* __restrict__ w, int6
                     if constexpr (kInt4)
                         acc[r] = fmaf(dot_int4x16_biased(make_uint2(wv[r][c].x, wv[r][c].y), xv) - xb[c], gs[r][c],
                                       acc[r]);
-                    else acc[r] = dot_fp8x16(wv[r][c], xv, acc[r]);
+                    else acc[r] = dot_fp8x16_regs(wv[r][c], xv, acc[r]);
                 }
             }
         }

@@ -82,7 +82,8 @@ def _device_array(structs, device) -> torch.Tensor:
 class _DecoderBase:
     """Owns the KV cache, the reference's scratch buffers, the workspace and the step state."""
 
-    _int8: bool = True
+    _int8: bool = True         # one-byte weights with per-row scales
+    _fp8: bool = False         # ... that are FP8 E4M3 codes rather than int8
 
     def _setup(self, embed, layer_tensors, final_norm, lm_head, cos_table, sin_table, num_layers,
                max_seq_len, layer_scales=None, lm_head_scale=None):
@@ -106,7 +107,7 @@ class _DecoderBase:
         if len(layer_tensors) != 11 * num_layers:
             raise ValueError(f"layer_weights_flat: expected {11 * num_layers} tensors (11 per layer), "
                              f"got {len(layer_tensors)}")
-        wdt = torch.int8 if self._int8 else torch.bfloat16
+        wdt = torch.uint8 if self._fp8 else torch.int8 if self._int8 else torch.bfloat16
         I = layer_tensors[8].shape[0]
         D = 128
         Q, KV = 16 * D, 8 * D
@@ -217,7 +218,8 @@ class _DecoderBase:
         a.workspace_bytes = ws_bytes
         a.spin_limit = 0
         self._args = a
-        self._step_fn = self._lib.mq_int8_decode_step if self._int8 else self._lib.mq_bf16_decode_step
+        self._step_fn = (self._lib.mq_fp8_decode_step if self._fp8 else
+                         self._lib.mq_int8_decode_step if self._int8 else self._lib.mq_bf16_decode_step)
         self._debug = False
 
     def _init_workspace(self):
@@ -370,7 +372,7 @@ class _DecoderBase:
         if self._pos + len(ids) + n_tokens - 1 > self.max_seq_len:
             raise ValueError(f"position {self._pos} + {len(ids) + n_tokens - 1} steps exceed max_seq_len "
                              f"{self.max_seq_len}")
-        if device_loop and self._int8:
+        if device_loop and self._int8 and not self._fp8:
             out = self._generate_one_launch(ids, n_tokens)
             if out is not None:
                 return out
@@ -460,6 +462,22 @@ class A10Int8MegakernelDecoder(_DecoderBase):
     def __init__(self, embed_weight, layer_weights_flat, layer_scales_all, lm_head_int8, lm_head_scale,
                  final_norm_weight, cos_table, sin_table, num_layers, max_seq_len):
         self._setup(embed_weight, layer_weights_flat, final_norm_weight, lm_head_int8, cos_table, sin_table,
+                    num_layers, max_seq_len, layer_scales=layer_scales_all, lm_head_scale=lm_head_scale)
+
+
+class A10Fp8MegakernelDecoder(_DecoderBase):
+    """FP8 E4M3 weights (no counterpart in the reference, which has INT8 and BF16):
+    the constructor of A10Int8MegakernelDecoder with every linear and the LM head
+    given as FP8 codes (uint8 [out, in], from ``quantize_fp8``) and their per-row
+    fp32 scales, in the same packing order. Hidden 1024 / intermediate 3072; one
+    launch of the XCD-aware kernel per step (mq_fp8_decode_step)."""
+
+    _int8 = True
+    _fp8 = True
+
+    def __init__(self, embed_weight, layer_weights_flat, layer_scales_all, lm_head_fp8, lm_head_scale,
+                 final_norm_weight, cos_table, sin_table, num_layers, max_seq_len):
+        self._setup(embed_weight, layer_weights_flat, final_norm_weight, lm_head_fp8, cos_table, sin_table,
                     num_layers, max_seq_len, layer_scales=layer_scales_all, lm_head_scale=lm_head_scale)
 
 

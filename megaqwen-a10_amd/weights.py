@@ -83,14 +83,19 @@ def state_digest(state: dict) -> str:
     return h.hexdigest()
 
 
-def quantize_state(state: dict, cfg: ModelConfig, device) -> dict:
+def quantize_state(state: dict, cfg: ModelConfig, device, weight_format: str = "int8") -> dict:
     """bench_int8.py:27-55 without the HF load: every projection and the LM head
-    become ``(int8, fp32 scale)`` pairs computed on ``device``; norms and the
-    embedding stay bf16 (moved to ``device``)."""
+    become ``(int8, fp32 scale)`` pairs computed on ``device`` (``weight_format="fp8"``:
+    ``(FP8 E4M3 codes, fp32 scale)`` pairs, no counterpart in the reference); norms and
+    the embedding stay bf16 (moved to ``device``). ``pack_int8`` packs either."""
+    if weight_format not in ("int8", "fp8"):
+        raise ValueError(f"weight_format must be 'int8' or 'fp8', got {weight_format!r}")
+    from .formats import quantize_fp8
+    quant = quantize_per_channel if weight_format == "int8" else quantize_fp8
     q = {}
     for k, v in state.items():
         if k == "lm_head.weight" or any(k.endswith(f"{p}.weight") for p in PROJ):
-            q[k] = quantize_per_channel(v.to(device))
+            q[k] = quant(v.to(device))
         else:
             q[k] = v.to(device)
     return q

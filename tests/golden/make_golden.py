@@ -14,7 +14,9 @@ Fixtures (all small; weights are regenerated from their seed, never stored):
                        theta=1e4 pair-duplicated table at 0, 1, 7, 2047.
 * tokens_<case>.json — prompt, 32 greedy tokens, per-step top-2 logit margins
                        and the sha256 of the generated weights, from the
-                       float64 oracle, for each decode case in CASES.
+                       float64 oracle, for each decode case in CASES (the
+                       _fp8 case: FP8 E4M3 weights from oracle/formats.py,
+                       decoded to their exact values for the oracle).
 """
 from __future__ import annotations
 
@@ -33,6 +35,7 @@ ROOT = HERE.parents[1]
 sys.path.insert(0, str(ROOT))
 
 import __graft_entry__  # noqa: E402
+from oracle import formats as oformats  # noqa: E402
 from oracle import quant as oquant  # noqa: E402
 from oracle import rope as orope  # noqa: E402
 from oracle.ref_cpu import Dims, RefDecoder, greedy_generate  # noqa: E402
@@ -42,6 +45,7 @@ mq = __graft_entry__.load_package()
 # name -> (config overrides, seed, int8, norm_jitter, max_seq_len, tokens)
 CASES = {
     "small_int8": (dict(num_layers=2, vocab_size=4096), 1, True, 0.1, 64, 32),
+    "qwen3_0.6b_fp8": (dict(), 0, True, 0.0, 64, 32),
     "qwen3_0.6b_int8": (dict(), 0, True, 0.0, 64, 32),
     "qwen3_0.6b_bf16": (dict(), 0, False, 0.0, 64, 32),
 }
@@ -99,9 +103,22 @@ def make_rope():
                         legacy_cos=bits(lc[lpos]), legacy_sin=bits(ls[lpos]))
 
 
+# one-byte weight format of a case whose int8 flag is set (default int8)
+FORMAT = {"qwen3_0.6b_fp8": "fp8"}
+
+
+def _quantize(w: torch.Tensor, fmt: str):
+    """(weights as the oracle multiplies them, fp32 row scales)."""
+    if fmt == "fp8":
+        q, s = oformats.quantize_fp8_rows(w)
+        return torch.from_numpy(oformats.fp8_decode_table()[q.numpy().astype(np.int64)]), s
+    return oquant.quantize_per_channel(w)
+
+
 def oracle_for(name: str, dtype=torch.float64):
     """Builds (RefDecoder, prompt, cfg, digest) for a fixture case on the CPU (quantizing with the oracle)."""
     over, seed, int8, jitter, S, _ = CASES[name]
+    fmt = FORMAT.get(name, "int8")
     cfg = mq.QWEN3_0_6B.with_(name=name, **over)
     state, prompt = mq.random_init_state(cfg, seed=seed, norm_jitter=jitter)
     digest = mq.state_digest(state)
@@ -115,7 +132,7 @@ def oracle_for(name: str, dtype=torch.float64):
             w = state[f"{p}.{n}.weight"]
             if not int8:
                 return w
-            qq, ss = oquant.quantize_per_channel(w)
+            qq, ss = _quantize(w, fmt)
             scales.append(ss)
             return qq
         layers.append(state[f"{p}.input_layernorm.weight"])
@@ -125,7 +142,7 @@ def oracle_for(name: str, dtype=torch.float64):
         layers.append(state[f"{p}.post_attention_layernorm.weight"])
         layers += [proj("mlp.gate_proj"), proj("mlp.up_proj"), proj("mlp.down_proj")]
     if int8:
-        lm, lms = oquant.quantize_per_channel(state["lm_head.weight"])
+        lm, lms = _quantize(state["lm_head.weight"], fmt)
     else:
         lm, lms = state["lm_head.weight"], None
     dec = RefDecoder(dims, state["model.embed_tokens.weight"], layers, scales if int8 else None,
@@ -139,6 +156,7 @@ def make_tokens(name: str):
     n = CASES[name][5]
     toks, margins = greedy_generate(dec, prompt.tolist(), n)
     rec = {"case": name, "config": cfg.__dict__, "seed": CASES[name][1], "int8": CASES[name][2],
+           "weight_format": FORMAT.get(name, "int8") if CASES[name][2] else "bf16",
            "norm_jitter": CASES[name][3], "max_seq_len": CASES[name][4], "prompt": prompt.tolist(),
            "tokens": toks, "top2_margins": margins, "weights_sha256": digest,
            "oracle": "oracle.ref_cpu.RefDecoder float64, rounding points of a10_int8_decode_kernel.cu"}

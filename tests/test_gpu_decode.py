@@ -34,9 +34,11 @@ def _build(mq, dev, name):
     S = d["max_seq_len"]
     cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
     if d["int8"]:
-        qstate = mq.quantize_state(state, cfg, dev)
+        fp8 = d.get("weight_format") == "fp8"
+        qstate = mq.quantize_state(state, cfg, dev, weight_format="fp8" if fp8 else "int8")
         embed, layers, scales, lm_q, lm_s, fnorm = mq.pack_int8(qstate, cfg)
-        dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+        cls = mq.A10Fp8MegakernelDecoder if fp8 else mq.A10Int8MegakernelDecoder
+        dec = cls(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
         keep = (embed, layers, scales, lm_q, lm_s, fnorm, cos, sin)
     else:
         embed, layers, fnorm, lm = mq.pack_bf16(state, cfg, dev)
@@ -520,5 +522,27 @@ def test_a10decoder_generate(mq, dev, int8):
     assert ids[:8] == d["prompt"]
     assert ids[8:] == d["tokens"], (ids[8:], d["tokens"])
     assert tok_s > 0 and len(times) == 31
+    del dec
+    torch.cuda.empty_cache()
+
+
+def test_forced_kernel_out_of_range_is_refused(mq, dev, small):
+    """A kernel forced by set_decode_variant that cannot run a step refuses it with MQError
+    (nothing launched, position unchanged) instead of running another kernel: the
+    async-wave kernel past its 64 positions."""
+    dec0, d, prompt, cfg, keep = small
+    embed, layers, scales, lm_q, lm_s, fnorm, _, _ = keep
+    S = 96
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+    dec.prefill_random_kv(70, seed=1)
+    mq.set_decode_variant("async")
+    try:
+        with pytest.raises(mq._lib.MQError, match="async-wave"):
+            dec.decode_step(int(prompt[0]))
+    finally:
+        mq.set_decode_variant("auto")
+    assert dec.position() == 70
+    assert 0 <= dec.decode_step(int(prompt[0])) < cfg.vocab_size          # the automatic choice runs it
     del dec
     torch.cuda.empty_cache()
