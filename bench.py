@@ -399,6 +399,45 @@ def run_formats(args, mq, torch):
     L = mq.QWEN3_0_6B.num_layers
     step = {f: round(L * sum(res[k][f]["us"] for k in ("qkv", "o", "gate_up", "down")) + res["lm_head"][f]["us"], 2)
             for f in ("int8", "int4", "fp8")}
+
+    # the whole config-1 decode step with FP8 weights, beside INT8 on the same (XCD-aware) kernel
+    cfg = mq.QWEN3_0_6B
+    state, prompt = mq.random_init_state(cfg, seed=args.seed)
+    S = PROMPT_LEN + args.steps + 8
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    decode = {}
+    events = _events(torch, args.steps)
+    for fmt in ("int8", "fp8"):
+        qstate = mq.quantize_state(state, cfg, dev, weight_format=fmt)
+        packed = mq.pack_int8(qstate, cfg)
+        del qstate
+        cls = mq.A10Fp8MegakernelDecoder if fmt == "fp8" else mq.A10Int8MegakernelDecoder
+        dec = cls(*packed, cos, sin, cfg.num_layers, S)
+        mq.set_decode_variant("xcd")
+        try:
+            def prefill():
+                dec.reset()
+                tok = None
+                for t in prompt.tolist():
+                    tok = dec.decode_step(int(t))
+                return tok
+            first = prefill()
+            toks, wall, _ = _timed_pass(torch, dec, first, args.steps, dec.wait_token)
+            first2 = prefill()
+            toks2, _, kern_ms = _timed_pass(torch, dec, first2, args.steps, dec.wait_token, events)
+        finally:
+            mq.set_decode_variant("auto")
+        decode[fmt] = {"tok_s": round(args.steps / wall, 1), "kernel_avg_us": round(sum(kern_ms) / args.steps * 1e3, 2),
+                       "kernel_pass_tokens_identical": toks2 == toks and first2 == first}
+        if fmt == "fp8":
+            fx = ROOT / "tests" / "golden" / "tokens_qwen3_0.6b_fp8.json"
+            if fx.exists() and args.seed == 0:
+                want = json.loads(fx.read_text())["tokens"]
+                n = min(len(want) - 1, args.steps)
+                decode[fmt]["fixture_match"] = [first] + toks[:n] == want[:n + 1]
+        print(f"decode {fmt}: {decode[fmt]}", file=sys.stderr, flush=True)
+        del dec, packed
+        torch.cuda.empty_cache()
     return {"metric": "matvec-only decode step time at the Qwen3-0.6B shapes, INT4 per-group weights "
                       "(steady state; INT8 and FP8 E4M3 beside it)",
             "value": step["int4"], "unit": "us", "n_gpus": 1, "steps": 1, "warmup": 1,
@@ -408,7 +447,8 @@ def run_formats(args, mq, torch):
                                    "per row, INT4 per group of 128, FP8 E4M3 per row; one launch of the format's "
                                    "steady-state matvec over rotating copies (about 2 GB), time / reps; error = rel. "
                                    "L2 of the format's product against the bf16 weights' float64 product",
-                       "step_us_28_layers_plus_lm_head": step, "shapes": res}}
+                       "step_us_28_layers_plus_lm_head": step, "shapes": res,
+                       "decode_config1_xcd_kernel": decode}}
 
 
 def run_positions(args, mq, torch):
