@@ -598,14 +598,18 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
         return set_error(MQ_ERR_UNSUPPORTED, "several steps per launch run on the async-wave kernel only (INT8, hidden "
                          "1024 / intermediate 3072, up to %d positions; here %d)", decode_async_max_len(),
                          a.position + plan->n_steps);
-    // split attention (XCD kernel only): a slice of at most kMaxAttnLen positions per workgroup
+    // split attention: the XCD kernel with a slice of at most kMaxAttnLen positions per
+    // workgroup; the async-wave kernel with slices of at most 64 (its own threshold)
     int split_min = a.attn_split_min == 0 ? kDefaultSplitMin : a.attn_split_min;
     split_min = split_min > 0 ? std::min(split_min, kMaxAttnLen + 1) : INT_MAX;
-    const int max_len = (variant == 2 && split_min != INT_MAX) ? kSplitRanks * kMaxAttnLen : kMaxAttnLen;
-    if (a.cache_len > max_len)
+    if (variant == 3) split_min = decode_async_split_min(a.attn_split_min);
+    const int last_len = plan ? a.position + plan->n_steps : a.cache_len;
+    const int max_len = variant == 3 ? decode_async_max_len()
+                        : (variant == 2 && split_min != INT_MAX) ? kSplitRanks * kMaxAttnLen : kMaxAttnLen;
+    if (last_len > max_len)
         return set_error(MQ_ERR_UNSUPPORTED, "cache_len %d exceeds the attention limit %d of the %s kernel%s",
-                         a.cache_len, max_len, variant == 2 ? "XCD-aware" : "single-level",
-                         variant == 2 ? " without split attention" : "");
+                         last_len, max_len, variant == 3 ? "async-wave" : variant == 2 ? "XCD-aware" : "single-level",
+                         variant == 2 && split_min == INT_MAX ? " without split attention" : "");
     KArgs k;
     k.token = a.input_token_id;
     k.out_token = a.output_token_id;

@@ -57,13 +57,16 @@ namespace {
 constexpr int kAH = 1024, kAI = 3072, kAD = 128;
 constexpr int kAX = 8;                     // XCDs
 constexpr int kAIX = kAI / kAX;            // intermediate channels per XCD
-constexpr int kAMaxLen = 64;               // cache_len this kernel attends over
+constexpr int kAMaxLen = 64;               // positions one workgroup holds in LDS (slot B)
+constexpr int kARanks = kNWG / kAX;        // workgroups (ranks) per XCD
+constexpr int kASplitLen = kARanks * kAMaxLen;   // cache_len with split attention: 32 slices of <= 64
+constexpr int kAPart = 4 + 2 * kAD;        // a rank's attention partial: (max, denominator) per head, numerators
 constexpr int kCW = 4;                     // compute waves
 // digit plane pitch in words: 68, not 64, so that the 8 planes one A-operand read
 // touches start in different LDS banks
 constexpr int kPlane = 68;
 
-enum AStage { AS_QKV = 0, AS_ACT = 2, AS_MLP = 4, AS_HID = 5 };
+enum AStage { AS_QKV = 0, AS_ATT = 1, AS_ACT = 2, AS_MLP = 4, AS_HID = 5 };
 constexpr uint32_t kAStages = 8;
 
 // LDS counters (sync[]): ready and consumed per loader slot, arrival per combine
@@ -76,7 +79,7 @@ enum AArr { AR_A = 0, AR_B = 1, AR_C = 2, AR_E = 3, AR_F = 4 };
 // of squares (low and high word each), so that one buffer load reaches both.
 constexpr int kVecWords = kAH + 64;
 struct ALayout {
-    size_t qkvx, hidx, actx, mlpx, po, pd, lmg, tok, total;
+    size_t qkvx, hidx, actx, mlpx, po, pd, lmg, apart, amrg, tok, total;
 };
 // After the other two kernels' regions, so that the three can alternate on one workspace.
 constexpr ALayout alayout_for(size_t base) {
@@ -89,7 +92,9 @@ constexpr ALayout alayout_for(size_t base) {
     o.po = off; off += round256((size_t)kAX * kAH * 8);        // packed fp64 partials [xcd][row]
     o.pd = off; off += round256((size_t)kAX * kAH * 8);
     o.lmg = off; off += round256((size_t)kNWG * 2 * 8);
-    o.tok = off; off += round256((size_t)kAMaxLen * 4);        // a launch's forced input tokens
+    o.apart = off; off += round256((size_t)kAX * kARanks * kAPart * 2 * 8);   // split attention partials (fp64 as two tagged words)
+    o.amrg = off; off += round256((size_t)kAX * 2 * kAD * 8);             // merged outputs [xcd][dim]
+    o.tok = off; off += round256((size_t)kASplitLen * 4);      // a launch's forced input tokens
     o.total = off;
     return o;
 }
@@ -387,6 +392,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     uint64_t* const po = reinterpret_cast<uint64_t*>(a.ws + kLay.po);     // packed [8][H]
     uint64_t* const pd = reinterpret_cast<uint64_t*>(a.ws + kLay.pd);
     uint64_t* const lmg = reinterpret_cast<uint64_t*>(a.ws + kLay.lmg);
+    uint64_t* const apart = reinterpret_cast<uint64_t*>(a.ws + kLay.apart) + (size_t)x * kARanks * kAPart * 2;
+    uint64_t* const amrg = reinterpret_cast<uint64_t*>(a.ws + kLay.amrg) + (size_t)x * 2 * kAD;
 
     const uint32_t E0 = __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const uint32_t AS0 = __hip_atomic_load(&hdr->asteps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -401,6 +408,21 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     auto trace = [&](int l, int point) {
         if (kDebug && a.trace != nullptr && tid0 == 0)
             a.trace[((int64_t)l * kTracePoints + point) * kNWG + g] = __builtin_amdgcn_s_memrealtime();
+    };
+    // The positions [s0, s0 + ns) of cache_len p + 1 this rank attends over: all of them up to
+    // kAMaxLen (below the split threshold), else slice r of 32 (<= kAMaxLen each); true when split.
+    const int split_min = a.split_min;
+    auto attn_slice = [&](int p, int& s0, int& ns) -> bool {
+        const int n = p + 1;
+        if (n <= kAMaxLen && n < split_min) {
+            s0 = 0;
+            ns = n;
+            return false;
+        }
+        const int cs = (n + kARanks - 1) / kARanks;
+        s0 = min(n, r * cs);
+        ns = min(n, s0 + cs) - s0;
+        return true;
     };
     if (x >= kAX) {
         if (tid0 == 0) __hip_atomic_store(&hdr->abort_flag, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -546,17 +568,22 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 // different banks
                 // (the lane is rederived per layer, so that its row addresses are not held
                 // through the layer loop alongside the 128 registers of rows)
+                // Slot row jl holds position s0 + jl of this rank's positions (all of them, or
+                // its slice with split attention); rows before pos come from the cache.
                 const int ln = opaque(lane);
                 const int64_t cb = ((int64_t)l * kAX + x) * kv_head_stride;
+                int s0, ns;
+                attn_slice(pos, s0, ns);
+                const int lim = min(ns, pos - s0);
                 uint4 rk[kAMaxLen / 4], rv[kAMaxLen / 4];
 #pragma unroll
                 for (int i = 0; i < kAMaxLen / 4; ++i) {
-                    const int j = 4 * i + ln / 16;
+                    const int jl = 4 * i + ln / 16;
                     rk[i] = make_uint4(0, 0, 0, 0);
                     rv[i] = make_uint4(0, 0, 0, 0);
-                    if (j < pos) {
-                        rk[i] = ldg16(a.kc + cb + (int64_t)j * D + 8 * (ln % 16));
-                        rv[i] = ldg16(a.vc + cb + (int64_t)j * D + 8 * (ln % 16));
+                    if (jl < lim) {
+                        rk[i] = ldg16(a.kc + cb + (int64_t)(s0 + jl) * D + 8 * (ln % 16));
+                        rv[i] = ldg16(a.vc + cb + (int64_t)(s0 + jl) * D + 8 * (ln % 16));
                     }
                 }
                 const uint32_t qn = ld32(static_cast<const uint8_t*>(lw.q_norm_weight) + 4 * ln);
@@ -569,10 +596,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 const int ls = opaque(ln);
 #pragma unroll
                 for (int i = 0; i < kAMaxLen / 4; ++i) {
-                    const int j = 4 * i + ls / 16;
-                    if (j < pos) {
-                        reinterpret_cast<uint4*>(S.kvk[j])[(ls % 16) ^ (j % 16)] = rk[i];
-                        reinterpret_cast<uint4*>(S.kvv[j])[(ls % 16) ^ (j % 16)] = rv[i];
+                    const int jl = 4 * i + ls / 16;
+                    if (jl < lim) {
+                        reinterpret_cast<uint4*>(S.kvk[jl])[(ls % 16) ^ (jl % 16)] = rk[i];
+                        reinterpret_cast<uint4*>(S.kvv[jl])[(ls % 16) ^ (jl % 16)] = rv[i];
                     }
                 }
                 put32(S.qkn[0], ls, qn);
@@ -654,11 +681,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
             // rotation pairs of RoPE; v dims 2l, 2l + 1 (the word layout of a cache row).
             float ao;
             {
-                const int n = pos + 1;
-                const int q0 = (n + kCW - 1) / kCW;                  // <= 16
-                const int j0 = min(n, c * q0), j1 = min(n, j0 + q0);
+                int s0, ns;
+                const bool split = attn_slice(pos, s0, ns);
+                const int q0 = (ns + kCW - 1) / kCW;                 // <= 16
+                const int j0 = s0 + min(ns, c * q0), j1 = s0 + min(ns, c * q0 + q0);
                 const int np = j1 - j0;
-                const bool owner = j0 <= pos && pos < j1;
+                const bool owner = j0 <= pos && pos < j1;            // one wave of one workgroup per XCD when split
                 float qv[2][2], kv2[2], vv[2];
                 {
                     const uint32_t w[4] = {2u * (uint32_t)lane, 128u + 2u * (uint32_t)lane, 256u + 2u * (uint32_t)lane,
@@ -714,17 +742,18 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                          bf16_bits_to_f32(S.qkn[1][lane + 64]), kr);
                     const uint32_t k0 = f32_to_bf16_bits(kr[0]), k1 = f32_to_bf16_bits(kr[1]);
                     const uint32_t vw = f32_to_bf16_bits(vv[0]) | (f32_to_bf16_bits(vv[1]) << 16);
-                    const int p16 = pos % 16;
-                    S.kvk[pos][8 * ((lane >> 3) ^ p16) + (lane & 7)] = (uint16_t)k0;
-                    S.kvk[pos][8 * (((lane + 64) >> 3) ^ p16) + (lane & 7)] = (uint16_t)k1;
-                    reinterpret_cast<uint32_t*>(S.kvv[pos])[4 * ((lane >> 2) ^ p16) + (lane & 3)] = vw;
-                    if (r == 0) {
+                    const int pl = pos - s0, p16 = pl % 16;
+                    S.kvk[pl][8 * ((lane >> 3) ^ p16) + (lane & 7)] = (uint16_t)k0;
+                    S.kvk[pl][8 * (((lane + 64) >> 3) ^ p16) + (lane & 7)] = (uint16_t)k1;
+                    reinterpret_cast<uint32_t*>(S.kvv[pl])[4 * ((lane >> 2) ^ p16) + (lane & 3)] = vw;
+                    if (split || r == 0) {
                         const int64_t cur = ((int64_t)l * kAX + x) * kv_head_stride + (int64_t)pos * D;
                         a.kc[cur + lane] = (uint16_t)k0;
                         a.kc[cur + lane + 64] = (uint16_t)k1;
                         reinterpret_cast<uint32_t*>(a.vc + cur)[lane] = vw;
-                        if (dbg && a.dbg_k) { a.dbg_k[x * D + lane] = kr[0]; a.dbg_k[x * D + lane + 64] = kr[1]; }
-                        if (dbg && a.dbg_v) { a.dbg_v[x * D + 2 * lane] = vv[0]; a.dbg_v[x * D + 2 * lane + 1] = vv[1]; }
+                        const bool dbgkv = kDebug && l == last;
+                        if (dbgkv && a.dbg_k) { a.dbg_k[x * D + lane] = kr[0]; a.dbg_k[x * D + lane + 64] = kr[1]; }
+                        if (dbgkv && a.dbg_v) { a.dbg_v[x * D + 2 * lane] = vv[0]; a.dbg_v[x * D + 2 * lane + 1] = vv[1]; }
                     }
                 }
                 lds_order();
@@ -742,8 +771,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                         for (int t = 0; t < 4; ++t) qd[h][t] = reinterpret_cast<const double2*>(&S.qa[c][h][8 * d16])[t];
 #pragma unroll
                     for (int p = 0; p < 4; ++p) {
-                        const int row = j0 + min(4 * p + jj, np - 1);
-                        kc[p] = reinterpret_cast<const uint4*>(S.kvk[row])[d16 ^ (row & 15)];
+                        const int rl = j0 - s0 + min(4 * p + jj, np - 1);      // slot row
+                        kc[p] = reinterpret_cast<const uint4*>(S.kvk[rl])[d16 ^ (rl & 15)];
                     }
                     double E[8];                         // entry 2p + h: partial score over the 8 dims
 #pragma unroll
@@ -805,9 +834,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
 #pragma unroll
                     for (int u = 0; u < 8; ++u) {
                         const int t = min(t0 + u, np - 1);
-                        const int row = j0 + t;
+                        const int rl = j0 - s0 + t;                              // slot row
                         pp[u] = *reinterpret_cast<const double2*>(S.pw[c][t]);
-                        vw[u] = reinterpret_cast<const uint32_t*>(S.kvv[row])[4 * ((lane >> 2) ^ (row & 15)) + (lane & 3)];
+                        vw[u] = reinterpret_cast<const uint32_t*>(S.kvv[rl])[4 * ((lane >> 2) ^ (rl & 15)) + (lane & 3)];
                     }
 #pragma unroll
                     for (int u = 0; u < 8; ++u) {
@@ -846,7 +875,61 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     num = fma(e, S.pacc[w][hh][dim], num);
                     den = fma(e, S.pml[w][hh][1], den);
                 }
-                ao = (float)(num * rcp_nr(den));
+                if (!split) {
+                    ao = (float)(num * rcp_nr(den));
+                } else {
+                    // This rank's partial over its slice: (max, denominator) of head hh and the
+                    // numerators of dims [64c, +64), fp64 as two tagged XCD-local words each.
+                    const uint32_t ta = tag(l, AS_ATT);
+                    auto put_d = [&](int k, double v) {
+                        const uint64_t u = (uint64_t)__double_as_longlong(v);
+                        ll_put_xcd(&apart[((size_t)r * kAPart + k) * 2], (uint32_t)u, ta);
+                        ll_put_xcd(&apart[((size_t)r * kAPart + k) * 2 + 1], (uint32_t)(u >> 32), ta);
+                    };
+                    put_d(4 + 64 * c + lane, num);
+                    if ((c & 1) == 0 && lane == 0) {
+                        put_d(2 * hh, M == -INFINITY ? -1e300 : M);          // an empty slice weighs 0
+                        put_d(2 * hh + 1, den);
+                    }
+                    // merge: this rank's output dims D0, D0 + 1 (wave c) over the 32 partials;
+                    // lane s < 32 reads rank s's (max, denominator) and numerators
+                    const int D0 = 8 * r + 2 * c, hm = D0 >> 7;
+                    const int sr = lane & 31;
+                    const uint32_t w4[4] = {(uint32_t)((sr * kAPart + 2 * hm) * 2), (uint32_t)((sr * kAPart + 2 * hm + 1) * 2),
+                                            (uint32_t)((sr * kAPart + 4 + D0) * 2), (uint32_t)((sr * kAPart + 5 + D0) * 2)};
+                    float o8[8];
+                    wt.get_pairs<4>(XRegion(apart, kARanks * kAPart * 2), w4, ta, o8, lane < 32 ? 4 : 0);
+                    auto dv = [&](int i) {
+                        return __longlong_as_double((long long)(((uint64_t)__float_as_uint(o8[2 * i + 1]) << 32) |
+                                                                __float_as_uint(o8[2 * i])));
+                    };
+                    const double Ms = lane < 32 ? dv(0) : -1e300;
+                    double Mx = Ms;
+                    Mx = fmax(Mx, partner64<1>(Mx));
+                    Mx = fmax(Mx, partner64<2>(Mx));
+                    Mx = fmax(Mx, partner64<4>(Mx));
+                    Mx = fmax(Mx, partner64<8>(Mx));
+                    Mx = fmax(Mx, partner64<16>(Mx));                    // lanes 0-31: max over the ranks
+                    const double wgt = lane < 32 ? exp(Ms - Mx) : 0.0;
+                    double sd = wgt * (lane < 32 ? dv(1) : 0.0);
+                    double s0n = wgt * (lane < 32 ? dv(2) : 0.0), s1n = wgt * (lane < 32 ? dv(3) : 0.0);
+#define MQ_SPLIT_LEVEL(Mk)                                                                    \
+                    sd += partner64<Mk>(sd);                                                  \
+                    s0n += partner64<Mk>(s0n);                                                \
+                    s1n += partner64<Mk>(s1n);
+                    MQ_SPLIT_LEVEL(1) MQ_SPLIT_LEVEL(2) MQ_SPLIT_LEVEL(4) MQ_SPLIT_LEVEL(8) MQ_SPLIT_LEVEL(16)
+#undef MQ_SPLIT_LEVEL
+                    if (lane == 0) {
+                        const double rd = rcp_nr(sd);
+                        ll_put_xcd(&amrg[D0], __float_as_uint((float)(s0n * rd)), ta);
+                        ll_put_xcd(&amrg[D0 + 1], __float_as_uint((float)(s1n * rd)), ta);
+                    }
+                    // gather dims [64c, +64) of the 256 merged outputs (8 ranks' words)
+                    const uint32_t wg[1] = {(uint32_t)(64 * c + 2 * (lane >> 1))};
+                    float o2[2];
+                    wt.get_pairs<1>(XRegion(amrg, 2 * kAD), wg, ta, o2);
+                    ao = o2[lane & 1];
+                }
                 if (kDebug && r == 0 && l == last && a.dbg_attn) a.dbg_attn[2 * D * x + 64 * c + lane] = ao;
             }
             if (c == 0) trace(l, 3);
@@ -1159,7 +1242,13 @@ size_t decode_async_workspace_bytes(const DecodeShape& s) {
 
 bool decode_async_supports(const DecodeShape& s, bool int8, int cache_len) {
     return int8 && !s.fp8 && s.H == kAH && s.I == kAI && s.NQ == 16 && s.NKV == 8 && s.D == kAD &&
-           cache_len <= kAMaxLen;
+           cache_len <= kASplitLen;
+}
+
+// The cache_len from which this kernel splits attention over the 32 ranks of an XCD:
+// past kAMaxLen always; `attn_split_min` > 0 lowers that (0 = default, < 0 = only when required).
+int decode_async_split_min(int attn_split_min) {
+    return attn_split_min > 0 ? std::min(attn_split_min, kAMaxLen + 1) : kAMaxLen + 1;
 }
 
 int launch_decode_async(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
@@ -1181,6 +1270,6 @@ size_t decode_async_token_offset(const DecodeShape& s) {
     return alayout_for(xlayout_total(kAH, kAI)).tok;
 }
 
-int decode_async_max_len() { return kAMaxLen; }
+int decode_async_max_len() { return kASplitLen; }
 
 }  // namespace mq

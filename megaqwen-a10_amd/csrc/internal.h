@@ -70,6 +70,7 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
 // kernel does not cover these dims), and the longest cache it attends over.
 size_t decode_async_token_offset(const DecodeShape& s);
 int decode_async_max_len();
+int decode_async_split_min(int attn_split_min);
 // True when the workgroups of each residue class g mod 8 run on one XCD (checked once per device).
 bool xcd_placement_ok();
 

@@ -6,7 +6,8 @@ bench_int8.py:218, a10_decode.py:358-393). Gates: the config-1 fixture's 32
 greedy tokens from one launch; one launch and one launch per step agreeing
 bitwise (tokens and KV caches), greedy and sampled; sampled tokens against the
 float64 oracle's Gumbel-max choice wherever its top-2 margin exceeds fp32
-logit error; the fallback beyond the async-wave kernel's 64 positions;
+logit error; a launch past one workgroup's 64-position slot (split attention);
+the fallback beyond the async-wave kernel's 2048 positions;
 argument validation; a forced in-kernel wait expiry that leaves the decoder
 where it started; a P-token prefill in one launch (P = 8 and 64) whose whole KV
 cache and first generated token match the oracle's per-token prefill
@@ -100,12 +101,33 @@ def test_sampled_tokens_match_oracle(small):
     assert len(set(toks)) > 1
 
 
-def test_beyond_kernel_range_falls_back(mq, dev, small):
-    """Past 64 positions generate() loops over single steps (the XCD-aware kernel) and gives
-    the per-step tokens."""
+def test_one_launch_past_one_slot(mq, dev, small):
+    """Past the 64 positions of one workgroup's LDS slot the launch splits attention over the
+    32 workgroups of an XCD: 8 prompt + 112 generated steps in one launch equal one launch
+    per step, tokens and KV caches."""
     dec0, d, prompt, cfg, keep = small
     embed, layers, scales, lm_q, lm_s, fnorm, _, _ = keep
-    S = 96
+    S = 128
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+    n = S - len(prompt) + 1
+    got = dec._generate_one_launch(prompt, n)
+    assert got is not None
+    k1, v1 = _caches(dec)
+    want = _greedy(dec, prompt, n)
+    k2, v2 = _caches(dec)
+    assert got == want
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    del dec
+    torch.cuda.empty_cache()
+
+
+def test_beyond_kernel_range_falls_back(mq, dev, small):
+    """Past the async-wave kernel's 2048 positions generate() loops over single steps (the
+    XCD-aware kernel) and gives the per-step tokens."""
+    dec0, d, prompt, cfg, keep = small
+    embed, layers, scales, lm_q, lm_s, fnorm, _, _ = keep
+    S = 2048 + 16
     cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
     dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
     n = S - len(prompt) + 1

@@ -8,7 +8,9 @@ The checks: tokens identical to the committed fixture with the split forced at
 every length (empty slices included), attention outputs of the split and the
 unsplit paths within 1e-6 relative L2 of each other, and, after a seeded N(0,1) bf16 KV
 pre-fill to depths past the unsplit limit of 1024, greedy tokens identical to
-the float64 oracle started from the same cache.
+the float64 oracle started from the same cache. The async-wave kernel splits
+the same way from 65 positions (slices of at most 64, held in its LDS slot) up to
+2048: the same fixture, split-vs-unsplit and oracle checks run on it.
 """
 from __future__ import annotations
 
@@ -25,6 +27,13 @@ pytestmark = pytest.mark.gpu
 @pytest.fixture
 def xcd(mq):
     mq.set_decode_variant("xcd")
+    yield
+    mq.set_decode_variant("auto")
+
+
+@pytest.fixture
+def asyncv(mq):
+    mq.set_decode_variant("async")
     yield
     mq.set_decode_variant("auto")
 
@@ -216,3 +225,43 @@ def test_length_limits(mq, dev):
         mq.set_decode_variant("auto")
     with pytest.raises(ValueError):
         dec.prefill_random_kv(1116)
+
+
+# ---- the async-wave kernel's split attention (32 slices of <= 64 positions) -------------------
+@pytest.mark.parametrize("split_min", [1, 5, 17])
+def test_async_split_tokens_match_fixture(asyncv, small, split_min):
+    """The split forced from cache_len 1 / 5 / 17: the 32-token fixture (empty slices included)."""
+    dec, d, prompt, cfg, _ = small
+    dec.set_attn_split(split_min)
+    try:
+        print(f"async: small_int8 32 steps, split from {split_min}", flush=True)
+        assert _greedy(dec, prompt, 32) == d["tokens"]
+    finally:
+        dec.set_attn_split(0)
+
+
+def test_async_split_attention_matches_unsplit(asyncv, small):
+    dec, d, prompt, cfg, _ = small
+    dec.enable_debug()
+    outs = []
+    try:
+        for split_min in (-1, 1):
+            dec.set_attn_split(split_min)
+            toks = _greedy(dec, prompt, 20)
+            outs.append((toks, dec.get_attn_out().clone()))
+    finally:
+        dec.set_attn_split(0)
+        dec.enable_debug(False)
+    (ta, aa), (tb, ab) = outs
+    assert ta == tb
+    e = float(torch.linalg.norm((aa - ab).double()) / torch.linalg.norm(aa.double()))
+    print(f"async split vs unsplit attention: rel L2 {e:.2e}, identical {float((aa == ab).double().mean()):.3f}")
+    assert e < 1e-6, e
+
+
+@pytest.mark.parametrize("depth", [100, 1000, 2040])
+def test_async_long_context_matches_oracle(asyncv, mq, dev, depth):
+    """Past the 64 positions of one workgroup's slot: 6 greedy steps after a seeded N(0,1) KV
+    pre-fill, against the oracle started from the same cache (the last step at cache_len 2046)."""
+    print(f"async long context depth {depth}", flush=True)
+    _check_long(mq, dev, *_long_case(mq, dev, depth), depth, 0)
