@@ -164,7 +164,7 @@ typedef struct mq_decode_args {
  * verify_correctness_a10.py:323-339) and args->output_token_id the last one.
  * args->input_token_id must equal prompt_tokens[0] and cache_len position + 1.
  * Runs on the async-wave kernel: INT8 Qwen3-0.6B layer shapes and
- * position + n_forced + n_generate - 1 <= 64; otherwise MQ_ERR_UNSUPPORTED
+ * position + n_forced + n_generate - 1 <= 2048; otherwise MQ_ERR_UNSUPPORTED
  * (nothing launched), and a loop over mq_int8_decode_step gives the same
  * tokens, sampled ones included. */
 typedef struct mq_generate_args {
@@ -290,7 +290,7 @@ int mq_int8_decode_batch_step(const mq_batch_args* args, hipStream_t stream);
  * 64 cached positions, otherwise the XCD-aware kernel, when the workgroups of
  * each residue class g mod 8 share one XCD and the 8 classes cover the 8 XCDs,
  * checked once per device), 1 = single-level exchange kernel, 2 = XCD-aware,
- * 3 = async-wave (INT8 Qwen3-0.6B shape, cache_len <= 64 only). */
+ * 3 = async-wave (INT8 Qwen3-0.6B shape, cache_len <= 2048 only). */
 int mq_decode_set_variant(int variant);
 /* The variant a short-context step (cache_len 1) with these dims would use now
  * (1, 2 or 3), or -status. */

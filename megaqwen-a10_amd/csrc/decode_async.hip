@@ -1,5 +1,5 @@
 // Asynchronous-wave persistent decode step: the INT8 Qwen3-0.6B shape (hidden
-// 1024, intermediate 3072, 16 / 8 heads of 128) up to 64 cached positions.
+// 1024, intermediate 3072, 16 / 8 heads of 128) up to 2048 cached positions.
 //
 // Same computation (a10_int8_decode_kernel.cu:21-815) and the same work split
 // over workgroups as decode_xcd.hip: workgroup g runs on XCD x = HW_REG_XCC_ID
@@ -16,26 +16,33 @@
 //    batch would wait for the whole batch) and never meet at an s_barrier:
 //    they synchronise through LDS counters, and a sum over the four waves is
 //    finished by whichever arrives last.
-//  * Waves 4-7 (loader waves) copy each layer's weights, scales, norm gains and
-//    cached K/V rows straight into LDS (global_load_lds), a slot as soon as the
-//    compute waves are done with the previous layer's contents of it, and raise
-//    that slot's ready counter once their copies have landed.
+//  * Waves 4-7 (loader waves) load each layer's weights, scales, norm gains and
+//    cached K/V rows into registers while the compute waves run the previous
+//    layer's attention, write each slot into LDS as soon as the compute waves are
+//    done with the previous layer's contents of it, and raise that slot's ready
+//    counter.
 //  * The products run on the int8 matrix cores (v_mfma_i32_16x16x64_i8). A
 //    compute wave writes its slice of the activation vector as a 55-bit fixed
 //    point number (scale from the slice's largest exponent) in eight 7-bit
 //    digits, the top one signed; the digit sums are exact integers, recombined
 //    in fp64, so every stored value is the correctly rounded value of the
 //    reference's expression, as in the fp64 kernels.
-//  * Attention runs on the four compute waves: wave c takes query head c & 1
-//    over half c >> 1 of the positions (scores, softmax numerators and P V in
-//    fp64), and the halves are merged with their log-sum-exp weights.
+//  * Attention runs on the four compute waves: each takes both query heads over
+//    a block of consecutive positions (scores, softmax numerators and P V in
+//    fp64), and the blocks are merged with their log-sum-exp weights. Up to 64
+//    cached positions every workgroup attends over all of them from its LDS
+//    slot; past that (to 2048) rank r takes slice r of 32 (<= 64 positions, in
+//    its slot), publishes its fp64 partial (max, denominator, numerators) as
+//    tagged XCD-local words, merges output dims [8r, +8) over the 32 partials,
+//    and the merged 256 outputs come back through one more XCD-local exchange.
 //
 // Per layer, compute wave c:
 //   A  hidden slice [256c, +256) (polled) and the sum of squares from the 32
 //      partial sums the hidden rows' producers published; RMSNorm, digits, 4
 //      MFMA steps over the rank's 16 q|k|v rows       -> last arriver: XCD-local words
-//   B  attention of head c & 1 over half c >> 1 of the positions; the four
+//   B  attention of both heads over the wave's block of positions; the four
 //      waves meet in LDS, and wave c merges attention dims [64c, +64)
+//      (with split attention: the rank's partial, the 32-rank merge, the gather)
 //   C  those dims x O rows [32r, +32), 2 MFMAs         -> last arriver: cross-XCD packed partials
 //   D  wave 0: the 8-XCD sum of its 32 rows, scale, residual
 //                                                      -> XCD-local act words + sum of squares
@@ -441,7 +448,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     }
     __syncthreads();
 
-    // Steps: step s decodes at position a.pos + s (cache_len = position + 1 <= kAMaxLen,
+    // Steps: step s decodes at position a.pos + s (cache_len = position + 1 <= kASplitLen,
     // checked by the host); its input token is a.step_tokens[s] for the first n_forced
     // steps (a.token when there is no list) and the previous step's output after them.
     // The LDS counters count layers over the whole launch (gl = s L + l).

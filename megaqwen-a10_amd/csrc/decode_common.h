@@ -266,7 +266,8 @@ __device__ __forceinline__ double rms_scale(double sumsq, int n, double eps) {
 // checked once per (kernel, device) with the occupancy calculator.
 int check_residency(const void* fn, int threads = kThreads);
 
-// Async-wave kernel (decode_async.hip): INT8 Qwen3-0.6B shape, cache_len <= 64.
+// Async-wave kernel (decode_async.hip): INT8 Qwen3-0.6B shape, cache_len <= 2048 (split
+// attention past 64).
 size_t decode_async_workspace_bytes(const DecodeShape& s);
 bool decode_async_supports(const DecodeShape& s, bool int8, int cache_len);
 int launch_decode_async(const KArgs& k, bool debug, hipStream_t stream, hipEvent_t t0, hipEvent_t t1);

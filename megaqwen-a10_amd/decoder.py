@@ -41,7 +41,7 @@ VARIANTS = {"auto": 0, "flat": 1, "xcd": 2, "async": 3}
 def set_decode_variant(name: str) -> None:
     """Select the decode kernel for all following steps in this process:
     ``"auto"`` (default: the async-wave kernel for INT8 Qwen3-0.6B-shape steps
-    up to 64 cached positions, else the XCD-aware kernel when the workgroups of
+    up to 2048 cached positions, else the XCD-aware kernel when the workgroups of
     each residue class g mod 8 share one XCD, checked once per device),
     ``"flat"`` (single-level exchanges), ``"xcd"`` or ``"async"``."""
     lib = _lib.load()
@@ -357,7 +357,7 @@ class _DecoderBase:
         """Feed ``prompt_ids`` from the current position and return ``n_tokens`` generated
         tokens, the first being the last prompt step's output (verify_correctness_a10.py:
         323-339). The tokens follow ``set_sampling``. Within the async-wave kernel's range
-        (INT8, hidden 1024, up to 64 positions) every step runs in ONE launch and hands its
+        (INT8, hidden 1024, up to 2048 positions) every step runs in ONE launch and hands its
         token to the next on the device (mq_int8_decode_generate); otherwise, or with
         ``device_loop=False``, one launch per step. Both give the same tokens. A failed
         launch leaves the decoder at the position it started from."""

@@ -69,7 +69,7 @@ def _use_variant(mq, name):
 @pytest.fixture(params=["xcd", "async"])
 def variant(request, mq, dev):
     """Runs a test once per decode kernel the library selects on MI355X (XCD-aware /
-    async-wave; the async-wave kernel covers the INT8 Qwen3-0.6B shape up to 64 cached
+    async-wave; the async-wave kernel covers the INT8 Qwen3-0.6B shape up to 2048 cached
     positions). The single-level fallback has its own fixture test below."""
     yield from _use_variant(mq, request.param)
 
