@@ -432,6 +432,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
     for (int l = 0; l < a.L; ++l) {
         const int tid = opaque(tid_all);
         const int lane = tid % kWave;
+        // the wave index too is rederived per layer: held through the loop, the addresses
+        // derived from it were spilled to scratch, and a reload in stage B (its line evicted
+        // from L2 by the layer's weight stream) waited about 2 us for memory
+        const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
         const LayerWeights& lw = s_lw[l];
         const ScalePointers& sp = s_sp[l];
         const uint32_t pb = pbit(l);

@@ -292,6 +292,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         const ScalePointers& sp = s_sp[l];
         const int tid = opaque(tid_all);
         const int lane = tid % kWave;
+        // the wave index too is rederived per layer: held through the loop, the addresses
+        // derived from it were spilled to scratch, and each reload (its line evicted from L2
+        // by the layer's weight stream) waited for memory
+        const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
         // bf16: stage B's QK-norm gains, at the start of stage A (no exchange poll before
         // their use, so the loads overlap stage A's work)
         if constexpr (kLateInputs) load_gains(lw);
