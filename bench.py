@@ -452,11 +452,19 @@ def run_formats(args, mq, torch):
 
 
 def run_positions(args, mq, torch):
-    """bf16 weights, tok/s at positions 1, 25, 50, 100, 200 (n / wall(reset + n steps))."""
+    """bf16 weights, tok/s at positions 1, 25, 50, 100, 200.
+
+    Two rates per position: the reference's definition n / wall(reset + n steps of token 0)
+    (bench_and_plot_int8.py:78-85, best of 3), and the marginal rate of 8 steps starting at that
+    position (wall with one token read-back per step, and each step's kernel time from HIP events).
+    The line also decodes the 8-token seed-0 prompt and 32 greedy tokens and compares them with the
+    bf16 float64-oracle fixture."""
     dev = torch.device("cuda:0")
     cfg = mq.QWEN3_0_6B
     state, prompt = mq.random_init_state(cfg, seed=args.seed)
-    S = PROMPT_LEN + 208
+    positions = (1, 25, 50, 100, 200)
+    marg = 8
+    S = PROMPT_LEN + max(positions) + marg + 8
     cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
     embed, layers, fnorm, lm = mq.pack_bf16(state, cfg, dev)
     del state
@@ -464,7 +472,7 @@ def run_positions(args, mq, torch):
     for _ in range(5):
         dec.decode_step(0)
     res = {}
-    for n in (1, 25, 50, 100, 200):
+    for n in positions:
         best = None
         for _ in range(3):
             torch.cuda.synchronize()
@@ -476,11 +484,45 @@ def run_positions(args, mq, torch):
             dt = time.perf_counter() - t0
             best = dt if best is None else min(best, dt)
         res[str(n)] = round(n / best, 1)
+    # marginal rate: steps at positions p .. p + 7 (cache_len p + 1 ..), token 0 as above
+    events = _events(torch, marg)
+    marginal = {}
+    for p0 in positions:
+        dec.reset()
+        for _ in range(p0):
+            dec.decode_step(0)
+        pos_state = dec.position()
+        _, wall, _ = _timed_pass(torch, dec, 0, marg, dec.wait_token)
+        dec.reset()
+        for _ in range(p0):
+            dec.decode_step(0)
+        _, _, kern_ms = _timed_pass(torch, dec, 0, marg, dec.wait_token, events)
+        kern_s = sum(kern_ms) / 1e3
+        nbytes = sum(cfg.bf16_step_bytes(cache_len=pos_state + i + 1) for i in range(marg))
+        marginal[str(p0)] = {"tok_s": round(marg / wall, 1), "kernel_avg_us": round(kern_s / marg * 1e6, 2),
+                             "hbm_frac": round(nbytes / kern_s / 1e9 / HBM_PEAK_GBS, 4)}
+    parity = None
+    fx = ROOT / "tests" / "golden" / "tokens_qwen3_0.6b_bf16.json"
+    if fx.exists() and args.seed == 0:
+        want = json.loads(fx.read_text())["tokens"]
+        dec.reset()
+        tok = None
+        for t in prompt.tolist():
+            tok = dec.decode_step(int(t))
+        got = [tok]
+        while len(got) < len(want):
+            got.append(dec.decode_step(got[-1]))
+        parity = {"fixture": fx.name, "checked": len(want), "match": got == want}
     return {"metric": "BF16 decode tok/s at positions (BASELINE config 3)", "value": res["200"], "unit": "tok/s",
             "n_gpus": 1, "steps": 200, "warmup": 5, "ms_per_step": round(1e3 / res["200"], 4),
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f64", "data": "synthetic",
             "config": {"workload": "config 3: bf16 weights, n / wall(reset + n decode_step(0)) (bench_and_plot_int8.py:78-85)",
-                       "tok_s_at_position": res}}
+                       "kernel": "mq::decode_xcd_kernel<1024, 3072, mq::Bf16W, false>",
+                       "tok_s_at_position": res,
+                       "marginal_at_position": marginal,
+                       "marginal_method": f"{marg} steps from the position; tok/s from wall with one read-back per step; "
+                                          + KERNEL_TIMING},
+            "parity": parity}
 
 
 def run_longctx(args, mq, torch):
