@@ -131,6 +131,7 @@ struct __align__(16) AsyncLds {
     __align__(16) float hs[kAH];                         // the layer's input (bf16 values): stage D's residual
     double part[4][kCW][32];               // per-wave row partials of the combines A, C, E, F
     uint32_t sync[16];
+    uint32_t noshift;                      // slot B: 1 when this layer's softmax needs no maximum (see the KV loader)
     // tail
     __align__(16) float4 xs[kAH / 4];                    // final normalized vector, per-lane layout
     double fss;                            // final sum of squares
@@ -599,6 +600,22 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 // step's last attention is done)
                 const uint32_t cw = l == 0 ? ld32(a.cos_t + (int64_t)pos * D + 2 * ln) : 0u;
                 const uint32_t sw = l == 0 ? ld32(a.sin_t + (int64_t)pos * D + 2 * ln) : 0u;
+                // Softmax without its running maximum. A query or key after the QK RMSNorm has
+                // norm <= sqrt(D) max|g| (the normalised vector's squares sum to at most D), RoPE
+                // with bf16 cos / sin scales a rotation pair by at most 1 + 2^-8, and the fp32
+                // (q) and bf16 (k) roundings add at most 2^-8; so every score of this layer is at
+                // most b = |attn_scale| D max|g_q| max|g_k| 1.02 in magnitude, for every key this
+                // kernel wrote. With b <= 64 (and keys written elsewhere within 10x that norm)
+                // e^s stays far inside fp64's range: the numerators are e^s itself, and the
+                // waves' and ranks' partials add without rescaling by their maxima. Otherwise
+                // (or for NaN gains) the compute waves subtract the maximum as usual.
+                const uint32_t gq = wave_max_u32(max(qn & 0x7fffu, (qn >> 16) & 0x7fffu));
+                const uint32_t gk = wave_max_u32(max(kn & 0x7fffu, (kn >> 16) & 0x7fffu));
+                // (the scale read from the kernel-argument segment here: a product of it held
+                // through the layer loop was spilled)
+                const double bound = fabs((double)kargs()->attn_scale) * D * (double)bf16_bits_to_f32(gq) *
+                                     (double)bf16_bits_to_f32(gk) * 1.02;
+                const uint32_t noshift = bound <= 64.0 ? 1u : 0u;
                 await_free(SL_B, gl);
                 const int ls = opaque(ln);
 #pragma unroll
@@ -611,6 +628,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 }
                 put32(S.qkn[0], ls, qn);
                 put32(S.qkn[1], ls, kn);
+                if (ls == 0) S.noshift = noshift;
                 if (l == 0) {
                     put32(S.rope[0], ls, cw);
                     put32(S.rope[1], ls, sw);
@@ -711,6 +729,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                         __hip_atomic_store(&S.sync[kWindow], (uint32_t)(gl + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
                 lds_wait(&S.sync[kReady + SL_B], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
+                // read before slot B is released (the loader then overwrites it)
+                const bool noshift = __builtin_amdgcn_readfirstlane(S.noshift) != 0u;
                 // QK-norm and RoPE: out[i] = y[i] cos[i] - y[i+64] sin[i],
                 // out[i+64] = y[i] sin[i+64] + y[i+64] cos[i+64] (i = lane)
                 const double cl = bf16_bits_to_f32(S.rope[0][lane]), ch = bf16_bits_to_f32(S.rope[0][lane + 64]);
@@ -815,12 +835,16 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     const int pe = 2 * ((lane >> 5) & 1) + ((lane >> 4) & 1);
                     const bool valid = 4 * pe + jj < np;
                     const double sc = valid ? E[0] * (double)a.attn_scale : -INFINITY;
-                    // max and numerator sum over the lanes of the same head (bits 0, 1, 4, 5)
-                    double m = sc;
-                    m = fmax(m, partner64<1>(m));
-                    m = fmax(m, partner64<2>(m));
-                    m = fmax(m, xmax16(m));
-                    m = fmax(m, xmax32(m));
+                    // max (unless the layer's scores need no shift) and numerator sum over the
+                    // lanes of the same head (bits 0, 1, 4, 5)
+                    double m = 0.0;
+                    if (!noshift) {
+                        m = sc;
+                        m = fmax(m, partner64<1>(m));
+                        m = fmax(m, partner64<2>(m));
+                        m = fmax(m, xmax16(m));
+                        m = fmax(m, xmax32(m));
+                    }
                     const double pv = valid ? exp(sc - m) : 0.0;
                     double ls = pv + partner64<1>(pv);
                     ls += partner64<2>(ls);
@@ -869,12 +893,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 lds_wait(&S.sync[kArrive + AR_B], (uint32_t)(kCW * (gl + 1)), lds_limit, &hdr->abort_flag);
                 // merge: wave c takes attention dims [64c, +64) (head c / 2) from the four blocks;
                 // lane w < 4 computes block w's weight e^(m_w - M), the others read it
+                // (without the shift every block's numerators share the scale e^0: weight 1;
+                // an empty block adds zeros)
                 const int hh = c >> 1, dim = 64 * (c & 1) + lane;
-                double M = -INFINITY;
+                double M = 0.0, ew = 1.0;
+                if (!noshift) {
+                    M = -INFINITY;
 #pragma unroll
-                for (int w = 0; w < kCW; ++w) M = fmax(M, S.pml[w][hh][0]);
-                const double mine = S.pml[lane & 3][hh][0];
-                const double ew = mine == -INFINITY ? 0.0 : exp(mine - M);
+                    for (int w = 0; w < kCW; ++w) M = fmax(M, S.pml[w][hh][0]);
+                    const double mine = S.pml[lane & 3][hh][0];
+                    ew = mine == -INFINITY ? 0.0 : exp(mine - M);
+                }
                 double num = 0.0, den = 0.0;
 #pragma unroll
                 for (int w = 0; w < kCW; ++w) {
@@ -910,14 +939,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                         return __longlong_as_double((long long)(((uint64_t)__float_as_uint(o8[2 * i + 1]) << 32) |
                                                                 __float_as_uint(o8[2 * i])));
                     };
-                    const double Ms = lane < 32 ? dv(0) : -1e300;
-                    double Mx = Ms;
-                    Mx = fmax(Mx, partner64<1>(Mx));
-                    Mx = fmax(Mx, partner64<2>(Mx));
-                    Mx = fmax(Mx, partner64<4>(Mx));
-                    Mx = fmax(Mx, partner64<8>(Mx));
-                    Mx = fmax(Mx, partner64<16>(Mx));                    // lanes 0-31: max over the ranks
-                    const double wgt = lane < 32 ? exp(Ms - Mx) : 0.0;
+                    double wgt = lane < 32 ? 1.0 : 0.0;                  // no shift: every slice at e^0
+                    if (!noshift) {
+                        const double Ms = lane < 32 ? dv(0) : -1e300;
+                        double Mx = Ms;
+                        Mx = fmax(Mx, partner64<1>(Mx));
+                        Mx = fmax(Mx, partner64<2>(Mx));
+                        Mx = fmax(Mx, partner64<4>(Mx));
+                        Mx = fmax(Mx, partner64<8>(Mx));
+                        Mx = fmax(Mx, partner64<16>(Mx));                // lanes 0-31: max over the ranks
+                        wgt = lane < 32 ? exp(Ms - Mx) : 0.0;
+                    }
                     double sd = wgt * (lane < 32 ? dv(1) : 0.0);
                     double s0n = wgt * (lane < 32 ? dv(2) : 0.0), s1n = wgt * (lane < 32 ? dv(3) : 0.0);
 #define MQ_SPLIT_LEVEL(Mk)                                                                    \
