@@ -515,8 +515,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
             issue_fence();
             if (loader) {
                 const int ln = opaque(lane);    // per-lane offsets are recomputed, not held across layers
-                attn_slice_k<4>(at, a.kc + cache_base, 0, apos, ln, wave - 4);
-                attn_slice_v_lds<kSliceB, 4>(vsl, a.vc + cache_base, 0, apos, ln, wave - 4);
+                // (from layer 1 on, the K and V rows were loaded at the end of the previous
+                // layer's stage F)
+                if (l == 0) {
+                    attn_slice_k<4>(at, a.kc + cache_base, 0, apos, ln, wave - 4);
+                    attn_slice_v_lds<kSliceB, 4>(vsl, a.vc + cache_base, 0, apos, ln, wave - 4);
+                }
             }
             {
                 // this sequence's 512 q|k|v rows straight from stage A's partials: thread t sums
@@ -809,6 +813,19 @@ __global__ void __launch_bounds__(kThreads, 1) decode_batch_kernel(BArgs a) {
                 load_a(l + 1);
                 prefetch_attn(l + 1);
                 issue_fence();
+                if (sliced) {
+                    // a short sequence's K and V rows of the next layer, straight into LDS (its
+                    // stage B waits for them): at.kst overlays this stage's pair partials, so
+                    // every wave's reads of them come first; vsl is stage B's alone, and stages
+                    // G and A do not touch at.kst
+                    __syncthreads();
+                    if (__builtin_amdgcn_readfirstlane(wave) >= 4) {
+                        const int ln = opaque(lane);
+                        const int64_t nb = (int64_t)r * seq_stride + ((int64_t)(l + 1) * 8 + x) * head_stride;
+                        attn_slice_k<4>(at, a.kc + nb, 0, apos, ln, wave - 4);
+                        attn_slice_v_lds<kSliceB, 4>(vsl, a.vc + nb, 0, apos, ln, wave - 4);
+                    }
+                }
             }
         }
 
