@@ -218,6 +218,8 @@ class _DecoderBase:
         a.workspace_bytes = ws_bytes
         a.spin_limit = 0
         self._args = a
+        self._args_ref = ctypes.byref(a)
+        self._tok_base = self.output_token.data_ptr()
         self._step_fn = (self._lib.mq_fp8_decode_step if self._fp8 else
                          self._lib.mq_int8_decode_step if self._int8 else self._lib.mq_bf16_decode_step)
         self._debug = False
@@ -232,23 +234,26 @@ class _DecoderBase:
         """Enqueue one decode step on the current stream without waiting for the token.
         Several steps may be launched before ``wait_token`` (for example a prefill whose
         tokens are not needed); ``wait_token`` then returns the last one's token."""
-        V = self.dims[2]
-        if not isinstance(input_token_id, int) or not 0 <= input_token_id < V:
-            raise ValueError(f"input_token_id {input_token_id!r} outside [0, {V})")
-        if self._pos >= self.max_seq_len:
-            raise ValueError(f"KV cache full: position {self._pos} == max_seq_len {self.max_seq_len}")
+        # (kept lean: this is on every step's host path, between one kernel and the next)
+        if not isinstance(input_token_id, int) or not 0 <= input_token_id < self.dims[2]:
+            raise ValueError(f"input_token_id {input_token_id!r} outside [0, {self.dims[2]})")
+        pos = self._pos
+        if pos >= self.max_seq_len:
+            raise ValueError(f"KV cache full: position {pos} == max_seq_len {self.max_seq_len}")
         slot = self._next_slot
-        if any(sl == slot for sl, _ in self._inflight):
-            # TOKEN_SLOTS steps already in flight: let them finish before this word is reused
+        if len(self._inflight) >= TOKEN_SLOTS:
+            # every token word is held by a step in flight (slots are handed out in turn):
+            # let them finish before this one is reused
             torch.cuda.current_stream(self.device).synchronize()
         a = self._args
         a.input_token_id = input_token_id
-        a.position = self._pos
-        a.cache_len = self._pos + 1
-        a.output_token_id = self.output_token.data_ptr() + 4 * slot
+        a.position = pos
+        a.cache_len = pos + 1
+        a.output_token_id = self._tok_base + 4 * slot
         self._tok_host[slot] = TOKEN_PENDING
-        st = self._step_fn(ctypes.byref(a), ctypes.c_void_p(_lib.stream_handle(self.device)))
-        _lib.check(st, "decode step")
+        st = self._step_fn(self._args_ref, _lib.stream_handle(self.device))
+        if st:
+            _lib.check(st, "decode step")
         self._inflight.append((slot, self._pos))
         self._next_slot = (slot + 1) % TOKEN_SLOTS
         self._pos += 1
@@ -265,8 +270,7 @@ class _DecoderBase:
         if not self._inflight:
             raise RuntimeError("no decode step in flight (call launch_step first)")
         slot = self._inflight[-1][0]
-        word = self._tok_host[slot:].ctypes.data
-        if self._lib.mq_wait_host_token(word, TOKEN_PENDING, WAIT_US) != _lib.MQ_OK:
+        if self._lib.mq_wait_host_token(self._tok_base + 4 * slot, TOKEN_PENDING, WAIT_US) != _lib.MQ_OK:
             torch.cuda.current_stream(self.device).synchronize()
         tok = int(self._tok_host[slot])
         if tok < 0:
