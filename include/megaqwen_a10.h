@@ -287,7 +287,7 @@ int mq_int8_decode_batch_step(const mq_batch_args* args, hipStream_t stream);
 
 /* Kernel variant for all following steps in this process: 0 = automatic
  * (default: the async-wave kernel for INT8 steps of the Qwen3-0.6B shape up to
- * 64 cached positions, otherwise the XCD-aware kernel, when the workgroups of
+ * 2048 cached positions, otherwise the XCD-aware kernel, when the workgroups of
  * each residue class g mod 8 share one XCD and the 8 classes cover the 8 XCDs,
  * checked once per device), 1 = single-level exchange kernel, 2 = XCD-aware,
  * 3 = async-wave (INT8 Qwen3-0.6B shape, cache_len <= 2048 only). */
