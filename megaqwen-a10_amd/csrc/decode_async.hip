@@ -605,10 +605,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 // with bf16 cos / sin scales a rotation pair by at most 1 + 2^-8, and the fp32
                 // (q) and bf16 (k) roundings add at most 2^-8; so every score of this layer is at
                 // most b = |attn_scale| D max|g_q| max|g_k| 1.02 in magnitude, for every key this
-                // kernel wrote. With b <= 64 (and keys written elsewhere within 10x that norm)
-                // e^s stays far inside fp64's range: the numerators are e^s itself, and the
-                // waves' and ranks' partials add without rescaling by their maxima. Otherwise
-                // (or for NaN gains) the compute waves subtract the maximum as usual.
+                // kernel wrote. With b <= 64 the numerators are e^s itself and the waves' and
+                // ranks' partials add without rescaling by their maxima: no sum of up to 2048
+                // terms e^s |v| (|v| <= the bf16 maximum) leaves fp64's range while every score is
+                // within 600, which also covers keys written elsewhere with up to 9x that norm.
+                // Otherwise (or for NaN gains) the compute waves subtract the maximum as usual.
                 const uint32_t gq = wave_max_u32(max(qn & 0x7fffu, (qn >> 16) & 0x7fffu));
                 const uint32_t gk = wave_max_u32(max(kn & 0x7fffu, (kn >> 16) & 0x7fffu));
                 // (the scale read from the kernel-argument segment here: a product of it held
