@@ -169,10 +169,15 @@ def stream_handle(device=None) -> int:
     """The raw hipStream_t of torch's current stream on ``device`` (default: the current
     device). Read without building a torch Stream object: this sits on every decode step's
     host path, where ``torch.cuda.current_stream(device).cuda_stream`` costs about 2 us."""
+    if _raw_stream is None:                 # a torch without the raw accessor
+        return torch.cuda.current_stream(device).cuda_stream
     if device is None:
         idx = torch.cuda.current_device()
     elif isinstance(device, int):
         idx = device
     else:
         idx = device.index if device.index is not None else torch.cuda.current_device()
-    return torch._C._cuda_getCurrentRawStream(idx)
+    return _raw_stream(idx)
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
