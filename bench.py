@@ -53,7 +53,8 @@ MEASURED_TRAFFIC = {"mq::decode_async_kernel<false, false>": 641_659_290,
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=32)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default: 32; the BASELINE counts for longctx, 64, and batched, 128)")
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-steps", type=int, default=112,
@@ -72,7 +73,10 @@ def parse():
                     help="do not attach timing events to the decode launches (for runs under rocprofv3 "
                          "--kernel-trace, which supplies the kernel durations itself); roofline.achieved then "
                          "uses the wall time per step")
-    return ap.parse_args()
+    args = ap.parse_args()
+    if args.steps is None:
+        args.steps = {"longctx": 64, "batched": 128}.get(args.workload, 32)
+    return args
 
 
 def cpu_baseline(keep, cfg, prompt, steps):
