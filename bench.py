@@ -117,8 +117,9 @@ def _events(torch, n):
     return ev
 
 
-def _timed_pass(torch, dec, first, steps, wait, events=None):
-    """`steps` greedy steps from `first` through launch_step + wait: (tokens, wall s, kernel ms).
+def _timed_pass(torch, dec, first, steps, wait, events=None, step=None):
+    """`steps` greedy steps from `first` through launch_step + wait (or `step`, e.g. the
+    decoder's decode_step): (tokens, wall s, kernel ms).
 
     With `events` every dispatch records its own start/end pair (hipExtLaunchKernel on the
     launch stream), which costs about 20 us of host time per launch. So the pass that sets
@@ -130,8 +131,11 @@ def _timed_pass(torch, dec, first, steps, wait, events=None):
     for i in range(steps):
         if events is not None:
             dec.set_timing_events(events[0][i], events[1][i])
-        dec.launch_step(tok)
-        tok = wait()
+        if step is not None:
+            tok = step(tok)
+        else:
+            dec.launch_step(tok)
+            tok = wait()
         toks.append(tok)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -172,9 +176,9 @@ def run_decode(args, mq, torch):
         tok = dec.decode_step(tok)
     events = None if args.no_kernel_events else _events(torch, args.steps)
 
-    # timed region: K greedy steps through the drop-in API
+    # timed region: K greedy steps through the drop-in API (decode_step, as bench_int8.py:217-218)
     first = prefill()
-    toks, wall, _ = _timed_pass(torch, dec, first, args.steps, dec.wait_token)
+    toks, wall, _ = _timed_pass(torch, dec, first, args.steps, None, step=dec.decode_step)
     repeat_identical = None
     if args.no_kernel_events:
         kern_ms = [wall * 1e3 / args.steps] * args.steps
