@@ -608,9 +608,18 @@ struct Waiter {
     template <int N>
     __device__ __forceinline__ void get_pairs(const XRegion& R, const uint32_t (&w)[N], uint32_t tag,
                                               float (&out)[2 * N], int count = N) {
+        get_pairs(R, w, tag, out, count, [] {});
+    }
+    // The same; `meanwhile()` runs once the first loads are issued and before any of
+    // them is waited for (work that overlaps the memory round trip).
+    template <int N, class F>
+    __device__ __forceinline__ void get_pairs(const XRegion& R, const uint32_t (&w)[N], uint32_t tag,
+                                              float (&out)[2 * N], int count, F&& meanwhile) {
         uint4 c[N];
 #pragma unroll
         for (int i = 0; i < N; ++i) c[i] = i < count ? R.load2(w[i]) : make_uint4(0, tag, 0, tag);
+        asm volatile("" ::: "memory");
+        meanwhile();
         uint32_t pending = 0;
 #pragma unroll
         for (int i = 0; i < N; ++i)

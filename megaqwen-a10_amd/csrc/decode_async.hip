@@ -258,14 +258,16 @@ __device__ __forceinline__ double wave_sum64_u(double v) {
 }
 
 // ---- digits ---------------------------------------------------------------------------
+// Maximum over the wave, uniform: the 16-lane row maxima by DPP, then the four rows'
+// read out (a cross-row permlane level costs about twice a DPP level).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     v = max(v, __float_as_uint(partner<1>(__uint_as_float(v))));
     v = max(v, __float_as_uint(partner<2>(__uint_as_float(v))));
     v = max(v, __float_as_uint(partner<4>(__uint_as_float(v))));
     v = max(v, __float_as_uint(partner<8>(__uint_as_float(v))));
-    v = max(v, __float_as_uint(partner<16>(__uint_as_float(v))));
-    v = max(v, __float_as_uint(partner<32>(__uint_as_float(v))));
-    return v;
+    const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+    const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+    return max(max(a, b), max(c, d));
 }
 __device__ __forceinline__ uint32_t exp_field(float v) { return (__float_as_uint(v) >> 23) & 0xffu; }
 
@@ -320,14 +322,24 @@ __device__ __forceinline__ void put_digits1(uint32_t (*planes)[kPlane], float v,
     for (int p = 0; p < 8; ++p) reinterpret_cast<uint8_t*>(planes[p])[lane] = (uint8_t)(d[p] & 0xff);
 }
 // MFMA A operand of K step s: lane l holds digit plane l % 16 (zero past plane 7) at
-// elements [64 s + 16 (l / 16), +16).
+// elements [64 s + 16 (l / 16), +16). Every lane reads (lanes past plane 7 the same
+// words as lane l - 8, a broadcast) and the zero is a select, so that a stage's
+// operand reads carry no branch and issue together ahead of its MFMAs.
 __device__ __forceinline__ i32x4_t a_frag(const uint32_t (*planes)[kPlane], int s, int lane) {
     const int p = lane % 16;
-    if (p >= 8) return i32x4_t{0, 0, 0, 0};
-    const uint4 w = *reinterpret_cast<const uint4*>(&planes[p][16 * s + 4 * (lane / 16)]);
-    return i32x4_t{(int)w.x, (int)w.y, (int)w.z, (int)w.w};
+    const uint4 w = *reinterpret_cast<const uint4*>(&planes[p & 7][16 * s + 4 * (lane / 16)]);
+    const bool z = p >= 8;
+    return i32x4_t{z ? 0 : (int)w.x, z ? 0 : (int)w.y, z ? 0 : (int)w.z, z ? 0 : (int)w.w};
 }
 __device__ __forceinline__ i32x4_t b_frag(const uint4& w) { return i32x4_t{(int)w.x, (int)w.y, (int)w.z, (int)w.w}; }
+// The operands a stage's MFMAs read, all in registers at this point: their LDS reads
+// are then issued together and waited for once (left to itself the scheduler reuses
+// registers and waits for each MFMA's two reads in turn, one LDS round trip each).
+template <int N>
+__device__ __forceinline__ void operands_ready(i32x4_t (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
 __device__ __forceinline__ i32x4_t mfma_i8(i32x4_t a, i32x4_t b, i32x4_t c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
@@ -344,24 +356,24 @@ __device__ __forceinline__ double tile_value(i32x4_t c, uint32_t emax) {
 // One round of polls over an XCD's vector block (kVecWords words at `block`, one tag):
 // elements [256 slice + 4 lane, +4) into v, and the 32 fp64 partial sums of squares
 // (lanes < 32 one each), returned summed in a fixed order (the same value in every lane).
+// `meanwhile()` runs while the first round of loads is in flight.
+template <class F>
 __device__ __forceinline__ double poll_slice(Waiter& wt, const uint64_t* block, uint32_t tag, int slice, int lane,
-                                             float (&v)[4]) {
+                                             float (&v)[4], F&& meanwhile) {
     uint32_t w[3] = {2u * (uint32_t)(128 * slice + 2 * lane), 2u * (uint32_t)(128 * slice + 2 * lane) + 2u,
                      (uint32_t)kAH + 2u * (uint32_t)(lane & 31)};
     float o[6];
-    wt.get_pairs<3>(XRegion(block, kVecWords), w, tag, o, lane < 32 ? 3 : 2);
+    wt.get_pairs<3>(XRegion(block, kVecWords), w, tag, o, lane < 32 ? 3 : 2, meanwhile);
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = o[i];
     double s = lane < 32 ? __longlong_as_double((long long)(((uint64_t)__float_as_uint(o[5]) << 32) |
                                                             __float_as_uint(o[4])))
                          : 0.0;
-    s += partner64<1>(s);
-    s += partner64<2>(s);
-    s += partner64<4>(s);
-    s += partner64<8>(s);
-    s += partner64<16>(s);
-    s += partner64<32>(s);             // lanes 32-63 hold 0: every lane gets the total
-    return s;
+    // lanes 32-63 hold 0: the two 16-lane row sums of lanes 0-31 by DPP, then added from
+    // lanes 0 and 16 (the same value in every lane; a cross-row permlane level costs
+    // about twice a DPP level)
+    s = row_sum64(s);
+    return readlane64(s, 0) + readlane64(s, 16);
 }
 
 }  // namespace
@@ -644,6 +656,20 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         for (int l = 0; l < a.L; ++l) {
             const int gl = step * a.L + l;
             // ---------------- A: RMSNorm + QKV ----------------
+            // The loader slots of this layer are filled a layer ahead: A checks those of
+            // stages A-C and E (while its hidden-slice loads are in flight) and E the
+            // one of F, so that no later stage waits an LDS round trip for its slot.
+            auto slots_ready = [&](uint32_t mask) {
+                uint32_t v[kSlots];
+#pragma unroll
+                for (int k = 0; k < kSlots; ++k) v[k] = (mask & (1u << k)) ? lds_load(&S.sync[kReady + k]) : 0u;
+#pragma unroll
+                for (int k = 0; k < kSlots; ++k)
+                    if ((mask & (1u << k)) && v[k] < (uint32_t)(gl + 1))
+                        lds_wait(&S.sync[kReady + k], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
+                lds_order();
+            };
+            constexpr uint32_t kSlotsA = (1u << SL_A) | (1u << SL_B) | (1u << SL_C) | (1u << SL_E);
             float hv[4];
             double ssq;
             if (l == 0) {
@@ -663,13 +689,13 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     s = fma(hi, hi, s);
                 }
                 ssq = wave_sum64(s);
+                slots_ready(kSlotsA);
             } else {
-                ssq = poll_slice(wt, hidx, tag(l - 1, AS_HID), c, lane, hv);
+                ssq = poll_slice(wt, hidx, tag(l - 1, AS_HID), c, lane, hv, [&] { slots_ready(kSlotsA); });
             }
             *reinterpret_cast<float4*>(&S.hs[256 * c + 4 * lane]) = make_float4(hv[0], hv[1], hv[2], hv[3]);
             trace(l, 0);
             const double rstd = rms_scale(ssq, H, kEps);
-            lds_wait(&S.sync[kReady + SL_A], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
             float nv[4];
             {
                 const uint2 gw = *reinterpret_cast<const uint2*>(&S.lnA[256 * c + 4 * lane]);
@@ -683,9 +709,16 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 em = wave_max_u32(em);
                 put_digits4(S.dig[c], nv, em, lane);
                 lds_order();
+                i32x4_t op[8];
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    op[2 * s] = a_frag(S.dig[c], s, lane);
+                    op[2 * s + 1] = b_frag(S.wA[c][s][lane]);
+                }
+                operands_ready(op);
                 i32x4_t acc = {0, 0, 0, 0};
 #pragma unroll
-                for (int s = 0; s < 4; ++s) acc = mfma_i8(a_frag(S.dig[c], s, lane), b_frag(S.wA[c][s][lane]), acc);
+                for (int s = 0; s < 4; ++s) acc = mfma_i8(op[2 * s], op[2 * s + 1], acc);
                 const double v = tile_value(acc, em);
                 if (lane < 16) S.part[0][c][lane] = v;
             }
@@ -729,7 +762,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     if (lane == 0)
                         __hip_atomic_store(&S.sync[kWindow], (uint32_t)(gl + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
-                lds_wait(&S.sync[kReady + SL_B], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
                 // read before slot B is released (the loader then overwrites it)
                 const bool noshift = __builtin_amdgcn_readfirstlane(S.noshift) != 0u;
                 // QK-norm and RoPE: out[i] = y[i] cos[i] - y[i+64] sin[i],
@@ -975,7 +1007,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
             if (c == 0) trace(l, 3);
 
             // ---------------- C: O partial over this XCD's attention dims ----------------
-            lds_wait(&S.sync[kReady + SL_C], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
             {
                 const uint32_t em = wave_max_u32(exp_field(ao));
                 put_digits1(S.dig[c], ao, em, lane);
@@ -1023,9 +1054,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
             // ---------------- E: RMSNorm + gate/up + SwiGLU ----------------
             {
                 float av[4];
-                const double ss = poll_slice(wt, actx, tag(l, AS_ACT), c, lane, av);
+                const double ss = poll_slice(wt, actx, tag(l, AS_ACT), c, lane, av,
+                                             [&] { slots_ready(1u << SL_F); });
                 const double rstd2 = rms_scale(ss, H, kEps);
-                lds_wait(&S.sync[kReady + SL_E], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
                 const uint2 gw = *reinterpret_cast<const uint2*>(&S.lnE[256 * c + 4 * lane]);
                 const float gl[4] = {bf16_bits_to_f32(gw.x & 0xffffu), bf16_bits_to_f32(gw.x >> 16),
                                      bf16_bits_to_f32(gw.y & 0xffffu), bf16_bits_to_f32(gw.y >> 16)};
@@ -1043,12 +1074,19 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 em = wave_max_u32(em);
                 put_digits4(S.dig[c], nv2, em, lane);
                 lds_order();
+                i32x4_t op[12];
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    op[3 * s] = a_frag(S.dig[c], s, lane);
+                    op[3 * s + 1] = b_frag(S.wE[c][s][0][lane]);
+                    op[3 * s + 2] = b_frag(S.wE[c][s][1][lane]);
+                }
+                operands_ready(op);
                 i32x4_t t0 = {0, 0, 0, 0}, t1 = {0, 0, 0, 0};
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
-                    const i32x4_t af = a_frag(S.dig[c], s, lane);
-                    t0 = mfma_i8(af, b_frag(S.wE[c][s][0][lane]), t0);
-                    t1 = mfma_i8(af, b_frag(S.wE[c][s][1][lane]), t1);
+                    t0 = mfma_i8(op[3 * s], op[3 * s + 1], t0);
+                    t1 = mfma_i8(op[3 * s], op[3 * s + 2], t1);
                 }
                 const double v0 = tile_value(t0, em), v1 = tile_value(t1, em);
                 if (lane < 16) { S.part[2][c][lane] = v0; S.part[2][c][16 + lane] = v1; }
@@ -1072,16 +1110,22 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 uint32_t w[1] = {2u * (uint32_t)(64 * c + lane)};
                 wt.get_pairs<1>(XRegion(mlpx, kAIX), w, tag(l, AS_MLP), mv);
                 if (c == 0) trace(l, 7);
-                lds_wait(&S.sync[kReady + SL_F], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
                 const uint32_t em = wave_max_u32(max(exp_field(mv[0]), exp_field(mv[1])));
                 put_digits2(S.dig[c], mv, em, lane);
                 lds_order();
+                i32x4_t op[6];
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    op[3 * s] = a_frag(S.dig[c], s, lane);
+                    op[3 * s + 1] = b_frag(S.wF[c][s][0][lane]);
+                    op[3 * s + 2] = b_frag(S.wF[c][s][1][lane]);
+                }
+                operands_ready(op);
                 i32x4_t t0 = {0, 0, 0, 0}, t1 = {0, 0, 0, 0};
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
-                    const i32x4_t af = a_frag(S.dig[c], s, lane);
-                    t0 = mfma_i8(af, b_frag(S.wF[c][s][0][lane]), t0);
-                    t1 = mfma_i8(af, b_frag(S.wF[c][s][1][lane]), t1);
+                    t0 = mfma_i8(op[3 * s], op[3 * s + 1], t0);
+                    t1 = mfma_i8(op[3 * s], op[3 * s + 2], t1);
                 }
                 const double v0 = tile_value(t0, em), v1 = tile_value(t1, em);
                 if (lane < 16) { S.part[3][c][lane] = v0; S.part[3][c][16 + lane] = v1; }
@@ -1123,7 +1167,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         // the final hidden vector and its sum of squares
         {
             float hv[4];
-            const double ssq = poll_slice(wt, hidx, tag(last, AS_HID), c, lane, hv);
+            const double ssq = poll_slice(wt, hidx, tag(last, AS_HID), c, lane, hv, [] {});
             *reinterpret_cast<float4*>(&S.hs[256 * c + 4 * lane]) = make_float4(hv[0], hv[1], hv[2], hv[3]);
             if (c == 0 && lane == 0) S.fss = ssq;
             if (kDebug && g == 0 && a.dbg_hidden) {
