@@ -583,9 +583,9 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 if (lane < 24) put32(S.scE, lane, scv);
                 raise(SL_E, gl);
             } else {
-                // K and V rows keep their 16-byte chunks XOR-permuted by row (chunk g of row j
-                // at g ^ (j % 16)), so that lanes reading the same chunk of different rows hit
-                // different banks
+                // K rows keep their 16-byte chunks XOR-permuted by row (chunk g of row j at
+                // g ^ (j % 16)), so that lanes reading the same chunk of different rows hit
+                // different banks; V rows are read whole by every lane and stay in order
                 // (the lane is rederived per layer, so that its row addresses are not held
                 // through the layer loop alongside the 128 registers of rows)
                 // Slot row jl holds position s0 + jl of this rank's positions (all of them, or
@@ -636,7 +636,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     const int jl = 4 * i + ls / 16;
                     if (jl < lim) {
                         reinterpret_cast<uint4*>(S.kvk[jl])[(ls % 16) ^ (jl % 16)] = rk[i];
-                        reinterpret_cast<uint4*>(S.kvv[jl])[(ls % 16) ^ (jl % 16)] = rv[i];
+                        reinterpret_cast<uint4*>(S.kvv[jl])[ls % 16] = rv[i];
                     }
                 }
                 put32(S.qkn[0], ls, qn);
@@ -805,7 +805,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     const int pl = pos - s0, p16 = pl % 16;
                     S.kvk[pl][8 * ((lane >> 3) ^ p16) + (lane & 7)] = (uint16_t)k0;
                     S.kvk[pl][8 * (((lane + 64) >> 3) ^ p16) + (lane & 7)] = (uint16_t)k1;
-                    reinterpret_cast<uint32_t*>(S.kvv[pl])[4 * ((lane >> 2) ^ p16) + (lane & 3)] = vw;
+                    reinterpret_cast<uint32_t*>(S.kvv[pl])[lane] = vw;
                     if (split || r == 0) {
                         const int64_t cur = ((int64_t)l * kAX + x) * kv_head_stride + (int64_t)pos * D;
                         a.kc[cur + lane] = (uint16_t)k0;
@@ -835,23 +835,32 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                         kc[p] = reinterpret_cast<const uint4*>(S.kvk[rl])[d16 ^ (rl & 15)];
                     }
                     double E[8];                         // entry 2p + h: partial score over the 8 dims
-#pragma unroll
-                    for (int p = 0; p < 4; ++p) {
+                    // passes in pairs without a bound check (rows past the block are its last
+                    // row; their scores are masked below), so that the four accumulation
+                    // chains of a pair interleave
+                    auto pass = [&](int p) {
                         double s0 = 0.0, s1 = 0.0;
-                        if (p < passes) {
-                            const uint32_t k4[4] = {kc[p].x, kc[p].y, kc[p].z, kc[p].w};
+                        const uint32_t k4[4] = {kc[p].x, kc[p].y, kc[p].z, kc[p].w};
 #pragma unroll
-                            for (int t = 0; t < 4; ++t) {
-                                const double klo = bf16_bits_to_f32(k4[t] & 0xffffu);
-                                const double khi = __uint_as_float(k4[t] & 0xffff0000u);
-                                s0 = fma(qd[0][t].x, klo, s0);
-                                s0 = fma(qd[0][t].y, khi, s0);
-                                s1 = fma(qd[1][t].x, klo, s1);
-                                s1 = fma(qd[1][t].y, khi, s1);
-                            }
+                        for (int t = 0; t < 4; ++t) {
+                            const double klo = bf16_bits_to_f32(k4[t] & 0xffffu);
+                            const double khi = __uint_as_float(k4[t] & 0xffff0000u);
+                            s0 = fma(qd[0][t].x, klo, s0);
+                            s0 = fma(qd[0][t].y, khi, s0);
+                            s1 = fma(qd[1][t].x, klo, s1);
+                            s1 = fma(qd[1][t].y, khi, s1);
                         }
                         E[2 * p] = s0;
                         E[2 * p + 1] = s1;
+                    };
+                    pass(0);
+                    pass(1);
+                    if (passes > 2) {
+                        pass(2);
+                        pass(3);
+                    } else {
+#pragma unroll
+                        for (int k = 4; k < 8; ++k) E[k] = 0.0;
                     }
                     // sum over d16 (lane bits 5, 4, 3, 2), transposed: the lane keeps entry
                     // 4 b5 + 2 b4 + b3, i.e. pass pe = 2 b5 + b4, head he = b3
@@ -885,37 +894,41 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     ls = tsum32(ls, ls);
                     mh = m;
                     lh = ls;
-                    // numerators to LDS: position 4 pe + jj, head he (one lane of each pair)
-                    if ((lane & 4) == 0 && valid) S.pw[c][4 * pe + jj][(lane >> 3) & 1] = pv;
+                    // numerators to LDS: position 4 pe + jj, head he (one lane of each pair);
+                    // all 16 entries, zero past the block, so that P V runs without bounds
+                    if ((lane & 4) == 0) S.pw[c][4 * pe + jj][(lane >> 3) & 1] = pv;
                 }
-                // P V: lane l accumulates dims 2l, 2l + 1 of both heads over the wave's block;
-                // the numerators come back from LDS as same-address (broadcast) reads
-                double pa[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
+                // P V: lane l accumulates dims 2l, 2l + 1 of both heads over the wave's block, in
+                // rounds of 8 positions without bounds checks (numerators past the block are 0,
+                // their V row is the block's last); two accumulator sets, even and odd positions
+                double pa[2][2][2] = {{{0.0, 0.0}, {0.0, 0.0}}, {{0.0, 0.0}, {0.0, 0.0}}};
                 lds_order();
-                for (int t0 = 0; t0 < np; t0 += 8) {
-                    double2 pp[8];
-                    uint32_t vw[8];
+                if (np > 0) {
+                    const uint32_t* const vrow = reinterpret_cast<const uint32_t*>(S.kvv[j0 - s0]) + lane;
+                    const int rounds = (np + 7) >> 3;               // <= 2
+                    for (int t0 = 0; t0 < 8 * rounds; t0 += 8) {
+                        double2 pp[8];
+                        uint32_t vw[8];
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) {
-                        const int t = min(t0 + u, np - 1);
-                        const int rl = j0 - s0 + t;                              // slot row
-                        pp[u] = *reinterpret_cast<const double2*>(S.pw[c][t]);
-                        vw[u] = reinterpret_cast<const uint32_t*>(S.kvv[rl])[4 * ((lane >> 2) ^ (rl & 15)) + (lane & 3)];
-                    }
+                        for (int u = 0; u < 8; ++u) {
+                            pp[u] = *reinterpret_cast<const double2*>(S.pw[c][t0 + u]);
+                            vw[u] = vrow[(kAD / 2) * min(t0 + u, np - 1)];
+                        }
 #pragma unroll
-                    for (int u = 0; u < 8; ++u) {
-                        if (t0 + u < np) {
+                        for (int u = 0; u < 8; ++u) {
                             const double vlo = bf16_bits_to_f32(vw[u] & 0xffffu), vhi = __uint_as_float(vw[u] & 0xffff0000u);
-                            pa[0][0] = fma(pp[u].x, vlo, pa[0][0]);
-                            pa[0][1] = fma(pp[u].x, vhi, pa[0][1]);
-                            pa[1][0] = fma(pp[u].y, vlo, pa[1][0]);
-                            pa[1][1] = fma(pp[u].y, vhi, pa[1][1]);
+                            double (&A)[2][2] = pa[u & 1];
+                            A[0][0] = fma(pp[u].x, vlo, A[0][0]);
+                            A[0][1] = fma(pp[u].x, vhi, A[0][1]);
+                            A[1][0] = fma(pp[u].y, vlo, A[1][0]);
+                            A[1][1] = fma(pp[u].y, vhi, A[1][1]);
                         }
                     }
                 }
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
-                    *reinterpret_cast<double2*>(&S.pacc[c][h][2 * lane]) = make_double2(pa[h][0], pa[h][1]);
+                    *reinterpret_cast<double2*>(&S.pacc[c][h][2 * lane]) =
+                        make_double2(pa[0][h][0] + pa[1][h][0], pa[0][h][1] + pa[1][h][1]);
                 if ((lane & ~8) == 0) {
                     S.pml[c][lane >> 3][0] = mh;
                     S.pml[c][lane >> 3][1] = lh;
