@@ -131,7 +131,6 @@ struct __align__(16) AsyncLds {
     __align__(16) float hs[kAH];                         // the layer's input (bf16 values): stage D's residual
     double part[4][kCW][32];               // per-wave row partials of the combines A, C, E, F
     uint32_t sync[16];
-    uint32_t noshift;                      // slot B: 1 when this layer's softmax needs no maximum (see the KV loader)
     // tail
     __align__(16) float4 xs[kAH / 4];                    // final normalized vector, per-lane layout
     double fss;                            // final sum of squares
@@ -612,23 +611,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 // step's last attention is done)
                 const uint32_t cw = l == 0 ? ld32(a.cos_t + (int64_t)pos * D + 2 * ln) : 0u;
                 const uint32_t sw = l == 0 ? ld32(a.sin_t + (int64_t)pos * D + 2 * ln) : 0u;
-                // Softmax without its running maximum. A query or key after the QK RMSNorm has
-                // norm <= sqrt(D) max|g| (the normalised vector's squares sum to at most D), RoPE
-                // with bf16 cos / sin scales a rotation pair by at most 1 + 2^-8, and the fp32
-                // (q) and bf16 (k) roundings add at most 2^-8; so every score of this layer is at
-                // most b = |attn_scale| D max|g_q| max|g_k| 1.02 in magnitude, for every key this
-                // kernel wrote. With b <= 64 the numerators are e^s itself and the waves' and
-                // ranks' partials add without rescaling by their maxima: no sum of up to 2048
-                // terms e^s |v| (|v| <= the bf16 maximum) leaves fp64's range while every score is
-                // within 600, which also covers keys written elsewhere with up to 9x that norm.
-                // Otherwise (or for NaN gains) the compute waves subtract the maximum as usual.
-                const uint32_t gq = wave_max_u32(max(qn & 0x7fffu, (qn >> 16) & 0x7fffu));
-                const uint32_t gk = wave_max_u32(max(kn & 0x7fffu, (kn >> 16) & 0x7fffu));
-                // (the scale read from the kernel-argument segment here: a product of it held
-                // through the layer loop was spilled)
-                const double bound = fabs((double)kargs()->attn_scale) * D * (double)bf16_bits_to_f32(gq) *
-                                     (double)bf16_bits_to_f32(gk) * 1.02;
-                const uint32_t noshift = bound <= 64.0 ? 1u : 0u;
                 await_free(SL_B, gl);
                 const int ls = opaque(ln);
 #pragma unroll
@@ -641,7 +623,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 }
                 put32(S.qkn[0], ls, qn);
                 put32(S.qkn[1], ls, kn);
-                if (ls == 0) S.noshift = noshift;
                 if (l == 0) {
                     put32(S.rope[0], ls, cw);
                     put32(S.rope[1], ls, sw);
@@ -762,8 +743,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     if (lane == 0)
                         __hip_atomic_store(&S.sync[kWindow], (uint32_t)(gl + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
-                // read before slot B is released (the loader then overwrites it)
-                const bool noshift = __builtin_amdgcn_readfirstlane(S.noshift) != 0u;
                 // QK-norm and RoPE: out[i] = y[i] cos[i] - y[i+64] sin[i],
                 // out[i+64] = y[i] sin[i+64] + y[i+64] cos[i+64] (i = lane)
                 const double cl = bf16_bits_to_f32(S.rope[0][lane]), ch = bf16_bits_to_f32(S.rope[0][lane + 64]);
@@ -877,10 +856,18 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     const int pe = 2 * ((lane >> 5) & 1) + ((lane >> 4) & 1);
                     const bool valid = 4 * pe + jj < np;
                     const double sc = valid ? E[0] * (double)a.attn_scale : -INFINITY;
-                    // max (unless the layer's scores need no shift) and numerator sum over the
-                    // lanes of the same head (bits 0, 1, 4, 5)
+                    // Softmax numerators e^s without the running maximum (m = 0) unless a valid
+                    // score of this wave's block exceeds 600 in magnitude: then e^(s - m) with
+                    // the block's maximum m per head (over the lanes of the same head, bits 0,
+                    // 1, 4, 5). Within 600 no sum of up to 2048 terms e^s |v| (|v| up to the
+                    // bf16 maximum, e^89) leaves fp64's range and e^-600 is a normal number, so
+                    // both forms equal the exact softmax to fp64 rounding whatever keys the cache
+                    // holds (rows written elsewhere included); each block's m travels with its
+                    // partials, and the merges below rescale only blocks whose m differs from
+                    // the largest.
+                    const bool shift = __any(valid && fabs(sc) > 600.0);
                     double m = 0.0;
-                    if (!noshift) {
+                    if (shift) {
                         m = sc;
                         m = fmax(m, partner64<1>(m));
                         m = fmax(m, partner64<2>(m));
@@ -938,18 +925,16 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 lds_add(&S.sync[kArrive + AR_B], lane);
                 lds_wait(&S.sync[kArrive + AR_B], (uint32_t)(kCW * (gl + 1)), lds_limit, &hdr->abort_flag);
                 // merge: wave c takes attention dims [64c, +64) (head c / 2) from the four blocks;
-                // lane w < 4 computes block w's weight e^(m_w - M), the others read it
-                // (without the shift every block's numerators share the scale e^0: weight 1;
-                // an empty block adds zeros)
+                // lane w < 4 computes block w's weight e^(m_w - M), the others read it (weight 1
+                // for blocks at the largest m, which is every block when none shifted, so that
+                // the exponential is not evaluated at all then; an empty block weighs 0)
                 const int hh = c >> 1, dim = 64 * (c & 1) + lane;
-                double M = 0.0, ew = 1.0;
-                if (!noshift) {
-                    M = -INFINITY;
+                double M = -INFINITY;
 #pragma unroll
-                    for (int w = 0; w < kCW; ++w) M = fmax(M, S.pml[w][hh][0]);
-                    const double mine = S.pml[lane & 3][hh][0];
-                    ew = mine == -INFINITY ? 0.0 : exp(mine - M);
-                }
+                for (int w = 0; w < kCW; ++w) M = fmax(M, S.pml[w][hh][0]);
+                const double mine = S.pml[lane & 3][hh][0];
+                double ew = mine == -INFINITY ? 0.0 : 1.0;
+                if (mine != M && mine != -INFINITY) ew = exp(mine - M);
                 double num = 0.0, den = 0.0;
 #pragma unroll
                 for (int w = 0; w < kCW; ++w) {
@@ -985,17 +970,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                         return __longlong_as_double((long long)(((uint64_t)__float_as_uint(o8[2 * i + 1]) << 32) |
                                                                 __float_as_uint(o8[2 * i])));
                     };
-                    double wgt = lane < 32 ? 1.0 : 0.0;                  // no shift: every slice at e^0
-                    if (!noshift) {
-                        const double Ms = lane < 32 ? dv(0) : -1e300;
-                        double Mx = Ms;
-                        Mx = fmax(Mx, partner64<1>(Mx));
-                        Mx = fmax(Mx, partner64<2>(Mx));
-                        Mx = fmax(Mx, partner64<4>(Mx));
-                        Mx = fmax(Mx, partner64<8>(Mx));
-                        Mx = fmax(Mx, partner64<16>(Mx));                // lanes 0-31: max over the ranks
-                        wgt = lane < 32 ? exp(Ms - Mx) : 0.0;
-                    }
+                    // slice weights e^(M_s - max M): 1 for the slices at the largest maximum (all
+                    // of them when none shifted), 0 for empty ones
+                    const double Ms = lane < 32 ? dv(0) : -1e300;
+                    double Mx = Ms;
+                    Mx = fmax(Mx, partner64<1>(Mx));
+                    Mx = fmax(Mx, partner64<2>(Mx));
+                    Mx = fmax(Mx, partner64<4>(Mx));
+                    Mx = fmax(Mx, partner64<8>(Mx));
+                    Mx = fmax(Mx, partner64<16>(Mx));                    // lanes 0-31: max over the ranks
+                    double wgt = (lane < 32 && Ms != -1e300) ? 1.0 : 0.0;
+                    if (lane < 32 && Ms != Mx && Ms != -1e300) wgt = exp(Ms - Mx);
                     double sd = wgt * (lane < 32 ? dv(1) : 0.0);
                     double s0n = wgt * (lane < 32 ? dv(2) : 0.0), s1n = wgt * (lane < 32 ? dv(3) : 0.0);
 #define MQ_SPLIT_LEVEL(Mk)                                                                    \
