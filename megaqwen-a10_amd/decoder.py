@@ -665,7 +665,12 @@ class A10Int8BatchDecoder(_DecoderBase):
 
 
 def load_checkpoint_state(model_path, cfg: ModelConfig) -> dict:
-    """bf16 state dict from a local HF safetensors checkpoint directory (no network)."""
+    """bf16 state dict from a local HF safetensors checkpoint directory (no network),
+    as the reference's ``_load_model`` takes it from the HF model (a10_decode.py:281-325):
+    every tensor of every ``*.safetensors`` file (shards merged) in bf16; ``lm_head.weight``
+    the embedding when the checkpoint ties it (absent key); a missing ``q_norm`` /
+    ``k_norm`` gain becomes ones (a10_decode.py:304-309). A missing projection, layer
+    norm, embedding or final norm raises ``KeyError`` naming the key."""
     from safetensors.torch import load_file
     path = Path(model_path)
     files = sorted(path.glob("*.safetensors"))
@@ -674,39 +679,79 @@ def load_checkpoint_state(model_path, cfg: ModelConfig) -> dict:
     state = {}
     for f in files:
         state.update({k: v.to(torch.bfloat16) for k, v in load_file(str(f)).items()})
-    if "lm_head.weight" not in state:
+    if "lm_head.weight" not in state and "model.embed_tokens.weight" in state:
         state["lm_head.weight"] = state["model.embed_tokens.weight"]
     for i in range(cfg.num_layers):
         p = f"model.layers.{i}.self_attn"
         state.setdefault(f"{p}.q_norm.weight", torch.ones(cfg.head_dim, dtype=torch.bfloat16))
         state.setdefault(f"{p}.k_norm.weight", torch.ones(cfg.head_dim, dtype=torch.bfloat16))
+    need = ["model.embed_tokens.weight", "model.norm.weight", "lm_head.weight"]
+    for i in range(cfg.num_layers):
+        p = f"model.layers.{i}"
+        need += [f"{p}.input_layernorm.weight", f"{p}.post_attention_layernorm.weight"]
+        need += [f"{p}.{proj}.weight" for proj in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                                                    "self_attn.o_proj", "mlp.gate_proj", "mlp.up_proj",
+                                                    "mlp.down_proj")]
+    for k in need:
+        if k not in state:
+            raise KeyError(f"checkpoint {path} has no tensor {k!r}")
     return state
+
+
+def config_from_checkpoint(model_path, default: ModelConfig) -> ModelConfig:
+    """The model shape of a checkpoint directory: HF ``config.json`` fields (layers, hidden
+    and intermediate sizes, heads, head_dim, vocabulary, RMSNorm eps, RoPE theta) over
+    ``default``; ``default`` itself when the directory has no ``config.json`` (the
+    reference hard-codes Qwen3-0.6B, a10_decode.py:22-31)."""
+    import json
+    f = Path(model_path) / "config.json"
+    if not f.exists():
+        return default
+    c = json.loads(f.read_text())
+    keys = {"num_hidden_layers": "num_layers", "hidden_size": "hidden_size",
+            "intermediate_size": "intermediate_size", "num_attention_heads": "num_q_heads",
+            "num_key_value_heads": "num_kv_heads", "head_dim": "head_dim", "vocab_size": "vocab_size",
+            "rms_norm_eps": "rms_eps", "rope_theta": "rope_theta", "tie_word_embeddings": "tie_word_embeddings"}
+    kw = {ours: c[theirs] for theirs, ours in keys.items() if theirs in c}
+    return default.with_(name=c.get("_name_or_path", Path(model_path).name) or default.name, **kw)
+
+
+def load_tokenizer(model_path):
+    """The checkpoint's tokenizer (``AutoTokenizer``, local files only), or None when the
+    directory holds none that transformers can load."""
+    try:
+        from transformers import AutoTokenizer
+        return AutoTokenizer.from_pretrained(str(model_path), local_files_only=True)
+    except Exception:
+        return None
 
 
 class A10Decoder:
     """a10_decode.py:35-393. ``A10Decoder(model_path, max_seq_len)`` loads a
-    local checkpoint; ``A10Decoder(seed=0)`` (or a missing ``model_path``)
-    builds seeded random-init weights of ``config``. ``int8=True`` quantizes
-    every linear and the LM head (bench_int8.py:27-55) and drives
-    ``A10Int8MegakernelDecoder``; otherwise the bf16 ``A10MegakernelDecoder``."""
+    local checkpoint directory (safetensors weights, its ``config.json`` shape when
+    present, its tokenizer when transformers can load one); ``A10Decoder(seed=0)``
+    (or a missing ``model_path``) builds seeded random-init weights of ``config``.
+    ``int8=True`` quantizes every linear and the LM head (bench_int8.py:27-55) and
+    drives ``A10Int8MegakernelDecoder``; otherwise the bf16 ``A10MegakernelDecoder``."""
 
     def __init__(self, model_path=None, max_seq_len: int = 2048, *, seed: int | None = None,
                  config: ModelConfig = QWEN3_0_6B, int8: bool = False, device="cuda"):
         self.max_seq_len = max_seq_len
         self.device = torch.device(device)
-        self.config = config
         self.tokenizer = None
         if model_path is not None and Path(model_path).exists():
+            config = config_from_checkpoint(model_path, config)
             state = load_checkpoint_state(model_path, config)
-            try:
-                from transformers import AutoTokenizer
-                self.tokenizer = AutoTokenizer.from_pretrained(str(model_path), local_files_only=True)
-            except Exception:
-                self.tokenizer = None
+            self.tokenizer = load_tokenizer(model_path)
         else:
             if model_path is not None and seed is None:
                 raise FileNotFoundError(f"checkpoint {model_path} not found (pass seed= for random weights)")
             state, _ = random_init_state(config, seed=0 if seed is None else seed)
+        if (config.num_q_heads, config.num_kv_heads, config.head_dim, config.rms_eps) != (16, 8, 128, 1e-6):
+            raise ValueError(f"the decode kernels are compiled for 16 query / 8 KV heads of 128 and RMSNorm eps "
+                             f"1e-6, got {config.num_q_heads} / {config.num_kv_heads} heads of {config.head_dim}, "
+                             f"eps {config.rms_eps}")
+        self.config = config
         self.cos_table, self.sin_table = precompute_rope_freqs(config.head_dim, max_seq_len, config.rope_theta,
                                                                device=self.device)
         if int8:
@@ -734,8 +779,10 @@ class A10Decoder:
         a temperature and ignores it, a10_decode.py:358). Within the INT8 async-wave
         kernel's range every step runs in one launch (``device_loop``), else one launch per
         step; the tokens are the same. Generation stops after an EOS token when the
-        tokenizer has one. Returns ``(text_or_ids, tok_per_s, per_token_ms)``: with one
-        launch, per_token_ms holds the launch's average time per step."""
+        tokenizer has one. Returns ``(text_or_ids, tok_per_s, per_token_ms)``: the prompt and
+        generated tokens decoded as text without special tokens (a10_decode.py:387) for a
+        string prompt, as ids for an id list; with one launch, per_token_ms holds the
+        launch's average time per step."""
         if isinstance(prompt, str):
             if self.tokenizer is None:
                 raise ValueError("a string prompt needs a checkpoint with a tokenizer; pass token ids")
@@ -760,5 +807,5 @@ class A10Decoder:
         times = [ms / steps] * (len(toks) - 1)          # the steps after the first generated token
         tok_s = 1e3 * steps / ms if ms > 0 else 0.0
         generated = list(ids) + toks
-        out = self.tokenizer.decode(generated) if self.tokenizer is not None else generated
+        out = self.tokenizer.decode(generated, skip_special_tokens=True) if isinstance(prompt, str) else generated
         return out, tok_s, times
