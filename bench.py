@@ -23,7 +23,9 @@ FP8 E4M3, steady state), ``positions`` (config 3 positions, bf16 weights),
 ``longctx`` (config 4: KV pre-filled to 1024 / 4096 / 8192, ``--steps 64``),
 ``batched`` (config 5: Qwen3-1.7B shape, B = 1 / 4 / 8 / 16, ``--steps 128``; one
 sequence per batch size teacher-force checked against the float64 oracle for
-``--check-steps`` tokens, reported as ``per_batch[B].parity``), and
+``--check-steps`` tokens, reported as ``per_batch[B].parity``), ``prefill`` (the
+prompt-batched prefill of 8 / 64 / 512 / 2040 tokens against one decode step per
+token, ``--prompt-lens``), and
 ``traffic``: a uint8 add over a 256 MiB buffer (reads and writes exactly
 256 MiB, the calibration for the FETCH_SIZE / WRITE_SIZE counters) followed
 by 8 decode steps, for ``rocprofv3 --pmc`` runs.
@@ -60,7 +62,8 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=112,
                     help="greedy steps of the CPU baseline sample (about 10 s on 16 host threads)")
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "matvec", "formats", "positions", "longctx", "batched", "traffic"])
+                    choices=["decode", "matvec", "formats", "positions", "longctx", "batched", "prefill", "traffic"])
+    ap.add_argument("--prompt-lens", default="8,64,512,2040", help="prefill: prompt lengths")
     ap.add_argument("--depths", default="1024,4096,8192", help="longctx: KV depths")
     ap.add_argument("--batches", default="1,4,8,16", help="batched: batch sizes")
     ap.add_argument("--split-min", type=int, default=0,
@@ -602,6 +605,93 @@ def run_longctx(args, mq, torch):
                          "timing": KERNEL_TIMING}}
 
 
+def _prefill_ops(cfg, P):
+    """int8 digit-plane products the prefill's matrix cores execute for P positions: every
+    product over the padded position count (multiples of 32), 8 digit planes per position,
+    the last layer's QKV only."""
+    H, I, Q, KV, L = cfg.hidden_size, cfg.intermediate_size, cfg.q_size, cfg.kv_size, cfg.num_layers
+    Pp = (P + 31) // 32 * 32
+    qkv = (Q + 2 * KV) * H
+    rest = H * Q + 2 * I * H + H * I
+    return 2 * 8 * Pp * (L * qkv + (L - 1) * rest)
+
+
+def run_prefill(args, mq, torch):
+    """Prompt-batched prefill: the K/V cache rows of a P-token prompt of the config-1
+    model written by A10Int8MegakernelDecoder.prefill (each layer's weights once for all P positions),
+    against the reference's way, P decode steps. HIP events around each prefill on its stream."""
+    dev = torch.device("cuda:0")
+    cfg = mq.QWEN3_0_6B
+    lens = [int(v) for v in args.prompt_lens.split(",")]
+    S = max(lens) + 8
+    state, _ = mq.random_init_state(cfg, seed=args.seed)
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    qstate = mq.quantize_state(state, cfg, dev)
+    del state
+    embed, layers, scales, lm_q, lm_s, fnorm = mq.pack_int8(qstate, cfg)
+    dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+    g = torch.Generator().manual_seed(args.seed + 1)
+    t0e, t1e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    per_len = {}
+    for P in lens:
+        ids = torch.randint(0, cfg.vocab_size, (P,), generator=g).tolist()
+        reps = max(3, min(20, 4096 // P))
+        dec.reset()
+        dec.prefill(ids)                                   # warm-up (workspace, code objects)
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(reps):
+            dec.reset()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            t0e.record()
+            dec.prefill(ids)
+            host = time.perf_counter() - t0
+            t1e.record()
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+            ms.append((t0e.elapsed_time(t1e), wall * 1e3, host * 1e3))
+        k_batched, v_batched = dec.k_cache[:, :, :P].clone(), dec.v_cache[:, :, :P].clone()
+        dev_ms = sum(m[0] for m in ms) / reps
+        wall_ms = sum(m[1] for m in ms) / reps
+        host_ms = sum(m[2] for m in ms) / reps
+        # the reference's way: one decode step per prompt token
+        dec.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in ids:
+            dec.decode_step(int(t))
+        steps_ms = (time.perf_counter() - t0) * 1e3
+        same = float(((dec.k_cache[:, :, :P] == k_batched).double().mean() +
+                      (dec.v_cache[:, :, :P] == v_batched).double().mean()) / 2)
+        ops = _prefill_ops(cfg, P)
+        w_bytes = cfg.int8_step_bytes() - cfg.vocab_size * (cfg.hidden_size + 4)     # layer weights, no LM head
+        per_len[str(P)] = {
+            "tok_s": round(P / (wall_ms / 1e3), 1), "device_ms": round(dev_ms, 3), "wall_ms": round(wall_ms, 3),
+            "host_call_ms": round(host_ms, 3),
+            "per_token_steps_ms": round(steps_ms, 2), "per_token_steps_tok_s": round(P / (steps_ms / 1e3), 1),
+            "speedup_vs_per_token_steps": round(steps_ms / wall_ms, 1),
+            "mfma_digit_tops": round(ops / (dev_ms / 1e3) / 1e12, 1),
+            "mfma_frac": round(ops / (dev_ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
+            "weight_GBs": round(w_bytes / (dev_ms / 1e3) / 1e9, 1),
+            "kv_rows_identical_to_per_token_steps": round(same, 6), "reps": reps}
+        print(f"prefill P={P}: {per_len[str(P)]}", file=sys.stderr, flush=True)
+    head = str(512 if 512 in lens else max(lens))
+    top = per_len[head]
+    return {"metric": f"INT8 prompt prefill tok/s, Qwen3-0.6B shape bs=1, prompt of {head} tokens (SURVEY f1)",
+            "value": top["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": top["reps"], "warmup": 1,
+            "ms_per_step": top["wall_ms"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "int8 digit products (exact), fp64 attention and norms", "data": "synthetic",
+            "config": {"workload": "prompt-batched prefill of P random tokens into an empty KV cache of the config-1 "
+                                   "model (random-init seed 0), K/V rows of all 28 layers; a step = one prefill",
+                       "prompt_lens": lens, "per_len": per_len},
+            "roofline": {"bound": "mfma", "achieved": top["mfma_digit_tops"], "peak": INT8_PEAK_TOPS,
+                         "unit": "TOP/s", "frac": top["mfma_frac"], "traffic": None,
+                         "timing": "int8 digit-plane products executed (8 planes per position, positions padded to "
+                                   "32) over the whole prefill's device time (HIP events around it: norms, "
+                                   "attention and launch gaps included)"}}
+
+
 def run_batched(args, mq, torch):
     """batched INT8 decode of the Qwen3-1.7B shape, B independent seeded
     8-token prompts, then K greedy steps timed per batch size (kernel time from HIP events)."""
@@ -758,7 +848,7 @@ def main():
         return 1
     fn = {"decode": run_decode, "matvec": run_matvec, "formats": run_formats, "positions": run_positions,
           "longctx": run_longctx,
-          "batched": run_batched, "traffic": run_traffic}[args.workload]
+          "batched": run_batched, "prefill": run_prefill, "traffic": run_traffic}[args.workload]
     out = fn(args, mq, torch)
     print(json.dumps(out), flush=True)
     return 0

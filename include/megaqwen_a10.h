@@ -265,6 +265,22 @@ int mq_fp8_decode_step(const mq_decode_args* args, hipStream_t stream);
 int mq_int8_decode_step_noalloc(const mq_decode_args* args, hipStream_t stream);
 /* Several steps per launch (see mq_generate_args). */
 int mq_int8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream);
+/* Prompt-batched prefill. The reference prefills a prompt one decode step per
+ * token (a10_decode.py:367-368, verify_correctness_a10.py:326-328, each step
+ * a10_int8_decode_kernel.cu:821-842); this writes the same K/V cache rows with
+ * each layer's weights read once for the whole prompt. tokens: HOST array of
+ * n_tokens ids (validated before anything is launched), prefilled at positions
+ * args->position + i (0 <= i < n_tokens <= max_seq_len - position); no logits
+ * and no token are produced: the decode step of the next token (the prompt's
+ * last, as in the reference's loop) gives the first generated token.
+ * args->input_token_id, output_token_id, cache_len and workspace are not used.
+ * INT8 Qwen3-0.6B shape only (MQ_ERR_UNSUPPORTED otherwise). workspace: device
+ * memory of mq_prefill_workspace_bytes(dims, m) bytes, 16-byte aligned; a
+ * longer prompt runs in chunks of m positions (m rounded up to a multiple of
+ * 32). Asynchronous on `stream`. */
+size_t mq_prefill_workspace_bytes(const mq_model_dims* dims, int max_tokens);
+int mq_int8_prefill(const mq_decode_args* args, const int* tokens, int n_tokens, void* workspace,
+                    size_t workspace_bytes, hipStream_t stream);
 /* Host-side wait for a token the kernel stores into host memory (pinned, e.g.
  * hipHostMalloc): spins until *token differs from `sentinel`, which the
  * caller wrote before the launch. MQ_OK, or MQ_ERR_TIMEOUT after timeout_us

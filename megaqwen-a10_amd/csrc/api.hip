@@ -354,6 +354,65 @@ int mq_int8_decode_generate(const mq_decode_args* args, const mq_generate_args* 
     return launch_decode(*args, s, true, stream, nullptr, &plan);
 }
 
+size_t mq_prefill_workspace_bytes(const mq_model_dims* dims, int max_tokens) {
+    clear_error();
+    DecodeShape s;
+    if (shape_of(dims, &s) != MQ_OK) return 0;
+    if (s.H != 1024 || s.I != 3072) {
+        set_error(MQ_ERR_UNSUPPORTED, "the prefill is compiled for hidden 1024 / intermediate 3072 only");
+        return 0;
+    }
+    if (max_tokens < 1) {
+        set_error(MQ_ERR_INVALID_ARGUMENT, "max_tokens %d < 1", max_tokens);
+        return 0;
+    }
+    return prefill_workspace_bytes(max_tokens);
+}
+
+int mq_int8_prefill(const mq_decode_args* a, const int* tokens, int n_tokens, void* workspace,
+                    size_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    if (a == nullptr) return set_error(MQ_ERR_INVALID_ARGUMENT, "args is NULL");
+    DecodeShape s;
+    int st = shape_of(a->dims, &s);
+    if (st != MQ_OK) return st;
+    if (s.H != 1024 || s.I != 3072)
+        return set_error(MQ_ERR_UNSUPPORTED, "the prefill is compiled for hidden 1024 / intermediate 3072 only");
+    if (a->num_layers < 1) return set_error(MQ_ERR_INVALID_ARGUMENT, "num_layers %d < 1", a->num_layers);
+    if (a->max_seq_len < 1) return set_error(MQ_ERR_INVALID_ARGUMENT, "max_seq_len %d < 1", a->max_seq_len);
+    if (n_tokens < 0) return set_error(MQ_ERR_INVALID_ARGUMENT, "n_tokens %d < 0", n_tokens);
+    if (n_tokens == 0) return MQ_OK;
+    if (tokens == nullptr) return set_error(MQ_ERR_INVALID_ARGUMENT, "tokens is NULL");
+    if (a->position < 0 || (int64_t)a->position + n_tokens > a->max_seq_len)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "positions [%d, %lld) outside [0, max_seq_len=%d)", a->position,
+                         (long long)a->position + n_tokens, a->max_seq_len);
+    for (int i = 0; i < n_tokens; ++i)
+        if (tokens[i] < 0 || tokens[i] >= s.V)
+            return set_error(MQ_ERR_INVALID_ARGUMENT, "tokens[%d] = %d outside [0, %d)", i, tokens[i], s.V);
+    if (!a->embed_weight || !a->layer_weights || !a->scales || !a->cos_table || !a->sin_table || !a->k_cache ||
+        !a->v_cache)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "a required pointer is NULL");
+    if (!aligned16(a->k_cache) || !aligned16(a->v_cache) || !aligned16(a->embed_weight))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "embed_weight and the KV caches must be 16-byte aligned");
+    if (!workspace || !aligned16(workspace))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "the prefill workspace must be non-NULL and 16-byte aligned");
+    if (prefill_capacity(workspace_bytes) < 1)
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "a prefill workspace of %zu bytes is below the %zu of one chunk",
+                         workspace_bytes, prefill_workspace_bytes(1));
+    const size_t cache = (size_t)a->num_layers * s.NKV * a->max_seq_len * s.D * 2;
+    const size_t table = (size_t)a->max_seq_len * s.D * 2;
+    if (!in_allocation(a->embed_weight, (size_t)s.H * s.V * 2))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "embed_weight holds fewer than vocab_size = %d rows of %d", s.V, s.H);
+    if (!in_allocation(a->k_cache, cache) || !in_allocation(a->v_cache, cache))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "the KV caches hold fewer than num_layers x %d x max_seq_len x %d "
+                         "bf16 values", s.NKV, s.D);
+    if (!in_allocation(a->cos_table, table) || !in_allocation(a->sin_table, table))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "the RoPE tables hold fewer than max_seq_len rows of %d", s.D);
+    if (!in_allocation(workspace, workspace_bytes))
+        return set_error(MQ_ERR_INVALID_ARGUMENT, "the prefill workspace is smaller than workspace_bytes");
+    return launch_prefill(*a, tokens, n_tokens, workspace, workspace_bytes, stream);
+}
+
 int mq_wait_host_token(const volatile int* token, int sentinel, unsigned int timeout_us) {
     clear_error();
     if (!token) return set_error(MQ_ERR_INVALID_ARGUMENT, "token is NULL");

@@ -74,6 +74,15 @@ int decode_async_split_min(int attn_split_min);
 // True when the workgroups of each residue class g mod 8 run on one XCD (checked once per device).
 bool xcd_placement_ok();
 
+// Prompt-batched prefill (prefill.hip): INT8 Qwen3-0.6B shape. The workspace of a chunk of
+// max_tokens positions, the positions a workspace of `bytes` holds per chunk, and the
+// launches that write the K/V cache rows of tokens[0, n_tokens) (host array) at positions
+// d.position + i.
+size_t prefill_workspace_bytes(int max_tokens);
+int prefill_capacity(size_t bytes);
+int launch_prefill(const mq_decode_args& d, const int* tokens, int n_tokens, void* ws, size_t ws_bytes,
+                   hipStream_t stream);
+
 // Batched INT8 decode (decode_batch.hip).
 size_t decode_batch_workspace_bytes(const DecodeShape& s);
 int launch_decode_batch(const mq_batch_args& a, const DecodeShape& s, hipStream_t stream);

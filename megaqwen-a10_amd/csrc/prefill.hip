@@ -1,0 +1,514 @@
+// Prompt-batched prefill: the KV-cache rows of P prompt positions, each layer's
+// weights passed over once for all P positions, on the int8 matrix cores.
+//
+// The reference prefills one decode step per prompt token (a10_decode.py:367-368,
+// verify_correctness_a10.py:326-328); the cache rows a step writes are those of
+// a10_int8_decode_kernel.cu:143-241. Here the P positions of a chunk go through a
+// layer together, as matrix products of P activation rows with each weight matrix.
+// The arithmetic is the decode-step kernels' (every stored value is the correctly
+// rounded value of the reference's expression, up to fp64 rounding of the sums):
+// each activation row becomes a 55-bit fixed-point number over its own
+// power-of-two scale (digits.h), the products are exact int32 digit-plane sums
+// on the int8 matrix cores recombined in fp64, and attention runs in fp64. So the
+// cache rows equal those of P decode steps, apart from fp32 roundings that the
+// fp64 summation order can move once in about 2^20 values.
+//
+// Per layer, eight launches over the chunk (P rows each):
+//   digits      RMSNorm of the layer input (the embedding rows in layer 0), its
+//               digit planes                                 one workgroup per position
+//   QKV         q|k|v rows on the matrix cores; the epilogue runs QK-norm and RoPE
+//               and writes this layer's K/V cache rows and the rotated queries
+//               (a 128-row tile is one head, so the norm and the rotation pairs
+//               are inside one wave)                        tiles of 32 positions x 128 rows
+//   attention   causal, fp64, one wave per (position, KV head) over cache rows
+//               [0, pos0 + p]; the output's digit planes
+//   O           + residual (the layer input)                 32 positions x 64 rows
+//   digits      post-attention RMSNorm
+//   gate|up     64 channels' gate and up rows per tile; SwiGLU in the epilogue
+//   digits      of the SwiGLU output
+//   down        + residual, bf16: the next layer's input
+// The last layer stops after its cache rows. The first generated token comes from
+// the decode step of the last prompt token, as in the reference's loop.
+#include <algorithm>
+
+#include "attention.h"
+#include "digits.h"
+
+namespace mq {
+
+namespace {
+
+constexpr int kFH = 1024, kFI = 3072, kFD = 128, kFQ = 2048, kFNKV = 8;
+constexpr int kFKB = kFI / 64;             // most 64-element K blocks of a product (down: 3072)
+constexpr int kTileP = 32;                 // positions per product tile: 4 waves x 4 pairs
+constexpr int kFThreads = 256;
+
+// Chunk workspace for Pp positions (a multiple of kTileP). Digit planes are laid out
+// [K block][position][plane][64 bytes], so that the MFMA A operand of a position pair
+// and K block (16 rows of 64 bytes) is 1 KB of contiguous memory.
+struct PfLayout {
+    size_t hid, x, q, m, dig, emax, tok, total;
+};
+constexpr PfLayout pf_layout(size_t Pp) {
+    PfLayout o{};
+    size_t off = 0;
+    o.hid = off; off += round256(Pp * kFH * 2);        // layer input, bf16
+    o.x = off; off += round256(Pp * kFH * 4);          // post-attention residual, fp32
+    o.q = off; off += round256(Pp * kFQ * 4);          // rotated queries, fp32
+    o.m = off; off += round256(Pp * kFI * 4);          // SwiGLU output, fp32
+    o.dig = off; off += round256(Pp * kFKB * 512);     // digit planes of the current product's input
+    o.emax = off; off += round256(Pp * 4);             // their exponents, one per position
+    o.tok = off; off += round256(Pp * 4);              // the chunk's tokens
+    o.total = off;
+    return o;
+}
+constexpr size_t kPfPerPos = pf_layout(1024).total / 1024 + 1;
+
+struct PfArgs {
+    const uint16_t* embed;
+    const LayerWeights* lw;
+    const ScalePointers* sp;
+    const uint16_t* cos_t;
+    const uint16_t* sin_t;
+    uint16_t* kc;
+    uint16_t* vc;
+    int layer, P, Pp, pos0, S;
+    float attn_scale;
+    uint8_t* ws;
+};
+
+enum PfSrc { SRC_EMBED = 0, SRC_HID = 1, SRC_X = 2, SRC_M = 3 };
+enum PfEpi { EPI_QKV = 0, EPI_O = 1, EPI_GU = 2, EPI_DOWN = 3 };
+
+template <class T>
+__device__ __forceinline__ T* pf_buf(const PfArgs& a, size_t off) {
+    return reinterpret_cast<T*>(a.ws + off);
+}
+
+// Digit planes of v (4 consecutive elements k0 .. k0 + 3 of position p) into the
+// chunk's plane buffer.
+__device__ __forceinline__ void store_digits4(uint8_t* dig, int Pp, int p, int k0, const float (&v)[4], uint32_t emax) {
+    int d[4][8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) digits55(v[i], emax, d[i]);
+    uint8_t* base = dig + ((size_t)(k0 / 64) * Pp + p) * 512 + (k0 % 64);
+#pragma unroll
+    for (int pl = 0; pl < 8; ++pl)
+        *reinterpret_cast<uint32_t*>(base + 64 * pl) = pack4(d[0][pl], d[1][pl], d[2][pl], d[3][pl]);
+}
+
+// Largest exponent field over a workgroup of kFThreads threads (uniform result).
+__device__ __forceinline__ uint32_t block_max_u32(uint32_t e, uint32_t* red, int wave, int lane, int nwaves) {
+    e = wave_max_u32(e);
+    if (lane == 0) red[wave] = e;
+    __syncthreads();
+    uint32_t r = red[0];
+    for (int w = 1; w < nwaves; ++w) r = max(r, red[w]);
+    return r;
+}
+
+// ---- row -> (RMSNorm) -> digit planes ------------------------------------------------
+// One workgroup per position. SRC_EMBED / SRC_HID: the layer input (bf16; in layer 0
+// the embedding row of the token, also stored as the layer input), input RMSNorm.
+// SRC_X: the post-attention residual, post-attention RMSNorm. SRC_M: the SwiGLU
+// output, no norm. The normalized value is fp32(r * rstd * gain) as in the decode
+// step (a10_int8_decode_kernel.cu:54-84, :421-457).
+template <int K, int SRC>
+__global__ void __launch_bounds__(kFThreads) pf_digits_kernel(PfArgs a) {
+    constexpr int G = K / 1024;            // groups of 4 consecutive elements per thread
+    static_assert(SRC == SRC_M || G == 1, "the normed rows are hidden-sized");
+    __shared__ double reds[4];
+    __shared__ uint32_t rede[4];
+    const PfLayout L = pf_layout((size_t)a.Pp);
+    const int p = blockIdx.x;
+    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+    float v[G][4];
+    if constexpr (SRC == SRC_EMBED || SRC == SRC_HID) {
+        uint16_t* hid = pf_buf<uint16_t>(a, L.hid) + (size_t)p * kFH;
+        const uint16_t* row = hid;
+        if constexpr (SRC == SRC_EMBED) row = a.embed + (size_t)pf_buf<int>(a, L.tok)[p] * kFH;
+        const uint2 u = *reinterpret_cast<const uint2*>(row + 4 * t);
+        if constexpr (SRC == SRC_EMBED) *reinterpret_cast<uint2*>(hid + 4 * t) = u;
+        v[0][0] = bf16_bits_to_f32(u.x & 0xffffu);
+        v[0][1] = bf16_bits_to_f32(u.x >> 16);
+        v[0][2] = bf16_bits_to_f32(u.y & 0xffffu);
+        v[0][3] = bf16_bits_to_f32(u.y >> 16);
+    } else {
+        const float* row = SRC == SRC_X ? pf_buf<float>(a, L.x) + (size_t)p * kFH : pf_buf<float>(a, L.m) + (size_t)p * K;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float4 f = *reinterpret_cast<const float4*>(row + 1024 * g + 4 * t);
+            v[g][0] = f.x; v[g][1] = f.y; v[g][2] = f.z; v[g][3] = f.w;
+        }
+    }
+    float n[G][4];
+    if constexpr (SRC != SRC_M) {
+        double ss = 0.0;
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ss = fma((double)v[g][i], (double)v[g][i], ss);
+        ss = wave_sum64(ss);
+        if (lane == 0) reds[wave] = ss;
+        __syncthreads();
+        const double rstd = rms_scale((reds[0] + reds[1]) + (reds[2] + reds[3]), K, kEps);
+        const LayerWeights lw = a.lw[a.layer];
+        const uint16_t* gain = static_cast<const uint16_t*>(SRC == SRC_X ? lw.post_attn_layernorm_weight
+                                                                         : lw.input_layernorm_weight);
+        const uint2 gu = *reinterpret_cast<const uint2*>(gain + 4 * t);
+        const float gv[4] = {bf16_bits_to_f32(gu.x & 0xffffu), bf16_bits_to_f32(gu.x >> 16),
+                             bf16_bits_to_f32(gu.y & 0xffffu), bf16_bits_to_f32(gu.y >> 16)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) n[0][i] = (float)((double)v[0][i] * rstd * (double)gv[i]);
+    } else {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) n[g][i] = v[g][i];
+    }
+    uint32_t e = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e = max(e, exp_field(n[g][i]));
+    e = block_max_u32(e, rede, wave, lane, kFThreads / kWave);
+    uint8_t* dig = pf_buf<uint8_t>(a, L.dig);
+#pragma unroll
+    for (int g = 0; g < G; ++g) store_digits4(dig, a.Pp, p, 1024 * g + 4 * t, n[g], e);
+    if (t == 0) pf_buf<uint32_t>(a, L.emax)[p] = e;
+}
+
+// ---- products on the int8 matrix cores -------------------------------------------------
+// Workgroup (row tile rt, position tile pt) of kFThreads threads: wave w takes positions
+// [32 pt + 8 w, +8) (four pairs) and the tile's NT row blocks of 16. Per 64-element K block
+// a wave loads its four A operands (a pair's 8 + 8 digit planes: 1 KB contiguous) and NT B
+// operands (16 weight rows x 64 bytes) and issues 4 NT MFMAs, with the next block's operands
+// in flight. The output tile of pair j, block t: lane l (bit 4 clear) ends with the value of
+// position 2j + l / 32 and weight row 16 t + l % 16 (tile_value).
+//
+// Row tiles: QKV 32 x 128 rows (q heads 0-15, k heads 0-7, v heads 0-7); O and down
+// 16 x 64 rows; gate|up 48 tiles of 64 channels, blocks 0-3 gate rows, 4-7 up rows.
+template <int EPI>
+struct GemmShape {
+    static constexpr int K = EPI == EPI_O ? kFQ : EPI == EPI_DOWN ? kFI : kFH;
+    static constexpr int NT = (EPI == EPI_QKV || EPI == EPI_GU) ? 8 : 4;
+    static constexpr int NRT = EPI == EPI_QKV ? 32 : EPI == EPI_GU ? 48 : 16;
+};
+
+template <int EPI>
+__global__ void __launch_bounds__(kFThreads) pf_gemm_kernel(PfArgs a) {
+    using GS = GemmShape<EPI>;
+    constexpr int K = GS::K, NT = GS::NT, NK = K / 64;
+    const PfLayout L = pf_layout((size_t)a.Pp);
+    const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+    const int rt = blockIdx.x % GS::NRT, pt = blockIdx.x / GS::NRT;
+    const int p0 = kTileP * pt + 8 * w;
+    const int l16 = lane % 16;
+    const LayerWeights lw = a.lw[a.layer];
+    const ScalePointers sp = a.sp[a.layer];
+
+    // the lane's weight row of each block, and its scale
+    const int8_t* wrow[NT];
+    const float* srow[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int8_t* base;
+        const float* sc;
+        int row;
+        if constexpr (EPI == EPI_QKV) {
+            if (rt < 16) { base = (const int8_t*)lw.q_proj_weight; sc = sp.q_scale; row = 128 * rt; }
+            else if (rt < 24) { base = (const int8_t*)lw.k_proj_weight; sc = sp.k_scale; row = 128 * (rt - 16); }
+            else { base = (const int8_t*)lw.v_proj_weight; sc = sp.v_scale; row = 128 * (rt - 24); }
+            row += 16 * t + l16;
+        } else if constexpr (EPI == EPI_GU) {
+            base = (const int8_t*)(t < 4 ? lw.gate_proj_weight : lw.up_proj_weight);
+            sc = t < 4 ? sp.gate_scale : sp.up_scale;
+            row = 64 * rt + 16 * (t % 4) + l16;
+        } else {
+            base = (const int8_t*)(EPI == EPI_O ? lw.o_proj_weight : lw.down_proj_weight);
+            sc = EPI == EPI_O ? sp.o_scale : sp.down_scale;
+            row = 64 * rt + 16 * t + l16;
+        }
+        wrow[t] = base + (size_t)row * K + 16 * (lane / 16);
+        srow[t] = sc + row;
+    }
+    const uint8_t* abase = pf_buf<uint8_t>(a, L.dig) + (size_t)p0 * 512 + l16 * 64 + 16 * (lane / 16);
+    const size_t kstride = (size_t)a.Pp * 512;
+
+    i32x4_t acc[4][NT];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[j][t] = i32x4_t{0, 0, 0, 0};
+    auto load = [&](int kb, i32x4_t (&A)[4], i32x4_t (&B)[NT]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint4 u = ldg16(abase + kb * kstride + 1024 * j);
+            A[j] = i32x4_t{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint4 u = ldg16(wrow[t] + 64 * kb);
+            B[t] = i32x4_t{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+        }
+    };
+    i32x4_t A[4], B[NT];
+    load(0, A, B);
+    for (int kb = 0; kb < NK; ++kb) {
+        i32x4_t An[4], Bn[NT];
+        if (kb + 1 < NK) load(kb + 1, An, Bn);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[j][t] = mfma_i8(A[j], B[t], acc[j][t]);
+        if (kb + 1 < NK) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) A[j] = An[j];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) B[t] = Bn[t];
+        }
+    }
+
+    // ---- epilogue ----
+    const bool owner = (lane & 16) == 0;       // after tile_value: lanes 0-15 (even pair member), 32-47 (odd)
+    const uint32_t* emax = pf_buf<uint32_t>(a, L.emax);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int p = p0 + 2 * j + (lane >> 5);            // chunk position of this lane's values
+        const uint32_t ex = emax[p];                        // p < Pp: in the buffer (padding rows unused)
+        double val[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) val[t] = tile_value(acc[j][t], ex);
+        const bool store = owner && p < a.P;
+        const int pos = a.pos0 + p;
+        if constexpr (EPI == EPI_QKV) {
+            if (rt < 24) {
+                // q or k head: fp32 value, QK RMSNorm over the head's 128 dims (8 blocks in the
+                // lane, 16 lanes of the row), RoPE on the pairs (i, i + 64) = blocks (t, t + 4)
+                float y[8];
+                double ss = 0.0;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    y[t] = (float)(val[t] * (double)*srow[t]);
+                    ss = fma((double)y[t], (double)y[t], ss);
+                }
+                ss += partner64<1>(ss);
+                ss += partner64<2>(ss);
+                ss += partner64<4>(ss);
+                ss += partner64<8>(ss);
+                if (store) {
+                    const double rs = rms_scale(ss, kFD, kEps);
+                    const uint16_t* gn = static_cast<const uint16_t*>(rt < 16 ? lw.q_norm_weight : lw.k_norm_weight);
+                    const uint16_t* cr = a.cos_t + (size_t)pos * kFD;
+                    const uint16_t* sr = a.sin_t + (size_t)pos * kFD;
+                    const int64_t crow = rt < 16 ? 0 : (((int64_t)a.layer * kFNKV + (rt - 16)) * a.S + pos) * kFD;
+                    float* qrow = pf_buf<float>(a, L.q) + (size_t)p * kFQ + 128 * rt;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const int i = 16 * t + l16;
+                        const double y0 = (double)y[t] * rs * (double)bf16_bits_to_f32(gn[i]);
+                        const double y1 = (double)y[t + 4] * rs * (double)bf16_bits_to_f32(gn[i + 64]);
+                        const double cl = bf16_bits_to_f32(cr[i]), ch = bf16_bits_to_f32(cr[i + 64]);
+                        const double sl = bf16_bits_to_f32(sr[i]), sh = bf16_bits_to_f32(sr[i + 64]);
+                        const float o0 = (float)(y0 * cl - y1 * sl);
+                        const float o1 = (float)(y0 * sh + y1 * ch);
+                        if (rt < 16) {
+                            qrow[i] = o0;
+                            qrow[i + 64] = o1;
+                        } else {
+                            a.kc[crow + i] = (uint16_t)f32_to_bf16_bits(o0);
+                            a.kc[crow + i + 64] = (uint16_t)f32_to_bf16_bits(o1);
+                        }
+                    }
+                }
+            } else if (store) {
+                const int64_t crow = (((int64_t)a.layer * kFNKV + (rt - 24)) * a.S + pos) * kFD;
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    a.vc[crow + 16 * t + l16] = (uint16_t)f32_to_bf16_bits((float)(val[t] * (double)*srow[t]));
+            }
+        } else if constexpr (EPI == EPI_O) {
+            if (store) {
+                const uint16_t* hid = pf_buf<uint16_t>(a, L.hid) + (size_t)p * kFH;
+                float* x = pf_buf<float>(a, L.x) + (size_t)p * kFH;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const int n = 64 * rt + 16 * t + l16;
+                    x[n] = (float)(val[t] * (double)*srow[t] + (double)bf16_bits_to_f32(hid[n]));
+                }
+            }
+        } else if constexpr (EPI == EPI_GU) {
+            if (store) {
+                float* m = pf_buf<float>(a, L.m) + (size_t)p * kFI;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const double gs = val[t] * (double)*srow[t];
+                    const double us = val[t + 4] * (double)*srow[t + 4];
+                    m[64 * rt + 16 * t + l16] = (float)silu_mul(gs, us);
+                }
+            }
+        } else {
+            if (store) {
+                const float* x = pf_buf<float>(a, L.x) + (size_t)p * kFH;
+                uint16_t* hid = pf_buf<uint16_t>(a, L.hid) + (size_t)p * kFH;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const int n = 64 * rt + 16 * t + l16;
+                    hid[n] = (uint16_t)f32_to_bf16_bits((float)(val[t] * (double)*srow[t] + (double)x[n]));
+                }
+            }
+        }
+    }
+}
+
+// ---- causal attention ------------------------------------------------------------------
+// One workgroup per position p (8 waves): wave x attends with query heads 2x, 2x + 1 over
+// the cache rows [0, pos0 + p] of KV head x (a10_int8_decode_kernel.cu:298-359), in blocks
+// of 64 keys: lane j takes key j of the block (the 128-dim dot products in fp64 against the
+// rotated queries, read from LDS), an online softmax in fp64 (running maximum and
+// denominator, e^(s - m)), and P V with lane l accumulating dims 2l, 2l + 1 of both heads.
+// The output (fp32, as the reference stores it) then becomes the O product's digit planes.
+__global__ void __launch_bounds__(512) pf_attention_kernel(PfArgs a) {
+    __shared__ double qa[kFNKV][2][kFD];
+    __shared__ __align__(16) float out[kFQ];
+    __shared__ uint32_t rede[8];
+    const PfLayout L = pf_layout((size_t)a.Pp);
+    const int p = blockIdx.x;
+    const int x = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const float* qrow = pf_buf<float>(a, L.q) + (size_t)p * kFQ + 256 * x;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        qa[x][h][lane] = qrow[128 * h + lane];
+        qa[x][h][lane + 64] = qrow[128 * h + lane + 64];
+    }
+    __syncthreads();
+    const int n = a.pos0 + p + 1;
+    const int64_t head = ((int64_t)a.layer * kFNKV + x) * a.S * kFD;
+    const uint16_t* kb = a.kc + head;
+    const uint16_t* vb = a.vc + head;
+    const double sc = (double)a.attn_scale;
+    double M0 = -INFINITY, M1 = -INFINITY, l0 = 0.0, l1 = 0.0;
+    double acc[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
+    for (int j0 = 0; j0 < n; j0 += kWave) {
+        const int j = j0 + lane;
+        const bool valid = j < n;
+        const uint4* krow = reinterpret_cast<const uint4*>(kb + (size_t)(valid ? j : n - 1) * kFD);
+        double s0 = 0.0, s1 = 0.0;
+#pragma unroll 4
+        for (int c = 0; c < 16; ++c) {
+            const uint4 kw = ldg16(krow + c);
+            const uint32_t k4[4] = {kw.x, kw.y, kw.z, kw.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 8 * c + 2 * i;
+                const double klo = bf16_bits_to_f32(k4[i] & 0xffffu), khi = __uint_as_float(k4[i] & 0xffff0000u);
+                s0 = fma(qa[x][0][d], klo, s0);
+                s0 = fma(qa[x][0][d + 1], khi, s0);
+                s1 = fma(qa[x][1][d], klo, s1);
+                s1 = fma(qa[x][1][d + 1], khi, s1);
+            }
+        }
+        s0 = valid ? s0 * sc : -INFINITY;
+        s1 = valid ? s1 * sc : -INFINITY;
+        const double N0 = fmax(M0, wave_max64(s0)), N1 = fmax(M1, wave_max64(s1));
+        const double c0 = exp(M0 - N0), c1 = exp(M1 - N1);     // 0 on the first block (M = -inf)
+        const double e0 = valid ? exp(s0 - N0) : 0.0, e1 = valid ? exp(s1 - N1) : 0.0;
+        l0 = fma(l0, c0, wave_sum64(e0));
+        l1 = fma(l1, c1, wave_sum64(e1));
+        acc[0][0] *= c0; acc[0][1] *= c0;
+        acc[1][0] *= c1; acc[1][1] *= c1;
+        M0 = N0;
+        M1 = N1;
+        const int nb = min(kWave, n - j0);
+        const uint32_t* vrow = reinterpret_cast<const uint32_t*>(vb + (size_t)j0 * kFD) + lane;
+        for (int u0 = 0; u0 < nb; u0 += 8) {
+            uint32_t vw[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) vw[u] = *gview(vrow + (kFD / 2) * min(u0 + u, nb - 1));
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const double q0 = readlane64(e0, u0 + u), q1 = readlane64(e1, u0 + u);   // 0 past the block
+                const double vlo = bf16_bits_to_f32(vw[u] & 0xffffu), vhi = __uint_as_float(vw[u] & 0xffff0000u);
+                acc[0][0] = fma(q0, vlo, acc[0][0]);
+                acc[0][1] = fma(q0, vhi, acc[0][1]);
+                acc[1][0] = fma(q1, vlo, acc[1][0]);
+                acc[1][1] = fma(q1, vhi, acc[1][1]);
+            }
+        }
+    }
+    const double r0 = rcp_nr(l0), r1 = rcp_nr(l1);
+    out[256 * x + 2 * lane] = (float)(acc[0][0] * r0);
+    out[256 * x + 2 * lane + 1] = (float)(acc[0][1] * r0);
+    out[256 * x + 128 + 2 * lane] = (float)(acc[1][0] * r1);
+    out[256 * x + 128 + 2 * lane + 1] = (float)(acc[1][1] * r1);
+    __syncthreads();
+    // digit planes of the 2048 outputs: thread t takes elements [4t, +4)
+    const int t = threadIdx.x;
+    const float4 o = reinterpret_cast<const float4*>(out)[t];
+    const float ov[4] = {o.x, o.y, o.z, o.w};
+    uint32_t e = max(max(exp_field(ov[0]), exp_field(ov[1])), max(exp_field(ov[2]), exp_field(ov[3])));
+    e = block_max_u32(e, rede, x, lane, 8);
+    store_digits4(pf_buf<uint8_t>(a, L.dig), a.Pp, p, 4 * t, ov, e);
+    if (t == 0) pf_buf<uint32_t>(a, L.emax)[p] = e;
+}
+
+}  // namespace
+
+size_t prefill_workspace_bytes(int max_tokens) {
+    if (max_tokens < 1) return 0;
+    const size_t Pp = (size_t)(max_tokens + kTileP - 1) / kTileP * kTileP;
+    return pf_layout(Pp).total;
+}
+
+// Positions one chunk holds in `bytes` of workspace (a multiple of kTileP), 0 if none.
+int prefill_capacity(size_t bytes) {
+    size_t Pp = bytes / kPfPerPos / kTileP * kTileP;
+    while (Pp >= (size_t)kTileP && pf_layout(Pp).total > bytes) Pp -= kTileP;
+    return (int)std::min(Pp, (size_t)1 << 20);
+}
+
+int launch_prefill(const mq_decode_args& d, const int* tokens, int n_tokens, void* ws, size_t ws_bytes,
+                   hipStream_t stream) {
+    const int cap = prefill_capacity(ws_bytes);
+    if (cap < kTileP) return set_error(MQ_ERR_INVALID_ARGUMENT, "prefill workspace of %zu bytes holds no chunk", ws_bytes);
+    PfArgs a{};
+    a.embed = static_cast<const uint16_t*>(d.embed_weight);
+    a.lw = d.layer_weights;
+    a.sp = d.scales;
+    a.cos_t = static_cast<const uint16_t*>(d.cos_table);
+    a.sin_t = static_cast<const uint16_t*>(d.sin_table);
+    a.kc = static_cast<uint16_t*>(d.k_cache);
+    a.vc = static_cast<uint16_t*>(d.v_cache);
+    a.S = d.max_seq_len;
+    a.attn_scale = d.attn_scale;
+    a.ws = static_cast<uint8_t*>(ws);
+    a.Pp = cap;
+    const PfLayout L = pf_layout((size_t)cap);
+    for (int c0 = 0; c0 < n_tokens; c0 += cap) {
+        const int P = std::min(cap, n_tokens - c0);
+        const int PT = (P + kTileP - 1) / kTileP;
+        a.P = P;
+        a.pos0 = d.position + c0;
+        const hipError_t e = hipMemcpyAsync(a.ws + L.tok, tokens + c0, (size_t)P * sizeof(int), hipMemcpyHostToDevice,
+                                            stream);
+        if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipMemcpyAsync(prefill tokens): %s", hipGetErrorString(e));
+        for (int l = 0; l < d.num_layers; ++l) {
+            a.layer = l;
+            if (l == 0) pf_digits_kernel<kFH, SRC_EMBED><<<P, kFThreads, 0, stream>>>(a);
+            else pf_digits_kernel<kFH, SRC_HID><<<P, kFThreads, 0, stream>>>(a);
+            pf_gemm_kernel<EPI_QKV><<<GemmShape<EPI_QKV>::NRT * PT, kFThreads, 0, stream>>>(a);
+            if (l == d.num_layers - 1) break;         // the last layer contributes its cache rows only
+            pf_attention_kernel<<<P, 512, 0, stream>>>(a);
+            pf_gemm_kernel<EPI_O><<<GemmShape<EPI_O>::NRT * PT, kFThreads, 0, stream>>>(a);
+            pf_digits_kernel<kFH, SRC_X><<<P, kFThreads, 0, stream>>>(a);
+            pf_gemm_kernel<EPI_GU><<<GemmShape<EPI_GU>::NRT * PT, kFThreads, 0, stream>>>(a);
+            pf_digits_kernel<kFI, SRC_M><<<P, kFThreads, 0, stream>>>(a);
+            pf_gemm_kernel<EPI_DOWN><<<GemmShape<EPI_DOWN>::NRT * PT, kFThreads, 0, stream>>>(a);
+        }
+        const int st = check_launch("prefill");
+        if (st != MQ_OK) return st;
+    }
+    return MQ_OK;
+}
+
+}  // namespace mq

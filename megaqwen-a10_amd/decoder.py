@@ -357,14 +357,17 @@ class _DecoderBase:
         self._args.temperature = t
         self._args.seed = seed
 
-    def generate(self, prompt_ids, n_tokens: int, device_loop: bool = True) -> list:
+    def generate(self, prompt_ids, n_tokens: int, device_loop: bool = True, batched_prefill: bool = True) -> list:
         """Feed ``prompt_ids`` from the current position and return ``n_tokens`` generated
         tokens, the first being the last prompt step's output (verify_correctness_a10.py:
-        323-339). The tokens follow ``set_sampling``. Within the async-wave kernel's range
-        (INT8, hidden 1024, up to 2048 positions) every step runs in ONE launch and hands its
-        token to the next on the device (mq_int8_decode_generate); otherwise, or with
-        ``device_loop=False``, one launch per step. Both give the same tokens. A failed
-        launch leaves the decoder at the position it started from."""
+        323-339). The tokens follow ``set_sampling``. With ``batched_prefill`` (INT8,
+        hidden 1024) and a prompt of more than ``PREFILL_MIN`` tokens, every prompt token but
+        the last goes through ``prefill`` (each layer's weights read once for the whole
+        prompt); the last prompt token and every generated step are decode steps. Within the async-wave kernel's range (INT8, hidden 1024, up
+        to 2048 positions) those steps run in ONE launch and hand their tokens on on the
+        device (mq_int8_decode_generate); otherwise, or with ``device_loop=False``, one
+        launch per step. All give the same tokens. A failed launch leaves the decoder at
+        the position where its decode steps started."""
         ids = [int(t) for t in prompt_ids]
         V = self.dims[2]
         if not ids:
@@ -376,6 +379,9 @@ class _DecoderBase:
         if self._pos + len(ids) + n_tokens - 1 > self.max_seq_len:
             raise ValueError(f"position {self._pos} + {len(ids) + n_tokens - 1} steps exceed max_seq_len "
                              f"{self.max_seq_len}")
+        if batched_prefill and len(ids) - 1 >= self.PREFILL_MIN and self.prefill_supported():
+            self.prefill(ids[:-1])
+            ids = ids[-1:]
         if device_loop and self._int8 and not self._fp8:
             out = self._generate_one_launch(ids, n_tokens)
             if out is not None:
@@ -388,6 +394,61 @@ class _DecoderBase:
             tok = self.decode_step(tok)
             out.append(tok)
         return out
+
+    PREFILL_CHUNK = 512      # positions per prefill chunk (workspace ~51 KB per position)
+    # shortest prompt prefix generate() sends through prefill(): the prefill's ~220 launches cost
+    # about as much as 8 decode steps in one launch, so shorter prompts run as decode steps
+    PREFILL_MIN = 32
+
+    def prefill_supported(self) -> bool:
+        """Whether ``prefill`` runs for this decoder (INT8 weights, hidden 1024)."""
+        return self._int8 and not self._fp8 and self.dims[:2] == (1024, 3072)
+
+    def prefill(self, token_ids) -> None:
+        """Write the K/V cache rows of ``token_ids`` at the next positions, as that many
+        decode steps would (a10_decode.py:367-368), with each layer's weights read once
+        for the whole prompt (mq_int8_prefill: products of all positions on the int8
+        matrix cores, causal attention in fp64). No token is produced: the decode step of
+        the following token gives the next output. Runs in chunks of ``PREFILL_CHUNK``
+        positions. Asynchronous on the current stream."""
+        ids = [int(t) for t in token_ids]
+        if not ids:
+            return
+        if not self.prefill_supported():
+            raise ValueError("prefill runs for INT8 weights of hidden 1024 / intermediate 3072 only")
+        V = self.dims[2]
+        if any(not 0 <= t < V for t in ids):
+            raise ValueError(f"token outside [0, {V})")
+        if self._pos + len(ids) > self.max_seq_len:
+            raise ValueError(f"positions {self._pos} + {len(ids)} exceed max_seq_len {self.max_seq_len}")
+        stream = _lib.stream_handle(self.device)
+        if self._inflight:
+            # steps in flight store into their token words when they end: let them land first
+            torch.cuda.current_stream(self.device).synchronize()
+            self._inflight.clear()
+        cap = min(self.PREFILL_CHUNK, (len(ids) + 63) // 64 * 64)
+        if getattr(self, "_pf_cap", 0) < cap:
+            nbytes = self._lib.mq_prefill_workspace_bytes(ctypes.byref(self._dims), cap)
+            if nbytes == 0:
+                raise ValueError(f"prefill: {_lib.last_error()}")
+            self._pf_ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+            self._pf_cap = cap
+        if getattr(self, "_pf_tokens", None) is None:
+            # pinned token list, reused: the library copies each chunk's tokens from it on the stream
+            self._pf_tokens = torch.empty(self.max_seq_len, dtype=torch.int32, pin_memory=True)
+            self._pf_done = torch.cuda.Event()
+        else:
+            self._pf_done.synchronize()          # the previous prefill's token copies have run
+        self._pf_tokens.numpy()[:len(ids)] = ids
+        a = self._args
+        a.position = self._pos
+        a.cache_len = self._pos + 1
+        st = self._lib.mq_int8_prefill(ctypes.byref(a), ctypes.c_void_p(self._pf_tokens.data_ptr()), len(ids),
+                                       ctypes.c_void_p(self._pf_ws.data_ptr()), self._pf_ws.numel(),
+                                       ctypes.c_void_p(stream))
+        self._pf_done.record(torch.cuda.current_stream(self.device))
+        _lib.check(st, "mq_int8_prefill")
+        self._pos += len(ids)
 
     def _generate_one_launch(self, ids, n_tokens):
         """mq_int8_decode_generate; None when the kernel's range does not cover the request."""
@@ -770,11 +831,12 @@ class A10Decoder:
         self.decoder.reset()
 
     def generate(self, prompt, max_new_tokens: int = 128, temperature: float = 0.0, seed: int = 0,
-                 device_loop: bool = True):
+                 device_loop: bool = True, batched_prefill: bool = True):
         """Generation from a string (needs a tokenizer) or a list of ids. The prompt is
-        prefilled one step per token and the last prefill output is the first generated
-        token (verify_correctness_a10.py:323-339; a10_decode.py:375 re-feeds the last prompt
-        token instead, which decodes it twice). ``temperature`` 0 is greedy; above 0 tokens
+        prefilled as by one decode step per token (INT8: all but its last token in one
+        prompt-batched pass, ``batched_prefill``) and the last prompt token's decode step
+        gives the first generated token (verify_correctness_a10.py:323-339; a10_decode.py:375
+        re-feeds the last prompt token instead, which decodes it twice). ``temperature`` 0 is greedy; above 0 tokens
         are sampled from softmax(logits / temperature) with ``seed`` (the reference accepts
         a temperature and ignores it, a10_decode.py:358). Within the INT8 async-wave
         kernel's range every step runs in one launch (``device_loop``), else one launch per
@@ -798,7 +860,7 @@ class A10Decoder:
         eos = getattr(self.tokenizer, "eos_token_id", None)
         torch.cuda.synchronize(self.device)
         t0 = time.perf_counter()
-        toks = self.decoder.generate(ids, max_new_tokens, device_loop=device_loop)
+        toks = self.decoder.generate(ids, max_new_tokens, device_loop=device_loop, batched_prefill=batched_prefill)
         torch.cuda.synchronize(self.device)
         ms = (time.perf_counter() - t0) * 1e3
         if eos is not None and eos in toks:
