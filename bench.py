@@ -532,6 +532,20 @@ def run_positions(args, mq, torch):
         nbytes = sum(cfg.bf16_step_bytes(cache_len=pos_state + i + 1) for i in range(marg))
         marginal[str(p0)] = {"tok_s": round(marg / wall, 1), "kernel_avg_us": round(kern_s / marg * 1e6, 2),
                              "hbm_frac": round(nbytes / kern_s / 1e9 / HBM_PEAK_GBS, 4)}
+    # the same greedy decoding as ONE launch (the XCD-aware kernel's multi-step form): the
+    # prompt and 200 generated steps, wall time of the call
+    dev_loop = {}
+    for _ in range(3):
+        dec.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        got1 = dec.generate(prompt, max(positions) + 1, device_loop=True, batched_prefill=False)
+        dt = time.perf_counter() - t0
+        steps1 = len(prompt) + max(positions)
+        if not dev_loop or steps1 / dt > dev_loop["tok_s"]:
+            dev_loop = {"tok_s": round(steps1 / dt, 1), "ms_per_step": round(dt * 1e3 / steps1, 4),
+                        "steps": steps1, "tokens_match_per_step_launches": got1 == tokens,
+                        "entry_point": "mq_bf16_decode_generate: one launch for the prompt and all generated steps"}
     parity = None
     fx = ROOT / "tests" / "golden" / "tokens_qwen3_0.6b_bf16.json"
     if fx.exists() and args.seed == 0:
@@ -549,6 +563,7 @@ def run_positions(args, mq, torch):
                        "marginal_at_position": marginal,
                        "marginal_method": f"{marg} steps from the position; tok/s from wall with one read-back per step; "
                                           + KERNEL_TIMING},
+            "device_loop": dev_loop,
             "parity": parity}
 
 

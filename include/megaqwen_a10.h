@@ -163,10 +163,8 @@ typedef struct mq_decode_args {
  * prefill step's output is the first generated token, the convention of
  * verify_correctness_a10.py:323-339) and args->output_token_id the last one.
  * args->input_token_id must equal prompt_tokens[0] and cache_len position + 1.
- * Runs on the async-wave kernel: INT8 Qwen3-0.6B layer shapes and
- * position + n_forced + n_generate - 1 <= 2048; otherwise MQ_ERR_UNSUPPORTED
- * (nothing launched), and a loop over mq_int8_decode_step gives the same
- * tokens, sampled ones included. */
+ * A loop over the one-step entry point of the same weight format gives the
+ * same tokens and KV cache, sampled tokens included. */
 typedef struct mq_generate_args {
     const int* prompt_tokens;         /* HOST int32[n_forced], each in [0, vocab_size)        */
     int n_forced;                     /* >= 1                                                 */
@@ -263,8 +261,14 @@ int mq_fp8_decode_step(const mq_decode_args* args, hipStream_t stream);
  * library allocation). Every call on a device shares that device's array:
  * calls that overlap on one device (other streams, other threads) race. */
 int mq_int8_decode_step_noalloc(const mq_decode_args* args, hipStream_t stream);
-/* Several steps per launch (see mq_generate_args). */
+/* Several steps per launch (see mq_generate_args): INT8, bf16 and FP8 weights.
+ * The async-wave kernel runs the launch within its range (INT8 Qwen3-0.6B shape,
+ * position + steps <= 2048), the XCD-aware kernel's multi-step form otherwise
+ * (every compiled shape and format, up to 32768 positions with split attention);
+ * MQ_ERR_UNSUPPORTED on the single-level kernel. */
 int mq_int8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream);
+int mq_bf16_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream);
+int mq_fp8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream);
 /* Prompt-batched prefill. The reference prefills a prompt one decode step per
  * token (a10_decode.py:367-368, verify_correctness_a10.py:326-328, each step
  * a10_int8_decode_kernel.cu:821-842); this writes the same K/V cache rows with

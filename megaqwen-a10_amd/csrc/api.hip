@@ -320,8 +320,10 @@ int mq_int8_decode_step_noalloc(const mq_decode_args* args, hipStream_t stream) 
     return launch_decode(a, s, true, stream);
 }
 
-int mq_int8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream) {
-    clear_error();
+// Several steps in one launch (mq_generate_args), any weight format: the async-wave kernel
+// within its range, else the XCD-aware kernel's multi-step instantiation.
+static int decode_generate(const mq_decode_args* args, const mq_generate_args* gen, bool int8, bool fp8,
+                           hipStream_t stream) {
     if (args == nullptr || gen == nullptr) return set_error(MQ_ERR_INVALID_ARGUMENT, "args is NULL");
     if (gen->prompt_tokens == nullptr || gen->output_tokens == nullptr)
         return set_error(MQ_ERR_INVALID_ARGUMENT, "prompt_tokens and output_tokens must be non-NULL");
@@ -329,29 +331,43 @@ int mq_int8_decode_generate(const mq_decode_args* args, const mq_generate_args* 
         return set_error(MQ_ERR_INVALID_ARGUMENT, "n_forced %d and n_generate %d must be >= 1", gen->n_forced,
                          gen->n_generate);
     DecodeShape s;
-    int st = validate_decode(args, true, &s);
+    int st = validate_decode(args, int8, &s);
     if (st != MQ_OK) return st;
+    s.fp8 = fp8;
     if (args->input_token_id != gen->prompt_tokens[0])
         return set_error(MQ_ERR_INVALID_ARGUMENT, "input_token_id %d != prompt_tokens[0] %d", args->input_token_id,
                          gen->prompt_tokens[0]);
-    for (int i = 0; i < gen->n_forced; ++i)
-        if (gen->prompt_tokens[i] < 0 || gen->prompt_tokens[i] >= s.V)
-            return set_error(MQ_ERR_INVALID_ARGUMENT, "prompt_tokens[%d] = %d outside [0, %d)", i, gen->prompt_tokens[i], s.V);
     const int64_t n_steps = (int64_t)gen->n_forced + gen->n_generate - 1;
     if (args->position + n_steps > args->max_seq_len)
         return set_error(MQ_ERR_INVALID_ARGUMENT, "position %d + %lld steps exceed max_seq_len %d", args->position,
                          (long long)n_steps, args->max_seq_len);
-    const size_t off = decode_async_token_offset(s);
-    if (off == 0 || args->position + n_steps > decode_async_max_len())
-        return set_error(MQ_ERR_UNSUPPORTED, "several steps per launch run on the async-wave kernel only (INT8, hidden "
-                         "1024 / intermediate 3072, up to %d positions; here %lld)", decode_async_max_len(),
-                         (long long)(args->position + n_steps));
-    int* dev_tokens = reinterpret_cast<int*>(static_cast<uint8_t*>(args->workspace) + off);
+    if (n_steps > kDecodeMaxForced)
+        return set_error(MQ_ERR_UNSUPPORTED, "%lld steps in one launch: at most %d", (long long)n_steps,
+                         kDecodeMaxForced);
+    for (int i = 0; i < gen->n_forced; ++i)
+        if (gen->prompt_tokens[i] < 0 || gen->prompt_tokens[i] >= s.V)
+            return set_error(MQ_ERR_INVALID_ARGUMENT, "prompt_tokens[%d] = %d outside [0, %d)", i, gen->prompt_tokens[i], s.V);
+    int* dev_tokens = reinterpret_cast<int*>(static_cast<uint8_t*>(args->workspace) + decode_token_offset(s));
     const hipError_t e = hipMemcpyAsync(dev_tokens, gen->prompt_tokens, (size_t)gen->n_forced * sizeof(int),
                                         hipMemcpyHostToDevice, stream);
     if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipMemcpyAsync(prompt tokens): %s", hipGetErrorString(e));
     const GenPlan plan{dev_tokens, gen->n_forced, (int)n_steps, gen->output_tokens};
-    return launch_decode(*args, s, true, stream, nullptr, &plan);
+    return launch_decode(*args, s, int8, stream, nullptr, &plan);
+}
+
+int mq_int8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream) {
+    clear_error();
+    return decode_generate(args, gen, true, false, stream);
+}
+
+int mq_bf16_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream) {
+    clear_error();
+    return decode_generate(args, gen, false, false, stream);
+}
+
+int mq_fp8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream) {
+    clear_error();
+    return decode_generate(args, gen, true, true, stream);
 }
 
 size_t mq_prefill_workspace_bytes(const mq_model_dims* dims, int max_tokens) {

@@ -591,13 +591,13 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
                   const GenPlan* plan) {
     if (a.num_layers > kMaxLayers)
         return set_error(MQ_ERR_UNSUPPORTED, "num_layers %d exceeds %d", a.num_layers, kMaxLayers);
-    // several steps per launch: the async-wave kernel, over every position the launch covers
+    // several steps per launch: the kernel chosen for the longest cache the launch reaches (the
+    // async-wave kernel within its range, else the XCD-aware kernel; not the single-level one)
     const int variant = decode_variant_for(s, int8, plan ? a.position + plan->n_steps : a.cache_len);
     if (variant < 0) return -variant;
-    if (plan && variant != 3)
-        return set_error(MQ_ERR_UNSUPPORTED, "several steps per launch run on the async-wave kernel only (INT8, hidden "
-                         "1024 / intermediate 3072, up to %d positions; here %d)", decode_async_max_len(),
-                         a.position + plan->n_steps);
+    if (plan && variant == 1)
+        return set_error(MQ_ERR_UNSUPPORTED, "several steps per launch run on the async-wave and XCD-aware kernels, "
+                         "not on the single-level kernel");
     // split attention: the XCD kernel with a slice of at most kMaxAttnLen positions per
     // workgroup; the async-wave kernel with slices of at most 64 (its own threshold)
     int split_min = a.attn_split_min == 0 ? kDefaultSplitMin : a.attn_split_min;

@@ -87,7 +87,7 @@ enum AArr { AR_A = 0, AR_B = 1, AR_C = 2, AR_E = 3, AR_F = 4 };
 // of squares (low and high word each), so that one buffer load reaches both.
 constexpr int kVecWords = kAH + 64;
 struct ALayout {
-    size_t qkvx, hidx, actx, mlpx, po, pd, lmg, apart, amrg, tok, total;
+    size_t qkvx, hidx, actx, mlpx, po, pd, lmg, apart, amrg, total;
 };
 // After the other two kernels' regions, so that the three can alternate on one workspace.
 constexpr ALayout alayout_for(size_t base) {
@@ -102,7 +102,6 @@ constexpr ALayout alayout_for(size_t base) {
     o.lmg = off; off += round256((size_t)kNWG * 2 * 8);
     o.apart = off; off += round256((size_t)kAX * kARanks * kAPart * 2 * 8);   // split attention partials (fp64 as two tagged words)
     o.amrg = off; off += round256((size_t)kAX * 2 * kAD * 8);             // merged outputs [xcd][dim]
-    o.tok = off; off += round256((size_t)kASplitLen * 4);      // a launch's forced input tokens
     o.total = off;
     return o;
 }
@@ -1293,11 +1292,6 @@ int launch_decode_async(const KArgs& ka, bool debug, hipStream_t stream, hipEven
     const hipError_t e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
     if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode_async): %s", hipGetErrorString(e));
     return MQ_OK;
-}
-
-size_t decode_async_token_offset(const DecodeShape& s) {
-    if (s.H != kAH || s.I != kAI) return 0;
-    return alayout_for(xlayout_total(kAH, kAI)).tok;
 }
 
 int decode_async_max_len() { return kASplitLen; }

@@ -109,7 +109,7 @@ constexpr uint32_t kXStages = 8;
 constexpr int kAttWords = 2 * 256 + 2 * 3;
 
 struct XLayout {
-    size_t qkvx, actx, mlpx, hidx, lmg, po, pd, attp, atto, total;
+    size_t qkvx, actx, mlpx, hidx, lmg, po, pd, attp, atto, tokw, tok, total;
 };
 // The regions follow the single-level kernel's (layout_for), so neither kernel
 // writes words the other could take for its own: the packed words below carry
@@ -126,6 +126,8 @@ constexpr XLayout xlayout_for(int H, int I) {
     o.pd = off; off += round256((size_t)kNX * H * 8);
     o.attp = off; off += round256((size_t)kNX * kGS * kAttWords * 8);
     o.atto = off; off += round256((size_t)kNX * 256 * 8);
+    o.tokw = off; off += 256;                                   // a multi-step launch's token word
+    o.tok = off; off += round256((size_t)kSplitRanks * kMaxAttnLen * 4);   // a launch's forced input tokens
     o.total = off;
     return o;
 }

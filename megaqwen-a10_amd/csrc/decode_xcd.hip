@@ -66,7 +66,11 @@ __device__ __forceinline__ void gather_xcd(Waiter& wt, const uint64_t* base, uin
         *reinterpret_cast<float2*>(&dst[2 * (lane + 64 * i)]) = make_float2(v[2 * i], v[2 * i + 1]);
 }
 
-template <int H, int I, class W, bool kDebug>
+// kMulti: a launch's steps in sequence (a.n_steps; step s decodes at position a.pos + s, its
+// input token is a.step_tokens[s] for the first a.n_forced steps and the previous step's
+// output after them, which workgroup (0, 0) hands to every workgroup through one tagged
+// word); otherwise one step, and the step loop disappears.
+template <int H, int I, class W, bool kDebug, bool kMulti = false>
 __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     constexpr int D = 128;
     constexpr int ES = W::kBytes;
@@ -110,7 +114,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     // loading, turning the prefetch into a wait), so it has no such path: its slices come
     // from the rows prefetched a layer ahead up to kKvLds positions, and from the cache
     // inside the loop beyond that.
-    constexpr bool kSliceRegs = kInt8;
+    constexpr bool kSliceRegs = kInt8 && !kMulti;       // (the multi-step form has no registers to spare either)
     constexpr int kSlice = !kSliceRegs ? kKvLds : H <= 1024 ? 320 : 256;
     __shared__ __align__(16) AttnShared<kSlice> at;
     __shared__ float lm_v[kWaves];
@@ -119,16 +123,45 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     __shared__ LayerWeights s_lw[kMaxLayers];
     __shared__ ScalePointers s_sp[kMaxLayers];
 
-    const int g = blockIdx.x;
-    const int x = (int)hw_xcc_id();
-    const int r = g / kNX;
-    const int tid = threadIdx.x;
-    const int lane = tid % kWave;
-    const int wave = tid / kWave;
+    const int g0 = blockIdx.x;
+    const int x0 = (int)hw_xcc_id();
+    const int tid0 = threadIdx.x;
     double* xdf = reinterpret_cast<double*>(xd);
     float* xsf = reinterpret_cast<float*>(xs);
 
     WsHeader* hdr = reinterpret_cast<WsHeader*>(a.ws);
+
+    // step-independent reads first
+    int token = (kMulti && a.step_tokens) ? *gview(a.step_tokens) : a.token;
+    float hv0[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) hv0[i] = bf16_bits_to_f32(gview(a.embed)[(int64_t)token * H + tid0 + i * kThreads]);
+    {
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.lw);
+        uint64_t* dst = reinterpret_cast<uint64_t*>(s_lw);
+        for (int i = tid0; i < a.L * 11; i += kThreads) dst[i] = src[i];
+        if (kInt8) {
+            const uint64_t* ssrc = reinterpret_cast<const uint64_t*>(a.sp);
+            uint64_t* sdst = reinterpret_cast<uint64_t*>(s_sp);
+            for (int i = tid0; i < a.L * 7; i += kThreads) sdst[i] = ssrc[i];
+        }
+    }
+    const uint32_t E0 = __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t XS0 = __hip_atomic_load(&hdr->xsteps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    Waiter wt(&hdr->abort_flag, a.spin_limit);
+    // A device with other than 8 XCDs cannot run this kernel: flag it (the waits
+    // then end at once and the host switches to the single-level kernel).
+    if (x0 >= kNX) {
+        if (tid0 == 0) __hip_atomic_store(&hdr->abort_flag, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+
+    const int n_steps = kMulti ? a.n_steps : 1;
+    for (int step = 0; step < n_steps; ++step) {
+    const int g = g0, x = x0;
+    const int r = g / kNX;
+    const int64_t kv_head_stride = (int64_t)a.S * D;
+    const int last = a.L - 1;
     uint64_t* const qkvx = reinterpret_cast<uint64_t*>(a.ws + kLay.qkvx) + (size_t)x * GR;
     uint64_t* const actx = reinterpret_cast<uint64_t*>(a.ws + kLay.actx) + (size_t)x * H;
     uint64_t* const mlpx = reinterpret_cast<uint64_t*>(a.ws + kLay.mlpx) + (size_t)x * IX;
@@ -138,28 +171,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     uint64_t* const pd = reinterpret_cast<uint64_t*>(a.ws + kLay.pd);    // packed [8][H]
     uint64_t* const attp = reinterpret_cast<uint64_t*>(a.ws + kLay.attp) + (size_t)x * kGS * kAttWords;
     uint64_t* const atto = reinterpret_cast<uint64_t*>(a.ws + kLay.atto) + (size_t)x * AD;
-
-    // step-independent reads first
-    float hv0[PT];
-#pragma unroll
-    for (int i = 0; i < PT; ++i) hv0[i] = bf16_bits_to_f32(gview(a.embed)[(int64_t)a.token * H + tid + i * kThreads]);
-    {
-        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.lw);
-        uint64_t* dst = reinterpret_cast<uint64_t*>(s_lw);
-        for (int i = tid; i < a.L * 11; i += kThreads) dst[i] = src[i];
-        if (kInt8) {
-            const uint64_t* ssrc = reinterpret_cast<const uint64_t*>(a.sp);
-            uint64_t* sdst = reinterpret_cast<uint64_t*>(s_sp);
-            for (int i = tid; i < a.L * 7; i += kThreads) sdst[i] = ssrc[i];
-        }
-    }
-    const uint32_t E = __hip_atomic_load(&hdr->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t XS = __hip_atomic_load(&hdr->xsteps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (g == 0 && tid == 0) {
-        // keep the header slots the single-level kernel counts on in a known state
-        __hip_atomic_store(&hdr->done[(E + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&hdr->best[(E + 1) & 1], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    uint64_t* const tokw = reinterpret_cast<uint64_t*>(a.ws + kLay.tokw);
+    const int tid = tid0;
+    const int lane = tid % kWave;
+    const int wave = tid / kWave;
+    const uint32_t E = E0 + (uint32_t)step;      // the step's epoch (tags) and packed-word step count
+    const uint32_t XS = XS0 + (uint32_t)step;
     const uint32_t tps = kXStages * (uint32_t)a.L + 4u;
     // tags end in binary 11 (the single-level kernel's end in 01): no overlap when
     // the two kernels share a workspace
@@ -167,25 +184,22 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     // one-bit tag of the packed cross-XCD words: po and pd are each written once
     // per layer, so their use count is XS * L + l + 1
     auto pbit = [&](int l) -> uint32_t { return (XS * (uint32_t)a.L + (uint32_t)l + 1u) & 1u; };
-    Waiter wt(&hdr->abort_flag, a.spin_limit);
     auto trace = [&](int l, int point) {
         if (kDebug && a.trace != nullptr && tid == 0)
             a.trace[((int64_t)l * kTracePoints + point) * kNWG + g] = __builtin_amdgcn_s_memrealtime();
     };
-    // A device with other than 8 XCDs cannot run this kernel: flag it (the waits
-    // then end at once and the host switches to the single-level kernel).
-    if (x >= kNX) {
-        if (tid == 0) __hip_atomic_store(&hdr->abort_flag, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
+    const int pos = a.pos + step;
+    const int cache_len = pos + 1;
+    if (g == 0 && tid == 0) {
+        // keep the header slots the single-level kernel counts on in a known state
+        __hip_atomic_store(&hdr->done[(E + 1) & 1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&hdr->best[(E + 1) & 1], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-
-    const int64_t kv_head_stride = (int64_t)a.S * D;
-    const int last = a.L - 1;
     // attention positions of this workgroup: all of them, or the r-th slice
-    const bool split = a.cache_len >= a.split_min;
-    const int cs = (a.cache_len + kGS - 1) / kGS;
-    const int sj0 = split ? min(a.cache_len, r * cs) : 0;
-    const int sj1 = split ? min(a.cache_len, sj0 + cs) : a.cache_len;
+    const bool split = cache_len >= a.split_min;
+    const int cs = (cache_len + kGS - 1) / kGS;
+    const int sj0 = split ? min(cache_len, r * cs) : 0;
+    const int sj1 = split ? min(cache_len, sj0 + cs) : cache_len;
     // split slices of at most kKvLds positions come wholly from the rows
     // prefetched during the previous layer (spre); up to kSlice positions, the
     // K rows go straight to LDS and the V words to registers ahead of the QKV
@@ -194,7 +208,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     const bool sdma = kSliceRegs && split && !spre && cs <= kSlice;
     // the range's first npre earlier positions prefetched into registers, staged
     // in LDS (the current one comes from the QKV words)
-    const int npre = sdma ? 0 : max(0, min(kKvLds, min(sj1, a.pos) - sj0));
+    const int npre = sdma ? 0 : max(0, min(kKvLds, min(sj1, pos) - sj0));
     const int R0 = RPW * r;                 // first O / down row of this workgroup
     const double attn_scale = (double)a.attn_scale;
     __syncthreads();
@@ -226,7 +240,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     // Stage B's step-independent inputs for a layer, loaded one stage ahead of
     // its QKV wait: O weights (consumed in stage C), the O scale, the QK-norm
     // gains and the K/V rows of the range's first npre positions.
-    const int crow = tid / LPR, clr = tid % LPR;   // stages C and F: row, lane in the row's group
+    const int crow_s = tid / LPR, clr_s = tid % LPR;   // stages C and F: row, lane in the row's group
     constexpr int kPreU4 = 2 * kKvLds * (D / 8) / kThreads;
     uint4 wo[PPL_O];
     uint4 pre[kPreU4];
@@ -245,7 +259,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             nw1 = ldg_bits(nw + lane + 64);
         }
     };
-    auto prefetch_b = [&](int ll) {
+    // t: the calling thread's index as the caller holds it (with several steps, rederived per
+    // layer, so that the addresses below are not held through the layer loop)
+    auto prefetch_b = [&](int ll, int t) {
+        const int crow = kMulti ? t / LPR : crow_s, clr = kMulti ? t % LPR : clr_s;
         const LayerWeights& lw = s_lw[ll];
         const uint8_t* ob = (const uint8_t*)lw.o_proj_weight;
 #pragma unroll
@@ -259,9 +276,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         const int64_t cb = ((int64_t)ll * kNX + x) * kv_head_stride + (int64_t)opaque(sj0) * D;
 #pragma unroll
         for (int i = 0; i < kPreU4; ++i) {
-            const int f = tid + i * kThreads;
-            const int side = f / (kKvLds * (D / 8));
-            const int rem = f % (kKvLds * (D / 8));
+            // K rows for the first half of the i, V rows for the second: a uniform choice (the
+            // thread index is below kThreads, which divides kKvLds * D / 8), so the cache pointer
+            // stays a scalar
+            static_assert((kKvLds * (D / 8)) % kThreads == 0, "prefetch split");
+            const int side = i * kThreads / (kKvLds * (D / 8));
+            const int rem = ((kMulti ? t : tid) + i * kThreads) % (kKvLds * (D / 8));
             const int j = rem / (D / 8), c = rem % (D / 8);
             pre[i] = make_uint4(0, 0, 0, 0);
             if (j < npre) pre[i] = ldg16((side == 0 ? a.kc : a.vc) + cb + (int64_t)j * D + c * 8);
@@ -272,18 +292,18 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
     uint32_t c0 = 0, s0 = 0, c1 = 0, s1 = 0;
     if constexpr (kLateInputs) {
         if (tid < 2 * D) {
-            const uint16_t* row = (tid < D ? a.cos_t : a.sin_t) + (int64_t)a.pos * D;
+            const uint16_t* row = (tid < D ? a.cos_t : a.sin_t) + (int64_t)pos * D;
             rope_s[tid / D][tid % D] = ldg_bits(row + tid % D);
         }
     } else if (wave < 3) {
-        const uint16_t* ct = a.cos_t + (int64_t)a.pos * D;
-        const uint16_t* stt = a.sin_t + (int64_t)a.pos * D;
+        const uint16_t* ct = a.cos_t + (int64_t)pos * D;
+        const uint16_t* stt = a.sin_t + (int64_t)pos * D;
         c0 = ldg_bits(ct + lane);
         s0 = ldg_bits(stt + lane);
         c1 = ldg_bits(ct + lane + 64);
         s1 = ldg_bits(stt + lane + 64);
     }
-    prefetch_b(0);
+    prefetch_b(0, tid);
 
     uint32_t wfn[PT];                       // final RMSNorm gains (raw bits, loaded in the last layer)
     const int tid_all = tid;
@@ -296,6 +316,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         // derived from it were spilled to scratch, and each reload (its line evicted from L2
         // by the layer's weight stream) waited for memory
         const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+        const int crow = kMulti ? tid / LPR : crow_s, clr = kMulti ? tid % LPR : clr_s;
         // bf16: stage B's QK-norm gains, at the start of stage A (no exchange poll before
         // their use, so the loads overlap stage A's work)
         if constexpr (kLateInputs) load_gains(lw);
@@ -348,8 +369,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             SliceRegs<kSlice> sr;
             if (sdma) {
                 const int oj0 = opaque(sj0);
-                attn_slice_k(at, a.kc + cache_base, oj0, min(sj1, a.pos), lane, tid / kWave);
-                attn_slice_v(sr, a.vc + cache_base, oj0, min(sj1, a.pos), lane, tid / kWave);
+                attn_slice_k(at, a.kc + cache_base, oj0, min(sj1, pos), lane, tid / kWave);
+                attn_slice_v(sr, a.vc + cache_base, oj0, min(sj1, pos), lane, tid / kWave);
             }
             {
                 float v1[1];
@@ -359,7 +380,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             if (sdma) wait_vmem();              // the K rows are in LDS after the barrier
             __syncthreads();
             trace(l, 2);
-            const int64_t cur = cache_base + (int64_t)a.pos * D;
+            const int64_t cur = cache_base + (int64_t)pos * D;
             const bool writer = (r == 0);           // rank 0 writes the cache rows
             const bool dbg = kDebug && writer && l == last;
             if constexpr (kLateInputs) {
@@ -374,7 +395,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                          wave, lane, spre || sdma);
             __syncthreads();
             if (!split) {
-                attn_core(at, a.kc + cache_base, a.vc + cache_base, sj1, a.pos, attn_scale, tid, lane, wave,
+                attn_core(at, a.kc + cache_base, a.vc + cache_base, sj1, pos, attn_scale, tid, lane, wave,
                           [&](int i, float v) {
                               attn_d[piece_index(i, EPP, PC_O)] = v;
                               if (dbg && a.dbg_attn) a.dbg_attn[AD * x + i] = v;
@@ -396,11 +417,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                     }
                 };
                 if (spre) {
-                    attn_partial_lds(at, sj0, sj1, a.pos, attn_scale, tid, lane, wave, publish, [](int) {});
+                    attn_partial_lds(at, sj0, sj1, pos, attn_scale, tid, lane, wave, publish, [](int) {});
                 } else if (sdma) {
-                    attn_partial_regs(at, sr, sj0, sj1, a.pos, attn_scale, tid, lane, wave, publish, [](int) {});
+                    attn_partial_regs(at, sr, sj0, sj1, pos, attn_scale, tid, lane, wave, publish, [](int) {});
                 } else
-                    attn_partial(at, a.kc + cache_base, a.vc + cache_base, sj0, sj1, a.pos, attn_scale, tid, lane,
+                    attn_partial(at, a.kc + cache_base, a.vc + cache_base, sj0, sj1, pos, attn_scale, tid, lane,
                                  wave, publish, [](int) {});
                 // merge output dims [8r, 8r+8) (query head r / 16) over the 32
                 // partials: thread (s, k) reads word k of rank s's slice, and
@@ -597,7 +618,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             // the next layer's stage B inputs: after the hidden gather, so that
             // neither exchange waits for them; stage A covers their latency
             issue_fence();
-            if (l < last) prefetch_b(l + 1);
+            if (l < last) prefetch_b(l + 1, tid);
             trace(l, 9);
         }
     }
@@ -659,7 +680,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
             if ((lane % span) == 0 && row < r1) {
                 float v = kInt8 ? s * scur : s;
                 // sampling: the Gumbel-max rule (see gumbel_noise)
-                if (a.inv_temp > 0.0f) v = v * a.inv_temp + gumbel_noise(a.seed, a.pos, row);
+                if (a.inv_temp > 0.0f) v = v * a.inv_temp + gumbel_noise(a.seed, pos, row);
                 if (v > best_v) { best_v = v; best_i = row; }
             }
 #pragma unroll
@@ -714,14 +735,40 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 #undef MQ_KEY_LEVEL
             if (lane == 0) {
                 const uint32_t flag = __hip_atomic_load(&hdr->abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                *a.out_token = (flag != 0u || wt.dead) ? -1 : (int)iv;
-                if (a.status_out) *a.status_out = flag != 0u ? flag : (wt.dead ? 1u : 0u);
-                __hip_atomic_store(&hdr->xsteps, XS + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(&hdr->epoch, E + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (kDebug && a.trace != nullptr)
-                    a.trace[((int64_t)a.L * kTracePoints + 2) * kNWG] = __builtin_amdgcn_s_memrealtime();
+                const int chosen = (flag != 0u || wt.dead) ? -1 : (int)iv;
+                if constexpr (kMulti) {
+                    // the next step's input, for every workgroup (a failed step's -1 becomes 0
+                    // there, which keeps the remaining steps' reads in bounds; they report -1)
+                    if (step + 1 < n_steps && step + 1 >= a.n_forced) ll_put(tokw, (uint32_t)max(chosen, 0), tag(a.L, 1));
+                    if (a.tokens_out != nullptr && step >= a.n_forced - 1) a.tokens_out[step - (a.n_forced - 1)] = chosen;
+                }
+                if (step == n_steps - 1) {
+                    *a.out_token = chosen;
+                    if (a.status_out) *a.status_out = flag != 0u ? flag : (wt.dead ? 1u : 0u);
+                    __hip_atomic_store(&hdr->xsteps, XS0 + (uint32_t)n_steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(&hdr->epoch, E0 + (uint32_t)n_steps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (kDebug && a.trace != nullptr)
+                        a.trace[((int64_t)a.L * kTracePoints + 2) * kNWG] = __builtin_amdgcn_s_memrealtime();
+                }
             }
         }
+    }
+    if constexpr (kMulti) {
+        if (step + 1 < n_steps) {
+            // the next step's input token: forced, or this step's output from workgroup (0, 0)
+            if (step + 1 < a.n_forced) {
+                token = *gview(a.step_tokens + step + 1);
+            } else {
+                if (tid == 0) lm_i[0] = (int)wt.get(tokw, tag(a.L, 1));
+                __syncthreads();
+                token = min(max(lm_i[0], 0), a.V - 1);      // an expired wait returns a stale word
+            }
+            issue_fence();
+#pragma unroll
+            for (int i = 0; i < PT; ++i)
+                hv0[i] = bf16_bits_to_f32(gview(a.embed)[(int64_t)token * H + opaque(tid) + i * kThreads]);
+        }
+    }
     }
 }
 
@@ -729,10 +776,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
 
 size_t decode_xcd_workspace_bytes(const DecodeShape& s) { return xlayout_for(s.H, s.I).total; }
 
+size_t decode_token_offset(const DecodeShape& s) {
+    static_assert(kSplitRanks * kMaxAttnLen == kDecodeMaxForced, "forced-token region");
+    return xlayout_for(s.H, s.I).tok;
+}
+
 template <int H, int I, class W>
 static int launch_xcd_t(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
-    auto fn = debug ? reinterpret_cast<const void*>(&decode_xcd_kernel<H, I, W, true>)
-                    : reinterpret_cast<const void*>(&decode_xcd_kernel<H, I, W, false>);
+    // several steps: the multi-step instantiation (without the debug outputs, which hold one step's values)
+    auto fn = ka.n_steps > 1 ? reinterpret_cast<const void*>(&decode_xcd_kernel<H, I, W, false, true>)
+              : debug        ? reinterpret_cast<const void*>(&decode_xcd_kernel<H, I, W, true>)
+                             : reinterpret_cast<const void*>(&decode_xcd_kernel<H, I, W, false>);
     int st = check_residency(fn);
     if (st != MQ_OK) return st;
     KArgs copy = ka;

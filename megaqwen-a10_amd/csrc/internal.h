@@ -66,9 +66,11 @@ struct GenPlan {
 // (0 = completed).
 int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipStream_t stream,
                   uint32_t* status_out = nullptr, const GenPlan* plan = nullptr);
-// Byte offset of the async-wave kernel's forced-token region in the workspace (0 when the
-// kernel does not cover these dims), and the longest cache it attends over.
-size_t decode_async_token_offset(const DecodeShape& s);
+// Byte offset in the workspace of a multi-step launch's forced input tokens (room for
+// kDecodeMaxForced of them, whichever kernel runs the launch), and the longest cache the
+// async-wave kernel attends over.
+constexpr int kDecodeMaxForced = 32768;
+size_t decode_token_offset(const DecodeShape& s);
 int decode_async_max_len();
 int decode_async_split_min(int attn_split_min);
 // True when the workgroups of each residue class g mod 8 run on one XCD (checked once per device).

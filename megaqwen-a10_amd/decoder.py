@@ -363,11 +363,13 @@ class _DecoderBase:
         323-339). The tokens follow ``set_sampling``. With ``batched_prefill`` (INT8,
         hidden 1024) and a prompt of more than ``PREFILL_MIN`` tokens, every prompt token but
         the last goes through ``prefill`` (each layer's weights read once for the whole
-        prompt); the last prompt token and every generated step are decode steps. Within the async-wave kernel's range (INT8, hidden 1024, up
-        to 2048 positions) those steps run in ONE launch and hand their tokens on on the
-        device (mq_int8_decode_generate); otherwise, or with ``device_loop=False``, one
-        launch per step. All give the same tokens. A failed launch leaves the decoder at
-        the position where its decode steps started."""
+        prompt); the last prompt token and every generated step are decode steps. With
+        ``device_loop`` those steps run in ONE launch and hand their tokens on on the device
+        (mq_int8/bf16/fp8_decode_generate: the async-wave kernel within its range, else the
+        XCD-aware kernel's multi-step form); with ``device_loop=False``, or where neither
+        kernel runs (the single-level fallback), one launch per step. All give the same
+        tokens. A failed launch leaves the decoder at the position where its decode steps
+        started."""
         ids = [int(t) for t in prompt_ids]
         V = self.dims[2]
         if not ids:
@@ -382,7 +384,7 @@ class _DecoderBase:
         if batched_prefill and len(ids) - 1 >= self.PREFILL_MIN and self.prefill_supported():
             self.prefill(ids[:-1])
             ids = ids[-1:]
-        if device_loop and self._int8 and not self._fp8:
+        if device_loop:
             out = self._generate_one_launch(ids, n_tokens)
             if out is not None:
                 return out
@@ -451,7 +453,7 @@ class _DecoderBase:
         self._pos += len(ids)
 
     def _generate_one_launch(self, ids, n_tokens):
-        """mq_int8_decode_generate; None when the kernel's range does not cover the request."""
+        """mq_int8/bf16/fp8_decode_generate; None when no multi-step kernel covers the request."""
         if self._inflight:
             torch.cuda.current_stream(self.device).synchronize()
             self._inflight.clear()
@@ -464,18 +466,19 @@ class _DecoderBase:
         a.output_token_id = self.output_token.data_ptr()
         self._tok_host[0] = TOKEN_PENDING
         g = _lib.GenerateArgs(ctypes.cast(prompt, ctypes.c_void_p), len(ids), n_tokens, out.data_ptr())
-        st = self._lib.mq_int8_decode_generate(ctypes.byref(a), ctypes.byref(g),
-                                               ctypes.c_void_p(_lib.stream_handle(self.device)))
+        fn = (self._lib.mq_fp8_decode_generate if self._fp8 else
+              self._lib.mq_int8_decode_generate if self._int8 else self._lib.mq_bf16_decode_generate)
+        st = fn(ctypes.byref(a), ctypes.byref(g), ctypes.c_void_p(_lib.stream_handle(self.device)))
         if st == _lib.MQ_ERR_UNSUPPORTED:
             return None
-        _lib.check(st, "mq_int8_decode_generate")
+        _lib.check(st, "decode generate")
         torch.cuda.current_stream(self.device).synchronize()
         toks = out.tolist()
         if min(toks) < 0:
             status = self._lib.mq_decode_check(self.workspace.data_ptr(),
                                                ctypes.c_void_p(_lib.stream_handle(self.device)))
             self._init_workspace()
-            _lib.check(status if status != _lib.MQ_OK else _lib.MQ_ERR_TIMEOUT, "mq_int8_decode_generate")
+            _lib.check(status if status != _lib.MQ_OK else _lib.MQ_ERR_TIMEOUT, "decode generate")
         self._pos += len(ids) + n_tokens - 1
         return toks
 

@@ -7,7 +7,8 @@ greedy tokens from one launch; one launch and one launch per step agreeing
 bitwise (tokens and KV caches), greedy and sampled; sampled tokens against the
 float64 oracle's Gumbel-max choice wherever its top-2 margin exceeds fp32
 logit error; a launch past one workgroup's 64-position slot (split attention);
-the fallback beyond the async-wave kernel's 2048 positions;
+one launch past the async-wave kernel's 2048 positions (the XCD-aware kernel's
+multi-step form);
 argument validation; a forced in-kernel wait expiry that leaves the decoder
 where it started; a P-token prefill in one launch (P = 8 and 64) whose whole KV
 cache and first generated token match the oracle's per-token prefill
@@ -122,20 +123,32 @@ def test_one_launch_past_one_slot(mq, dev, small):
     torch.cuda.empty_cache()
 
 
-def test_beyond_kernel_range_falls_back(mq, dev, small):
-    """Past the async-wave kernel's 2048 positions generate() loops over single steps (the
-    XCD-aware kernel) and gives the per-step tokens."""
+def test_one_launch_beyond_async_range(mq, dev, small):
+    """Past the async-wave kernel's 2048 positions the launch runs on the XCD-aware kernel's
+    multi-step form (split attention): one launch equals one launch per step on that kernel,
+    tokens and caches. (Per-step launches below 2048 positions would take the async-wave
+    kernel, whose split attention rounds differently in the last fp32 bits: same tokens here,
+    a few cache values one bf16 ulp apart.)"""
     dec0, d, prompt, cfg, keep = small
     embed, layers, scales, lm_q, lm_s, fnorm, _, _ = keep
     S = 2048 + 16
     cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
     dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
     n = S - len(prompt) + 1
-    assert dec._generate_one_launch(prompt, n) is None           # nothing launched
-    assert dec.position() == 0
-    got = dec.generate(prompt, n)
+    print(f"2-layer model: {len(prompt)} + {n - 1} steps in one launch past 2048 positions", flush=True)
+    got = dec._generate_one_launch(prompt, n)
+    assert got is not None
     assert dec.position() == S
-    assert got == _greedy(dec, prompt, n)
+    k1, v1 = _caches(dec)
+    mq.set_decode_variant("xcd")
+    try:
+        assert got == _greedy(dec, prompt, n)
+    finally:
+        mq.set_decode_variant("auto")
+    k2, v2 = _caches(dec)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    del dec
+    torch.cuda.empty_cache()
 
 
 def test_generate_validation(small):
