@@ -435,7 +435,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         //   d = 1: slots C and F (O and down rows, their scales)
         //   d = 2: slot E (gate|up rows, post-attention norm gains, scales)
         //   d = 3: slot B (cached K and V rows of positions [0, pos), QK-norm gains), and
-        //          once per step this position's RoPE row and the final norm gains
+        //          once per step this position's RoPE row and the final norm gains; it also
+        //          stores the position's new K and V rows into the cache (store_row)
         const int d = wave - kCW;
         auto await_free = [&](int slot, int l) {
             lds_wait(&S.sync[kConsumed + slot], (uint32_t)(kCW * l), lds_limit, &hdr->abort_flag);
@@ -447,6 +448,27 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         };
         auto ld32 = [&](const void* q) -> uint32_t { return *gview(static_cast<const uint32_t*>(q)); };
         auto put32 = [&](void* base, int word, uint32_t v) { static_cast<uint32_t*>(base)[word] = v; };
+        // The cache row of this step's position in layer ll: the owner compute wave put it in
+        // slot B (K chunks permuted); one rank per XCD stores it from there once the compute
+        // waves have released the slot (rank 0, or with split attention the rank whose slice
+        // holds the position). The store is issued here rather than by the owner wave: a
+        // compute wave's stores count against the same counter as its exchange polls, and
+        // the owner's store held its rank's attention back by about 0.75 us per layer.
+        auto store_row = [&](int ll) {
+            int s0, ns;
+            const bool sp_ = attn_slice(pos, s0, ns);
+            if (!(sp_ ? (pos >= s0 && pos < s0 + ns) : r == 0)) return;
+            const int pl = pos - s0;
+            const int ls = opaque(lane);
+            const int64_t row = ((int64_t)ll * kAX + x) * kv_head_stride + (int64_t)pos * D;
+            if (ls < 16) {
+                const uint4 kw = reinterpret_cast<const uint4*>(S.kvk[pl])[ls ^ (pl % 16)];
+                *reinterpret_cast<uint4*>(a.kc + row + 8 * ls) = kw;
+            } else if (ls < 32) {
+                const uint4 vw = reinterpret_cast<const uint4*>(S.kvv[pl])[ls - 16];
+                *reinterpret_cast<uint4*>(a.vc + row + 8 * (ls - 16)) = vw;
+            }
+        };
         for (int l = 0; l < a.L; ++l) {
             const int gl = step * a.L + l;
             if (gl > 0) lds_wait(&S.sync[kWindow], (uint32_t)gl, lds_limit, &hdr->abort_flag);
@@ -559,6 +581,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 const uint32_t cw = l == 0 ? ld32(a.cos_t + (int64_t)pos * D + 2 * ln) : 0u;
                 const uint32_t sw = l == 0 ? ld32(a.sin_t + (int64_t)pos * D + 2 * ln) : 0u;
                 await_free(SL_B, gl);
+                if (l > 0) store_row(l - 1);
                 const int ls = opaque(ln);
 #pragma unroll
                 for (int i = 0; i < kAMaxLen / 4; ++i) {
@@ -576,6 +599,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 }
                 raise(SL_B, gl);
             }
+        }
+        if (d == 3) {
+            // the step's last layer, once its attention has released slot B
+            await_free(SL_B, (step + 1) * a.L);
+            store_row(a.L - 1);
         }
     } else {
         // =============================== compute waves ================================
@@ -722,7 +750,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 }
                 if (owner) {
                     // this position's K and V rows, into the LDS copies the loops below read
-                    // (K chunks permuted as the loader stores them) and, once per XCD, the cache
+                    // (K chunks permuted as the loader stores them), from where the KV loader
+                    // of one rank per XCD stores them into the cache
                     float kr[2];
                     rope(rms_scale(ssk, D, kEps), kv2, bf16_bits_to_f32(S.qkn[1][lane]),
                          bf16_bits_to_f32(S.qkn[1][lane + 64]), kr);
@@ -732,11 +761,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     S.kvk[pl][8 * ((lane >> 3) ^ p16) + (lane & 7)] = (uint16_t)k0;
                     S.kvk[pl][8 * (((lane + 64) >> 3) ^ p16) + (lane & 7)] = (uint16_t)k1;
                     reinterpret_cast<uint32_t*>(S.kvv[pl])[lane] = vw;
+                    // (the KV loader stores the row into the cache from this slot: store_row)
                     if (split || r == 0) {
-                        const int64_t cur = ((int64_t)l * kAX + x) * kv_head_stride + (int64_t)pos * D;
-                        a.kc[cur + lane] = (uint16_t)k0;
-                        a.kc[cur + lane + 64] = (uint16_t)k1;
-                        reinterpret_cast<uint32_t*>(a.vc + cur)[lane] = vw;
                         const bool dbgkv = kDebug && l == last;
                         if (dbgkv && a.dbg_k) { a.dbg_k[x * D + lane] = kr[0]; a.dbg_k[x * D + lane + 64] = kr[1]; }
                         if (dbgkv && a.dbg_v) { a.dbg_v[x * D + 2 * lane] = vv[0]; a.dbg_v[x * D + 2 * lane + 1] = vv[1]; }
