@@ -631,6 +631,42 @@ def _prefill_ops(cfg, P):
     return 2 * 8 * Pp * (L * qkv + (L - 1) * rest)
 
 
+PREFILL_PHASES = ("input_digits", "qkv", "attention", "o", "post_attn_digits", "gate_up", "swiglu_digits", "down")
+
+
+def _prefill_phases(dec, ids, torch):
+    """Phase timeline of the prefill's last chunk (the kernel's optional trace, 100 MHz clock):
+    per phase, the time from the grid barrier before it (the last workgroup out) to the last
+    workgroup done, and the barrier after it (last workgroup done to last workgroup out);
+    microseconds averaged over layers 1 .. L-2 and 3 prefills."""
+    import numpy as np
+    L = dec.num_layers
+    ncu = torch.cuda.get_device_properties(dec.device).multi_processor_count
+    buf = torch.zeros(L * 16 * ncu, dtype=torch.int64, device=dec.device)
+    split = len(ids) - (len(ids) - 1) % dec.PREFILL_CHUNK - 1         # all chunks but the last untraced
+    recs = []
+    for _ in range(3):
+        dec.reset()
+        if split:
+            dec.prefill(ids[:split])
+        dec.set_prefill_trace(buf)
+        buf.zero_()
+        dec.prefill(ids[split:])
+        dec.set_prefill_trace(None)
+        torch.cuda.synchronize()
+        recs.append(buf.view(L, 16, ncu).cpu().numpy().astype(np.float64) / 100.0)
+    T = np.stack(recs)[:, :L - 1]
+    out = {}
+    for k, name in enumerate(PREFILL_PHASES):
+        done, passed = T[:, 1:, 2 * k, :], T[:, 1:, 2 * k + 1, :]
+        start = T[:, :-1, 15, :] if k == 0 else T[:, 1:, 2 * k - 1, :]
+        work = (done.max(axis=2) - start.max(axis=2)).mean()
+        barrier = (passed.max(axis=2) - done.max(axis=2)).mean()
+        out[name] = [round(float(work), 1), round(float(barrier), 1)]
+    out["layer"] = round(float((T[:, 1:, 15, :].max(axis=2) - T[:, :-1, 15, :].max(axis=2)).mean()), 1)
+    return out
+
+
 def run_prefill(args, mq, torch):
     """Prompt-batched prefill: the K/V cache rows of a P-token prompt of the config-1
     model written by A10Int8MegakernelDecoder.prefill (each layer's weights once for all P positions),
@@ -689,7 +725,8 @@ def run_prefill(args, mq, torch):
             "mfma_digit_tops": round(ops / (dev_ms / 1e3) / 1e12, 1),
             "mfma_frac": round(ops / (dev_ms / 1e3) / 1e12 / INT8_PEAK_TOPS, 4),
             "weight_GBs": round(w_bytes / (dev_ms / 1e3) / 1e9, 1),
-            "kv_rows_identical_to_per_token_steps": round(same, 6), "reps": reps}
+            "kv_rows_identical_to_per_token_steps": round(same, 6), "reps": reps,
+            "last_chunk_phase_us_work_barrier": _prefill_phases(dec, ids, torch)}
         print(f"prefill P={P}: {per_len[str(P)]}", file=sys.stderr, flush=True)
     head = str(512 if 512 in lens else max(lens))
     top = per_len[head]

@@ -134,7 +134,15 @@ typedef struct mq_decode_args {
      * 5 residual rows gathered, 6 gate/up output written, 7 SwiGLU outputs
      * gathered, 8 down partial written, 9 hidden rows gathered.
      * Layer num_layers holds p = 0 final-norm input ready, p = 1 LM head done,
-     * and [(L*10 + 2) * 256] the token publication. */
+     * and [(L*10 + 2) * 256] the token publication.
+     * mq_int8_prefill: uint64 [num_layers * 16 * G], G = the prefill grid
+     * (one workgroup per compute unit, 256 on MI355X); entry
+     * [(l * 16 + 2 k + e) * G + g] is when workgroup g finished phase k of
+     * layer l (e = 0) or passed the grid barrier after it (e = 1); phases
+     * 0 input digit planes, 1 QKV, 2 attention, 3 O, 4 post-attention digit
+     * planes, 5 gate/up, 6 SwiGLU digit planes, 7 down; the last layer
+     * writes points 0-2 only. A prefill of several chunks leaves the last
+     * chunk's timeline. */
     void* trace;
     /* Attention split (XCD-aware kernel): from cache_len >= attn_split_min on,
      * each of the 32 workgroups sharing a KV head attends over 1/32 of the
@@ -281,10 +289,15 @@ int mq_fp8_decode_generate(const mq_decode_args* args, const mq_generate_args* g
  * INT8 Qwen3-0.6B shape only (MQ_ERR_UNSUPPORTED otherwise). workspace: device
  * memory of mq_prefill_workspace_bytes(dims, m) bytes, 16-byte aligned; a
  * longer prompt runs in chunks of m positions (m rounded up to a multiple of
- * 32). Asynchronous on `stream`. */
+ * 32), one persistent launch per chunk (one workgroup per compute unit, grid
+ * barriers between its phases). Asynchronous on `stream`. */
 size_t mq_prefill_workspace_bytes(const mq_model_dims* dims, int max_tokens);
 int mq_int8_prefill(const mq_decode_args* args, const int* tokens, int n_tokens, void* workspace,
                     size_t workspace_bytes, hipStream_t stream);
+/* After mq_int8_prefill: synchronises `stream`; MQ_ERR_TIMEOUT if the prefill's
+ * grid-wide waits expired (its launch needs every compute unit; args->spin_limit
+ * bounds each wait), else MQ_OK. The cache rows are then unusable: prefill again. */
+int mq_prefill_check(void* workspace, size_t workspace_bytes, hipStream_t stream);
 /* Host-side wait for a token the kernel stores into host memory (pinned, e.g.
  * hipHostMalloc): spins until *token differs from `sentinel`, which the
  * caller wrote before the launch. MQ_OK, or MQ_ERR_TIMEOUT after timeout_us

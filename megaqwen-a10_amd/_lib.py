@@ -115,6 +115,7 @@ _SIGNATURES = {
     "mq_fp8_decode_generate": (c_int, [POINTER(DecodeArgs), POINTER(GenerateArgs), c_void_p]),
     "mq_prefill_workspace_bytes": (c_size_t, [POINTER(ModelDims), c_int]),
     "mq_int8_prefill": (c_int, [POINTER(DecodeArgs), c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
+    "mq_prefill_check": (c_int, [c_void_p, c_size_t, c_void_p]),
     "mq_decode_check": (c_int, [c_void_p, c_void_p]),
     "mq_wait_host_token": (c_int, [c_void_p, c_int, c_uint]),
     "mq_decode_set_variant": (c_int, [c_int]),

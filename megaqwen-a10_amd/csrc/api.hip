@@ -429,6 +429,12 @@ int mq_int8_prefill(const mq_decode_args* a, const int* tokens, int n_tokens, vo
     return launch_prefill(*a, tokens, n_tokens, workspace, workspace_bytes, stream);
 }
 
+int mq_prefill_check(void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    clear_error();
+    if (!workspace) return set_error(MQ_ERR_INVALID_ARGUMENT, "workspace is NULL");
+    return prefill_check(workspace, workspace_bytes, stream);
+}
+
 int mq_wait_host_token(const volatile int* token, int sentinel, unsigned int timeout_us) {
     clear_error();
     if (!token) return set_error(MQ_ERR_INVALID_ARGUMENT, "token is NULL");

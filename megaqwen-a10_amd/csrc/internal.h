@@ -84,6 +84,9 @@ size_t prefill_workspace_bytes(int max_tokens);
 int prefill_capacity(size_t bytes);
 int launch_prefill(const mq_decode_args& d, const int* tokens, int n_tokens, void* ws, size_t ws_bytes,
                    hipStream_t stream);
+// After the prefill launches on `stream` (synchronises it): MQ_ERR_TIMEOUT if a grid barrier of the
+// last chunk expired, else MQ_OK.
+int prefill_check(void* ws, size_t ws_bytes, hipStream_t stream);
 
 // Batched INT8 decode (decode_batch.hip).
 size_t decode_batch_workspace_bytes(const DecodeShape& s);

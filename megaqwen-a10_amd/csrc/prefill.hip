@@ -13,22 +13,24 @@
 // cache rows equal those of P decode steps, apart from fp32 roundings that the
 // fp64 summation order can move once in about 2^20 values.
 //
-// Per layer, eight launches over the chunk (P rows each):
+// One persistent launch per chunk (a workgroup per compute unit, all resident); per layer
+// eight phases over the chunk's P positions, separated by grid barriers:
 //   digits      RMSNorm of the layer input (the embedding rows in layer 0), its
 //               digit planes                                 one workgroup per position
 //   QKV         q|k|v rows on the matrix cores; the epilogue runs QK-norm and RoPE
 //               and writes this layer's K/V cache rows and the rotated queries
 //               (a 128-row tile is one head, so the norm and the rotation pairs
 //               are inside one wave)                        tiles of 32 positions x 128 rows
-//   attention   causal, fp64, one wave per (position, KV head) over cache rows
-//               [0, pos0 + p]; the output's digit planes
+//   attention   causal, fp64, a workgroup per position, each wave two KV heads over
+//               cache rows [0, pos0 + p]; the output's digit planes
 //   O           + residual (the layer input)                 32 positions x 64 rows
 //   digits      post-attention RMSNorm
 //   gate|up     64 channels' gate and up rows per tile; SwiGLU in the epilogue
 //   digits      of the SwiGLU output
 //   down        + residual, bf16: the next layer's input
 // The last layer stops after its cache rows. The first generated token comes from
-// the decode step of the last prompt token, as in the reference's loop.
+// the decode step of the last prompt token, as in the reference's loop. A phase's work
+// items (positions or product tiles) are dealt round-robin over the workgroups.
 #include <algorithm>
 
 #include "attention.h"
@@ -47,11 +49,12 @@ constexpr int kFThreads = 256;
 // [K block][position][plane][64 bytes], so that the MFMA A operand of a position pair
 // and K block (16 rows of 64 bytes) is 1 KB of contiguous memory.
 struct PfLayout {
-    size_t hid, x, q, m, dig, emax, tok, total;
+    size_t sync, hid, x, q, m, dig, emax, tok, total;
 };
 constexpr PfLayout pf_layout(size_t Pp) {
     PfLayout o{};
     size_t off = 0;
+    o.sync = off; off += 1024;                         // grid-barrier counters, abort flag
     o.hid = off; off += round256(Pp * kFH * 2);        // layer input, bf16
     o.x = off; off += round256(Pp * kFH * 4);          // post-attention residual, fp32
     o.q = off; off += round256(Pp * kFQ * 4);          // rotated queries, fp32
@@ -72,13 +75,54 @@ struct PfArgs {
     const uint16_t* sin_t;
     uint16_t* kc;
     uint16_t* vc;
-    int layer, P, Pp, pos0, S;
+    int layer, P, Pp, pos0, S, L;
     float attn_scale;
+    uint32_t spin_limit;
     uint8_t* ws;
+    uint64_t* trace;                       // optional phase timeline (kPfTracePoints per layer)
+};
+
+// Grid-barrier state. Counters are cumulative over a launch (zeroed before it), each on a
+// 64-byte line of its own.
+constexpr int kPfXcd = 8;
+constexpr int kPfTracePoints = 16;            // phase k of a layer: 2 k phase done, 2 k + 1 barrier passed
+struct PfSync {
+    uint32_t count;                        // XCD leaders that reached the current barrier
+    uint32_t abort;                        // set when a barrier wait expired
+    uint32_t pad0[14];
+    struct {
+        uint32_t arrived;                  // workgroups of the XCD that reached the current barrier
+        uint32_t released;                 // the last barrier the XCD's leader has passed
+        uint32_t pad[14];
+    } xcd[kPfXcd];
+};
+static_assert(sizeof(PfSync) <= 1024, "barrier state");
+
+// LDS of a workgroup, shared by the phases
+struct PfShared {
+    double qa[kFNKV][2][kFD];              // attention: the rotated queries of each KV head's two heads
+    __align__(16) float out[kFQ];          // attention: the position's outputs
+    double reds[4];
+    uint32_t rede[4];
 };
 
 enum PfSrc { SRC_EMBED = 0, SRC_HID = 1, SRC_X = 2, SRC_M = 3 };
 enum PfEpi { EPI_QKV = 0, EPI_O = 1, EPI_GU = 2, EPI_DOWN = 3 };
+
+// The kernel runs every phase of every layer in one body. Values that depend only on the
+// thread or workgroup index are the same in every layer, and the compiler would otherwise
+// compute them once, before the layer loop, and keep them all live through every phase (more
+// than the register file holds). Reading the index through an empty volatile asm makes it
+// new in each phase, so each phase computes what it needs at its start.
+__device__ __forceinline__ int pf_fresh(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+__device__ __forceinline__ int pf_fresh_uniform(int v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
 
 template <class T>
 __device__ __forceinline__ T* pf_buf(const PfArgs& a, size_t off) {
@@ -108,20 +152,19 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t e, uint32_t* red, int
 }
 
 // ---- row -> (RMSNorm) -> digit planes ------------------------------------------------
-// One workgroup per position. SRC_EMBED / SRC_HID: the layer input (bf16; in layer 0
+// One work item per position. SRC_EMBED / SRC_HID: the layer input (bf16; in layer 0
 // the embedding row of the token, also stored as the layer input), input RMSNorm.
 // SRC_X: the post-attention residual, post-attention RMSNorm. SRC_M: the SwiGLU
 // output, no norm. The normalized value is fp32(r * rstd * gain) as in the decode
 // step (a10_int8_decode_kernel.cu:54-84, :421-457).
 template <int K, int SRC>
-__global__ void __launch_bounds__(kFThreads) pf_digits_kernel(PfArgs a) {
+__device__ void pf_digits(const PfArgs& a, int p, PfShared& sh) {
     constexpr int G = K / 1024;            // groups of 4 consecutive elements per thread
     static_assert(SRC == SRC_M || G == 1, "the normed rows are hidden-sized");
-    __shared__ double reds[4];
-    __shared__ uint32_t rede[4];
+    double* const reds = sh.reds;
+    uint32_t* const rede = sh.rede;
     const PfLayout L = pf_layout((size_t)a.Pp);
-    const int p = blockIdx.x;
-    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+    const int t = pf_fresh(threadIdx.x), lane = t % kWave, wave = t / kWave;
     float v[G][4];
     if constexpr (SRC == SRC_EMBED || SRC == SRC_HID) {
         uint16_t* hid = pf_buf<uint16_t>(a, L.hid) + (size_t)p * kFH;
@@ -179,7 +222,7 @@ __global__ void __launch_bounds__(kFThreads) pf_digits_kernel(PfArgs a) {
 }
 
 // ---- products on the int8 matrix cores -------------------------------------------------
-// Workgroup (row tile rt, position tile pt) of kFThreads threads: wave w takes positions
+// Work item (row tile rt, position tile pt) of a workgroup of kFThreads threads: wave w takes positions
 // [32 pt + 8 w, +8) (four pairs) and the tile's NT row blocks of 16. Per 64-element K block
 // a wave loads its four A operands (a pair's 8 + 8 digit planes: 1 KB contiguous) and NT B
 // operands (16 weight rows x 64 bytes) and issues 4 NT MFMAs, with the next block's operands
@@ -196,12 +239,12 @@ struct GemmShape {
 };
 
 template <int EPI>
-__global__ void __launch_bounds__(kFThreads) pf_gemm_kernel(PfArgs a) {
+__device__ void pf_gemm(const PfArgs& a, int tile) {
     using GS = GemmShape<EPI>;
     constexpr int K = GS::K, NT = GS::NT, NK = K / 64;
     const PfLayout L = pf_layout((size_t)a.Pp);
-    const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
-    const int rt = blockIdx.x % GS::NRT, pt = blockIdx.x / GS::NRT;
+    const int tid = pf_fresh(threadIdx.x), lane = tid % kWave, w = tid / kWave;
+    const int rt = tile % GS::NRT, pt = tile / GS::NRT;
     const int p0 = kTileP * pt + 8 * w;
     const int l16 = lane % 16;
     const LayerWeights lw = a.lw[a.layer];
@@ -362,95 +405,230 @@ __global__ void __launch_bounds__(kFThreads) pf_gemm_kernel(PfArgs a) {
 }
 
 // ---- causal attention ------------------------------------------------------------------
-// One workgroup per position p (8 waves): wave x attends with query heads 2x, 2x + 1 over
-// the cache rows [0, pos0 + p] of KV head x (a10_int8_decode_kernel.cu:298-359), in blocks
-// of 64 keys: lane j takes key j of the block (the 128-dim dot products in fp64 against the
-// rotated queries, read from LDS), an online softmax in fp64 (running maximum and
-// denominator, e^(s - m)), and P V with lane l accumulating dims 2l, 2l + 1 of both heads.
-// The output (fp32, as the reference stores it) then becomes the O product's digit planes.
-__global__ void __launch_bounds__(512) pf_attention_kernel(PfArgs a) {
-    __shared__ double qa[kFNKV][2][kFD];
-    __shared__ __align__(16) float out[kFQ];
-    __shared__ uint32_t rede[8];
+// One work item per position p: wave w attends for KV heads w and w + 4, each with its two
+// query heads, over the cache rows [0, pos0 + p] (a10_int8_decode_kernel.cu:298-359), in
+// blocks of 64 keys: lane j takes key j of the block (the 128-dim dot products in fp64
+// against the rotated queries, read from LDS), an online softmax in fp64 (running maximum
+// and denominator, e^(s - m)), and P V with lane l accumulating dims 2l, 2l + 1 of both
+// heads. The output (fp32, as the reference stores it) then becomes the O product's digit
+// planes.
+__device__ void pf_attention(const PfArgs& a, int p, PfShared& sh) {
     const PfLayout L = pf_layout((size_t)a.Pp);
-    const int p = blockIdx.x;
-    const int x = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-    const float* qrow = pf_buf<float>(a, L.q) + (size_t)p * kFQ + 256 * x;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        qa[x][h][lane] = qrow[128 * h + lane];
-        qa[x][h][lane + 64] = qrow[128 * h + lane + 64];
-    }
-    __syncthreads();
+    const int tid = pf_fresh(threadIdx.x), w = tid / kWave, lane = tid % kWave;
     const int n = a.pos0 + p + 1;
-    const int64_t head = ((int64_t)a.layer * kFNKV + x) * a.S * kFD;
-    const uint16_t* kb = a.kc + head;
-    const uint16_t* vb = a.vc + head;
     const double sc = (double)a.attn_scale;
-    double M0 = -INFINITY, M1 = -INFINITY, l0 = 0.0, l1 = 0.0;
-    double acc[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
-    for (int j0 = 0; j0 < n; j0 += kWave) {
-        const int j = j0 + lane;
-        const bool valid = j < n;
-        const uint4* krow = reinterpret_cast<const uint4*>(kb + (size_t)(valid ? j : n - 1) * kFD);
-        double s0 = 0.0, s1 = 0.0;
-#pragma unroll 4
-        for (int c = 0; c < 16; ++c) {
-            const uint4 kw = ldg16(krow + c);
-            const uint32_t k4[4] = {kw.x, kw.y, kw.z, kw.w};
+#pragma unroll 1
+    for (int hh = 0; hh < 2; ++hh) {
+        const int x = w + 4 * hh;
+        const float* qrow = pf_buf<float>(a, L.q) + (size_t)p * kFQ + 256 * x;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int d = 8 * c + 2 * i;
-                const double klo = bf16_bits_to_f32(k4[i] & 0xffffu), khi = __uint_as_float(k4[i] & 0xffff0000u);
-                s0 = fma(qa[x][0][d], klo, s0);
-                s0 = fma(qa[x][0][d + 1], khi, s0);
-                s1 = fma(qa[x][1][d], klo, s1);
-                s1 = fma(qa[x][1][d + 1], khi, s1);
+        for (int h = 0; h < 2; ++h) {
+            sh.qa[x][h][lane] = qrow[128 * h + lane];
+            sh.qa[x][h][lane + 64] = qrow[128 * h + lane + 64];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int64_t head = ((int64_t)a.layer * kFNKV + x) * a.S * kFD;
+        const uint16_t* kb = a.kc + head;
+        const uint16_t* vb = a.vc + head;
+        double M0 = -INFINITY, M1 = -INFINITY, l0 = 0.0, l1 = 0.0;
+        double acc[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
+        // With one workgroup of four waves per compute unit there are few waves to hide memory
+        // latency behind, so a block's 16 K chunks are all in flight together, and the next
+        // block's are issued before this block's P V.
+        uint4 kr[16];
+        auto load_k = [&](int j0) {
+            const int j = min(j0 + lane, n - 1);
+            const uint4* krow = reinterpret_cast<const uint4*>(kb + (size_t)j * kFD);
+#pragma unroll
+            for (int c = 0; c < 16; ++c) kr[c] = ldg16(krow + c);
+        };
+        load_k(0);
+        for (int j0 = 0; j0 < n; j0 += kWave) {
+            const bool valid = j0 + lane < n;
+            // The queries are read from LDS in every block (kept in registers they would take 512
+            // of them). The read offset of chunk c is passed through an empty asm that depends on
+            // the sums after chunk c - 2, so no more than two chunks' queries (64 registers) are
+            // read ahead of their use.
+            int qo = pf_fresh(0);
+            double s0 = 0.0, s1 = 0.0, sprev = 0.0, slag = 0.0;
+#pragma unroll
+            for (int c = 0; c < 16; ++c) {
+                if (c >= 2) asm volatile("" : "+v"(qo) : "v"(slag));
+                const uint32_t k4[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int d = 8 * c + 2 * i + qo;
+                    const double klo = bf16_bits_to_f32(k4[i] & 0xffffu), khi = __uint_as_float(k4[i] & 0xffff0000u);
+                    s0 = fma(sh.qa[x][0][d], klo, s0);
+                    s0 = fma(sh.qa[x][0][d + 1], khi, s0);
+                    s1 = fma(sh.qa[x][1][d], klo, s1);
+                    s1 = fma(sh.qa[x][1][d + 1], khi, s1);
+                }
+                slag = sprev;
+                sprev = s0 + s1;
+            }
+            if (j0 + kWave < n) load_k(j0 + kWave);
+            s0 = valid ? s0 * sc : -INFINITY;
+            s1 = valid ? s1 * sc : -INFINITY;
+            const double N0 = fmax(M0, wave_max64(s0)), N1 = fmax(M1, wave_max64(s1));
+            const double c0 = exp(M0 - N0), c1 = exp(M1 - N1);     // 0 on the first block (M = -inf)
+            const double e0 = valid ? exp(s0 - N0) : 0.0, e1 = valid ? exp(s1 - N1) : 0.0;
+            l0 = fma(l0, c0, wave_sum64(e0));
+            l1 = fma(l1, c1, wave_sum64(e1));
+            acc[0][0] *= c0; acc[0][1] *= c0;
+            acc[1][0] *= c1; acc[1][1] *= c1;
+            M0 = N0;
+            M1 = N1;
+            const int nb = min(kWave, n - j0);
+            const uint32_t* vrow = reinterpret_cast<const uint32_t*>(vb + (size_t)j0 * kFD) + lane;
+            for (int u0 = 0; u0 < nb; u0 += 16) {
+                uint32_t vw[16];
+#pragma unroll
+                for (int u = 0; u < 16; ++u) vw[u] = *gview(vrow + (kFD / 2) * min(u0 + u, nb - 1));
+#pragma unroll
+                for (int u = 0; u < 16; ++u) {
+                    const double q0 = readlane64(e0, u0 + u), q1 = readlane64(e1, u0 + u);   // 0 past the block
+                    const double vlo = bf16_bits_to_f32(vw[u] & 0xffffu), vhi = __uint_as_float(vw[u] & 0xffff0000u);
+                    acc[0][0] = fma(q0, vlo, acc[0][0]);
+                    acc[0][1] = fma(q0, vhi, acc[0][1]);
+                    acc[1][0] = fma(q1, vlo, acc[1][0]);
+                    acc[1][1] = fma(q1, vhi, acc[1][1]);
+                }
             }
         }
-        s0 = valid ? s0 * sc : -INFINITY;
-        s1 = valid ? s1 * sc : -INFINITY;
-        const double N0 = fmax(M0, wave_max64(s0)), N1 = fmax(M1, wave_max64(s1));
-        const double c0 = exp(M0 - N0), c1 = exp(M1 - N1);     // 0 on the first block (M = -inf)
-        const double e0 = valid ? exp(s0 - N0) : 0.0, e1 = valid ? exp(s1 - N1) : 0.0;
-        l0 = fma(l0, c0, wave_sum64(e0));
-        l1 = fma(l1, c1, wave_sum64(e1));
-        acc[0][0] *= c0; acc[0][1] *= c0;
-        acc[1][0] *= c1; acc[1][1] *= c1;
-        M0 = N0;
-        M1 = N1;
-        const int nb = min(kWave, n - j0);
-        const uint32_t* vrow = reinterpret_cast<const uint32_t*>(vb + (size_t)j0 * kFD) + lane;
-        for (int u0 = 0; u0 < nb; u0 += 8) {
-            uint32_t vw[8];
+        const double r0 = rcp_nr(l0), r1 = rcp_nr(l1);
+        sh.out[256 * x + 2 * lane] = (float)(acc[0][0] * r0);
+        sh.out[256 * x + 2 * lane + 1] = (float)(acc[0][1] * r0);
+        sh.out[256 * x + 128 + 2 * lane] = (float)(acc[1][0] * r1);
+        sh.out[256 * x + 128 + 2 * lane + 1] = (float)(acc[1][1] * r1);
+    }
+    __syncthreads();
+    // digit planes of the 2048 outputs: thread t takes elements [4t, +4) and [1024 + 4t, +4)
+    const int t = tid;
+    float ov[2][4];
+    uint32_t e = 0;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) vw[u] = *gview(vrow + (kFD / 2) * min(u0 + u, nb - 1));
+    for (int g = 0; g < 2; ++g) {
+        const float4 o = reinterpret_cast<const float4*>(sh.out)[256 * g + t];
+        ov[g][0] = o.x; ov[g][1] = o.y; ov[g][2] = o.z; ov[g][3] = o.w;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const double q0 = readlane64(e0, u0 + u), q1 = readlane64(e1, u0 + u);   // 0 past the block
-                const double vlo = bf16_bits_to_f32(vw[u] & 0xffffu), vhi = __uint_as_float(vw[u] & 0xffff0000u);
-                acc[0][0] = fma(q0, vlo, acc[0][0]);
-                acc[0][1] = fma(q0, vhi, acc[0][1]);
-                acc[1][0] = fma(q1, vlo, acc[1][0]);
-                acc[1][1] = fma(q1, vhi, acc[1][1]);
-            }
+        for (int i = 0; i < 4; ++i) e = max(e, exp_field(ov[g][i]));
+    }
+    e = block_max_u32(e, sh.rede, w, lane, kFThreads / kWave);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) store_digits4(pf_buf<uint8_t>(a, L.dig), a.Pp, p, 1024 * g + 4 * t, ov[g], e);
+    if (t == 0) pf_buf<uint32_t>(a, L.emax)[p] = e;
+    __syncthreads();                        // sh.out / sh.rede are reused by the next item
+}
+
+// ---- grid barrier ----------------------------------------------------------------------
+// Two levels. A workgroup's results are in its XCD's L2 once it reaches the barrier (the
+// workgroup barrier first waits for its stores). The last workgroup of an XCD to arrive is
+// that XCD's leader: its agent-scope release writes the XCD's L2 back to memory (once per XCD
+// and barrier: one write-back per workgroup, 32 per XCD, cost 26-90 us per barrier), then it
+// arrives at the grid counter, waits for the other seven leaders, drops stale lines of the
+// L2 (acquire) and releases its XCD's workgroups, which drop their own stale lines. Barrier
+// number b completes when the counters reach b times their arrivals. A wait that expires
+// sets the abort flag, and every later wait of the launch then returns at once, so the
+// grid always drains (the host reports MQ_ERR_TIMEOUT, mq_prefill_check). Needs the
+// workgroups dealt round-robin over the 8 XCDs (checked by the host).
+__device__ __forceinline__ bool pf_wait_ge(const uint32_t* p, uint32_t target, PfSync* sy, uint32_t limit) {
+    uint32_t n = 0;
+    while (__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+        if (__hip_atomic_load(&sy->abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return false;
+        __builtin_amdgcn_s_sleep(2);
+        if (++n >= limit) {
+            __hip_atomic_store(&sy->abort, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return false;
         }
     }
-    const double r0 = rcp_nr(l0), r1 = rcp_nr(l1);
-    out[256 * x + 2 * lane] = (float)(acc[0][0] * r0);
-    out[256 * x + 2 * lane + 1] = (float)(acc[0][1] * r0);
-    out[256 * x + 128 + 2 * lane] = (float)(acc[1][0] * r1);
-    out[256 * x + 128 + 2 * lane + 1] = (float)(acc[1][1] * r1);
-    __syncthreads();
-    // digit planes of the 2048 outputs: thread t takes elements [4t, +4)
-    const int t = threadIdx.x;
-    const float4 o = reinterpret_cast<const float4*>(out)[t];
-    const float ov[4] = {o.x, o.y, o.z, o.w};
-    uint32_t e = max(max(exp_field(ov[0]), exp_field(ov[1])), max(exp_field(ov[2]), exp_field(ov[3])));
-    e = block_max_u32(e, rede, x, lane, 8);
-    store_digits4(pf_buf<uint8_t>(a, L.dig), a.Pp, p, 4 * t, ov, e);
-    if (t == 0) pf_buf<uint32_t>(a, L.emax)[p] = e;
+    return true;
 }
+
+__device__ __forceinline__ void pf_grid_barrier(PfSync* sy, uint32_t b, uint32_t limit) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t x = hw_xcc_id() % kPfXcd;
+        const uint32_t per_xcd = gridDim.x / kPfXcd;
+        const uint32_t old = __hip_atomic_fetch_add(&sy->xcd[x].arrived, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == b * per_xcd - 1u) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            __hip_atomic_fetch_add(&sy->count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            pf_wait_ge(&sy->count, b * kPfXcd, sy, limit);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            __hip_atomic_store(&sy->xcd[x].released, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            pf_wait_ge(&sy->xcd[x].released, b, sy, limit);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        }
+    }
+    __syncthreads();
+}
+
+// The whole chunk in one launch: every layer's eight phases, each phase's work items dealt
+// over the workgroups: product tiles round-robin as rt + NRT pt (with NRT a multiple of 8 a
+// row tile's position tiles all run on one XCD and share its L2 copy of the weights),
+// attention positions in snake order.
+__global__ void __launch_bounds__(kFThreads, 1) pf_chunk_kernel(PfArgs a) {
+    __shared__ PfShared sh;
+    const PfLayout L0 = pf_layout((size_t)a.Pp);
+    PfSync* const sy = pf_buf<PfSync>(a, L0.sync);
+    const int G = (int)gridDim.x, g = (int)blockIdx.x;
+    const int PT = (a.P + kTileP - 1) / kTileP;
+    uint32_t nb = 0;
+    int l = 0;
+    auto stamp = [&](int point) {
+        if (a.trace != nullptr && threadIdx.x == 0)
+            a.trace[((size_t)l * kPfTracePoints + point) * G + g] = __builtin_amdgcn_s_memrealtime();
+    };
+    auto barrier = [&](int k) {
+        stamp(2 * k);
+        pf_grid_barrier(sy, ++nb, a.spin_limit);
+        stamp(2 * k + 1);
+    };
+    for (l = 0; l < a.L; ++l) {
+        PfArgs b = a;
+        b.layer = l;
+        for (int p = pf_fresh_uniform(g); p < a.P; p += G) {
+            if (l == 0) pf_digits<kFH, SRC_EMBED>(b, p, sh);
+            else pf_digits<kFH, SRC_HID>(b, p, sh);
+        }
+        barrier(0);
+        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_QKV>::NRT * PT; t += G) pf_gemm<EPI_QKV>(b, t);
+        if (l == a.L - 1) { stamp(2); break; }                 // the last layer contributes its cache rows only
+        barrier(1);
+        // attention items in snake order (round r takes r G + g, or r G + G - 1 - g when r is
+        // odd), so a workgroup's short and long contexts even out
+        for (int r = 0, gr = pf_fresh_uniform(g); r * G < a.P; ++r) {
+            const int p = r * G + (r % 2 == 0 ? gr : G - 1 - gr);
+            if (p < a.P) pf_attention(b, p, sh);
+        }
+        barrier(2);
+        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_O>::NRT * PT; t += G) pf_gemm<EPI_O>(b, t);
+        barrier(3);
+        for (int p = pf_fresh_uniform(g); p < a.P; p += G) pf_digits<kFH, SRC_X>(b, p, sh);
+        barrier(4);
+        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_GU>::NRT * PT; t += G) pf_gemm<EPI_GU>(b, t);
+        barrier(5);
+        for (int p = pf_fresh_uniform(g); p < a.P; p += G) pf_digits<kFI, SRC_M>(b, p, sh);
+        barrier(6);
+        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_DOWN>::NRT * PT; t += G) pf_gemm<EPI_DOWN>(b, t);
+        barrier(7);
+    }
+}
+
+__global__ void pf_sync_reset_kernel(PfSync* sy) {
+    sy->count = 0u;
+    sy->abort = 0u;
+    for (int x = 0; x < kPfXcd; ++x) {
+        sy->xcd[x].arrived = 0u;
+        sy->xcd[x].released = 0u;
+    }
+}
+
+__global__ void pf_sync_status_kernel(const PfSync* sy, uint32_t* out) { *out = sy->abort; }
 
 }  // namespace
 
@@ -467,10 +645,34 @@ int prefill_capacity(size_t bytes) {
     return (int)std::min(Pp, (size_t)1 << 20);
 }
 
+// The chunk kernel's grid: one workgroup per compute unit (its barriers need every workgroup
+// resident; checked with the occupancy calculator).
+static int prefill_grid(int* grid) {
+    static thread_local int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(MQ_ERR_HIP, "hipGetDevice failed");
+    if (cached[dev] == 0) {
+        int ncu = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&pf_chunk_kernel),
+                                                         kFThreads, 0) != hipSuccess)
+            return set_error(MQ_ERR_HIP, "occupancy query failed");
+        if (ncu < kPfXcd || ncu % kPfXcd != 0 || per_cu < 1 || !xcd_placement_ok())
+            return set_error(MQ_ERR_UNSUPPORTED, "the prefill kernel needs its workgroups dealt round-robin over "
+                             "8 XCDs (%d compute units)", ncu);
+        cached[dev] = ncu;
+    }
+    *grid = cached[dev];
+    return MQ_OK;
+}
+
 int launch_prefill(const mq_decode_args& d, const int* tokens, int n_tokens, void* ws, size_t ws_bytes,
                    hipStream_t stream) {
     const int cap = prefill_capacity(ws_bytes);
     if (cap < kTileP) return set_error(MQ_ERR_INVALID_ARGUMENT, "prefill workspace of %zu bytes holds no chunk", ws_bytes);
+    int grid = 0;
+    int st = prefill_grid(&grid);
+    if (st != MQ_OK) return st;
     PfArgs a{};
     a.embed = static_cast<const uint16_t*>(d.embed_weight);
     a.lw = d.layer_weights;
@@ -480,35 +682,44 @@ int launch_prefill(const mq_decode_args& d, const int* tokens, int n_tokens, voi
     a.kc = static_cast<uint16_t*>(d.k_cache);
     a.vc = static_cast<uint16_t*>(d.v_cache);
     a.S = d.max_seq_len;
+    a.L = d.num_layers;
     a.attn_scale = d.attn_scale;
+    a.spin_limit = d.spin_limit ? d.spin_limit : (1u << 21);
     a.ws = static_cast<uint8_t*>(ws);
+    a.trace = static_cast<uint64_t*>(d.trace);
     a.Pp = cap;
     const PfLayout L = pf_layout((size_t)cap);
+    PfSync* sy = reinterpret_cast<PfSync*>(a.ws + L.sync);
     for (int c0 = 0; c0 < n_tokens; c0 += cap) {
-        const int P = std::min(cap, n_tokens - c0);
-        const int PT = (P + kTileP - 1) / kTileP;
-        a.P = P;
+        a.P = std::min(cap, n_tokens - c0);
         a.pos0 = d.position + c0;
-        const hipError_t e = hipMemcpyAsync(a.ws + L.tok, tokens + c0, (size_t)P * sizeof(int), hipMemcpyHostToDevice,
-                                            stream);
+        const hipError_t e = hipMemcpyAsync(a.ws + L.tok, tokens + c0, (size_t)a.P * sizeof(int),
+                                            hipMemcpyHostToDevice, stream);
         if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipMemcpyAsync(prefill tokens): %s", hipGetErrorString(e));
-        for (int l = 0; l < d.num_layers; ++l) {
-            a.layer = l;
-            if (l == 0) pf_digits_kernel<kFH, SRC_EMBED><<<P, kFThreads, 0, stream>>>(a);
-            else pf_digits_kernel<kFH, SRC_HID><<<P, kFThreads, 0, stream>>>(a);
-            pf_gemm_kernel<EPI_QKV><<<GemmShape<EPI_QKV>::NRT * PT, kFThreads, 0, stream>>>(a);
-            if (l == d.num_layers - 1) break;         // the last layer contributes its cache rows only
-            pf_attention_kernel<<<P, 512, 0, stream>>>(a);
-            pf_gemm_kernel<EPI_O><<<GemmShape<EPI_O>::NRT * PT, kFThreads, 0, stream>>>(a);
-            pf_digits_kernel<kFH, SRC_X><<<P, kFThreads, 0, stream>>>(a);
-            pf_gemm_kernel<EPI_GU><<<GemmShape<EPI_GU>::NRT * PT, kFThreads, 0, stream>>>(a);
-            pf_digits_kernel<kFI, SRC_M><<<P, kFThreads, 0, stream>>>(a);
-            pf_gemm_kernel<EPI_DOWN><<<GemmShape<EPI_DOWN>::NRT * PT, kFThreads, 0, stream>>>(a);
-        }
-        const int st = check_launch("prefill");
+        // a fill kernel, not a memset, so that the launch sequence can be captured in a graph
+        pf_sync_reset_kernel<<<1, 1, 0, stream>>>(sy);
+        pf_chunk_kernel<<<grid, kFThreads, 0, stream>>>(a);
+        st = check_launch("prefill");
         if (st != MQ_OK) return st;
     }
     return MQ_OK;
+}
+
+int prefill_check(void* ws, size_t ws_bytes, hipStream_t stream) {
+    const int cap = prefill_capacity(ws_bytes);
+    if (cap < kTileP) return set_error(MQ_ERR_INVALID_ARGUMENT, "prefill workspace of %zu bytes holds no chunk", ws_bytes);
+    uint32_t* flag = nullptr;
+    if (hipHostMalloc(reinterpret_cast<void**>(&flag), sizeof(uint32_t), hipHostMallocDefault) != hipSuccess)
+        return set_error(MQ_ERR_HIP, "hipHostMalloc failed");
+    *flag = 0u;
+    const PfLayout L = pf_layout((size_t)cap);
+    pf_sync_status_kernel<<<1, 1, 0, stream>>>(reinterpret_cast<const PfSync*>(static_cast<uint8_t*>(ws) + L.sync), flag);
+    int st = check_launch("prefill check");
+    if (st == MQ_OK && hipStreamSynchronize(stream) != hipSuccess) st = set_error(MQ_ERR_HIP, "hipStreamSynchronize failed");
+    const uint32_t v = *flag;
+    (void)hipHostFree(flag);
+    if (st != MQ_OK) return st;
+    return v ? set_error(MQ_ERR_TIMEOUT, "a grid barrier of the prefill expired (were all compute units free?)") : MQ_OK;
 }
 
 }  // namespace mq

@@ -406,13 +406,15 @@ class _DecoderBase:
         """Whether ``prefill`` runs for this decoder (INT8 weights, hidden 1024)."""
         return self._int8 and not self._fp8 and self.dims[:2] == (1024, 3072)
 
-    def prefill(self, token_ids) -> None:
+    def prefill(self, token_ids, check: bool = True) -> None:
         """Write the K/V cache rows of ``token_ids`` at the next positions, as that many
         decode steps would (a10_decode.py:367-368), with each layer's weights read once
         for the whole prompt (mq_int8_prefill: products of all positions on the int8
         matrix cores, causal attention in fp64). No token is produced: the decode step of
         the following token gives the next output. Runs in chunks of ``PREFILL_CHUNK``
-        positions. Asynchronous on the current stream."""
+        positions, one launch each. With ``check`` (default) the call waits for the prefill
+        and raises MQTimeoutError if its grid-wide waits expired; otherwise it returns once
+        the launches are queued on the current stream."""
         ids = [int(t) for t in token_ids]
         if not ids:
             return
@@ -445,12 +447,35 @@ class _DecoderBase:
         a = self._args
         a.position = self._pos
         a.cache_len = self._pos + 1
-        st = self._lib.mq_int8_prefill(ctypes.byref(a), ctypes.c_void_p(self._pf_tokens.data_ptr()), len(ids),
-                                       ctypes.c_void_p(self._pf_ws.data_ptr()), self._pf_ws.numel(),
-                                       ctypes.c_void_p(stream))
+        step_trace, a.trace = a.trace, getattr(self, "_pf_trace_ptr", None)   # the prefill's own timeline
+        try:
+            st = self._lib.mq_int8_prefill(ctypes.byref(a), ctypes.c_void_p(self._pf_tokens.data_ptr()), len(ids),
+                                           ctypes.c_void_p(self._pf_ws.data_ptr()), self._pf_ws.numel(),
+                                           ctypes.c_void_p(stream))
+        finally:
+            a.trace = step_trace
         self._pf_done.record(torch.cuda.current_stream(self.device))
         _lib.check(st, "mq_int8_prefill")
+        if check:
+            # waits for the prefill; a grid barrier that expired (compute units held by other
+            # work) leaves the position unchanged
+            _lib.check(self._lib.mq_prefill_check(ctypes.c_void_p(self._pf_ws.data_ptr()), self._pf_ws.numel(),
+                                                  ctypes.c_void_p(stream)), "prefill")
         self._pos += len(ids)
+
+    def set_prefill_trace(self, buf) -> None:
+        """Record the phase timeline of the following prefills' last chunk into ``buf`` (int64,
+        at least ``num_layers * 16 * n_cu`` entries on the decoder's device, n_cu = the device's
+        compute units, entry ``(l * 16 + 2 k + e) * n_cu + g``: workgroup g done with phase k of
+        layer l, e = 1 past the grid barrier after it); ``None`` stops it."""
+        if buf is None:
+            self._pf_trace_ptr = None
+            return
+        need = self.num_layers * 16 * torch.cuda.get_device_properties(self.device).multi_processor_count
+        if buf.dtype != torch.int64 or buf.numel() < need or buf.device != self.device or not buf.is_contiguous():
+            raise ValueError(f"prefill trace buffer must be a contiguous int64 tensor of >= {need} entries on {self.device}")
+        self._pf_trace_buf = buf
+        self._pf_trace_ptr = buf.data_ptr()
 
     def _generate_one_launch(self, ids, n_tokens):
         """mq_int8/bf16/fp8_decode_generate; None when no multi-step kernel covers the request."""
