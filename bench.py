@@ -48,7 +48,7 @@ PROMPT_LEN = 8
 # Memory traffic per decode launch of each kernel, measured with rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE runs of megaqwen-a10_amd/profile_decode.py, each scaled by the counter's reading for a
 # 256 MiB copy (the commands and numbers are in profiles/decode_*_kernel_int8_qwen3-0.6b_traffic.txt).
-MEASURED_TRAFFIC = {"mq::decode_async_kernel<false, false>": 641_659_290,
+MEASURED_TRAFFIC = {"mq::decode_async_kernel<false, false, false>": 641_659_290,
                     "mq::decode_xcd_kernel<1024, 3072, mq::Int8W, false>": 639_234_240}
 
 
@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--workload", default="decode",
                     choices=["decode", "matvec", "formats", "positions", "longctx", "batched", "prefill", "traffic"])
     ap.add_argument("--prompt-lens", default="8,64,512,2040", help="prefill: prompt lengths")
+    ap.add_argument("--weight-format", default="int8", choices=["int8", "int4"],
+                    help="decode: INT8 per row (config 1), or INT4 per group of 128 with the LM head INT8")
     ap.add_argument("--depths", default="1024,4096,8192", help="longctx: KV depths")
     ap.add_argument("--batches", default="1,4,8,16", help="batched: batch sizes")
     ap.add_argument("--split-min", type=int, default=0,
@@ -160,11 +162,13 @@ def run_decode(args, mq, torch):
     state, prompt = mq.random_init_state(cfg, seed=args.seed)
     S = PROMPT_LEN + max(args.steps, args.warmup, 0 if args.no_cpu else args.cpu_steps) + 8
     cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
-    qstate = mq.quantize_state(state, cfg, dev)
+    w4 = args.weight_format == "int4"
+    qstate = mq.quantize_state(state, cfg, dev, weight_format=args.weight_format)
     del state
     embed, layers, scales, lm_q, lm_s, fnorm = mq.pack_int8(qstate, cfg)
     keep = (embed, layers, scales, lm_q, lm_s, fnorm, cos, sin)
-    dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+    cls = mq.A10Int4MegakernelDecoder if w4 else mq.A10Int8MegakernelDecoder
+    dec = cls(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
     prompt = prompt.tolist()
 
     def prefill():
@@ -193,8 +197,8 @@ def run_decode(args, mq, torch):
         status = dec._lib.mq_decode_check(dec.workspace.data_ptr(), None)
         raise RuntimeError(f"decode step {toks.index(min(toks))} of the timed region failed: "
                            f"status {status}: {mq._lib.last_error()}")
-    variant = mq.decode_variant(cfg.hidden_size, cfg.intermediate_size, int8=True)
-    kernel = {"async": "mq::decode_async_kernel<false, false>",
+    variant = "async" if w4 else mq.decode_variant(cfg.hidden_size, cfg.intermediate_size, int8=True)
+    kernel = {"async": f"mq::decode_async_kernel<false, false, {'true' if w4 else 'false'}>",
               "xcd": "mq::decode_xcd_kernel<1024, 3072, mq::Int8W, false>",
               "flat": "mq::decode_kernel<1024, 3072, mq::Int8W, false>"}[variant]
     arithmetic = ("matrix products as exact sums of int8 digits of a 55-bit fixed-point activation on the int8 "
@@ -203,7 +207,8 @@ def run_decode(args, mq, torch):
                   "layer stages fp64 (rounded to fp32/bf16 where the reference stores), LM head fp32")
 
     # algorithmic bytes of each timed launch: positions PROMPT_LEN .. PROMPT_LEN+K-1
-    bytes_total = sum(cfg.int8_step_bytes(cache_len=PROMPT_LEN + i + 1) for i in range(args.steps))
+    step_bytes = cfg.int4_step_bytes if w4 else cfg.int8_step_bytes
+    bytes_total = sum(step_bytes(cache_len=PROMPT_LEN + i + 1) for i in range(args.steps))
     kern_s = sum(kern_ms) / 1e3
     achieved = bytes_total / kern_s / 1e9
 
@@ -223,11 +228,11 @@ def run_decode(args, mq, torch):
             if toks3 is not None:
                 device_loop = {"tok_s": round(args.steps / wall3, 1),
                                "ms_per_step": round(wall3 / args.steps * 1e3, 4),
-                               "entry_point": "mq_int8_decode_generate: one launch for all K steps",
+                               "entry_point": f"mq_{args.weight_format}_decode_generate: one launch for all K steps",
                                "tokens_match_per_step_launches": first3 == first and toks3 == toks}
 
     parity = None
-    fx = ROOT / "tests" / "golden" / "tokens_qwen3_0.6b_int8.json"
+    fx = ROOT / "tests" / "golden" / f"tokens_qwen3_0.6b_{args.weight_format}.json"
     if fx.exists() and args.seed == 0:
         want = json.loads(fx.read_text())["tokens"]
         n = min(len(want) - 1, args.steps)
@@ -236,7 +241,8 @@ def run_decode(args, mq, torch):
 
     value = args.steps / wall
     out = {
-        "metric": "INT8 decode tok/s, Qwen3-0.6B shape bs=1; achieved HBM GB/s vs peak",
+        "metric": ("INT4-g128 decode tok/s (LM head INT8), Qwen3-0.6B shape bs=1; achieved HBM GB/s vs peak" if w4
+                   else "INT8 decode tok/s, Qwen3-0.6B shape bs=1; achieved HBM GB/s vs peak"),
         "value": round(value, 2),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -250,7 +256,9 @@ def run_decode(args, mq, torch):
         "data": "synthetic",
         "config": {"workload": "config 1: INT8 greedy decode, Qwen3-0.6B architecture random-init (seed 0), "
                                "bs=1, 8-token random prompt prefilled untimed, K greedy steps timed",
-                   "weights": "int8 per-output-channel (scale=bf16(absmax/127)); embed/norms/RoPE/KV bf16",
+                   "weights": ("int4 per group of 128 (scale=bf16(absmax/7)), LM head int8 per row; "
+                               "embed/norms/RoPE/KV bf16") if w4 else
+                              "int8 per-output-channel (scale=bf16(absmax/127)); embed/norms/RoPE/KV bf16",
                    "arithmetic": arithmetic, "kernel_variant": variant,
                    "layers": cfg.num_layers, "hidden": cfg.hidden_size, "vocab": cfg.vocab_size,
                    "batch": 1, "prompt_len": PROMPT_LEN, "parallelism": "single GPU"},
@@ -265,7 +273,9 @@ def run_decode(args, mq, torch):
         "device_loop": device_loop,
         "parity": parity,
     }
-    if not args.no_cpu:
+    if w4:
+        out["config"]["workload"] = out["config"]["workload"].replace("config 1: INT8", "INT4-g128")
+    if not args.no_cpu and not w4:
         cb = cpu_baseline(keep, cfg, prompt, args.cpu_steps)
         cpu_toks = cb.pop("tokens")
         gpu_ref = [first] + toks

@@ -259,6 +259,17 @@ int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream);
  * hold). Every stored intermediate is the correctly rounded value of the
  * dequantized weights' expression, as for INT8. */
 int mq_fp8_decode_step(const mq_decode_args* args, hipStream_t stream);
+/* Same with INT4 weights per group of 128 inputs for the seven layer
+ * projections: codes from mq_quantize_int4_groups_bf16 (two's complement
+ * nibbles, uint8 [out, in / 2], the low nibble the even element) with their
+ * fp32 group scales [out, in / 128] in place of the per-row scales (same
+ * packing order); the LM head stays INT8 per row (lm_head_weight,
+ * lm_head_scale). No counterpart in the reference. Hidden 1024 / intermediate
+ * 3072 up to 2048 cached positions, on the async-wave kernel (MQ_ERR_UNSUPPORTED
+ * otherwise): each group's exact digit-plane sum is scaled by its group scale
+ * in fp64, so every stored intermediate is the correctly rounded value of the
+ * dequantized weights' expression. */
+int mq_int4_decode_step(const mq_decode_args* args, hipStream_t stream);
 /* Allocation-free variant of mq_int8_decode_step. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
@@ -277,6 +288,8 @@ int mq_int8_decode_step_noalloc(const mq_decode_args* args, hipStream_t stream);
 int mq_int8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream);
 int mq_bf16_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream);
 int mq_fp8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream);
+/* INT4 layer weights (see mq_int4_decode_step): the async-wave kernel only. */
+int mq_int4_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream);
 /* Prompt-batched prefill. The reference prefills a prompt one decode step per
  * token (a10_decode.py:367-368, verify_correctness_a10.py:326-328, each step
  * a10_int8_decode_kernel.cu:821-842); this writes the same K/V cache rows with

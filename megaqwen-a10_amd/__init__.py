@@ -11,8 +11,8 @@ library (``lib/libmegaqwen_a10.so``, declared in include/megaqwen_a10.h):
 * ``A10Int8MegakernelDecoder`` / ``A10MegakernelDecoder`` / ``A10Decoder`` —
   the reference's decoder classes (bench_int8.py:119-255, a10_decode.py:35-393),
   one persistent-kernel launch per token.
-* ``A10Fp8MegakernelDecoder`` — the same step with FP8 E4M3 weights (no counterpart
-  in the reference).
+* ``A10Fp8MegakernelDecoder`` / ``A10Int4MegakernelDecoder`` — the same step with FP8
+  E4M3 weights, or INT4 weights per group of 128 (no counterpart in the reference).
 * ``A10Int8BatchDecoder`` — up to 16 independent sequences per step on the int8
   matrix cores (Qwen3-1.7B shapes; no counterpart in the reference).
 * ``precompute_rope_freqs`` / ``make_rope`` — RoPE tables.
@@ -20,8 +20,8 @@ library (``lib/libmegaqwen_a10.so``, declared in include/megaqwen_a10.h):
   seeded weights and the reference's tensor packing.
 """
 from .config import QWEN3_0_6B, QWEN3_1_7B, ModelConfig
-from .decoder import (A10Decoder, A10Fp8MegakernelDecoder, A10Int8BatchDecoder, A10Int8MegakernelDecoder,
-                      A10MegakernelDecoder, config_from_checkpoint, decode_variant, load_checkpoint_state,
+from .decoder import (A10Decoder, A10Fp8MegakernelDecoder, A10Int4MegakernelDecoder, A10Int8BatchDecoder,
+                      A10Int8MegakernelDecoder, A10MegakernelDecoder, config_from_checkpoint, decode_variant, load_checkpoint_state,
                       load_tokenizer, set_decode_variant)
 from .formats import fp8_gemv, fp8_gemv_repeat, int4_gemv, int4_gemv_repeat, quantize_fp8, quantize_int4
 from .gemv import int8_gemv, int8_gemv_repeat
@@ -31,7 +31,7 @@ from .weights import pack_bf16, pack_int8, quantize_state, random_init_state, st
 
 __all__ = [
     "ModelConfig", "QWEN3_0_6B", "QWEN3_1_7B",
-    "A10Decoder", "A10Fp8MegakernelDecoder", "A10Int8BatchDecoder", "A10Int8MegakernelDecoder", "A10MegakernelDecoder", "set_decode_variant",
+    "A10Decoder", "A10Fp8MegakernelDecoder", "A10Int4MegakernelDecoder", "A10Int8BatchDecoder", "A10Int8MegakernelDecoder", "A10MegakernelDecoder", "set_decode_variant",
     "decode_variant", "config_from_checkpoint", "load_checkpoint_state", "load_tokenizer",
     "int8_gemv", "int8_gemv_repeat", "quantize_per_channel",
     "quantize_fp8", "quantize_int4", "fp8_gemv", "int4_gemv", "fp8_gemv_repeat", "int4_gemv_repeat", "make_rope", "precompute_rope_freqs",

@@ -108,11 +108,13 @@ _SIGNATURES = {
     "mq_workspace_init": (c_int, [c_void_p, c_size_t, c_void_p]),
     "mq_int8_decode_step": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mq_fp8_decode_step": (c_int, [POINTER(DecodeArgs), c_void_p]),
+    "mq_int4_decode_step": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mq_bf16_decode_step": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mq_int8_decode_step_noalloc": (c_int, [POINTER(DecodeArgs), c_void_p]),
     "mq_int8_decode_generate": (c_int, [POINTER(DecodeArgs), POINTER(GenerateArgs), c_void_p]),
     "mq_bf16_decode_generate": (c_int, [POINTER(DecodeArgs), POINTER(GenerateArgs), c_void_p]),
     "mq_fp8_decode_generate": (c_int, [POINTER(DecodeArgs), POINTER(GenerateArgs), c_void_p]),
+    "mq_int4_decode_generate": (c_int, [POINTER(DecodeArgs), POINTER(GenerateArgs), c_void_p]),
     "mq_prefill_workspace_bytes": (c_size_t, [POINTER(ModelDims), c_int]),
     "mq_int8_prefill": (c_int, [POINTER(DecodeArgs), c_void_p, c_int, c_void_p, c_size_t, c_void_p]),
     "mq_prefill_check": (c_int, [c_void_p, c_size_t, c_void_p]),

@@ -48,6 +48,17 @@ class ModelConfig:
         kv = L * 2 * self.num_kv_heads * D * 2 * (cache_len + 1)
         return L * per_layer + lm + 2 * H + 2 * H + kv
 
+    def int4_step_bytes(self, cache_len: int = 0) -> int:
+        """The same for INT4 layer projections per group of 128 (half a byte per weight, an
+        fp32 scale per group) with the LM head INT8 per row."""
+        H, I, Q, KV, L, V, D = (self.hidden_size, self.intermediate_size, self.q_size, self.kv_size,
+                                self.num_layers, self.vocab_size, self.head_dim)
+        proj = Q * H + 2 * KV * H + H * Q + 2 * I * H + H * I
+        per_layer = proj // 2 + 4 * (proj // 128) + 2 * (2 * H + 2 * D)
+        lm = V * H + 4 * V
+        kv = L * 2 * self.num_kv_heads * D * 2 * (cache_len + 1)
+        return L * per_layer + lm + 2 * H + 2 * H + kv
+
     def bf16_step_bytes(self, cache_len: int = 0) -> int:
         H, I, Q, KV, L, V, D = (self.hidden_size, self.intermediate_size, self.q_size, self.kv_size,
                                 self.num_layers, self.vocab_size, self.head_dim)

@@ -286,6 +286,15 @@ int mq_fp8_decode_step(const mq_decode_args* args, hipStream_t stream) {
     return launch_decode(*args, s, true, stream);
 }
 
+int mq_int4_decode_step(const mq_decode_args* args, hipStream_t stream) {
+    clear_error();
+    DecodeShape s;
+    int st = validate_decode(args, true, &s);
+    if (st != MQ_OK) return st;
+    s.int4 = true;
+    return launch_decode(*args, s, true, stream);
+}
+
 int mq_bf16_decode_step(const mq_decode_args* args, hipStream_t stream) {
     clear_error();
     DecodeShape s;
@@ -323,7 +332,7 @@ int mq_int8_decode_step_noalloc(const mq_decode_args* args, hipStream_t stream) 
 // Several steps in one launch (mq_generate_args), any weight format: the async-wave kernel
 // within its range, else the XCD-aware kernel's multi-step instantiation.
 static int decode_generate(const mq_decode_args* args, const mq_generate_args* gen, bool int8, bool fp8,
-                           hipStream_t stream) {
+                           hipStream_t stream, bool int4 = false) {
     if (args == nullptr || gen == nullptr) return set_error(MQ_ERR_INVALID_ARGUMENT, "args is NULL");
     if (gen->prompt_tokens == nullptr || gen->output_tokens == nullptr)
         return set_error(MQ_ERR_INVALID_ARGUMENT, "prompt_tokens and output_tokens must be non-NULL");
@@ -334,6 +343,7 @@ static int decode_generate(const mq_decode_args* args, const mq_generate_args* g
     int st = validate_decode(args, int8, &s);
     if (st != MQ_OK) return st;
     s.fp8 = fp8;
+    s.int4 = int4;
     if (args->input_token_id != gen->prompt_tokens[0])
         return set_error(MQ_ERR_INVALID_ARGUMENT, "input_token_id %d != prompt_tokens[0] %d", args->input_token_id,
                          gen->prompt_tokens[0]);
@@ -368,6 +378,11 @@ int mq_bf16_decode_generate(const mq_decode_args* args, const mq_generate_args* 
 int mq_fp8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream) {
     clear_error();
     return decode_generate(args, gen, true, true, stream);
+}
+
+int mq_int4_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream) {
+    clear_error();
+    return decode_generate(args, gen, true, false, stream, true);
 }
 
 size_t mq_prefill_workspace_bytes(const mq_model_dims* dims, int max_tokens) {

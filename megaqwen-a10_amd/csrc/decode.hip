@@ -527,6 +527,15 @@ bool xcd_placement_ok() {
 // number, so it must not share the positive range).
 int decode_variant_for(const DecodeShape& s, bool int8, int cache_len) {
     const int v = g_variant.load();
+    // INT4 weights run on the async-wave kernel only
+    if (s.int4) {
+        if (v == 1 || v == 2 || !xcd_placement_ok() || !decode_async_supports(s, true, cache_len))
+            return -set_error(MQ_ERR_UNSUPPORTED, "INT4 weights run on the async-wave kernel only: hidden 1024 / "
+                              "intermediate 3072, up to %d cached positions (cache_len %d, variant %d%s)",
+                              decode_async_max_len(), cache_len, v,
+                              xcd_placement_ok() ? "" : ", workgroup placement unsupported");
+        return 3;
+    }
     const bool have_xcd = decode_xcd_kernel_ptr(s, int8, false) != nullptr;
     // FP8 weights run on the XCD-aware kernel only
     if (s.fp8) {
@@ -656,7 +665,7 @@ int launch_decode(const mq_decode_args& a, const DecodeShape& s, bool int8, hipS
                        a.block_max_idxs || a.trace;
 
     hipEvent_t t0 = static_cast<hipEvent_t>(a.timing_start), t1 = static_cast<hipEvent_t>(a.timing_stop);
-    if (variant == 3) return launch_decode_async(k, debug, stream, t0, t1);
+    if (variant == 3) return launch_decode_async(k, debug, s.int4, stream, t0, t1);
     if (variant == 2) return launch_decode_xcd(k, s, int8, debug, stream, t0, t1);
     if (s.H == 1024 && s.I == 3072) {
         return int8 ? launch_t<1024, 3072, Int8W>(k, debug, stream, t0, t1) : launch_t<1024, 3072, Bf16W>(k, debug, stream, t0, t1);

@@ -117,7 +117,11 @@ struct __align__(16) AsyncLds {
     __align__(16) uint16_t lnA[kAH];                     // input RMSNorm gains
     __align__(16) uint16_t lnE[kAH];                     // post-attention RMSNorm gains
     uint16_t qkn[2][kAD];                  // q / k norm gains
-    float scA[16], scC[32], scE[24], scF[32];
+    float scA[16], scC[32], scE[24], scF[32];     // row scales (1 with INT4 weights)
+    // INT4 weights: the scales of each row's groups of 128 inputs that this workgroup's
+    // products touch (A: 16 rows x 8 groups; C: 32 O rows x the XCD's 2 groups of
+    // attention dims; E: 24 gate|up rows x 8; F: 32 down rows x the XCD's 3 groups)
+    float gsA[16][8], gsC[32][2], gsE[24][8], gsF[32][3];
     uint16_t rope[2][kAD];                 // cos / sin at this position (once per step)
     uint16_t fnorm[kAH];                   // final RMSNorm gains (once per step)
     // compute waves
@@ -298,6 +302,31 @@ __device__ __forceinline__ void operands_ready(i32x4_t (&v)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
 }
+// ---- INT4 weights -----------------------------------------------------------------------
+// 16 two's complement nibbles (8 bytes, the low nibble of a byte the even element) as 16
+// int8 values in element order: the MFMA B operand the int8 path reads from LDS.
+__device__ __forceinline__ uint32_t sext_nibble_bytes(uint32_t v) {
+    return v | ((v & 0x08080808u) * 0x1Eu);        // bytes 8-15 -> 0xF8-0xFF (v - 16)
+}
+__device__ __forceinline__ uint4 nibbles_to_i8(uint2 p) {
+    uint32_t o[4];
+    const uint32_t w[2] = {p.x, p.y};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t lo = sext_nibble_bytes(w[i] & 0x0F0F0F0Fu);          // elements 0, 2, 4, 6 of the word
+        const uint32_t hi = sext_nibble_bytes((w[i] >> 4) & 0x0F0F0F0Fu);   // elements 1, 3, 5, 7
+        o[2 * i] = (lo & 0xFFu) | ((hi & 0xFFu) << 8) | ((lo & 0xFF00u) << 8) | ((hi & 0xFF00u) << 16);
+        o[2 * i + 1] = ((lo >> 16) & 0xFFu) | ((hi >> 8) & 0xFF00u) | ((lo >> 8) & 0xFF0000u) | (hi & 0xFF000000u);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+// 8-byte weight load with the non-temporal hint (INT4 rows: 16 elements)
+__device__ __forceinline__ uint2 ldg8_stream(const void* p) {
+    typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t v = __builtin_nontemporal_load((const __attribute__((address_space(1))) u32x2_t*)p);
+    return make_uint2(v.x, v.y);
+}
+
 // ---- polls ----------------------------------------------------------------------------
 // One round of polls over an XCD's vector block (kVecWords words at `block`, one tag):
 // elements [256 slice + 4 lane, +4) into v, and the 32 fp64 partial sums of squares
@@ -335,7 +364,9 @@ __device__ __forceinline__ const volatile KArgs* kargs() {
 // kMulti: several steps per launch (a.n_steps); otherwise one, and the step loop
 // disappears (held across a loop back-edge, the kernel's long-lived values would
 // cost register spills in the one-step kernel too).
-template <bool kDebug, bool kMulti>
+// kW4: the layer projections are INT4 per group of 128 inputs (packed nibbles [out, in / 2],
+// scales [out, in / 128]); the LM head stays INT8 per row.
+template <bool kDebug, bool kMulti, bool kW4 = false>
 __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     constexpr int H = kAH, D = kAD;
     constexpr ALayout kLay = alayout_for(xlayout_total(kAH, kAI));
@@ -481,74 +512,143 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 if (r < 16) { base = (const uint8_t*)lw.q_proj_weight; sc = sp.q_scale; mrow0 = 2 * x * D + 16 * r; }
                 else if (r < 24) { base = (const uint8_t*)lw.k_proj_weight; sc = sp.k_scale; mrow0 = x * D + 16 * (r - 16); }
                 else { base = (const uint8_t*)lw.v_proj_weight; sc = sp.v_scale; mrow0 = x * D + 16 * (r - 24); }
-                const uint8_t* rowp = base + (int64_t)(mrow0 + lane % 16) * H + 16 * (lane / 16);
-                uint4 w[16];
+                // lane: row mrow0 + lane % 16, inputs [256 c + 64 s + 16 (lane / 16), +16) of K step
+                // (c, s) = (i / 4, i % 4)
+                uint4 w[kW4 ? 1 : 16];
+                uint2 w4[kW4 ? 16 : 1];
+                if constexpr (kW4) {
+                    const uint8_t* rowp = base + (int64_t)(mrow0 + lane % 16) * (H / 2) + 8 * (lane / 16);
 #pragma unroll
-                for (int i = 0; i < 16; ++i) w[i] = ldg16_stream(rowp + 256 * (i / 4) + 64 * (i % 4));
+                    for (int i = 0; i < 16; ++i) w4[i] = ldg8_stream(rowp + 128 * (i / 4) + 32 * (i % 4));
+                } else {
+                    const uint8_t* rowp = base + (int64_t)(mrow0 + lane % 16) * H + 16 * (lane / 16);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) w[i] = ldg16_stream(rowp + 256 * (i / 4) + 64 * (i % 4));
+                }
                 uint32_t gw[H / 128];
 #pragma unroll
                 for (int i = 0; i < H / 128; ++i) gw[i] = ld32(static_cast<const uint8_t*>(lw.input_layernorm_weight) + 256 * i + 4 * lane);
-                const uint32_t scv = lane < 16 ? ld32(sc + mrow0 + lane) : 0u;
+                // INT4: the 16 rows' 8 group scales (rows mrow0.. are contiguous: 128 floats)
+                const uint32_t scv = kW4 ? 0x3F800000u : lane < 16 ? ld32(sc + mrow0 + lane) : 0u;
+                const uint32_t gs0 = kW4 ? ld32(sc + (int64_t)mrow0 * 8 + 2 * lane) : 0u;
+                const uint32_t gs1 = kW4 ? ld32(sc + (int64_t)mrow0 * 8 + 2 * lane + 1) : 0u;
                 await_free(SL_A, gl);
 #pragma unroll
-                for (int i = 0; i < 16; ++i) S.wA[i / 4][i % 4][lane] = w[i];
+                for (int i = 0; i < 16; ++i) S.wA[i / 4][i % 4][lane] = kW4 ? nibbles_to_i8(w4[i]) : w[i];
 #pragma unroll
                 for (int i = 0; i < H / 128; ++i) put32(S.lnA, 64 * i + lane, gw[i]);
                 if (lane < 16) put32(S.scA, lane, scv);
+                if (kW4) {
+                    put32(S.gsA, 2 * lane, gs0);
+                    put32(S.gsA, 2 * lane + 1, gs1);
+                }
                 raise(SL_A, gl);
             } else if (d == 1) {
-                const uint8_t* ob = (const uint8_t*)lw.o_proj_weight + (int64_t)(32 * r + lane % 16) * 2048 + 256 * x +
-                                    16 * (lane / 16);
-                uint4 wc[8];
+                // O: lane row 32 r + 16 t + lane % 16, inputs 256 x + 64 c + 16 (lane / 16) (i = 2 c + t);
+                // down: row 32 r + 16 t + lane % 16, inputs 384 x + 64 (2 c + s) + 16 (lane / 16)
+                uint4 wc[kW4 ? 1 : 8], wf[kW4 ? 1 : 12];
+                uint2 wc4[kW4 ? 8 : 1], wf4[kW4 ? 12 : 1];
+                uint32_t so, sdv, gc = 0u, gf0 = 0u, gf1 = 0u;
+                if constexpr (kW4) {
+                    const uint8_t* ob = (const uint8_t*)lw.o_proj_weight + (int64_t)(32 * r + lane % 16) * 1024 + 128 * x +
+                                        8 * (lane / 16);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) wc[i] = ldg16_stream(ob + (int64_t)16 * (i % 2) * 2048 + 64 * (i / 2));
-                const uint32_t so = lane < 32 ? ld32(sp.o_scale + 32 * r + lane) : 0u;
-                const uint8_t* db = (const uint8_t*)lw.down_proj_weight + (int64_t)(32 * r + lane % 16) * kAI + kAIX * x +
-                                    16 * (lane / 16);
-                uint4 wf[12];
+                    for (int i = 0; i < 8; ++i) wc4[i] = ldg8_stream(ob + (int64_t)16 * (i % 2) * 1024 + 32 * (i / 2));
+                    const uint8_t* db = (const uint8_t*)lw.down_proj_weight + (int64_t)(32 * r + lane % 16) * (kAI / 2) +
+                                        (kAIX / 2) * x + 8 * (lane / 16);
 #pragma unroll
-                for (int i = 0; i < 12; ++i)                 // i = (2 c + s) * 2 + t
-                    wf[i] = ldg16_stream(db + (int64_t)16 * (i % 2) * kAI + 64 * (i / 2));
-                const uint32_t sdv = lane < 32 ? ld32(sp.down_scale + 32 * r + lane) : 0u;
+                    for (int i = 0; i < 12; ++i)             // i = (2 c + s) * 2 + t
+                        wf4[i] = ldg8_stream(db + (int64_t)16 * (i % 2) * (kAI / 2) + 32 * (i / 2));
+                    so = sdv = 0x3F800000u;
+                    // group scales: O rows 32 r.. x groups 2 x, 2 x + 1 of 16; down rows x groups 3 x.. of 24
+                    gc = ld32(sp.o_scale + (int64_t)(32 * r + lane / 2) * 16 + 2 * x + lane % 2);
+                    gf0 = ld32(sp.down_scale + (int64_t)(32 * r + lane / 3) * 24 + 3 * x + lane % 3);
+                    gf1 = lane < 32 ? ld32(sp.down_scale + (int64_t)(32 * r + (lane + 64) / 3) * 24 + 3 * x + (lane + 64) % 3)
+                                    : 0u;
+                } else {
+                    const uint8_t* ob = (const uint8_t*)lw.o_proj_weight + (int64_t)(32 * r + lane % 16) * 2048 + 256 * x +
+                                        16 * (lane / 16);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) wc[i] = ldg16_stream(ob + (int64_t)16 * (i % 2) * 2048 + 64 * (i / 2));
+                    const uint8_t* db = (const uint8_t*)lw.down_proj_weight + (int64_t)(32 * r + lane % 16) * kAI + kAIX * x +
+                                        16 * (lane / 16);
+#pragma unroll
+                    for (int i = 0; i < 12; ++i)             // i = (2 c + s) * 2 + t
+                        wf[i] = ldg16_stream(db + (int64_t)16 * (i % 2) * kAI + 64 * (i / 2));
+                    so = lane < 32 ? ld32(sp.o_scale + 32 * r + lane) : 0u;
+                    sdv = lane < 32 ? ld32(sp.down_scale + 32 * r + lane) : 0u;
+                }
                 await_free(SL_C, gl);
 #pragma unroll
-                for (int i = 0; i < 8; ++i) S.wC[i / 2][i % 2][lane] = wc[i];
+                for (int i = 0; i < 8; ++i) S.wC[i / 2][i % 2][lane] = kW4 ? nibbles_to_i8(wc4[i]) : wc[i];
                 if (lane < 32) put32(S.scC, lane, so);
+                if (kW4) put32(S.gsC, lane, gc);
                 raise(SL_C, gl);
                 await_free(SL_F, gl);
 #pragma unroll
-                for (int i = 0; i < 12; ++i) S.wF[i / 4][(i / 2) % 2][i % 2][lane] = wf[i];
+                for (int i = 0; i < 12; ++i) S.wF[i / 4][(i / 2) % 2][i % 2][lane] = kW4 ? nibbles_to_i8(wf4[i]) : wf[i];
                 if (lane < 32) put32(S.scF, lane, sdv);
+                if (kW4) {
+                    put32(S.gsF, lane, gf0);
+                    if (lane < 32) put32(S.gsF, 64 + lane, gf1);
+                }
                 raise(SL_F, gl);
             } else if (d == 2) {
                 const int c0 = kAIX * x + 12 * r;
-                uint4 we[32];                                  // i = (4 c + s) * 2 + t; tile rows 24-31 zero
+                uint4 we[kW4 ? 1 : 32];                        // i = (4 c + s) * 2 + t; tile rows 24-31 zero
+                uint2 we4[kW4 ? 32 : 1];
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
                     const int j = 16 * t + lane % 16;
-                    const uint8_t* rowp = (j < 12 ? (const uint8_t*)lw.gate_proj_weight + (int64_t)(c0 + j) * H
-                                                  : (const uint8_t*)lw.up_proj_weight + (int64_t)(c0 + min(j, 23) - 12) * H) +
-                                          16 * (lane / 16);
+                    if constexpr (kW4) {
+                        const uint8_t* rowp = (j < 12 ? (const uint8_t*)lw.gate_proj_weight + (int64_t)(c0 + j) * (H / 2)
+                                                      : (const uint8_t*)lw.up_proj_weight + (int64_t)(c0 + min(j, 23) - 12) * (H / 2)) +
+                                              8 * (lane / 16);
 #pragma unroll
-                    for (int k = 0; k < 16; ++k) {
-                        we[2 * k + t] = make_uint4(0, 0, 0, 0);
-                        if (j < 24) we[2 * k + t] = ldg16_stream(rowp + 64 * k);
+                        for (int k = 0; k < 16; ++k) {
+                            we4[2 * k + t] = make_uint2(0, 0);
+                            if (j < 24) we4[2 * k + t] = ldg8_stream(rowp + 32 * k);
+                        }
+                    } else {
+                        const uint8_t* rowp = (j < 12 ? (const uint8_t*)lw.gate_proj_weight + (int64_t)(c0 + j) * H
+                                                      : (const uint8_t*)lw.up_proj_weight + (int64_t)(c0 + min(j, 23) - 12) * H) +
+                                              16 * (lane / 16);
+#pragma unroll
+                        for (int k = 0; k < 16; ++k) {
+                            we[2 * k + t] = make_uint4(0, 0, 0, 0);
+                            if (j < 24) we[2 * k + t] = ldg16_stream(rowp + 64 * k);
+                        }
                     }
                 }
                 uint32_t gw[H / 128];
 #pragma unroll
                 for (int i = 0; i < H / 128; ++i)
                     gw[i] = ld32(static_cast<const uint8_t*>(lw.post_attn_layernorm_weight) + 256 * i + 4 * lane);
-                const uint32_t scv = lane < 12 ? ld32(sp.gate_scale + c0 + lane)
+                const uint32_t scv = kW4 ? 0x3F800000u
+                                   : lane < 12 ? ld32(sp.gate_scale + c0 + lane)
                                    : lane < 24 ? ld32(sp.up_scale + c0 + lane - 12) : 0u;
+                // INT4: 24 rows (gate 0-11, up 12-23) x 8 group scales, entry 64 m + lane
+                uint32_t ge[3] = {0u, 0u, 0u};
+                if constexpr (kW4) {
+#pragma unroll
+                    for (int m = 0; m < 3; ++m) {
+                        const int idx = 64 * m + lane, j = idx / 8, grp = idx % 8;
+                        ge[m] = ld32(j < 12 ? sp.gate_scale + (int64_t)(c0 + j) * 8 + grp
+                                            : sp.up_scale + (int64_t)(c0 + j - 12) * 8 + grp);
+                    }
+                }
                 await_free(SL_E, gl);
 #pragma unroll
                 for (int k = 0; k < 16; ++k)
 #pragma unroll
-                    for (int t = 0; t < 2; ++t) S.wE[k / 4][k % 4][t][lane] = we[2 * k + t];
+                    for (int t = 0; t < 2; ++t) S.wE[k / 4][k % 4][t][lane] = kW4 ? nibbles_to_i8(we4[2 * k + t]) : we[2 * k + t];
 #pragma unroll
                 for (int i = 0; i < H / 128; ++i) put32(S.lnE, 64 * i + lane, gw[i]);
                 if (lane < 24) put32(S.scE, lane, scv);
+                if (kW4) {
+#pragma unroll
+                    for (int m = 0; m < 3; ++m) put32(S.gsE, 64 * m + lane, ge[m]);
+                }
                 raise(SL_E, gl);
             } else {
                 // K rows keep their 16-byte chunks XOR-permuted by row (chunk g of row j at
@@ -672,10 +772,23 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     op[2 * s + 1] = b_frag(S.wA[c][s][lane]);
                 }
                 operands_ready(op);
-                i32x4_t acc = {0, 0, 0, 0};
+                double v;
+                if constexpr (kW4) {
+                    // K steps 0-1 and 2-3 are the slice's two groups of 128: one sum each, scaled
+                    i32x4_t a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
 #pragma unroll
-                for (int s = 0; s < 4; ++s) acc = mfma_i8(op[2 * s], op[2 * s + 1], acc);
-                const double v = tile_value(acc, em);
+                    for (int s = 0; s < 2; ++s) {
+                        a0 = mfma_i8(op[2 * s], op[2 * s + 1], a0);
+                        a1 = mfma_i8(op[2 * s + 4], op[2 * s + 5], a1);
+                    }
+                    const int row = lane % 16;
+                    v = tile_value(a0, em) * (double)S.gsA[row][2 * c] + tile_value(a1, em) * (double)S.gsA[row][2 * c + 1];
+                } else {
+                    i32x4_t acc = {0, 0, 0, 0};
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) acc = mfma_i8(op[2 * s], op[2 * s + 1], acc);
+                    v = tile_value(acc, em);
+                }
                 if (lane < 16) S.part[0][c][lane] = v;
             }
             if (last_arrival(&S.sync[kArrive + AR_A], lane)) {
@@ -985,7 +1098,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 const i32x4_t af = a_frag(S.dig[c], 0, lane);
                 const i32x4_t t0 = mfma_i8(af, b_frag(S.wC[c][0][lane]), i32x4_t{0, 0, 0, 0});
                 const i32x4_t t1 = mfma_i8(af, b_frag(S.wC[c][1][lane]), i32x4_t{0, 0, 0, 0});
-                const double v0 = tile_value(t0, em), v1 = tile_value(t1, em);
+                double v0 = tile_value(t0, em), v1 = tile_value(t1, em);
+                if constexpr (kW4) {      // the wave's 64 dims lie in the XCD's group c / 2
+                    v0 *= (double)S.gsC[lane % 16][c / 2];
+                    v1 *= (double)S.gsC[16 + lane % 16][c / 2];
+                }
                 if (lane < 16) { S.part[1][c][lane] = v0; S.part[1][c][16 + lane] = v1; }
             }
             if (last_arrival(&S.sync[kArrive + AR_C], lane)) {
@@ -1053,13 +1170,28 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     op[3 * s + 2] = b_frag(S.wE[c][s][1][lane]);
                 }
                 operands_ready(op);
-                i32x4_t t0 = {0, 0, 0, 0}, t1 = {0, 0, 0, 0};
+                double v0, v1;
+                if constexpr (kW4) {
+                    // one sum per tile and group of 128 (K steps 0-1, 2-3), scaled
+                    i32x4_t t0[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}}, t1[2] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
 #pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    t0 = mfma_i8(op[3 * s], op[3 * s + 1], t0);
-                    t1 = mfma_i8(op[3 * s], op[3 * s + 2], t1);
+                    for (int s = 0; s < 4; ++s) {
+                        t0[s / 2] = mfma_i8(op[3 * s], op[3 * s + 1], t0[s / 2]);
+                        t1[s / 2] = mfma_i8(op[3 * s], op[3 * s + 2], t1[s / 2]);
+                    }
+                    const int j0 = lane % 16, j1 = min(16 + lane % 16, 23);      // tile rows 24-31 are zero
+                    v0 = tile_value(t0[0], em) * (double)S.gsE[j0][2 * c] + tile_value(t0[1], em) * (double)S.gsE[j0][2 * c + 1];
+                    v1 = tile_value(t1[0], em) * (double)S.gsE[j1][2 * c] + tile_value(t1[1], em) * (double)S.gsE[j1][2 * c + 1];
+                } else {
+                    i32x4_t t0 = {0, 0, 0, 0}, t1 = {0, 0, 0, 0};
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        t0 = mfma_i8(op[3 * s], op[3 * s + 1], t0);
+                        t1 = mfma_i8(op[3 * s], op[3 * s + 2], t1);
+                    }
+                    v0 = tile_value(t0, em);
+                    v1 = tile_value(t1, em);
                 }
-                const double v0 = tile_value(t0, em), v1 = tile_value(t1, em);
                 if (lane < 16) { S.part[2][c][lane] = v0; S.part[2][c][16 + lane] = v1; }
             }
             if (last_arrival(&S.sync[kArrive + AR_E], lane)) {
@@ -1098,7 +1230,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     t0 = mfma_i8(op[3 * s], op[3 * s + 1], t0);
                     t1 = mfma_i8(op[3 * s], op[3 * s + 2], t1);
                 }
-                const double v0 = tile_value(t0, em), v1 = tile_value(t1, em);
+                double v0 = tile_value(t0, em), v1 = tile_value(t1, em);
+                if constexpr (kW4) {      // the wave's 128 channels are the XCD's group c
+                    v0 *= (double)S.gsF[lane % 16][c];
+                    v1 *= (double)S.gsF[16 + lane % 16][c];
+                }
                 if (lane < 16) { S.part[3][c][lane] = v0; S.part[3][c][16 + lane] = v1; }
             }
             if (last_arrival(&S.sync[kArrive + AR_F], lane)) {      // wave 3 has no F slice: waves 0-2 sum
@@ -1306,11 +1442,15 @@ int decode_async_split_min(int attn_split_min) {
     return attn_split_min > 0 ? std::min(attn_split_min, kAMaxLen + 1) : kAMaxLen + 1;
 }
 
-int launch_decode_async(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
-    const void* fn;
-    if (ka.n_steps > 1) fn = reinterpret_cast<const void*>(&decode_async_kernel<false, true>);
-    else if (debug) fn = reinterpret_cast<const void*>(&decode_async_kernel<true, false>);
-    else fn = reinterpret_cast<const void*>(&decode_async_kernel<false, false>);
+template <bool kW4>
+static const void* async_kernel_ptr(const KArgs& ka, bool debug) {
+    if (ka.n_steps > 1) return reinterpret_cast<const void*>(&decode_async_kernel<false, true, kW4>);
+    if (debug) return reinterpret_cast<const void*>(&decode_async_kernel<true, false, kW4>);
+    return reinterpret_cast<const void*>(&decode_async_kernel<false, false, kW4>);
+}
+
+int launch_decode_async(const KArgs& ka, bool debug, bool int4, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
+    const void* fn = int4 ? async_kernel_ptr<true>(ka, debug) : async_kernel_ptr<false>(ka, debug);
     int st = check_residency(fn);
     if (st != MQ_OK) return st;
     KArgs copy = ka;

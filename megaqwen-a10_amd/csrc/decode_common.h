@@ -272,7 +272,7 @@ int check_residency(const void* fn, int threads = kThreads);
 // attention past 64).
 size_t decode_async_workspace_bytes(const DecodeShape& s);
 bool decode_async_supports(const DecodeShape& s, bool int8, int cache_len);
-int launch_decode_async(const KArgs& k, bool debug, hipStream_t stream, hipEvent_t t0, hipEvent_t t1);
+int launch_decode_async(const KArgs& k, bool debug, bool int4, hipStream_t stream, hipEvent_t t0, hipEvent_t t1);
 
 // XCD-aware kernel (decode_xcd.hip).
 size_t decode_xcd_workspace_bytes(const DecodeShape& s);

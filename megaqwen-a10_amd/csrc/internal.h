@@ -43,6 +43,7 @@ static_assert(sizeof(WsHeader) == 256, "workspace header is 256 bytes");
 struct DecodeShape {
     int H, I, NQ, NKV, D, V;
     bool fp8 = false;          // one-byte weights are FP8 E4M3 codes (with per-row scales), not int8
+    bool int4 = false;         // layer projections INT4 per group of 128 (the LM head INT8 per row)
 };
 
 size_t decode_workspace_bytes(const DecodeShape& s);

@@ -84,6 +84,7 @@ class _DecoderBase:
 
     _int8: bool = True         # one-byte weights with per-row scales
     _fp8: bool = False         # ... that are FP8 E4M3 codes rather than int8
+    _int4: bool = False        # layer projections INT4 per group of 128 (LM head INT8 per row)
 
     def _setup(self, embed, layer_tensors, final_norm, lm_head, cos_table, sin_table, num_layers,
                max_seq_len, layer_scales=None, lm_head_scale=None):
@@ -107,11 +108,14 @@ class _DecoderBase:
         if len(layer_tensors) != 11 * num_layers:
             raise ValueError(f"layer_weights_flat: expected {11 * num_layers} tensors (11 per layer), "
                              f"got {len(layer_tensors)}")
-        wdt = torch.uint8 if self._fp8 else torch.int8 if self._int8 else torch.bfloat16
+        wdt = torch.uint8 if (self._fp8 or self._int4) else torch.int8 if self._int8 else torch.bfloat16
         I = layer_tensors[8].shape[0]
         D = 128
         Q, KV = 16 * D, 8 * D
-        shapes = [(H,), (Q, H), (KV, H), (KV, H), (D,), (D,), (H, Q), (H,), (I, H), (I, H), (H, I)]
+        # INT4: packed rows of in / 2 bytes, one scale per group of 128 inputs
+        w_ = (lambda o, i: (o, i // 2)) if self._int4 else (lambda o, i: (o, i))
+        s_ = (lambda o, i: (o, i // 128)) if self._int4 else (lambda o, i: (o,))
+        shapes = [(H,), w_(Q, H), w_(KV, H), w_(KV, H), (D,), (D,), w_(H, Q), (H,), w_(I, H), w_(I, H), w_(H, I)]
         dtypes = [torch.bfloat16, wdt, wdt, wdt, torch.bfloat16, torch.bfloat16, wdt, torch.bfloat16,
                   wdt, wdt, wdt]
         for i, t in enumerate(layer_tensors):
@@ -119,11 +123,11 @@ class _DecoderBase:
         if self._int8:
             if layer_scales is None or len(layer_scales) != 7 * num_layers:
                 raise ValueError(f"layer_scales_all: expected {7 * num_layers} tensors (7 per layer)")
-            sshapes = [(Q,), (KV,), (KV,), (H,), (I,), (I,), (H,)]
+            sshapes = [s_(Q, H), s_(KV, H), s_(KV, H), s_(H, Q), s_(I, H), s_(I, H), s_(H, I)]
             for i, t in enumerate(layer_scales):
                 _check_tensor(t, f"layer_scales_all[{i}]", torch.float32, sshapes[i % 7], dev)
             _check_tensor(lm_head_scale, "lm_head_scale", torch.float32, (V,), dev)
-        _check_tensor(lm_head, "lm_head", wdt, (V, H), dev)
+        _check_tensor(lm_head, "lm_head", torch.int8 if self._int4 else wdt, (V, H), dev)
         _check_tensor(final_norm, "final_norm_weight", torch.bfloat16, (H,), dev)
         _check_tensor(cos_table, "cos_table", torch.bfloat16, None, dev)
         _check_tensor(sin_table, "sin_table", torch.bfloat16, None, dev)
@@ -221,6 +225,7 @@ class _DecoderBase:
         self._args_ref = ctypes.byref(a)
         self._tok_base = self.output_token.data_ptr()
         self._step_fn = (self._lib.mq_fp8_decode_step if self._fp8 else
+                         self._lib.mq_int4_decode_step if self._int4 else
                          self._lib.mq_int8_decode_step if self._int8 else self._lib.mq_bf16_decode_step)
         self._debug = False
 
@@ -404,7 +409,7 @@ class _DecoderBase:
 
     def prefill_supported(self) -> bool:
         """Whether ``prefill`` runs for this decoder (INT8 weights, hidden 1024)."""
-        return self._int8 and not self._fp8 and self.dims[:2] == (1024, 3072)
+        return self._int8 and not self._fp8 and not self._int4 and self.dims[:2] == (1024, 3072)
 
     def prefill(self, token_ids, check: bool = True) -> None:
         """Write the K/V cache rows of ``token_ids`` at the next positions, as that many
@@ -478,7 +483,7 @@ class _DecoderBase:
         self._pf_trace_ptr = buf.data_ptr()
 
     def _generate_one_launch(self, ids, n_tokens):
-        """mq_int8/bf16/fp8_decode_generate; None when no multi-step kernel covers the request."""
+        """mq_int8/int4/bf16/fp8_decode_generate; None when no multi-step kernel covers the request."""
         if self._inflight:
             torch.cuda.current_stream(self.device).synchronize()
             self._inflight.clear()
@@ -492,6 +497,7 @@ class _DecoderBase:
         self._tok_host[0] = TOKEN_PENDING
         g = _lib.GenerateArgs(ctypes.cast(prompt, ctypes.c_void_p), len(ids), n_tokens, out.data_ptr())
         fn = (self._lib.mq_fp8_decode_generate if self._fp8 else
+              self._lib.mq_int4_decode_generate if self._int4 else
               self._lib.mq_int8_decode_generate if self._int8 else self._lib.mq_bf16_decode_generate)
         st = fn(ctypes.byref(a), ctypes.byref(g), ctypes.c_void_p(_lib.stream_handle(self.device)))
         if st == _lib.MQ_ERR_UNSUPPORTED:
@@ -571,6 +577,25 @@ class A10Fp8MegakernelDecoder(_DecoderBase):
     def __init__(self, embed_weight, layer_weights_flat, layer_scales_all, lm_head_fp8, lm_head_scale,
                  final_norm_weight, cos_table, sin_table, num_layers, max_seq_len):
         self._setup(embed_weight, layer_weights_flat, final_norm_weight, lm_head_fp8, cos_table, sin_table,
+                    num_layers, max_seq_len, layer_scales=layer_scales_all, lm_head_scale=lm_head_scale)
+
+
+class A10Int4MegakernelDecoder(_DecoderBase):
+    """INT4 weights per group of 128 inputs (no counterpart in the reference, which has
+    INT8 and BF16): the constructor of A10Int8MegakernelDecoder with the seven layer
+    projections given as packed nibbles (uint8 [out, in / 2], from ``quantize_int4``) and
+    their fp32 group scales ([out, in / 128]) in the same packing order, and the LM head
+    INT8 per row (``quantize_state(..., weight_format="int4")`` + ``pack_int8``). Hidden
+    1024 / intermediate 3072 up to 2048 positions, on the async-wave kernel
+    (mq_int4_decode_step; one launch for a whole generation with
+    mq_int4_decode_generate). No batched prefill (prompts run as decode steps)."""
+
+    _int8 = True
+    _int4 = True
+
+    def __init__(self, embed_weight, layer_weights_flat, layer_scales_all, lm_head_int8, lm_head_scale,
+                 final_norm_weight, cos_table, sin_table, num_layers, max_seq_len):
+        self._setup(embed_weight, layer_weights_flat, final_norm_weight, lm_head_int8, cos_table, sin_table,
                     num_layers, max_seq_len, layer_scales=layer_scales_all, lm_head_scale=lm_head_scale)
 
 

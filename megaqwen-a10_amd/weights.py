@@ -85,16 +85,20 @@ def state_digest(state: dict) -> str:
 
 def quantize_state(state: dict, cfg: ModelConfig, device, weight_format: str = "int8") -> dict:
     """bench_int8.py:27-55 without the HF load: every projection and the LM head
-    become ``(int8, fp32 scale)`` pairs computed on ``device`` (``weight_format="fp8"``:
-    ``(FP8 E4M3 codes, fp32 scale)`` pairs, no counterpart in the reference); norms and
-    the embedding stay bf16 (moved to ``device``). ``pack_int8`` packs either."""
-    if weight_format not in ("int8", "fp8"):
-        raise ValueError(f"weight_format must be 'int8' or 'fp8', got {weight_format!r}")
-    from .formats import quantize_fp8
-    quant = quantize_per_channel if weight_format == "int8" else quantize_fp8
+    become ``(int8, fp32 scale)`` pairs computed on ``device``. No counterpart in the
+    reference: ``weight_format="fp8"`` gives ``(FP8 E4M3 codes, fp32 row scale)`` pairs;
+    ``"int4"`` gives the seven layer projections as ``(packed nibbles uint8 [out, in / 2],
+    fp32 group scales [out, in / 128])`` and keeps the LM head INT8 per row. Norms and the
+    embedding stay bf16 (moved to ``device``). ``pack_int8`` packs any of them."""
+    if weight_format not in ("int8", "fp8", "int4"):
+        raise ValueError(f"weight_format must be 'int8', 'fp8' or 'int4', got {weight_format!r}")
+    from .formats import quantize_fp8, quantize_int4
+    quant = {"int8": quantize_per_channel, "fp8": quantize_fp8, "int4": quantize_int4}[weight_format]
     q = {}
     for k, v in state.items():
-        if k == "lm_head.weight" or any(k.endswith(f"{p}.weight") for p in PROJ):
+        if k == "lm_head.weight":
+            q[k] = (quantize_per_channel if weight_format == "int4" else quant)(v.to(device))
+        elif any(k.endswith(f"{p}.weight") for p in PROJ):
             q[k] = quant(v.to(device))
         else:
             q[k] = v.to(device)

@@ -16,7 +16,9 @@ Fixtures (all small; weights are regenerated from their seed, never stored):
                        and the sha256 of the generated weights, from the
                        float64 oracle, for each decode case in CASES (the
                        _fp8 case: FP8 E4M3 weights from oracle/formats.py,
-                       decoded to their exact values for the oracle).
+                       decoded to their exact values for the oracle; the _int4
+                       case: INT4-g128 layer projections dequantized exactly,
+                       the LM head INT8 per row).
 """
 from __future__ import annotations
 
@@ -46,6 +48,7 @@ mq = __graft_entry__.load_package()
 CASES = {
     "small_int8": (dict(num_layers=2, vocab_size=4096), 1, True, 0.1, 64, 32),
     "qwen3_0.6b_fp8": (dict(), 0, True, 0.0, 64, 32),
+    "qwen3_0.6b_int4": (dict(), 0, True, 0.0, 64, 32),
     "qwen3_0.6b_int8": (dict(), 0, True, 0.0, 64, 32),
     "qwen3_0.6b_bf16": (dict(), 0, False, 0.0, 64, 32),
 }
@@ -104,7 +107,7 @@ def make_rope():
 
 
 # one-byte weight format of a case whose int8 flag is set (default int8)
-FORMAT = {"qwen3_0.6b_fp8": "fp8"}
+FORMAT = {"qwen3_0.6b_fp8": "fp8", "qwen3_0.6b_int4": "int4"}
 
 
 def _quantize(w: torch.Tensor, fmt: str):
@@ -112,6 +115,10 @@ def _quantize(w: torch.Tensor, fmt: str):
     if fmt == "fp8":
         q, s = oformats.quantize_fp8_rows(w)
         return torch.from_numpy(oformats.fp8_decode_table()[q.numpy().astype(np.int64)]), s
+    if fmt == "int4":
+        # the dequantized values (nibble x group scale, exact in fp64), row scales of 1
+        q, s = oformats.quantize_int4_groups(w)
+        return torch.from_numpy(oformats.dequant_int4(q, s)), torch.ones(w.shape[0], dtype=torch.float32)
     return oquant.quantize_per_channel(w)
 
 
@@ -142,7 +149,8 @@ def oracle_for(name: str, dtype=torch.float64):
         layers.append(state[f"{p}.post_attention_layernorm.weight"])
         layers += [proj("mlp.gate_proj"), proj("mlp.up_proj"), proj("mlp.down_proj")]
     if int8:
-        lm, lms = _quantize(state["lm_head.weight"], fmt)
+        # INT4 models keep the LM head INT8 per row
+        lm, lms = _quantize(state["lm_head.weight"], "int8" if fmt == "int4" else fmt)
     else:
         lm, lms = state["lm_head.weight"], None
     dec = RefDecoder(dims, state["model.embed_tokens.weight"], layers, scales if int8 else None,

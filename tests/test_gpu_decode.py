@@ -34,10 +34,10 @@ def _build(mq, dev, name):
     S = d["max_seq_len"]
     cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
     if d["int8"]:
-        fp8 = d.get("weight_format") == "fp8"
-        qstate = mq.quantize_state(state, cfg, dev, weight_format="fp8" if fp8 else "int8")
+        fmt = d.get("weight_format", "int8")
+        qstate = mq.quantize_state(state, cfg, dev, weight_format=fmt)
         embed, layers, scales, lm_q, lm_s, fnorm = mq.pack_int8(qstate, cfg)
-        cls = mq.A10Fp8MegakernelDecoder if fp8 else mq.A10Int8MegakernelDecoder
+        cls = {"fp8": mq.A10Fp8MegakernelDecoder, "int4": mq.A10Int4MegakernelDecoder}.get(fmt, mq.A10Int8MegakernelDecoder)
         dec = cls(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
         keep = (embed, layers, scales, lm_q, lm_s, fnorm, cos, sin)
     else:

@@ -158,6 +158,8 @@ def test_c_api_rejects_bad_arguments_without_launching(mq):
     assert "input_token_id" in _lib.last_error()
     assert lib.mq_fp8_decode_step(ctypes.byref(a), None) == _lib.MQ_ERR_INVALID_ARGUMENT
     assert "input_token_id" in _lib.last_error()
+    assert lib.mq_int4_decode_step(ctypes.byref(a), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+    assert "input_token_id" in _lib.last_error()
     a.input_token_id, a.position, a.cache_len = 5, 16, 17        # position == max_seq_len
     assert lib.mq_int8_decode_step(ctypes.byref(a), None) == _lib.MQ_ERR_INVALID_ARGUMENT
     assert "position" in _lib.last_error()
