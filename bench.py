@@ -641,7 +641,8 @@ def _prefill_ops(cfg, P):
     return 2 * 8 * Pp * (L * qkv + (L - 1) * rest)
 
 
-PREFILL_PHASES = ("input_digits", "qkv", "attention", "o", "post_attn_digits", "gate_up", "swiglu_digits", "down")
+PREFILL_PHASES = ("input_digits", "qkv", "attention", "attn_digits", "o", "post_attn_digits", "gate_up",
+                  "swiglu_digits", "down")
 
 
 def _prefill_phases(dec, ids, torch):
@@ -652,7 +653,7 @@ def _prefill_phases(dec, ids, torch):
     import numpy as np
     L = dec.num_layers
     ncu = torch.cuda.get_device_properties(dec.device).multi_processor_count
-    buf = torch.zeros(L * 16 * ncu, dtype=torch.int64, device=dec.device)
+    buf = torch.zeros(L * 18 * ncu, dtype=torch.int64, device=dec.device)
     split = len(ids) - (len(ids) - 1) % dec.PREFILL_CHUNK - 1         # all chunks but the last untraced
     recs = []
     for _ in range(3):
@@ -664,16 +665,16 @@ def _prefill_phases(dec, ids, torch):
         dec.prefill(ids[split:])
         dec.set_prefill_trace(None)
         torch.cuda.synchronize()
-        recs.append(buf.view(L, 16, ncu).cpu().numpy().astype(np.float64) / 100.0)
+        recs.append(buf.view(L, 18, ncu).cpu().numpy().astype(np.float64) / 100.0)
     T = np.stack(recs)[:, :L - 1]
     out = {}
     for k, name in enumerate(PREFILL_PHASES):
         done, passed = T[:, 1:, 2 * k, :], T[:, 1:, 2 * k + 1, :]
-        start = T[:, :-1, 15, :] if k == 0 else T[:, 1:, 2 * k - 1, :]
+        start = T[:, :-1, 17, :] if k == 0 else T[:, 1:, 2 * k - 1, :]
         work = (done.max(axis=2) - start.max(axis=2)).mean()
         barrier = (passed.max(axis=2) - done.max(axis=2)).mean()
         out[name] = [round(float(work), 1), round(float(barrier), 1)]
-    out["layer"] = round(float((T[:, 1:, 15, :].max(axis=2) - T[:, :-1, 15, :].max(axis=2)).mean()), 1)
+    out["layer"] = round(float((T[:, 1:, 17, :].max(axis=2) - T[:, :-1, 17, :].max(axis=2)).mean()), 1)
     return out
 
 

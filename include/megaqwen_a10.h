@@ -135,13 +135,13 @@ typedef struct mq_decode_args {
      * gathered, 8 down partial written, 9 hidden rows gathered.
      * Layer num_layers holds p = 0 final-norm input ready, p = 1 LM head done,
      * and [(L*10 + 2) * 256] the token publication.
-     * mq_int8_prefill: uint64 [num_layers * 16 * G], G = the prefill grid
+     * mq_int8_prefill: uint64 [num_layers * 18 * G], G = the prefill grid
      * (one workgroup per compute unit, 256 on MI355X); entry
-     * [(l * 16 + 2 k + e) * G + g] is when workgroup g finished phase k of
+     * [(l * 18 + 2 k + e) * G + g] is when workgroup g finished phase k of
      * layer l (e = 0) or passed the grid barrier after it (e = 1); phases
-     * 0 input digit planes, 1 QKV, 2 attention, 3 O, 4 post-attention digit
-     * planes, 5 gate/up, 6 SwiGLU digit planes, 7 down; the last layer
-     * writes points 0-2 only. A prefill of several chunks leaves the last
+     * 0 input digit planes, 1 QKV, 2 attention, 3 attention-output digit
+     * planes, 4 O, 5 post-attention digit planes, 6 gate/up, 7 SwiGLU digit
+     * planes, 8 down; the last layer writes points 0-2 only. A prefill of several chunks leaves the last
      * chunk's timeline. */
     void* trace;
     /* Attention split (XCD-aware kernel): from cache_len >= attn_split_min on,

@@ -14,15 +14,16 @@
 // fp64 summation order can move once in about 2^20 values.
 //
 // One persistent launch per chunk (a workgroup per compute unit, all resident); per layer
-// eight phases over the chunk's P positions, separated by grid barriers:
+// nine phases over the chunk's P positions, separated by grid barriers:
 //   digits      RMSNorm of the layer input (the embedding rows in layer 0), its
 //               digit planes                                 one workgroup per position
 //   QKV         q|k|v rows on the matrix cores; the epilogue runs QK-norm and RoPE
 //               and writes this layer's K/V cache rows and the rotated queries
 //               (a 128-row tile is one head, so the norm and the rotation pairs
 //               are inside one wave)                        tiles of 32 positions x 128 rows
-//   attention   causal, fp64, a workgroup per position, each wave two KV heads over
-//               cache rows [0, pos0 + p]; the output's digit planes
+//   attention   causal, fp64 on the matrix cores, a wave per (KV head, 8 positions):
+//               its 16 queries over cache rows [0, pos0 + p]
+//   digits      of the attention output
 //   O           + residual (the layer input)                 32 positions x 64 rows
 //   digits      post-attention RMSNorm
 //   gate|up     64 channels' gate and up rows per tile; SwiGLU in the epilogue
@@ -85,7 +86,7 @@ struct PfArgs {
 // Grid-barrier state. Counters are cumulative over a launch (zeroed before it), each on a
 // 64-byte line of its own.
 constexpr int kPfXcd = 8;
-constexpr int kPfTracePoints = 16;            // phase k of a layer: 2 k phase done, 2 k + 1 barrier passed
+constexpr int kPfTracePoints = 18;            // phase k (9 per layer): 2 k phase done, 2 k + 1 barrier passed
 struct PfSync {
     uint32_t count;                        // XCD leaders that reached the current barrier
     uint32_t abort;                        // set when a barrier wait expired
@@ -100,13 +101,12 @@ static_assert(sizeof(PfSync) <= 1024, "barrier state");
 
 // LDS of a workgroup, shared by the phases
 struct PfShared {
-    double qa[kFNKV][2][kFD];              // attention: the rotated queries of each KV head's two heads
-    __align__(16) float out[kFQ];          // attention: the position's outputs
+    double am[2][kWave][34];               // attention: a wave pair's second half (m, denominator, outputs)
     double reds[4];
     uint32_t rede[4];
 };
 
-enum PfSrc { SRC_EMBED = 0, SRC_HID = 1, SRC_X = 2, SRC_M = 3 };
+enum PfSrc { SRC_EMBED = 0, SRC_HID = 1, SRC_X = 2, SRC_M = 3, SRC_A = 4 };
 enum PfEpi { EPI_QKV = 0, EPI_O = 1, EPI_GU = 2, EPI_DOWN = 3 };
 
 // The kernel runs every phase of every layer in one body. Values that depend only on the
@@ -155,12 +155,12 @@ __device__ __forceinline__ uint32_t block_max_u32(uint32_t e, uint32_t* red, int
 // One work item per position. SRC_EMBED / SRC_HID: the layer input (bf16; in layer 0
 // the embedding row of the token, also stored as the layer input), input RMSNorm.
 // SRC_X: the post-attention residual, post-attention RMSNorm. SRC_M: the SwiGLU
-// output, no norm. The normalized value is fp32(r * rstd * gain) as in the decode
+// output, SRC_A: the attention output (in the query buffer), no norm. The normalized value is fp32(r * rstd * gain) as in the decode
 // step (a10_int8_decode_kernel.cu:54-84, :421-457).
 template <int K, int SRC>
 __device__ void pf_digits(const PfArgs& a, int p, PfShared& sh) {
     constexpr int G = K / 1024;            // groups of 4 consecutive elements per thread
-    static_assert(SRC == SRC_M || G == 1, "the normed rows are hidden-sized");
+    static_assert(SRC == SRC_M || SRC == SRC_A || G == 1, "the normed rows are hidden-sized");
     double* const reds = sh.reds;
     uint32_t* const rede = sh.rede;
     const PfLayout L = pf_layout((size_t)a.Pp);
@@ -177,7 +177,8 @@ __device__ void pf_digits(const PfArgs& a, int p, PfShared& sh) {
         v[0][2] = bf16_bits_to_f32(u.y & 0xffffu);
         v[0][3] = bf16_bits_to_f32(u.y >> 16);
     } else {
-        const float* row = SRC == SRC_X ? pf_buf<float>(a, L.x) + (size_t)p * kFH : pf_buf<float>(a, L.m) + (size_t)p * K;
+        const float* row = SRC == SRC_X ? pf_buf<float>(a, L.x) + (size_t)p * kFH
+                         : SRC == SRC_A ? pf_buf<float>(a, L.q) + (size_t)p * kFQ : pf_buf<float>(a, L.m) + (size_t)p * K;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float4 f = *reinterpret_cast<const float4*>(row + 1024 * g + 4 * t);
@@ -185,7 +186,7 @@ __device__ void pf_digits(const PfArgs& a, int p, PfShared& sh) {
         }
     }
     float n[G][4];
-    if constexpr (SRC != SRC_M) {
+    if constexpr (SRC != SRC_M && SRC != SRC_A) {
         double ss = 0.0;
 #pragma unroll
         for (int g = 0; g < G; ++g)
@@ -404,123 +405,151 @@ __device__ void pf_gemm(const PfArgs& a, int tile) {
     }
 }
 
-// ---- causal attention ------------------------------------------------------------------
-// One work item per position p: wave w attends for KV heads w and w + 4, each with its two
-// query heads, over the cache rows [0, pos0 + p] (a10_int8_decode_kernel.cu:298-359), in
-// blocks of 64 keys: lane j takes key j of the block (the 128-dim dot products in fp64
-// against the rotated queries, read from LDS), an online softmax in fp64 (running maximum
-// and denominator, e^(s - m)), and P V with lane l accumulating dims 2l, 2l + 1 of both
-// heads. The output (fp32, as the reference stores it) then becomes the O product's digit
-// planes.
-__device__ void pf_attention(const PfArgs& a, int p, PfShared& sh) {
+// ---- causal attention on the fp64 matrix cores -------------------------------------------
+// Work item (KV head x, tile of 8 positions p0..p0+7) of one wave: its 16 queries (lane
+// column q = lane % 16: position p0 + q % 8, query head 2x + q / 8) attend over the cache
+// rows [0, pos0 + p], 16 keys per block, with v_mfma_f64_16x16x4f64 (A: lane l holds
+// A[l % 16][l / 16]; B: B[l / 16][l % 16]; D: register i of lane l holds D[4 i + l / 16]
+// [l % 16]). Both products are transposed so that each lane works for its own query:
+//   scores S^T = K Q^T: A = K (key rows x dim slots), B = Q^T; instruction j's slot g is
+//     dim 32 g + j, so lane l reads 32 contiguous dims of key row l % 16 and of its query;
+//     register i of lane l then holds key 4 i + g (g = l / 16) of query q;
+//   outputs O^T = V^T P^T: A = V^T, B = P^T; instruction j's slot g is key 4 j + g, which
+//     is register j of the lane's own scores, and row c of tile t is dim 8 c + t, so lane
+//     l reads 8 contiguous dims of V row 4 j + g; register i of tile t then holds dim
+//     32 i + 8 g + t of query q.
+// Softmax in fp64: e = exp(s - m) with the query's shift m raised only when a block's
+// maximum exceeds it by more than 2^8 (then the accumulators are rescaled), so e stays
+// below e^256; the lane's partial denominator covers its keys and the four lane groups'
+// are added at the end. Each K and V row is read once per item (8 positions share it),
+// where the per-position form read it once per position. The outputs (fp32, as the
+// reference stores them) replace the item's queries in the query buffer.
+typedef double f64x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f64x4_t mfma_f64(double a, double b, f64x4_t c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+// Item (x, p0) is split over a wave pair: wave `half` takes the key blocks k0 = 16 (half +
+// 2 n); wave 1 leaves its shift, partial denominators and outputs in `am` and wave 0 merges
+// them with its own (each side scaled by e^(m_side - m)) after a workgroup barrier that
+// every wave of the workgroup reaches (`active` false: no item this round).
+__device__ void pf_attention_tile(const PfArgs& a, int x, int p0, int half, bool active, PfShared& sh, int pair) {
     const PfLayout L = pf_layout((size_t)a.Pp);
-    const int tid = pf_fresh(threadIdx.x), w = tid / kWave, lane = tid % kWave;
-    const int n = a.pos0 + p + 1;
+    const int lane = pf_fresh(threadIdx.x) % kWave;
+    const int q = lane % 16, g = lane / 16;
+    const int pq = p0 + q % 8;                              // chunk position of the lane's query
+    const bool qvalid = active && pq < a.P;
+    const int qpos = a.pos0 + pq;                           // its cache position: keys [0, qpos]
+    const int klast = active ? a.pos0 + min(p0 + 7, a.P - 1) : -1;   // the tile's last key
     const double sc = (double)a.attn_scale;
-#pragma unroll 1
-    for (int hh = 0; hh < 2; ++hh) {
-        const int x = w + 4 * hh;
-        const float* qrow = pf_buf<float>(a, L.q) + (size_t)p * kFQ + 256 * x;
+    float* const qrow = pf_buf<float>(a, L.q) + (size_t)max(0, min(pq, a.P - 1)) * kFQ + 256 * x + 128 * (q / 8);
+    double qd[32];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            sh.qa[x][h][lane] = qrow[128 * h + lane];
-            sh.qa[x][h][lane + 64] = qrow[128 * h + lane + 64];
+    for (int j = 0; j < 8; ++j) {
+        const float4 f = qvalid ? reinterpret_cast<const float4*>(qrow + 32 * g)[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        qd[4 * j] = f.x; qd[4 * j + 1] = f.y; qd[4 * j + 2] = f.z; qd[4 * j + 3] = f.w;
+    }
+    const int64_t head = ((int64_t)a.layer * kFNKV + x) * a.S * kFD;
+    const uint16_t* kb = a.kc + head;
+    const uint16_t* vb = a.vc + head;
+    f64x4_t acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = f64x4_t{0.0, 0.0, 0.0, 0.0};
+    double m = -INFINITY, lsum = 0.0;
+    // K row k0 + q (dims 32 g..), V rows k0 + 4 j + g (dims 8 q..), clamped into the cache;
+    // the next block's are in flight while a block is computed
+    uint4 kw[4], vw[4];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) kw[j] = ldg16(reinterpret_cast<const uint4*>(kb + (size_t)min(k0 + q, klast) * kFD + 32 * g) + j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vw[j] = ldg16(vb + (size_t)min(k0 + 4 * j + g, klast) * kFD + 8 * q);
+    };
+    const int step = 32, kfirst = 16 * half;
+    if (kfirst <= klast) load(kfirst);
+    for (int k0 = kfirst; k0 <= klast; k0 += step) {
+        const uint4 kc[4] = {kw[0], kw[1], kw[2], kw[3]};
+        const uint4 vc[4] = {vw[0], vw[1], vw[2], vw[3]};
+        if (k0 + step <= klast) load(k0 + step);
+        f64x4_t sa = {0.0, 0.0, 0.0, 0.0}, sb = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const uint4 w4 = kc[j / 8];
+            const uint32_t w = (j % 8) < 2 ? w4.x : (j % 8) < 4 ? w4.y : (j % 8) < 6 ? w4.z : w4.w;
+            const double kv = (j % 2) ? (double)__uint_as_float(w & 0xffff0000u) : (double)bf16_bits_to_f32(w & 0xffffu);
+            if (j % 2) sb = mfma_f64(kv, qd[j], sb);
+            else sa = mfma_f64(kv, qd[j], sa);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int64_t head = ((int64_t)a.layer * kFNKV + x) * a.S * kFD;
-        const uint16_t* kb = a.kc + head;
-        const uint16_t* vb = a.vc + head;
-        double M0 = -INFINITY, M1 = -INFINITY, l0 = 0.0, l1 = 0.0;
-        double acc[2][2] = {{0.0, 0.0}, {0.0, 0.0}};
-        // With one workgroup of four waves per compute unit there are few waves to hide memory
-        // latency behind, so a block's 16 K chunks are all in flight together, and the next
-        // block's are issued before this block's P V.
-        uint4 kr[16];
-        auto load_k = [&](int j0) {
-            const int j = min(j0 + lane, n - 1);
-            const uint4* krow = reinterpret_cast<const uint4*>(kb + (size_t)j * kFD);
+        double e[4], mb = -INFINITY;
 #pragma unroll
-            for (int c = 0; c < 16; ++c) kr[c] = ldg16(krow + c);
-        };
-        load_k(0);
-        for (int j0 = 0; j0 < n; j0 += kWave) {
-            const bool valid = j0 + lane < n;
-            // The queries are read from LDS in every block (kept in registers they would take 512
-            // of them). The read offset of chunk c is passed through an empty asm that depends on
-            // the sums after chunk c - 2, so no more than two chunks' queries (64 registers) are
-            // read ahead of their use.
-            int qo = pf_fresh(0);
-            double s0 = 0.0, s1 = 0.0, sprev = 0.0, slag = 0.0;
+        for (int i = 0; i < 4; ++i) {
+            const int key = k0 + 4 * i + g;
+            e[i] = (qvalid && key <= qpos) ? (sa[i] + sb[i]) * sc : -INFINITY;
+            mb = fmax(mb, e[i]);
+        }
+        mb = fmax(mb, partner64<16>(mb));
+        mb = fmax(mb, partner64<32>(mb));
+        // raise the shift when the block's maximum exceeds it by more than 2^8 (always on
+        // the first block with a valid key); the same decision in the query's four lanes
+        const bool raise = mb > m + 256.0;
+        if (__any(raise)) {
+            const double alpha = raise ? exp(m - mb) : 1.0;      // 0 while m is -inf
+            lsum *= alpha;
 #pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                if (c >= 2) asm volatile("" : "+v"(qo) : "v"(slag));
-                const uint32_t k4[4] = {kr[c].x, kr[c].y, kr[c].z, kr[c].w};
+            for (int t = 0; t < 8; ++t) acc[t] *= alpha;
+            m = raise ? mb : m;
+        }
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int d = 8 * c + 2 * i + qo;
-                    const double klo = bf16_bits_to_f32(k4[i] & 0xffffu), khi = __uint_as_float(k4[i] & 0xffff0000u);
-                    s0 = fma(sh.qa[x][0][d], klo, s0);
-                    s0 = fma(sh.qa[x][0][d + 1], khi, s0);
-                    s1 = fma(sh.qa[x][1][d], klo, s1);
-                    s1 = fma(sh.qa[x][1][d + 1], khi, s1);
-                }
-                slag = sprev;
-                sprev = s0 + s1;
-            }
-            if (j0 + kWave < n) load_k(j0 + kWave);
-            s0 = valid ? s0 * sc : -INFINITY;
-            s1 = valid ? s1 * sc : -INFINITY;
-            const double N0 = fmax(M0, wave_max64(s0)), N1 = fmax(M1, wave_max64(s1));
-            const double c0 = exp(M0 - N0), c1 = exp(M1 - N1);     // 0 on the first block (M = -inf)
-            const double e0 = valid ? exp(s0 - N0) : 0.0, e1 = valid ? exp(s1 - N1) : 0.0;
-            l0 = fma(l0, c0, wave_sum64(e0));
-            l1 = fma(l1, c1, wave_sum64(e1));
-            acc[0][0] *= c0; acc[0][1] *= c0;
-            acc[1][0] *= c1; acc[1][1] *= c1;
-            M0 = N0;
-            M1 = N1;
-            const int nb = min(kWave, n - j0);
-            const uint32_t* vrow = reinterpret_cast<const uint32_t*>(vb + (size_t)j0 * kFD) + lane;
-            for (int u0 = 0; u0 < nb; u0 += 16) {
-                uint32_t vw[16];
+        for (int i = 0; i < 4; ++i) {
+            e[i] = e[i] == -INFINITY ? 0.0 : exp(e[i] - m);
+            lsum += e[i];
+        }
 #pragma unroll
-                for (int u = 0; u < 16; ++u) vw[u] = *gview(vrow + (kFD / 2) * min(u0 + u, nb - 1));
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t vv[4] = {vc[j].x, vc[j].y, vc[j].z, vc[j].w};
 #pragma unroll
-                for (int u = 0; u < 16; ++u) {
-                    const double q0 = readlane64(e0, u0 + u), q1 = readlane64(e1, u0 + u);   // 0 past the block
-                    const double vlo = bf16_bits_to_f32(vw[u] & 0xffffu), vhi = __uint_as_float(vw[u] & 0xffff0000u);
-                    acc[0][0] = fma(q0, vlo, acc[0][0]);
-                    acc[0][1] = fma(q0, vhi, acc[0][1]);
-                    acc[1][0] = fma(q1, vlo, acc[1][0]);
-                    acc[1][1] = fma(q1, vhi, acc[1][1]);
-                }
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t w = vv[t / 2];
+                const double v = (t % 2) ? (double)__uint_as_float(w & 0xffff0000u) : (double)bf16_bits_to_f32(w & 0xffffu);
+                acc[t] = mfma_f64(v, e[j], acc[t]);
             }
         }
-        const double r0 = rcp_nr(l0), r1 = rcp_nr(l1);
-        sh.out[256 * x + 2 * lane] = (float)(acc[0][0] * r0);
-        sh.out[256 * x + 2 * lane + 1] = (float)(acc[0][1] * r0);
-        sh.out[256 * x + 128 + 2 * lane] = (float)(acc[1][0] * r1);
-        sh.out[256 * x + 128 + 2 * lane + 1] = (float)(acc[1][1] * r1);
+    }
+    // wave 1 leaves its half in LDS; wave 0 merges (both barriers in every wave, unconditionally)
+    double* const slot = sh.am[pair][lane];
+    if (half == 1) {
+        slot[0] = m;
+        slot[1] = lsum;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) slot[2 + 4 * t + i] = acc[t][i];
     }
     __syncthreads();
-    // digit planes of the 2048 outputs: thread t takes elements [4t, +4) and [1024 + 4t, +4)
-    const int t = tid;
-    float ov[2][4];
-    uint32_t e = 0;
+    if (half == 0) {
+        const double m1 = slot[0];
+        const double mm = fmax(m, m1);
+        const double f0 = m == -INFINITY ? 0.0 : exp(m - mm), f1 = m1 == -INFINITY ? 0.0 : exp(m1 - mm);
+        lsum = lsum * f0 + slot[1] * f1;
+        lsum += partner64<16>(lsum);        // the query's four lanes: all valid or all not
+        lsum += partner64<32>(lsum);
+        const double r = rcp_nr(lsum);
+        float o[4][8];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) {
-        const float4 o = reinterpret_cast<const float4*>(sh.out)[256 * g + t];
-        ov[g][0] = o.x; ov[g][1] = o.y; ov[g][2] = o.z; ov[g][3] = o.w;
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) e = max(e, exp_field(ov[g][i]));
+            for (int t = 0; t < 8; ++t) o[i][t] = (float)((acc[t][i] * f0 + slot[2 + 4 * t + i] * f1) * r);
+        if (qvalid) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float4* dst = reinterpret_cast<float4*>(qrow + 32 * i + 8 * g);
+                dst[0] = make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
+                dst[1] = make_float4(o[i][4], o[i][5], o[i][6], o[i][7]);
+            }
+        }
     }
-    e = block_max_u32(e, sh.rede, w, lane, kFThreads / kWave);
-#pragma unroll
-    for (int g = 0; g < 2; ++g) store_digits4(pf_buf<uint8_t>(a, L.dig), a.Pp, p, 1024 * g + 4 * t, ov[g], e);
-    if (t == 0) pf_buf<uint32_t>(a, L.emax)[p] = e;
-    __syncthreads();                        // sh.out / sh.rede are reused by the next item
+    __syncthreads();                        // the slot is read before the next round writes it
 }
 
 // ---- grid barrier ----------------------------------------------------------------------
@@ -599,23 +628,32 @@ __global__ void __launch_bounds__(kFThreads, 1) pf_chunk_kernel(PfArgs a) {
         for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_QKV>::NRT * PT; t += G) pf_gemm<EPI_QKV>(b, t);
         if (l == a.L - 1) { stamp(2); break; }                 // the last layer contributes its cache rows only
         barrier(1);
-        // attention items in snake order (round r takes r G + g, or r G + G - 1 - g when r is
-        // odd), so a workgroup's short and long contexts even out
-        for (int r = 0, gr = pf_fresh_uniform(g); r * G < a.P; ++r) {
-            const int p = r * G + (r % 2 == 0 ? gr : G - 1 - gr);
-            if (p < a.P) pf_attention(b, p, sh);
+        {
+            // attention items (KV head, tile of 8 positions), one per wave pair (waves 0-1, 2-3):
+            // pair w of workgroup g is slot w G + g of the grid, so the items of a round spread
+            // over every workgroup before a workgroup's second pair takes one; rounds alternate
+            // direction (snake), so that short and long contexts even out
+            const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+            const int ns = 2 * G, slot = pf_fresh_uniform((w / 2) * G + g);
+            const int items = kFNKV * ((a.P + 7) / 8);
+            for (int r = 0; r * ns < items; ++r) {
+                const int it = r * ns + (r % 2 == 0 ? slot : ns - 1 - slot);
+                pf_attention_tile(b, it % kFNKV, 8 * (it / kFNKV), w % 2, it < items, sh, w / 2);
+            }
         }
         barrier(2);
-        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_O>::NRT * PT; t += G) pf_gemm<EPI_O>(b, t);
+        for (int p = pf_fresh_uniform(g); p < a.P; p += G) pf_digits<kFQ, SRC_A>(b, p, sh);
         barrier(3);
-        for (int p = pf_fresh_uniform(g); p < a.P; p += G) pf_digits<kFH, SRC_X>(b, p, sh);
+        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_O>::NRT * PT; t += G) pf_gemm<EPI_O>(b, t);
         barrier(4);
-        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_GU>::NRT * PT; t += G) pf_gemm<EPI_GU>(b, t);
+        for (int p = pf_fresh_uniform(g); p < a.P; p += G) pf_digits<kFH, SRC_X>(b, p, sh);
         barrier(5);
-        for (int p = pf_fresh_uniform(g); p < a.P; p += G) pf_digits<kFI, SRC_M>(b, p, sh);
+        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_GU>::NRT * PT; t += G) pf_gemm<EPI_GU>(b, t);
         barrier(6);
-        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_DOWN>::NRT * PT; t += G) pf_gemm<EPI_DOWN>(b, t);
+        for (int p = pf_fresh_uniform(g); p < a.P; p += G) pf_digits<kFI, SRC_M>(b, p, sh);
         barrier(7);
+        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_DOWN>::NRT * PT; t += G) pf_gemm<EPI_DOWN>(b, t);
+        barrier(8);
     }
 }
 

@@ -470,13 +470,13 @@ class _DecoderBase:
 
     def set_prefill_trace(self, buf) -> None:
         """Record the phase timeline of the following prefills' last chunk into ``buf`` (int64,
-        at least ``num_layers * 16 * n_cu`` entries on the decoder's device, n_cu = the device's
-        compute units, entry ``(l * 16 + 2 k + e) * n_cu + g``: workgroup g done with phase k of
+        at least ``num_layers * 18 * n_cu`` entries on the decoder's device, n_cu = the device's
+        compute units, entry ``(l * 18 + 2 k + e) * n_cu + g``: workgroup g done with phase k of
         layer l, e = 1 past the grid barrier after it); ``None`` stops it."""
         if buf is None:
             self._pf_trace_ptr = None
             return
-        need = self.num_layers * 16 * torch.cuda.get_device_properties(self.device).multi_processor_count
+        need = self.num_layers * 18 * torch.cuda.get_device_properties(self.device).multi_processor_count
         if buf.dtype != torch.int64 or buf.numel() < need or buf.device != self.device or not buf.is_contiguous():
             raise ValueError(f"prefill trace buffer must be a contiguous int64 tensor of >= {need} entries on {self.device}")
         self._pf_trace_buf = buf
