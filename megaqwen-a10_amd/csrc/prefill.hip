@@ -102,6 +102,7 @@ static_assert(sizeof(PfSync) <= 1024, "barrier state");
 // LDS of a workgroup, shared by the phases
 struct PfShared {
     double am[2][kWave][34];               // attention: a wave pair's second half (m, denominator, outputs)
+    uint4 gb[2][8][kWave];                 // products: a K block's weight operands (B), shared by the waves
     double reds[4];
     uint32_t rede[4];
 };
@@ -240,7 +241,7 @@ struct GemmShape {
 };
 
 template <int EPI>
-__device__ void pf_gemm(const PfArgs& a, int tile) {
+__device__ void pf_gemm(const PfArgs& a, int tile, PfShared& sh) {
     using GS = GemmShape<EPI>;
     constexpr int K = GS::K, NT = GS::NT, NK = K / 64;
     const PfLayout L = pf_layout((size_t)a.Pp);
@@ -284,45 +285,117 @@ __device__ void pf_gemm(const PfArgs& a, int tile) {
     for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[j][t] = i32x4_t{0, 0, 0, 0};
-    auto load = [&](int kb, i32x4_t (&A)[4], i32x4_t (&B)[NT]) {
+    // Each wave loads a quarter of a K block's weight tile (NB of the NT row blocks) and
+    // shares it through LDS: the four waves would otherwise each load the whole tile, and
+    // those loads (16 rows x 64 bytes per instruction) were most of a product's time.
+    constexpr int NB = NT / 4;
+    auto load = [&](int kb, i32x4_t (&A)[4], uint4 (&Bs)[NB]) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint4 u = ldg16(abase + kb * kstride + 1024 * j);
             A[j] = i32x4_t{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
         }
 #pragma unroll
+        for (int u = 0; u < NB; ++u) Bs[u] = ldg16(wrow[NB * w + u] + 64 * kb);
+    };
+    // three K blocks' operands in registers (stage kb % 3): block kb + 3's loads go into the
+    // registers block kb has just used, so each load has three blocks of work to arrive in
+    i32x4_t A0[4], A1[4], A2[4];
+    uint4 B0[NB], B1[NB], B2[NB];
+    load(0, A0, B0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (NK > 1) load(1, A1, B1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (NK > 2) load(2, A2, B2);
+    __builtin_amdgcn_sched_barrier(0);
+    auto step = [&](int kb, i32x4_t (&A)[4], uint4 (&Bs)[NB]) {
+        // the wave's share into LDS buffer kb % 2; after the barrier every wave has finished
+        // block kb - 1, whose buffer kb + 1 will overwrite
+        uint4 (*gb)[kWave] = sh.gb[kb % 2];
+#pragma unroll
+        for (int u = 0; u < NB; ++u) gb[NB * w + u][lane] = Bs[u];
+        __syncthreads();
+        i32x4_t B[NT];
+#pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const uint4 u = ldg16(wrow[t] + 64 * kb);
+            const uint4 u = gb[t][lane];
             B[t] = i32x4_t{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
         }
-    };
-    i32x4_t A[4], B[NT];
-    load(0, A, B);
-    for (int kb = 0; kb < NK; ++kb) {
-        i32x4_t An[4], Bn[NT];
-        if (kb + 1 < NK) load(kb + 1, An, Bn);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int t = 0; t < NT; ++t) acc[j][t] = mfma_i8(A[j], B[t], acc[j][t]);
-        if (kb + 1 < NK) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) A[j] = An[j];
-#pragma unroll
-            for (int t = 0; t < NT; ++t) B[t] = Bn[t];
-        }
+        if (kb + 3 < NK) load(kb + 3, A, Bs);
+        // kept in this order: left to itself the scheduler moves later blocks' MFMAs up to
+        // the loads and waits for nearly every load in flight before the first of them
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int kb = 0; kb < NK; kb += 3) {
+        step(kb, A0, B0);
+        if (kb + 1 < NK) step(kb + 1, A1, B1);
+        if (kb + 2 < NK) step(kb + 2, A2, B2);
     }
+    __syncthreads();                        // the last blocks' buffers are read before the next tile writes them
 
     // ---- epilogue ----
+    // Every global value the epilogue reads is requested first, for all four pairs, so that
+    // they come back in one memory round trip (issued pair by pair, each pair waited for
+    // its own: four round trips per tile).
     const bool owner = (lane & 16) == 0;       // after tile_value: lanes 0-15 (even pair member), 32-47 (odd)
     const uint32_t* emax = pf_buf<uint32_t>(a, L.emax);
+    int pj[4];
+    uint32_t exv[4];
+    float scv[NT];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int p = p0 + 2 * j + (lane >> 5);            // chunk position of this lane's values
-        const uint32_t ex = emax[p];                        // p < Pp: in the buffer (padding rows unused)
+        pj[j] = p0 + 2 * j + (lane >> 5);                  // chunk position of this lane's values (< Pp)
+        exv[j] = emax[pj[j]];
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) scv[t] = *srow[t];
+    // QKV: QK-norm gains and the positions' RoPE rows (bf16, rows clamped into the table);
+    // O / down: the residual rows
+    uint32_t gnv[8], cs[4][16];
+    float res[4][NT];
+    if constexpr (EPI == EPI_QKV) {
+        if (rt < 24) {
+            const uint16_t* gn = static_cast<const uint16_t*>(rt < 16 ? lw.q_norm_weight : lw.k_norm_weight);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                gnv[t] = gn[16 * t + l16];
+                gnv[t + 4] = gn[16 * t + l16 + 64];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int pos = min(a.pos0 + pj[j], a.S - 1);
+                const uint16_t* cr = a.cos_t + (size_t)pos * kFD;
+                const uint16_t* sr = a.sin_t + (size_t)pos * kFD;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int i = 16 * t + l16;
+                    cs[j][t] = cr[i];
+                    cs[j][4 + t] = cr[i + 64];
+                    cs[j][8 + t] = sr[i];
+                    cs[j][12 + t] = sr[i + 64];
+                }
+            }
+        }
+    } else if constexpr (EPI == EPI_O || EPI == EPI_DOWN) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int n = 64 * rt + 16 * t + l16;
+                if constexpr (EPI == EPI_O) res[j][t] = bf16_bits_to_f32(pf_buf<uint16_t>(a, L.hid)[(size_t)pj[j] * kFH + n]);
+                else res[j][t] = pf_buf<float>(a, L.x)[(size_t)pj[j] * kFH + n];
+            }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int p = pj[j];
         double val[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) val[t] = tile_value(acc[j][t], ex);
+        for (int t = 0; t < NT; ++t) val[t] = tile_value(acc[j][t], exv[j]);
         const bool store = owner && p < a.P;
         const int pos = a.pos0 + p;
         if constexpr (EPI == EPI_QKV) {
@@ -333,7 +406,7 @@ __device__ void pf_gemm(const PfArgs& a, int tile) {
                 double ss = 0.0;
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
-                    y[t] = (float)(val[t] * (double)*srow[t]);
+                    y[t] = (float)(val[t] * (double)scv[t]);
                     ss = fma((double)y[t], (double)y[t], ss);
                 }
                 ss += partner64<1>(ss);
@@ -342,18 +415,15 @@ __device__ void pf_gemm(const PfArgs& a, int tile) {
                 ss += partner64<8>(ss);
                 if (store) {
                     const double rs = rms_scale(ss, kFD, kEps);
-                    const uint16_t* gn = static_cast<const uint16_t*>(rt < 16 ? lw.q_norm_weight : lw.k_norm_weight);
-                    const uint16_t* cr = a.cos_t + (size_t)pos * kFD;
-                    const uint16_t* sr = a.sin_t + (size_t)pos * kFD;
                     const int64_t crow = rt < 16 ? 0 : (((int64_t)a.layer * kFNKV + (rt - 16)) * a.S + pos) * kFD;
                     float* qrow = pf_buf<float>(a, L.q) + (size_t)p * kFQ + 128 * rt;
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
                         const int i = 16 * t + l16;
-                        const double y0 = (double)y[t] * rs * (double)bf16_bits_to_f32(gn[i]);
-                        const double y1 = (double)y[t + 4] * rs * (double)bf16_bits_to_f32(gn[i + 64]);
-                        const double cl = bf16_bits_to_f32(cr[i]), ch = bf16_bits_to_f32(cr[i + 64]);
-                        const double sl = bf16_bits_to_f32(sr[i]), sh = bf16_bits_to_f32(sr[i + 64]);
+                        const double y0 = (double)y[t] * rs * (double)bf16_bits_to_f32(gnv[t]);
+                        const double y1 = (double)y[t + 4] * rs * (double)bf16_bits_to_f32(gnv[t + 4]);
+                        const double cl = bf16_bits_to_f32(cs[j][t]), ch = bf16_bits_to_f32(cs[j][4 + t]);
+                        const double sl = bf16_bits_to_f32(cs[j][8 + t]), sh = bf16_bits_to_f32(cs[j][12 + t]);
                         const float o0 = (float)(y0 * cl - y1 * sl);
                         const float o1 = (float)(y0 * sh + y1 * ch);
                         if (rt < 16) {
@@ -369,16 +439,15 @@ __device__ void pf_gemm(const PfArgs& a, int tile) {
                 const int64_t crow = (((int64_t)a.layer * kFNKV + (rt - 24)) * a.S + pos) * kFD;
 #pragma unroll
                 for (int t = 0; t < 8; ++t)
-                    a.vc[crow + 16 * t + l16] = (uint16_t)f32_to_bf16_bits((float)(val[t] * (double)*srow[t]));
+                    a.vc[crow + 16 * t + l16] = (uint16_t)f32_to_bf16_bits((float)(val[t] * (double)scv[t]));
             }
         } else if constexpr (EPI == EPI_O) {
             if (store) {
-                const uint16_t* hid = pf_buf<uint16_t>(a, L.hid) + (size_t)p * kFH;
                 float* x = pf_buf<float>(a, L.x) + (size_t)p * kFH;
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
                     const int n = 64 * rt + 16 * t + l16;
-                    x[n] = (float)(val[t] * (double)*srow[t] + (double)bf16_bits_to_f32(hid[n]));
+                    x[n] = (float)(val[t] * (double)scv[t] + (double)res[j][t]);
                 }
             }
         } else if constexpr (EPI == EPI_GU) {
@@ -386,19 +455,18 @@ __device__ void pf_gemm(const PfArgs& a, int tile) {
                 float* m = pf_buf<float>(a, L.m) + (size_t)p * kFI;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    const double gs = val[t] * (double)*srow[t];
-                    const double us = val[t + 4] * (double)*srow[t + 4];
+                    const double gs = val[t] * (double)scv[t];
+                    const double us = val[t + 4] * (double)scv[t + 4];
                     m[64 * rt + 16 * t + l16] = (float)silu_mul(gs, us);
                 }
             }
         } else {
             if (store) {
-                const float* x = pf_buf<float>(a, L.x) + (size_t)p * kFH;
                 uint16_t* hid = pf_buf<uint16_t>(a, L.hid) + (size_t)p * kFH;
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
                     const int n = 64 * rt + 16 * t + l16;
-                    hid[n] = (uint16_t)f32_to_bf16_bits((float)(val[t] * (double)*srow[t] + (double)x[n]));
+                    hid[n] = (uint16_t)f32_to_bf16_bits((float)(val[t] * (double)scv[t] + (double)res[j][t]));
                 }
             }
         }
@@ -625,7 +693,7 @@ __global__ void __launch_bounds__(kFThreads, 1) pf_chunk_kernel(PfArgs a) {
             else pf_digits<kFH, SRC_HID>(b, p, sh);
         }
         barrier(0);
-        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_QKV>::NRT * PT; t += G) pf_gemm<EPI_QKV>(b, t);
+        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_QKV>::NRT * PT; t += G) pf_gemm<EPI_QKV>(b, t, sh);
         if (l == a.L - 1) { stamp(2); break; }                 // the last layer contributes its cache rows only
         barrier(1);
         {
@@ -644,15 +712,15 @@ __global__ void __launch_bounds__(kFThreads, 1) pf_chunk_kernel(PfArgs a) {
         barrier(2);
         for (int p = pf_fresh_uniform(g); p < a.P; p += G) pf_digits<kFQ, SRC_A>(b, p, sh);
         barrier(3);
-        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_O>::NRT * PT; t += G) pf_gemm<EPI_O>(b, t);
+        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_O>::NRT * PT; t += G) pf_gemm<EPI_O>(b, t, sh);
         barrier(4);
         for (int p = pf_fresh_uniform(g); p < a.P; p += G) pf_digits<kFH, SRC_X>(b, p, sh);
         barrier(5);
-        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_GU>::NRT * PT; t += G) pf_gemm<EPI_GU>(b, t);
+        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_GU>::NRT * PT; t += G) pf_gemm<EPI_GU>(b, t, sh);
         barrier(6);
         for (int p = pf_fresh_uniform(g); p < a.P; p += G) pf_digits<kFI, SRC_M>(b, p, sh);
         barrier(7);
-        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_DOWN>::NRT * PT; t += G) pf_gemm<EPI_DOWN>(b, t);
+        for (int t = pf_fresh_uniform(g); t < GemmShape<EPI_DOWN>::NRT * PT; t += G) pf_gemm<EPI_DOWN>(b, t, sh);
         barrier(8);
     }
 }
