@@ -403,9 +403,10 @@ class _DecoderBase:
         return out
 
     PREFILL_CHUNK = 512      # positions per prefill chunk (workspace ~51 KB per position)
-    # shortest prompt prefix generate() sends through prefill(): the prefill's ~220 launches cost
-    # about as much as 8 decode steps in one launch, so shorter prompts run as decode steps
-    PREFILL_MIN = 32
+    # shortest prompt prefix generate() sends through prefill(): a prefill of a few positions
+    # takes about 4 ms (one pass over the weights per product phase), as long as 12 decode steps
+    # in one launch, so shorter prompts run as decode steps
+    PREFILL_MIN = 16
 
     def prefill_supported(self) -> bool:
         """Whether ``prefill`` runs for this decoder (INT8 weights, hidden 1024)."""
