@@ -338,6 +338,16 @@ int mq_int8_decode_batch_step(const mq_batch_args* args, hipStream_t stream);
  * checked once per device), 1 = single-level exchange kernel, 2 = XCD-aware,
  * 3 = async-wave (INT8 Qwen3-0.6B shape, cache_len <= 2048 only). */
 int mq_decode_set_variant(int variant);
+/* Launch mode of the persistent kernels (decode steps, generation, batched
+ * steps, prefill chunks) for all following calls in this process. 0 (default):
+ * plain launches; every workgroup must be resident at once, which is checked
+ * with the occupancy calculator but not guaranteed when other work holds compute
+ * units (the step's bounded waits then end it with MQ_ERR_TIMEOUT). 1:
+ * cooperative launches, which the runtime starts only when all workgroups can
+ * be resident (about 10 us more per launch; timing events are recorded around
+ * the launch instead of by the dispatch). No counterpart in the reference,
+ * whose launchers are cooperative. */
+int mq_decode_set_cooperative(int enable);
 /* The variant a short-context step (cache_len 1) with these dims would use now
  * (1, 2 or 3), or -status. */
 int mq_decode_variant(const mq_model_dims* dims, int int8);

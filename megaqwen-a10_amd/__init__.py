@@ -22,7 +22,7 @@ library (``lib/libmegaqwen_a10.so``, declared in include/megaqwen_a10.h):
 from .config import QWEN3_0_6B, QWEN3_1_7B, ModelConfig
 from .decoder import (A10Decoder, A10Fp8MegakernelDecoder, A10Int4MegakernelDecoder, A10Int8BatchDecoder,
                       A10Int8MegakernelDecoder, A10MegakernelDecoder, config_from_checkpoint, decode_variant, load_checkpoint_state,
-                      load_tokenizer, set_decode_variant)
+                      load_tokenizer, set_cooperative_launch, set_decode_variant)
 from .formats import fp8_gemv, fp8_gemv_repeat, int4_gemv, int4_gemv_repeat, quantize_fp8, quantize_int4
 from .gemv import int8_gemv, int8_gemv_repeat
 from .quant import quantize_per_channel
@@ -32,7 +32,7 @@ from .weights import pack_bf16, pack_int8, quantize_state, random_init_state, st
 __all__ = [
     "ModelConfig", "QWEN3_0_6B", "QWEN3_1_7B",
     "A10Decoder", "A10Fp8MegakernelDecoder", "A10Int4MegakernelDecoder", "A10Int8BatchDecoder", "A10Int8MegakernelDecoder", "A10MegakernelDecoder", "set_decode_variant",
-    "decode_variant", "config_from_checkpoint", "load_checkpoint_state", "load_tokenizer",
+    "decode_variant", "set_cooperative_launch", "config_from_checkpoint", "load_checkpoint_state", "load_tokenizer",
     "int8_gemv", "int8_gemv_repeat", "quantize_per_channel",
     "quantize_fp8", "quantize_int4", "fp8_gemv", "int4_gemv", "fp8_gemv_repeat", "int4_gemv_repeat", "make_rope", "precompute_rope_freqs",
     "pack_bf16", "pack_int8", "quantize_state", "random_init_state", "state_digest",

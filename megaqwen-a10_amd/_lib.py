@@ -121,6 +121,7 @@ _SIGNATURES = {
     "mq_decode_check": (c_int, [c_void_p, c_void_p]),
     "mq_wait_host_token": (c_int, [c_void_p, c_int, c_uint]),
     "mq_decode_set_variant": (c_int, [c_int]),
+    "mq_decode_set_cooperative": (c_int, [c_int]),
     "mq_decode_variant": (c_int, [c_void_p, c_int]),
     "mq_batch_workspace_bytes": (c_size_t, [c_void_p]),
     "mq_int8_decode_batch_step": (c_int, [POINTER(BatchArgs), c_void_p]),

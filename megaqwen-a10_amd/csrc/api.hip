@@ -530,6 +530,11 @@ int mq_decode_set_variant(int variant) {
     return set_decode_variant(variant);
 }
 
+int mq_decode_set_cooperative(int enable) {
+    clear_error();
+    return set_cooperative_launch(enable);
+}
+
 int mq_decode_variant(const mq_model_dims* dims, int int8) {
     clear_error();
     DecodeShape s;

@@ -564,6 +564,23 @@ int decode_variant_in_use(const DecodeShape& s, bool int8) { return decode_varia
 // barrier), so they are launched plainly: on this runtime a cooperative launch
 // cost about 10 us more per step. If other work holds CUs when a step starts,
 // its bounded waits end the step with MQ_ERR_TIMEOUT instead of hanging.
+static std::atomic<int> g_cooperative{0};
+
+int set_cooperative_launch(int on) {
+    g_cooperative = on ? 1 : 0;
+    return MQ_OK;
+}
+
+hipError_t launch_resident(const void* fn, dim3 grid, dim3 block, void** args, hipStream_t stream, hipEvent_t t0,
+                           hipEvent_t t1) {
+    if (g_cooperative.load() == 0) return hipExtLaunchKernel(fn, grid, block, args, 0, stream, t0, t1, 0);
+    hipError_t e = hipSuccess;
+    if (t0 != nullptr && (e = hipEventRecord(t0, stream)) != hipSuccess) return e;
+    if ((e = hipLaunchCooperativeKernel(fn, grid, block, args, 0, stream)) != hipSuccess) return e;
+    if (t1 != nullptr) e = hipEventRecord(t1, stream);
+    return e;
+}
+
 int check_residency(const void* fn, int threads) {
     static thread_local const void* checked_fn[64] = {nullptr};
     static thread_local int checked[64] = {0};
@@ -591,8 +608,8 @@ static int launch_t(const KArgs& ka, bool debug, hipStream_t stream, hipEvent_t 
     KArgs copy = ka;
     void* args[] = {&copy};
     // a plain launch (start/stop events when given): see check_residency
-    const hipError_t e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
-    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode): %s", hipGetErrorString(e));
+    const hipError_t e = launch_resident(fn, dim3(kNWG), dim3(kThreads), args, stream, t0, t1);
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "launch(decode): %s", hipGetErrorString(e));
     return MQ_OK;
 }
 

@@ -1455,8 +1455,8 @@ int launch_decode_async(const KArgs& ka, bool debug, bool int4, hipStream_t stre
     if (st != MQ_OK) return st;
     KArgs copy = ka;
     void* args[] = {&copy};
-    const hipError_t e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
-    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode_async): %s", hipGetErrorString(e));
+    const hipError_t e = launch_resident(fn, dim3(kNWG), dim3(kThreads), args, stream, t0, t1);
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "launch(decode_async): %s", hipGetErrorString(e));
     return MQ_OK;
 }
 

@@ -1110,8 +1110,8 @@ int launch_decode_batch(const mq_batch_args& a, const DecodeShape& s, hipStream_
     void* args[] = {&k};
     hipEvent_t t0 = static_cast<hipEvent_t>(a.timing_start), t1 = static_cast<hipEvent_t>(a.timing_stop);
     // a plain launch (start/stop events when given): see check_residency
-    const hipError_t e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
-    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode_batch): %s", hipGetErrorString(e));
+    const hipError_t e = launch_resident(fn, dim3(kNWG), dim3(kThreads), args, stream, t0, t1);
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "launch(decode_batch): %s", hipGetErrorString(e));
     return MQ_OK;
 }
 

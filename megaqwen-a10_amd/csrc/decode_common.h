@@ -267,6 +267,12 @@ __device__ __forceinline__ double rms_scale(double sumsq, int n, double eps) {
 // All kNWG workgroups wait on each other, so they must be resident at once:
 // checked once per (kernel, device) with the occupancy calculator.
 int check_residency(const void* fn, int threads = kThreads);
+// Launch of a kernel whose workgroups wait on each other: a plain launch (start/stop events
+// recorded by the dispatch when given), or with set_cooperative_launch(1) a cooperative one,
+// which the runtime starts only when every workgroup can be resident at once (events then
+// recorded around it on the stream).
+hipError_t launch_resident(const void* fn, dim3 grid, dim3 block, void** args, hipStream_t stream,
+                           hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
 
 // Async-wave kernel (decode_async.hip): INT8 Qwen3-0.6B shape, cache_len <= 2048 (split
 // attention past 64).

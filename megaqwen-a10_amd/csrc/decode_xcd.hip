@@ -792,8 +792,8 @@ static int launch_xcd_t(const KArgs& ka, bool debug, hipStream_t stream, hipEven
     KArgs copy = ka;
     void* args[] = {&copy};
     // a plain launch (start/stop events when given): see check_residency
-    const hipError_t e = hipExtLaunchKernel(fn, dim3(kNWG), dim3(kThreads), args, 0, stream, t0, t1, 0);
-    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipExtLaunchKernel(decode_xcd): %s", hipGetErrorString(e));
+    const hipError_t e = launch_resident(fn, dim3(kNWG), dim3(kThreads), args, stream, t0, t1);
+    if (e != hipSuccess) return set_error(MQ_ERR_HIP, "launch(decode_xcd): %s", hipGetErrorString(e));
     return MQ_OK;
 }
 

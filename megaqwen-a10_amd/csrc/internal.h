@@ -50,6 +50,9 @@ size_t decode_workspace_bytes(const DecodeShape& s);
 // Kernel variant: 0 = automatic (XCD-aware when the workgroups of each residue
 // class g mod 8 share one XCD), 1 = single-level exchange kernel, 2 = XCD-aware.
 int set_decode_variant(int variant);
+// 1: the persistent kernels are launched cooperatively (co-residency guaranteed by the
+// runtime, about 10 us more per launch); 0 (default): plain launches.
+int set_cooperative_launch(int on);
 int decode_variant_in_use(const DecodeShape& s, bool int8);
 // After an in-kernel placement failure: use the single-level kernel from now on.
 void mark_xcd_unusable();

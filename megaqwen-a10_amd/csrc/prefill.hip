@@ -804,7 +804,10 @@ int launch_prefill(const mq_decode_args& d, const int* tokens, int n_tokens, voi
         if (e != hipSuccess) return set_error(MQ_ERR_HIP, "hipMemcpyAsync(prefill tokens): %s", hipGetErrorString(e));
         // a fill kernel, not a memset, so that the launch sequence can be captured in a graph
         pf_sync_reset_kernel<<<1, 1, 0, stream>>>(sy);
-        pf_chunk_kernel<<<grid, kFThreads, 0, stream>>>(a);
+        void* args[] = {&a};
+        const hipError_t le = launch_resident(reinterpret_cast<const void*>(&pf_chunk_kernel), dim3(grid),
+                                              dim3(kFThreads), args, stream);
+        if (le != hipSuccess) return set_error(MQ_ERR_HIP, "launch(prefill): %s", hipGetErrorString(le));
         st = check_launch("prefill");
         if (st != MQ_OK) return st;
     }

@@ -48,6 +48,13 @@ def set_decode_variant(name: str) -> None:
     _lib.check(lib.mq_decode_set_variant(VARIANTS[name]), "mq_decode_set_variant")
 
 
+def set_cooperative_launch(enable: bool) -> None:
+    """Launch the persistent kernels cooperatively from now on (``True``): the runtime then
+    starts a step only when all of its workgroups can be resident at once, at about 10 us
+    per launch; ``False`` (default) launches plainly (mq_decode_set_cooperative)."""
+    _lib.check(_lib.load().mq_decode_set_cooperative(int(bool(enable))), "mq_decode_set_cooperative")
+
+
 def decode_variant(hidden_size: int = 1024, intermediate_size: int = 3072, int8: bool = True) -> str:
     """The kernel a step with these dims would use now."""
     lib = _lib.load()
