@@ -100,8 +100,21 @@ def test_generate_api_rejects_bad_arguments_without_launching(mq):
     assert lib.mq_int8_decode_generate(ctypes.byref(a), ctypes.byref(g), None) == _lib.MQ_ERR_INVALID_ARGUMENT
     prompt = (ctypes.c_int * 2)(1, 2)
     g = _lib.GenerateArgs(ctypes.cast(prompt, ctypes.c_void_p), 0, 4, 1234)
-    assert lib.mq_int8_decode_generate(ctypes.byref(a), ctypes.byref(g), None) == _lib.MQ_ERR_INVALID_ARGUMENT
-    assert "n_forced" in _lib.last_error()
+    for fn in (lib.mq_int8_decode_generate, lib.mq_int4_decode_generate, lib.mq_fp8_decode_generate,
+               lib.mq_bf16_decode_generate):
+        assert fn(ctypes.byref(a), ctypes.byref(g), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+        assert "n_forced" in _lib.last_error()
+        assert fn(None, ctypes.byref(g), None) == _lib.MQ_ERR_INVALID_ARGUMENT
+
+
+def test_cooperative_switch_is_host_only(mq):
+    """mq_decode_set_cooperative only sets the launch mode (no device work, any value is 0/1)."""
+    from megaqwen_a10_amd import _lib
+    lib = _lib.load()
+    assert lib.mq_decode_set_cooperative(1) == _lib.MQ_OK
+    assert lib.mq_decode_set_cooperative(7) == _lib.MQ_OK
+    assert lib.mq_decode_set_cooperative(0) == _lib.MQ_OK
+    mq.set_cooperative_launch(False)
 
 
 def test_batch_api_rejects_bad_arguments_without_launching(mq):
