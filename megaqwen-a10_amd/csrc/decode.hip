@@ -582,11 +582,15 @@ hipError_t launch_resident(const void* fn, dim3 grid, dim3 block, void** args, h
 }
 
 int check_residency(const void* fn, int threads) {
-    static thread_local const void* checked_fn[64] = {nullptr};
-    static thread_local int checked[64] = {0};
+    // the (device, kernel) pairs that passed, so that alternating kernels (per-step and
+    // multi-step decode, prefill) do not repeat the occupancy query
+    struct Passed { int dev; const void* fn; };
+    static thread_local Passed passed[32];
+    static thread_local int n_passed = 0, next = 0;      // entries in use (<= 32), slot written next
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return set_error(MQ_ERR_HIP, "hipGetDevice failed");
-    if (checked[dev] && checked_fn[dev] == fn) return MQ_OK;
+    for (int i = 0; i < n_passed; ++i)
+        if (passed[i].dev == dev && passed[i].fn == fn) return MQ_OK;
     int ncu = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, 0) != hipSuccess)
@@ -594,8 +598,9 @@ int check_residency(const void* fn, int threads) {
     if ((int64_t)ncu * per_cu < kNWG)
         return set_error(MQ_ERR_UNSUPPORTED, "device holds %d x %d resident workgroups, the decode kernel needs %d",
                          ncu, per_cu, kNWG);
-    checked[dev] = 1;
-    checked_fn[dev] = fn;
+    passed[next] = Passed{dev, fn};
+    next = (next + 1) % 32;
+    if (n_passed < 32) ++n_passed;
     return MQ_OK;
 }
 

@@ -495,7 +495,12 @@ class _DecoderBase:
         if self._inflight:
             torch.cuda.current_stream(self.device).synchronize()
             self._inflight.clear()
-        out = torch.full((n_tokens,), TOKEN_PENDING, dtype=torch.int32, pin_memory=True)
+        # pinned output words, kept between calls (allocating pinned memory costs about a
+        # decode step's time); each call ends synchronised, so the buffer is free here
+        if getattr(self, "_gen_out", None) is None or self._gen_out.numel() < n_tokens:
+            self._gen_out = torch.empty(max(n_tokens, 256), dtype=torch.int32, pin_memory=True)
+        out = self._gen_out[:n_tokens]
+        out.fill_(TOKEN_PENDING)
         prompt = (ctypes.c_int * len(ids))(*ids)
         a = self._args
         a.input_token_id = ids[0]
