@@ -21,8 +21,10 @@
 //               and writes this layer's K/V cache rows and the rotated queries
 //               (a 128-row tile is one head, so the norm and the rotation pairs
 //               are inside one wave)                        tiles of 32 positions x 128 rows
-//   attention   causal, fp64 on the matrix cores, a wave per (KV head, 8 positions):
-//               its 16 queries over cache rows [0, pos0 + p]
+//   attention   causal, fp64 on the matrix cores, per (KV head, 8 positions) its 16
+//               queries over cache rows [0, pos0 + p]; a workgroup takes one such
+//               item or two of complementary length, its key blocks cut evenly over
+//               the four waves
 //   digits      of the attention output
 //   O           + residual (the layer input)                 32 positions x 64 rows
 //   digits      post-attention RMSNorm
@@ -101,7 +103,7 @@ static_assert(sizeof(PfSync) <= 1024, "barrier state");
 
 // LDS of a workgroup, shared by the phases
 struct PfShared {
-    double am[2][kWave][34];               // attention: a wave pair's second half (m, denominator, outputs)
+    double am[3][kWave][34];               // attention: parts handed to an item's leader wave (m, denominator, outputs)
     uint4 gb[2][8][kWave];                 // products: a K block's weight operands (B), shared by the waves
     double reds[4];
     uint32_t rede[4];
@@ -474,7 +476,7 @@ __device__ void pf_gemm(const PfArgs& a, int tile, PfShared& sh) {
 }
 
 // ---- causal attention on the fp64 matrix cores -------------------------------------------
-// Work item (KV head x, tile of 8 positions p0..p0+7) of one wave: its 16 queries (lane
+// Work item (KV head x, tile of 8 positions p0..p0+7): its 16 queries (lane
 // column q = lane % 16: position p0 + q % 8, query head 2x + q / 8) attend over the cache
 // rows [0, pos0 + p], 16 keys per block, with v_mfma_f64_16x16x4f64 (A: lane l holds
 // A[l % 16][l / 16]; B: B[l / 16][l % 16]; D: register i of lane l holds D[4 i + l / 16]
@@ -498,20 +500,25 @@ __device__ __forceinline__ f64x4_t mfma_f64(double a, double b, f64x4_t c) {
     return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
 }
 
-// Item (x, p0) is split over a wave pair: wave `half` takes the key blocks k0 = 16 (half +
-// 2 n); wave 1 leaves its shift, partial denominators and outputs in `am` and wave 0 merges
-// them with its own (each side scaled by e^(m_side - m)) after a workgroup barrier that
-// every wave of the workgroup reaches (`active` false: no item this round).
-__device__ void pf_attention_tile(const PfArgs& a, int x, int p0, int half, bool active, PfShared& sh, int pair) {
+// The key blocks [b0, b1) (16 keys each) of item (x, p0) in one wave: the partial softmax
+// state of the lane's query over them (shift m, partial denominator lsum, outputs acc, not
+// yet divided). An empty range leaves m = -inf, lsum = 0, acc = 0.
+__device__ __forceinline__ void pf_attn_blocks(const PfArgs& a, int x, int p0, int b0, int b1, double& m, double& lsum,
+                                               f64x4_t (&acc)[8]) {
     const PfLayout L = pf_layout((size_t)a.Pp);
     const int lane = pf_fresh(threadIdx.x) % kWave;
     const int q = lane % 16, g = lane / 16;
     const int pq = p0 + q % 8;                              // chunk position of the lane's query
-    const bool qvalid = active && pq < a.P;
+    const bool qvalid = pq < a.P;
     const int qpos = a.pos0 + pq;                           // its cache position: keys [0, qpos]
-    const int klast = active ? a.pos0 + min(p0 + 7, a.P - 1) : -1;   // the tile's last key
+    const int klast = a.pos0 + min(p0 + 7, a.P - 1);        // the item's last key
     const double sc = (double)a.attn_scale;
-    float* const qrow = pf_buf<float>(a, L.q) + (size_t)max(0, min(pq, a.P - 1)) * kFQ + 256 * x + 128 * (q / 8);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = f64x4_t{0.0, 0.0, 0.0, 0.0};
+    m = -INFINITY;
+    lsum = 0.0;
+    if (b0 >= b1) return;
+    const float* const qrow = pf_buf<float>(a, L.q) + (size_t)min(pq, a.P - 1) * kFQ + 256 * x + 128 * (q / 8);
     double qd[32];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -521,10 +528,6 @@ __device__ void pf_attention_tile(const PfArgs& a, int x, int p0, int half, bool
     const int64_t head = ((int64_t)a.layer * kFNKV + x) * a.S * kFD;
     const uint16_t* kb = a.kc + head;
     const uint16_t* vb = a.vc + head;
-    f64x4_t acc[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) acc[t] = f64x4_t{0.0, 0.0, 0.0, 0.0};
-    double m = -INFINITY, lsum = 0.0;
     // K row k0 + q (dims 32 g..), V rows k0 + 4 j + g (dims 8 q..), clamped into the cache;
     // the next block's are in flight while a block is computed
     uint4 kw[4], vw[4];
@@ -534,12 +537,12 @@ __device__ void pf_attention_tile(const PfArgs& a, int x, int p0, int half, bool
 #pragma unroll
         for (int j = 0; j < 4; ++j) vw[j] = ldg16(vb + (size_t)min(k0 + 4 * j + g, klast) * kFD + 8 * q);
     };
-    const int step = 32, kfirst = 16 * half;
-    if (kfirst <= klast) load(kfirst);
-    for (int k0 = kfirst; k0 <= klast; k0 += step) {
+    load(16 * b0);
+    for (int bk = b0; bk < b1; ++bk) {
+        const int k0 = 16 * bk;
         const uint4 kc[4] = {kw[0], kw[1], kw[2], kw[3]};
         const uint4 vc[4] = {vw[0], vw[1], vw[2], vw[3]};
-        if (k0 + step <= klast) load(k0 + step);
+        if (bk + 1 < b1) load(k0 + 16);
         f64x4_t sa = {0.0, 0.0, 0.0, 0.0}, sb = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
         for (int j = 0; j < 32; ++j) {
@@ -584,40 +587,111 @@ __device__ void pf_attention_tile(const PfArgs& a, int x, int p0, int half, bool
             }
         }
     }
-    // wave 1 leaves its half in LDS; wave 0 merges (both barriers in every wave, unconditionally)
-    double* const slot = sh.am[pair][lane];
-    if (half == 1) {
-        slot[0] = m;
-        slot[1] = lsum;
+}
+
+// Number of 16-key blocks of item (x, p0): keys [0, pos0 + min(p0 + 7, P - 1)].
+__device__ __forceinline__ int pf_attn_nblocks(const PfArgs& a, int p0) {
+    return (a.pos0 + min(p0 + 7, a.P - 1)) / 16 + 1;
+}
+
+// One attention unit on the workgroup's four waves: item A = (KV head x, positions pa ..
+// pa + 7) and, if pb >= 0, item B = (x, pb .. pb + 7). The unit's T = nA + nB key blocks (A's,
+// then B's) are cut into four contiguous ranges [T w / 4, T (w + 1) / 4), one per wave w, so
+// a wave's range may hold the end of A and the start of B. Wave 0 merges A's partial states
+// and writes A's outputs, wave 3 does the same for B. The other parts go through LDS: A's part
+// of wave w (w > 0) to slot w - 1, B's part of wave w (w < 3) to slot w (slot k cannot hold
+// both: A's part of wave k + 1 needs T (k + 1) / 4 < nA, B's part of wave k needs it > nA).
+// A leader computes its own part last, so that it stays in registers. Both workgroup
+// barriers are reached by every wave.
+__device__ void pf_attention_unit(const PfArgs& a, int x, int pa, int pb, PfShared& sh) {
+    const int w = __builtin_amdgcn_readfirstlane(pf_fresh(threadIdx.x) / kWave);
+    const int lane = pf_fresh(threadIdx.x) % kWave;
+    const int nA = pf_attn_nblocks(a, pa), nB = pb >= 0 ? pf_attn_nblocks(a, pb) : 0, T = nA + nB;
+    auto cut = [&](int i) { return (T * i) / 4; };
+    // the wave's parts, leader part last: (item, first block, end block, slot or -1 to keep)
+    int part_p[2], part_b0[2], part_b1[2], part_slot[2];
+    {
+        const int r0 = cut(w), r1 = cut(w + 1);
+        const int a0 = r0, a1 = min(r1, nA);                   // A's blocks of the range
+        const int c0 = max(r0, nA) - nA, c1 = r1 - nA;         // B's blocks of the range
+        if (w == 0) {
+            part_p[0] = pb; part_b0[0] = c0; part_b1[0] = nB > 0 ? c1 : c0; part_slot[0] = 0;
+            part_p[1] = pa; part_b0[1] = a0; part_b1[1] = a1; part_slot[1] = -1;
+        } else if (w == 3 && nB > 0) {
+            part_p[0] = pa; part_b0[0] = a0; part_b1[0] = a1; part_slot[0] = 2;
+            part_p[1] = pb; part_b0[1] = c0; part_b1[1] = c1; part_slot[1] = -1;
+        } else {
+            part_p[0] = pa; part_b0[0] = a0; part_b1[0] = a1; part_slot[0] = w - 1;
+            part_p[1] = pb; part_b0[1] = c0; part_b1[1] = nB > 0 ? c1 : c0; part_slot[1] = w;
+        }
+    }
+    double m = -INFINITY, lsum = 0.0;
+    f64x4_t acc[8];
+#pragma unroll 1
+    for (int k = 0; k < 2; ++k) {
+        const int pk = __builtin_amdgcn_readfirstlane(k == 0 ? part_p[0] : part_p[1]);
+        const int b0 = __builtin_amdgcn_readfirstlane(k == 0 ? part_b0[0] : part_b0[1]);
+        const int b1 = __builtin_amdgcn_readfirstlane(k == 0 ? part_b1[0] : part_b1[1]);
+        const int sl = __builtin_amdgcn_readfirstlane(k == 0 ? part_slot[0] : part_slot[1]);
+        if (sl >= 0 && b0 >= b1) continue;                     // no part to hand over
+        pf_attn_blocks(a, x, pk, b0, b1, m, lsum, acc);
+        if (sl >= 0) {
+            double* const slot = sh.am[sl][lane];
+            slot[0] = m;
+            slot[1] = lsum;
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
+            for (int t = 0; t < 8; ++t)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) slot[2 + 4 * t + i] = acc[t][i];
+                for (int i = 0; i < 4; ++i) slot[2 + 4 * t + i] = acc[t][i];
+        }
     }
     __syncthreads();
-    if (half == 0) {
-        const double m1 = slot[0];
-        const double mm = fmax(m, m1);
-        const double f0 = m == -INFINITY ? 0.0 : exp(m - mm), f1 = m1 == -INFINITY ? 0.0 : exp(m1 - mm);
-        lsum = lsum * f0 + slot[1] * f1;
+    const bool leadA = w == 0, leadB = w == 3 && nB > 0;
+    if (leadA || leadB) {
+        // the other waves' parts of this item: wave i's is in slot i - 1 (item A) or i (item B)
+        auto has = [&](int i) {
+            return leadA ? (i > 0 && cut(i) < min(cut(i + 1), nA)) : (i < 3 && max(cut(i), nA) < cut(i + 1));
+        };
+        double mm = m;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (has(i)) mm = fmax(mm, sh.am[leadA ? max(i - 1, 0) : min(i, 2)][lane][0]);
+        const double f0 = m == -INFINITY ? 0.0 : exp(m - mm);
+        lsum *= f0;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) acc[t] *= f0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (!has(i)) continue;
+            const double* const slot = sh.am[leadA ? max(i - 1, 0) : min(i, 2)][lane];
+            const double mj = slot[0];
+            const double fj = mj == -INFINITY ? 0.0 : exp(mj - mm);
+            lsum += slot[1] * fj;
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[t][j] += slot[2 + 4 * t + j] * fj;
+        }
         lsum += partner64<16>(lsum);        // the query's four lanes: all valid or all not
         lsum += partner64<32>(lsum);
         const double r = rcp_nr(lsum);
-        float o[4][8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int t = 0; t < 8; ++t) o[i][t] = (float)((acc[t][i] * f0 + slot[2 + 4 * t + i] * f1) * r);
-        if (qvalid) {
+        const int p0 = leadA ? pa : pb;
+        const int q = lane % 16, g = lane / 16;
+        const int pq = p0 + q % 8;
+        if (pq < a.P) {
+            float* const orow = pf_buf<float>(a, pf_layout((size_t)a.Pp).q) + (size_t)pq * kFQ + 256 * x + 128 * (q / 8);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float4* dst = reinterpret_cast<float4*>(qrow + 32 * i + 8 * g);
-                dst[0] = make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
-                dst[1] = make_float4(o[i][4], o[i][5], o[i][6], o[i][7]);
+                float o[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) o[t] = (float)(acc[t][i] * r);
+                float4* dst = reinterpret_cast<float4*>(orow + 32 * i + 8 * g);
+                dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+                dst[1] = make_float4(o[4], o[5], o[6], o[7]);
             }
         }
     }
-    __syncthreads();                        // the slot is read before the next round writes it
+    __syncthreads();                        // the slots are read before the next unit writes them
 }
 
 // ---- grid barrier ----------------------------------------------------------------------
@@ -667,7 +741,7 @@ __device__ __forceinline__ void pf_grid_barrier(PfSync* sy, uint32_t b, uint32_t
 // The whole chunk in one launch: every layer's eight phases, each phase's work items dealt
 // over the workgroups: product tiles round-robin as rt + NRT pt (with NRT a multiple of 8 a
 // row tile's position tiles all run on one XCD and share its L2 copy of the weights),
-// attention positions in snake order.
+// attention items in units of even length (pf_attention_unit).
 __global__ void __launch_bounds__(kFThreads, 1) pf_chunk_kernel(PfArgs a) {
     __shared__ PfShared sh;
     const PfLayout L0 = pf_layout((size_t)a.Pp);
@@ -697,16 +771,16 @@ __global__ void __launch_bounds__(kFThreads, 1) pf_chunk_kernel(PfArgs a) {
         if (l == a.L - 1) { stamp(2); break; }                 // the last layer contributes its cache rows only
         barrier(1);
         {
-            // attention items (KV head, tile of 8 positions), one per wave pair (waves 0-1, 2-3):
-            // pair w of workgroup g is slot w G + g of the grid, so the items of a round spread
-            // over every workgroup before a workgroup's second pair takes one; rounds alternate
-            // direction (snake), so that short and long contexts even out
-            const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-            const int ns = 2 * G, slot = pf_fresh_uniform((w / 2) * G + g);
-            const int items = kFNKV * ((a.P + 7) / 8);
-            for (int r = 0; r * ns < items; ++r) {
-                const int it = r * ns + (r % 2 == 0 ? slot : ns - 1 - slot);
-                pf_attention_tile(b, it % kFNKV, 8 * (it / kFNKV), w % 2, it < items, sh, w / 2);
+            // attention units, one per workgroup: a chunk of at most G items (KV head, tile of 8
+            // positions) gives each workgroup one item; a longer one pairs tile j with tile
+            // np - 1 - j of the same head, so that every unit holds about as many key blocks.
+            // Unit u runs KV head u % 8, on the XCD whose L2 then holds that head's rows.
+            const int np = (a.P + 7) / 8, items = kFNKV * np;
+            const bool paired = items > G;
+            const int units = paired ? kFNKV * ((np + 1) / 2) : items;
+            for (int u = pf_fresh_uniform(g); u < units; u += G) {
+                const int j = u / kFNKV, jb = np - 1 - j;
+                pf_attention_unit(b, u % kFNKV, 8 * j, paired && jb > j ? 8 * jb : -1, sh);
             }
         }
         barrier(2);
