@@ -68,6 +68,8 @@ def parse():
                     help="decode: INT8 per row (config 1), or INT4 per group of 128 with the LM head INT8")
     ap.add_argument("--depths", default="1024,4096,8192", help="longctx: KV depths")
     ap.add_argument("--batches", default="1,4,8,16", help="batched: batch sizes")
+    ap.add_argument("--variant", default="auto", choices=["auto", "xcd", "async"],
+                    help="longctx: decode kernel (auto: the library's choice per step)")
     ap.add_argument("--split-min", type=int, default=0,
                     help="longctx: attention split threshold (0 = library default, -1 = never)")
     ap.add_argument("--seed", type=int, default=0)
@@ -592,6 +594,7 @@ def run_longctx(args, mq, torch):
     embed, layers, scales, lm_q, lm_s, fnorm = mq.pack_int8(qstate, cfg)
     dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
     dec.set_attn_split(args.split_min)
+    mq.set_decode_variant(args.variant)
     first = int(prompt[-1])
     events = _events(torch, steps)
     per_depth = {}
@@ -613,10 +616,12 @@ def run_longctx(args, mq, torch):
             "tok_s": round(steps / wall, 1), "kernel_avg_us": round(sum(kern_ms) / steps * 1e3, 2),
             "device_tok_s": round(steps / (sum(kern_ms) / 1e3), 1), "achieved_GBs": round(achieved, 1),
             "frac": round(achieved / HBM_PEAK_GBS, 4), "roofline_tok_s": round(roof_tok_s, 1),
-            "bytes_per_launch_avg": int(bytes_total / steps), "kernel_pass_tokens_identical": toks2 == toks}
+            "bytes_per_launch_avg": int(bytes_total / steps), "kernel_pass_tokens_identical": toks2 == toks,
+            "kernel": mq.decode_variant(cfg.hidden_size, cfg.intermediate_size, int8=True, cache_len=depth + 1)}
         print(f"depth {depth}: {per_depth[str(depth)]}", file=sys.stderr, flush=True)
     top = per_depth[str(max(depths))]
-    variant = mq.decode_variant(cfg.hidden_size, cfg.intermediate_size, int8=True)
+    mq.set_decode_variant("auto")
+    variant = args.variant
     return {"metric": f"INT8 decode tok/s at KV depth {max(depths)}, Qwen3-0.6B shape bs=1 (BASELINE config 4)",
             "value": top["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
             "ms_per_step": round(1e3 / top["tok_s"], 4), "higher_is_better": True, "scaling": "weak",

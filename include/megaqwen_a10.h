@@ -265,7 +265,7 @@ int mq_fp8_decode_step(const mq_decode_args* args, hipStream_t stream);
  * fp32 group scales [out, in / 128] in place of the per-row scales (same
  * packing order); the LM head stays INT8 per row (lm_head_weight,
  * lm_head_scale). No counterpart in the reference. Hidden 1024 / intermediate
- * 3072 up to 2048 cached positions, on the async-wave kernel (MQ_ERR_UNSUPPORTED
+ * 3072 up to 10240 cached positions, on the async-wave kernel (MQ_ERR_UNSUPPORTED
  * otherwise): each group's exact digit-plane sum is scaled by its group scale
  * in fp64, so every stored intermediate is the correctly rounded value of the
  * dequantized weights' expression. */
@@ -282,7 +282,7 @@ int mq_int4_decode_step(const mq_decode_args* args, hipStream_t stream);
 int mq_int8_decode_step_noalloc(const mq_decode_args* args, hipStream_t stream);
 /* Several steps per launch (see mq_generate_args): INT8, bf16 and FP8 weights.
  * The async-wave kernel runs the launch within its range (INT8 Qwen3-0.6B shape,
- * position + steps <= 2048), the XCD-aware kernel's multi-step form otherwise
+ * position + steps <= 7168; 10240 when forced), the XCD-aware kernel's multi-step form otherwise
  * (every compiled shape and format, up to 32768 positions with split attention);
  * MQ_ERR_UNSUPPORTED on the single-level kernel. */
 int mq_int8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream);
@@ -333,10 +333,10 @@ int mq_int8_decode_batch_step(const mq_batch_args* args, hipStream_t stream);
 
 /* Kernel variant for all following steps in this process: 0 = automatic
  * (default: the async-wave kernel for INT8 steps of the Qwen3-0.6B shape up to
- * 2048 cached positions, otherwise the XCD-aware kernel, when the workgroups of
+ * 7168 cached positions, otherwise the XCD-aware kernel, when the workgroups of
  * each residue class g mod 8 share one XCD and the 8 classes cover the 8 XCDs,
  * checked once per device), 1 = single-level exchange kernel, 2 = XCD-aware,
- * 3 = async-wave (INT8 Qwen3-0.6B shape, cache_len <= 2048 only). */
+ * 3 = async-wave (INT8 Qwen3-0.6B shape, cache_len <= 10240 only). */
 int mq_decode_set_variant(int variant);
 /* Launch mode of the persistent kernels (decode steps, generation, batched
  * steps, prefill chunks) for all following calls in this process. 0 (default):
@@ -351,6 +351,10 @@ int mq_decode_set_cooperative(int enable);
 /* The variant a short-context step (cache_len 1) with these dims would use now
  * (1, 2 or 3), or -status. */
 int mq_decode_variant(const mq_model_dims* dims, int int8);
+/* The same for a step that attends over `cache_len` cached positions (the choice can depend
+ * on the context length); minus MQ_ERR_INVALID_ARGUMENT for cache_len < 1. No counterpart in the
+ * reference. */
+int mq_decode_variant_at(const mq_model_dims* dims, int int8, int cache_len);
 
 /* ---- reference-signature entry points (drop-in for the CUDA launchers) --- */
 /* a10_int8_decode_kernel.cu:821-842. Uses a library-owned workspace per

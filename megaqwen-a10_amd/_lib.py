@@ -123,6 +123,7 @@ _SIGNATURES = {
     "mq_decode_set_variant": (c_int, [c_int]),
     "mq_decode_set_cooperative": (c_int, [c_int]),
     "mq_decode_variant": (c_int, [c_void_p, c_int]),
+    "mq_decode_variant_at": (c_int, [c_void_p, c_int, c_int]),
     "mq_batch_workspace_bytes": (c_size_t, [c_void_p]),
     "mq_int8_decode_batch_step": (c_int, [POINTER(BatchArgs), c_void_p]),
     "launch_a10_int8_decode": (None, [c_int, c_void_p] + [c_void_p] * 20 + [c_int] * 4 + [c_float, c_void_p, c_void_p]),

@@ -543,6 +543,15 @@ int mq_decode_variant(const mq_model_dims* dims, int int8) {
     return decode_variant_in_use(s, int8 != 0);            // the variant, or minus the refusal's status
 }
 
+int mq_decode_variant_at(const mq_model_dims* dims, int int8, int cache_len) {
+    clear_error();
+    DecodeShape s;
+    int st = shape_of(dims, &s);
+    if (st != MQ_OK) return -st;
+    if (cache_len < 1) return -set_error(MQ_ERR_INVALID_ARGUMENT, "cache_len %d < 1", cache_len);
+    return decode_variant_for(s, int8 != 0, cache_len);
+}
+
 void launch_a10_int8_decode(int input_token_id, int* output_token_id, const void* embed_weight,
                             const LayerWeights* layer_weights, const void* final_norm_weight,
                             const void* lm_head_weight, const float* lm_head_scale, const void* cos_table,

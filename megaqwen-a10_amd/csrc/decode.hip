@@ -521,8 +521,9 @@ bool xcd_placement_ok() {
 }
 
 // The kernel a step of these dims with `cache_len` cached positions uses: the async-wave
-// kernel (3) for the INT8 Qwen3-0.6B shape up to 2048 positions, the XCD-aware kernel (2)
-// otherwise when the workgroup placement allows, else the single-level kernel (1).
+// kernel (3) for the INT8 Qwen3-0.6B shape up to 7168 positions (it runs to 10240 when forced;
+// past 7168 the XCD-aware kernel is faster), the XCD-aware kernel (2) otherwise when the
+// workgroup placement allows, else the single-level kernel (1).
 // A refusal returns its status negated (MQ_ERR_UNSUPPORTED is 2, the XCD-aware kernel's
 // number, so it must not share the positive range).
 int decode_variant_for(const DecodeShape& s, bool int8, int cache_len) {
@@ -551,9 +552,9 @@ int decode_variant_for(const DecodeShape& s, bool int8, int cache_len) {
         return decode_async_supports(s, int8, cache_len)
                    ? 3
                    : -set_error(MQ_ERR_UNSUPPORTED, "the async-wave kernel covers INT8 hidden 1024 / intermediate 3072 "
-                                                   "up to 2048 cached positions (cache_len %d)", cache_len);
+                                                   "up to %d cached positions (cache_len %d)", decode_async_max_len(), cache_len);
     if (!(have_xcd && xcd_placement_ok())) return 1;
-    return decode_async_supports(s, int8, cache_len) ? 3 : 2;
+    return decode_async_supports(s, int8, cache_len) && cache_len <= decode_async_auto_len() ? 3 : 2;
 }
 
 int decode_variant_in_use(const DecodeShape& s, bool int8) { return decode_variant_for(s, int8, 1); }

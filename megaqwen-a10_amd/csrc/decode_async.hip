@@ -1,5 +1,5 @@
 // Asynchronous-wave persistent decode step: the INT8 Qwen3-0.6B shape (hidden
-// 1024, intermediate 3072, 16 / 8 heads of 128) up to 2048 cached positions.
+// 1024, intermediate 3072, 16 / 8 heads of 128) up to 10240 cached positions.
 //
 // Same computation (a10_int8_decode_kernel.cu:21-815) and the same work split
 // over workgroups as decode_xcd.hip: workgroup g runs on XCD x = HW_REG_XCC_ID
@@ -31,8 +31,10 @@
 //    a block of consecutive positions (scores, softmax numerators and P V in
 //    fp64), and the blocks are merged with their log-sum-exp weights. Up to 64
 //    cached positions every workgroup attends over all of them from its LDS
-//    slot; past that (to 2048) rank r takes slice r of 32 (<= 64 positions, in
-//    its slot), publishes its fp64 partial (max, denominator, numerators) as
+//    slot; past that (to 10240) rank r takes slice r of 32 (<= 320 positions,
+//    streamed through its slot in chunks of 64 by the KV loader, one chunk in
+//    flight while the compute waves attend over the one before it), publishes
+//    its fp64 partial (max, denominator, numerators) as
 //    tagged XCD-local words, merges output dims [8r, +8) over the 32 partials,
 //    and the merged 256 outputs come back through one more XCD-local exchange.
 //
@@ -58,6 +60,7 @@
 
 #include <hip/hip_ext.h>
 
+
 namespace mq {
 
 namespace {
@@ -65,9 +68,10 @@ namespace {
 constexpr int kAH = 1024, kAI = 3072, kAD = 128;
 constexpr int kAX = 8;                     // XCDs
 constexpr int kAIX = kAI / kAX;            // intermediate channels per XCD
-constexpr int kAMaxLen = 64;               // positions one workgroup holds in LDS (slot B)
+constexpr int kAMaxLen = 64;               // positions one workgroup holds in LDS (slot B): one chunk
+constexpr int kAMaxChunks = 5;             // chunks of a rank's slice, streamed through slot B in turn
 constexpr int kARanks = kNWG / kAX;        // workgroups (ranks) per XCD
-constexpr int kASplitLen = kARanks * kAMaxLen;   // cache_len with split attention: 32 slices of <= 64
+constexpr int kASplitLen = kARanks * kAMaxLen * kAMaxChunks;   // longest cache_len: 32 slices of <= 320
 constexpr int kAPart = 4 + 2 * kAD;        // a rank's attention partial: (max, denominator) per head, numerators
 constexpr int kCW = 4;                     // compute waves
 // digit plane pitch in words: 68, not 64, so that the 8 planes one A-operand read
@@ -366,7 +370,9 @@ __device__ __forceinline__ const volatile KArgs* kargs() {
 // cost register spills in the one-step kernel too).
 // kW4: the layer projections are INT4 per group of 128 inputs (packed nibbles [out, in / 2],
 // scales [out, in / 128]); the LM head stays INT8 per row.
-template <bool kDebug, bool kMulti, bool kW4 = false>
+// kDeep: a rank's slice may take several slot-B chunks (cache_len past 2048); without it the
+// kernel holds every slice in one chunk and the host launches it only up to 2048 positions.
+template <bool kDebug, bool kMulti, bool kW4 = false, bool kDeep = false>
 __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     constexpr int H = kAH, D = kAD;
     constexpr ALayout kLay = alayout_for(xlayout_total(kAH, kAI));
@@ -421,6 +427,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         ns = min(n, s0 + cs) - s0;
         return true;
     };
+    // Slot-B chunks of this rank's positions at cache_len p + 1: ceil(ns / kAMaxLen), at least 1
+    // (the first carries the QK-norm gains and, in layer 0, the RoPE row). Slot B's ready and
+    // consumed counters count chunks over the launch: chunk k of layer l of a step is number
+    // cbase + l nch + k, cbase being the chunks of the launch's earlier steps.
+    auto chunks_at = [&](int p) -> int {
+        int s0, ns;
+        attn_slice(p, s0, ns);
+        return max(1, (ns + kAMaxLen - 1) / kAMaxLen);
+    };
+    uint32_t cbase = 0;
+    int nch = 1;
     if (x >= kAX) {
         if (tid0 == 0) __hip_atomic_store(&hdr->abort_flag, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
@@ -454,6 +471,10 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
     E = E0 + (uint32_t)step;
     AS = AS0 + (uint32_t)step;
     pos = a.pos + step;
+    if (kDeep) {
+        if (step > 0) cbase += (uint32_t)(a.L * nch);
+        nch = chunks_at(pos);
+    }
 
     if (wave >= kCW) {
         // ================================ loader waves ================================
@@ -465,7 +486,8 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
         //   d = 0: slot A (the rank's q|k|v rows, input norm gains, row scales)
         //   d = 1: slots C and F (O and down rows, their scales)
         //   d = 2: slot E (gate|up rows, post-attention norm gains, scales)
-        //   d = 3: slot B (cached K and V rows of positions [0, pos), QK-norm gains), and
+        //   d = 3: slot B (cached K and V rows of positions [0, pos), QK-norm gains; past 2048
+        //          positions a rank's slice in chunks of 64, one after another), and
         //          once per step this position's RoPE row and the final norm gains; it also
         //          stores the position's new K and V rows into the cache (store_row)
         const int d = wave - kCW;
@@ -489,7 +511,7 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
             int s0, ns;
             const bool sp_ = attn_slice(pos, s0, ns);
             if (!(sp_ ? (pos >= s0 && pos < s0 + ns) : r == 0)) return;
-            const int pl = pos - s0;
+            const int pl = pos - s0 - kAMaxLen * (nch - 1);       // its row in the last chunk
             const int ls = opaque(lane);
             const int64_t row = ((int64_t)ll * kAX + x) * kv_head_stride + (int64_t)pos * D;
             if (ls < 16) {
@@ -650,59 +672,71 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     for (int m = 0; m < 3; ++m) put32(S.gsE, 64 * m + lane, ge[m]);
                 }
                 raise(SL_E, gl);
-            } else {
+            }
+            if (d == 3) {
                 // K rows keep their 16-byte chunks XOR-permuted by row (chunk g of row j at
                 // g ^ (j % 16)), so that lanes reading the same chunk of different rows hit
                 // different banks; V rows are read whole by every lane and stay in order
                 // (the lane is rederived per layer, so that its row addresses are not held
                 // through the layer loop alongside the 128 registers of rows)
-                // Slot row jl holds position s0 + jl of this rank's positions (all of them, or
-                // its slice with split attention); rows before pos come from the cache.
-                const int ln = opaque(lane);
+                // Slot row jl of chunk k holds position s0 + kAMaxLen k + jl of this rank's positions
+                // (all of them, or its slice with split attention); rows before pos come from the
+                // cache. Chunk 0 is loaded once compute wave 0 has begun the previous layer's
+                // attention, each later one as soon as the one before it is in the slot, so that
+                // it is in flight while the compute waves attend over that one. (Loader 0 taking
+                // every other chunk, so that two were in flight, measured slower: 563 against
+                // 547 us per step at depth 4096.)
                 const int64_t cb = ((int64_t)l * kAX + x) * kv_head_stride;
                 int s0, ns;
                 attn_slice(pos, s0, ns);
-                const int lim = min(ns, pos - s0);
-                uint4 rk[kAMaxLen / 4], rv[kAMaxLen / 4];
+                const uint32_t ci0 = kDeep ? cbase + (uint32_t)(l * nch) : (uint32_t)gl;
+                for (int k = 0; k < nch; ++k) {
+                    const int ln = opaque(lane);
+                    const int lim = min(min(ns, pos - s0) - kAMaxLen * k, kAMaxLen);   // rows from the cache
+                    const int64_t kb0 = cb + (int64_t)(s0 + kAMaxLen * k) * D;
+                    uint4 rk[kAMaxLen / 4], rv[kAMaxLen / 4];
 #pragma unroll
-                for (int i = 0; i < kAMaxLen / 4; ++i) {
-                    const int jl = 4 * i + ln / 16;
-                    rk[i] = make_uint4(0, 0, 0, 0);
-                    rv[i] = make_uint4(0, 0, 0, 0);
-                    if (jl < lim) {
-                        rk[i] = ldg16(a.kc + cb + (int64_t)(s0 + jl) * D + 8 * (ln % 16));
-                        rv[i] = ldg16(a.vc + cb + (int64_t)(s0 + jl) * D + 8 * (ln % 16));
+                    for (int i = 0; i < kAMaxLen / 4; ++i) {
+                        const int jl = 4 * i + ln / 16;
+                        rk[i] = make_uint4(0, 0, 0, 0);
+                        rv[i] = make_uint4(0, 0, 0, 0);
+                        if (jl < lim) {
+                            rk[i] = ldg16(a.kc + kb0 + (int64_t)jl * D + 8 * (ln % 16));
+                            rv[i] = ldg16(a.vc + kb0 + (int64_t)jl * D + 8 * (ln % 16));
+                        }
                     }
-                }
-                const uint32_t qn = ld32(static_cast<const uint8_t*>(lw.q_norm_weight) + 4 * ln);
-                const uint32_t kn = ld32(static_cast<const uint8_t*>(lw.k_norm_weight) + 4 * ln);
-                // this step's RoPE row rides with layer 0's slot B (free once the previous
-                // step's last attention is done)
-                const uint32_t cw = l == 0 ? ld32(a.cos_t + (int64_t)pos * D + 2 * ln) : 0u;
-                const uint32_t sw = l == 0 ? ld32(a.sin_t + (int64_t)pos * D + 2 * ln) : 0u;
-                await_free(SL_B, gl);
-                if (l > 0) store_row(l - 1);
-                const int ls = opaque(ln);
+                    const uint32_t qn = k == 0 ? ld32(static_cast<const uint8_t*>(lw.q_norm_weight) + 4 * ln) : 0u;
+                    const uint32_t kn = k == 0 ? ld32(static_cast<const uint8_t*>(lw.k_norm_weight) + 4 * ln) : 0u;
+                    // this step's RoPE row rides with layer 0's first chunk (slot B is free once
+                    // the previous step's last attention is done)
+                    const uint32_t cw = l == 0 && k == 0 ? ld32(a.cos_t + (int64_t)pos * D + 2 * ln) : 0u;
+                    const uint32_t sw = l == 0 && k == 0 ? ld32(a.sin_t + (int64_t)pos * D + 2 * ln) : 0u;
+                    await_free(SL_B, (int)(ci0 + k));
+                    if (l > 0 && k == 0) store_row(l - 1);
+                    const int ls = opaque(ln);
 #pragma unroll
-                for (int i = 0; i < kAMaxLen / 4; ++i) {
-                    const int jl = 4 * i + ls / 16;
-                    if (jl < lim) {
-                        reinterpret_cast<uint4*>(S.kvk[jl])[(ls % 16) ^ (jl % 16)] = rk[i];
-                        reinterpret_cast<uint4*>(S.kvv[jl])[ls % 16] = rv[i];
+                    for (int i = 0; i < kAMaxLen / 4; ++i) {
+                        const int jl = 4 * i + ls / 16;
+                        if (jl < lim) {
+                            reinterpret_cast<uint4*>(S.kvk[jl])[(ls % 16) ^ (jl % 16)] = rk[i];
+                            reinterpret_cast<uint4*>(S.kvv[jl])[ls % 16] = rv[i];
+                        }
                     }
+                    if (k == 0) {
+                        put32(S.qkn[0], ls, qn);
+                        put32(S.qkn[1], ls, kn);
+                        if (l == 0) {
+                            put32(S.rope[0], ls, cw);
+                            put32(S.rope[1], ls, sw);
+                        }
+                    }
+                    raise(SL_B, (int)(ci0 + k));
                 }
-                put32(S.qkn[0], ls, qn);
-                put32(S.qkn[1], ls, kn);
-                if (l == 0) {
-                    put32(S.rope[0], ls, cw);
-                    put32(S.rope[1], ls, sw);
-                }
-                raise(SL_B, gl);
             }
         }
         if (d == 3) {
             // the step's last layer, once its attention has released slot B
-            await_free(SL_B, (step + 1) * a.L);
+            await_free(SL_B, kDeep ? (int)(cbase + (uint32_t)(a.L * nch)) : (step + 1) * a.L);
             store_row(a.L - 1);
         }
     } else {
@@ -715,14 +749,17 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
             // The loader slots of this layer are filled a layer ahead: A checks those of
             // stages A-C and E (while its hidden-slice loads are in flight) and E the
             // one of F, so that no later stage waits an LDS round trip for its slot.
+            // (slot B: its first chunk of the layer)
+            const uint32_t ci0 = kDeep ? cbase + (uint32_t)(l * nch) : (uint32_t)gl;
             auto slots_ready = [&](uint32_t mask) {
                 uint32_t v[kSlots];
 #pragma unroll
                 for (int k = 0; k < kSlots; ++k) v[k] = (mask & (1u << k)) ? lds_load(&S.sync[kReady + k]) : 0u;
 #pragma unroll
-                for (int k = 0; k < kSlots; ++k)
-                    if ((mask & (1u << k)) && v[k] < (uint32_t)(gl + 1))
-                        lds_wait(&S.sync[kReady + k], (uint32_t)(gl + 1), lds_limit, &hdr->abort_flag);
+                for (int k = 0; k < kSlots; ++k) {
+                    const uint32_t want = k == SL_B ? ci0 + 1u : (uint32_t)(gl + 1);
+                    if ((mask & (1u << k)) && v[k] < want) lds_wait(&S.sync[kReady + k], want, lds_limit, &hdr->abort_flag);
+                }
                 lds_order();
             };
             constexpr uint32_t kSlotsA = (1u << SL_A) | (1u << SL_B) | (1u << SL_C) | (1u << SL_E);
@@ -811,10 +848,14 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
             {
                 int s0, ns;
                 const bool split = attn_slice(pos, s0, ns);
-                const int q0 = (ns + kCW - 1) / kCW;                 // <= 16
-                const int j0 = s0 + min(ns, c * q0), j1 = s0 + min(ns, c * q0 + q0);
-                const int np = j1 - j0;
-                const bool owner = j0 <= pos && pos < j1;            // one wave of one workgroup per XCD when split
+                // The slice runs as nch chunks of <= kAMaxLen positions through slot B; in chunk k
+                // wave c takes the block of its q0 = ceil(nk / 4) consecutive positions. The owner
+                // of this position (one wave of one workgroup per XCD when split) is the wave whose
+                // block of the last chunk holds it.
+                const int c_last = kAMaxLen * (nch - 1);                // the last chunk's first slice row
+                const int n_last = ns - c_last;
+                const int q_last = (n_last + kCW - 1) / kCW;
+                const bool owner = s0 + c_last + min(n_last, c * q_last) <= pos && pos < s0 + c_last + min(n_last, c * q_last + q_last);
                 float qv[2][2], kv2[2], vv[2];
                 {
                     const uint32_t w[4] = {2u * (uint32_t)lane, 128u + 2u * (uint32_t)lane, 256u + 2u * (uint32_t)lane,
@@ -861,19 +902,26 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                         a.dbg_q[(2 * x + h) * D + lane + 64] = qr[h][1];
                     }
                 }
+                uint32_t own_k = 0u, own_v = 0u;
                 if (owner) {
-                    // this position's K and V rows, into the LDS copies the loops below read
-                    // (K chunks permuted as the loader stores them), from where the KV loader
-                    // of one rank per XCD stores them into the cache
+                    // this position's K and V rows, into the LDS copies the loops below read (K
+                    // chunks permuted as the loader stores them; with several chunks, into the last
+                    // one once it is in the slot), from where the KV loader of one rank per XCD
+                    // stores them into the cache
                     float kr[2];
                     rope(rms_scale(ssk, D, kEps), kv2, bf16_bits_to_f32(S.qkn[1][lane]),
                          bf16_bits_to_f32(S.qkn[1][lane + 64]), kr);
                     const uint32_t k0 = f32_to_bf16_bits(kr[0]), k1 = f32_to_bf16_bits(kr[1]);
                     const uint32_t vw = f32_to_bf16_bits(vv[0]) | (f32_to_bf16_bits(vv[1]) << 16);
-                    const int pl = pos - s0, p16 = pl % 16;
-                    S.kvk[pl][8 * ((lane >> 3) ^ p16) + (lane & 7)] = (uint16_t)k0;
-                    S.kvk[pl][8 * (((lane + 64) >> 3) ^ p16) + (lane & 7)] = (uint16_t)k1;
-                    reinterpret_cast<uint32_t*>(S.kvv[pl])[lane] = vw;
+                    if constexpr (kDeep) {
+                        own_k = k0 | (k1 << 16);
+                        own_v = vw;
+                    } else {
+                        const int pl = pos - s0, p16 = pl % 16;
+                        S.kvk[pl][8 * ((lane >> 3) ^ p16) + (lane & 7)] = (uint16_t)k0;
+                        S.kvk[pl][8 * (((lane + 64) >> 3) ^ p16) + (lane & 7)] = (uint16_t)k1;
+                        reinterpret_cast<uint32_t*>(S.kvv[pl])[lane] = vw;
+                    }
                     // (the KV loader stores the row into the cache from this slot: store_row)
                     if (split || r == 0) {
                         const bool dbgkv = kDebug && l == last;
@@ -881,121 +929,171 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                         if (dbgkv && a.dbg_v) { a.dbg_v[x * D + 2 * lane] = vv[0]; a.dbg_v[x * D + 2 * lane + 1] = vv[1]; }
                     }
                 }
-                lds_order();
-                // Scores. Lane = jj + 4 d16: jj (bits 0-1) takes the positions j0 + 4p + jj of
-                // passes p < ceil(np / 4), d16 (bits 2-5) the dims [8 d16, +8), both heads.
-                double mh = -INFINITY, lh = 0.0;         // block max and numerator sum of head (lane >> 3) & 1
+                // Running softmax state over the chunks: shift mh and numerator sum lh of head
+                // (lane >> 3) & 1, P V sums pa (dims 2 lane, 2 lane + 1 of both heads, even and
+                // odd positions).
+                double mh = -INFINITY, lh = 0.0;
+                double pa[2][2][2];                      // (zeroed where its sums begin)
                 const int jj = lane & 3, d16 = lane >> 2;
-                if (np > 0) {
-                    const int passes = (np + 3) >> 2;    // <= 4
-                    double2 qd[2][4];
-                    uint4 kc[4];
+                // (the kDeep kernel keeps a running shift over the chunks; the other holds one chunk)
+                {
+                    constexpr bool kMC = kDeep;
+                    // several chunks: the sums run over all of them; one chunk: zeroed just before
+                    // P V, so that they are not live through the scores
+                    if constexpr (kMC) {
 #pragma unroll
-                    for (int h = 0; h < 2; ++h)
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) qd[h][t] = reinterpret_cast<const double2*>(&S.qa[c][h][8 * d16])[t];
-#pragma unroll
-                    for (int p = 0; p < 4; ++p) {
-                        const int rl = j0 - s0 + min(4 * p + jj, np - 1);      // slot row
-                        kc[p] = reinterpret_cast<const uint4*>(S.kvk[rl])[d16 ^ (rl & 15)];
+                        for (int u = 0; u < 8; ++u) (&pa[0][0][0])[u] = 0.0;
                     }
-                    double E[8];                         // entry 2p + h: partial score over the 8 dims
-                    // passes in pairs without a bound check (rows past the block are its last
-                    // row; their scores are masked below), so that the four accumulation
-                    // chains of a pair interleave
-                    auto pass = [&](int p) {
-                        double s0 = 0.0, s1 = 0.0;
-                        const uint32_t k4[4] = {kc[p].x, kc[p].y, kc[p].z, kc[p].w};
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) {
-                            const double klo = bf16_bits_to_f32(k4[t] & 0xffffu);
-                            const double khi = __uint_as_float(k4[t] & 0xffff0000u);
-                            s0 = fma(qd[0][t].x, klo, s0);
-                            s0 = fma(qd[0][t].y, khi, s0);
-                            s1 = fma(qd[1][t].x, klo, s1);
-                            s1 = fma(qd[1][t].y, khi, s1);
+                    for (int k = 0; k < (kMC ? nch : 1); ++k) {
+                        const int ck = kAMaxLen * k, nk = min(ns - ck, kAMaxLen);
+                        const int q0 = (nk + kCW - 1) / kCW;                    // <= 16
+                        const int jb = min(nk, c * q0);                           // the wave's first slot row
+                        const int np = max(0, min(nk, c * q0 + q0) - jb);
+                        if (kMC && k > 0)
+                            lds_wait(&S.sync[kReady + SL_B], ci0 + (uint32_t)k + 1u, lds_limit, &hdr->abort_flag);
+                        if (kDeep && owner && k == nch - 1) {
+                            const int pl = pos - s0 - ck, p16 = pl % 16;
+                            S.kvk[pl][8 * ((lane >> 3) ^ p16) + (lane & 7)] = (uint16_t)(own_k & 0xffffu);
+                            S.kvk[pl][8 * (((lane + 64) >> 3) ^ p16) + (lane & 7)] = (uint16_t)(own_k >> 16);
+                            reinterpret_cast<uint32_t*>(S.kvv[pl])[lane] = own_v;
                         }
-                        E[2 * p] = s0;
-                        E[2 * p + 1] = s1;
-                    };
-                    pass(0);
-                    pass(1);
-                    if (passes > 2) {
-                        pass(2);
-                        pass(3);
-                    } else {
+                        lds_order();
+                        // Scores. Lane = jj + 4 d16: jj (bits 0-1) takes the slot rows jb + 4p + jj of
+                        // passes p < ceil(np / 4), d16 (bits 2-5) the dims [8 d16, +8), both heads.
+                        if (np > 0) {
+                            const int passes = (np + 3) >> 2;    // <= 4
+                            double2 qd[2][4];
+                            uint4 kc[4];
 #pragma unroll
-                        for (int k = 4; k < 8; ++k) E[k] = 0.0;
-                    }
-                    // sum over d16 (lane bits 5, 4, 3, 2), transposed: the lane keeps entry
-                    // 4 b5 + 2 b4 + b3, i.e. pass pe = 2 b5 + b4, head he = b3
+                            for (int h = 0; h < 2; ++h)
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) E[k] = tsum32(E[k], E[k + 4]);
+                                for (int t = 0; t < 4; ++t) qd[h][t] = reinterpret_cast<const double2*>(&S.qa[c][h][8 * d16])[t];
 #pragma unroll
-                    for (int k = 0; k < 2; ++k) E[k] = tsum16(E[k], E[k + 2]);
-                    {
-                        const bool u3 = (lane & 8) != 0;
-                        const double keep = u3 ? E[1] : E[0], send = u3 ? E[0] : E[1];
-                        E[0] = keep + xor8_64(send);
-                        E[0] += xor4_64(E[0]);
-                    }
-                    const int pe = 2 * ((lane >> 5) & 1) + ((lane >> 4) & 1);
-                    const bool valid = 4 * pe + jj < np;
-                    const double sc = valid ? E[0] * (double)a.attn_scale : -INFINITY;
-                    // Softmax numerators e^s without the running maximum (m = 0) unless a valid
-                    // score of this wave's block exceeds 600 in magnitude: then e^(s - m) with
-                    // the block's maximum m per head (over the lanes of the same head, bits 0,
-                    // 1, 4, 5). Within 600 no sum of up to 2048 terms e^s |v| (|v| up to the
-                    // bf16 maximum, e^89) leaves fp64's range and e^-600 is a normal number, so
-                    // both forms equal the exact softmax to fp64 rounding whatever keys the cache
-                    // holds (rows written elsewhere included); each block's m travels with its
-                    // partials, and the merges below rescale only blocks whose m differs from
-                    // the largest.
-                    const bool shift = __any(valid && fabs(sc) > 600.0);
-                    double m = 0.0;
-                    if (shift) {
-                        m = sc;
-                        m = fmax(m, partner64<1>(m));
-                        m = fmax(m, partner64<2>(m));
-                        m = fmax(m, xmax16(m));
-                        m = fmax(m, xmax32(m));
-                    }
-                    const double pv = valid ? exp(sc - m) : 0.0;
-                    double ls = pv + partner64<1>(pv);
-                    ls += partner64<2>(ls);
-                    ls = tsum16(ls, ls);
-                    ls = tsum32(ls, ls);
-                    mh = m;
-                    lh = ls;
-                    // numerators to LDS: position 4 pe + jj, head he (one lane of each pair);
-                    // all 16 entries, zero past the block, so that P V runs without bounds
-                    if ((lane & 4) == 0) S.pw[c][4 * pe + jj][(lane >> 3) & 1] = pv;
-                }
-                // P V: lane l accumulates dims 2l, 2l + 1 of both heads over the wave's block, in
-                // rounds of 8 positions without bounds checks (numerators past the block are 0,
-                // their V row is the block's last); two accumulator sets, even and odd positions
-                double pa[2][2][2] = {{{0.0, 0.0}, {0.0, 0.0}}, {{0.0, 0.0}, {0.0, 0.0}}};
-                lds_order();
-                if (np > 0) {
-                    const uint32_t* const vrow = reinterpret_cast<const uint32_t*>(S.kvv[j0 - s0]) + lane;
-                    const int rounds = (np + 7) >> 3;               // <= 2
-                    for (int t0 = 0; t0 < 8 * rounds; t0 += 8) {
-                        double2 pp[8];
-                        uint32_t vw[8];
+                            for (int p = 0; p < 4; ++p) {
+                                const int rl = jb + min(4 * p + jj, np - 1);            // slot row
+                                kc[p] = reinterpret_cast<const uint4*>(S.kvk[rl])[d16 ^ (rl & 15)];
+                            }
+                            double E[8];                         // entry 2p + h: partial score over the 8 dims
+                            // passes in pairs without a bound check (rows past the block are its last
+                            // row; their scores are masked below), so that the four accumulation
+                            // chains of a pair interleave
+                            auto pass = [&](int p) {
+                                double s0 = 0.0, s1 = 0.0;
+                                const uint32_t k4[4] = {kc[p].x, kc[p].y, kc[p].z, kc[p].w};
 #pragma unroll
-                        for (int u = 0; u < 8; ++u) {
-                            pp[u] = *reinterpret_cast<const double2*>(S.pw[c][t0 + u]);
-                            vw[u] = vrow[(kAD / 2) * min(t0 + u, np - 1)];
+                                for (int t = 0; t < 4; ++t) {
+                                    const double klo = bf16_bits_to_f32(k4[t] & 0xffffu);
+                                    const double khi = __uint_as_float(k4[t] & 0xffff0000u);
+                                    s0 = fma(qd[0][t].x, klo, s0);
+                                    s0 = fma(qd[0][t].y, khi, s0);
+                                    s1 = fma(qd[1][t].x, klo, s1);
+                                    s1 = fma(qd[1][t].y, khi, s1);
+                                }
+                                E[2 * p] = s0;
+                                E[2 * p + 1] = s1;
+                            };
+                            pass(0);
+                            pass(1);
+                            if (passes > 2) {
+                                pass(2);
+                                pass(3);
+                            } else {
+#pragma unroll
+                                for (int k = 4; k < 8; ++k) E[k] = 0.0;
+                            }
+                            // sum over d16 (lane bits 5, 4, 3, 2), transposed: the lane keeps entry
+                            // 4 b5 + 2 b4 + b3, i.e. pass pe = 2 b5 + b4, head he = b3
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) E[k] = tsum32(E[k], E[k + 4]);
+#pragma unroll
+                            for (int k = 0; k < 2; ++k) E[k] = tsum16(E[k], E[k + 2]);
+                            {
+                                const bool u3 = (lane & 8) != 0;
+                                const double keep = u3 ? E[1] : E[0], send = u3 ? E[0] : E[1];
+                                E[0] = keep + xor8_64(send);
+                                E[0] += xor4_64(E[0]);
+                            }
+                            const int pe = 2 * ((lane >> 5) & 1) + ((lane >> 4) & 1);
+                            const bool valid = 4 * pe + jj < np;
+                            const double sc = valid ? E[0] * (double)a.attn_scale : -INFINITY;
+                            // Softmax numerators e^s without the running maximum (m = 0) unless a valid
+                            // score of this wave's block exceeds 600 in magnitude: then e^(s - m) with
+                            // the block's maximum m per head (over the lanes of the same head, bits 0,
+                            // 1, 4, 5). Within 600 no sum of up to 10240 terms e^s |v| (|v| up to the
+                            // bf16 maximum, e^89) leaves fp64's range and e^-600 is a normal number, so
+                            // both forms equal the exact softmax to fp64 rounding whatever keys the cache
+                            // holds (rows written elsewhere included); each block's m travels with its
+                            // partials, and the merges below rescale only blocks whose m differs from
+                            // the largest.
+                            const bool shift = __any(valid && fabs(sc) > 600.0);
+                            double m = 0.0;
+                            if (shift) {
+                                m = sc;
+                                m = fmax(m, partner64<1>(m));
+                                m = fmax(m, partner64<2>(m));
+                                m = fmax(m, xmax16(m));
+                                m = fmax(m, xmax32(m));
+                            }
+                            // onto the running shift: M = max(mh, m); earlier chunks' sums scale by
+                            // e^(mh - M), this chunk's numerators by e^(m - M) (1 unless a shift moved it)
+                            // (no earlier chunk with a valid key: its sums are 0, any factor will do; the
+                            // exponentials only when a shift moved, behind a wave-uniform branch)
+                            const double Mn = kMC ? fmax(mh, m) : m;
+                            double fo = 1.0, fn = 1.0;
+                            if (kMC && __any(m != Mn || (mh != Mn && mh != -INFINITY))) {
+                                fo = (mh == Mn || mh == -INFINITY) ? 1.0 : exp(mh - Mn);
+                                fn = m == Mn ? 1.0 : exp(m - Mn);
+                            }
+                            const double pv = valid ? (kMC ? exp(sc - m) * fn : exp(sc - m)) : 0.0;
+                            double ls = pv + partner64<1>(pv);
+                            ls += partner64<2>(ls);
+                            ls = tsum16(ls, ls);
+                            ls = tsum32(ls, ls);
+                            if (kMC && __any(fo != 1.0)) {
+                                const double f0 = readlane64(fo, 0), f1 = readlane64(fo, 8);   // heads 0 and 1
+#pragma unroll
+                                for (int u = 0; u < 2; ++u) {
+                                    pa[u][0][0] *= f0; pa[u][0][1] *= f0;
+                                    pa[u][1][0] *= f1; pa[u][1][1] *= f1;
+                                }
+                            }
+                            mh = Mn;
+                            lh = kMC ? lh * fo + ls : ls;
+                            // numerators to LDS: position 4 pe + jj, head he (one lane of each pair);
+                            // all 16 entries, zero past the block, so that P V runs without bounds
+                            if ((lane & 4) == 0) S.pw[c][4 * pe + jj][(lane >> 3) & 1] = pv;
                         }
+                        // P V: lane l accumulates dims 2l, 2l + 1 of both heads over the wave's block, in
+                        // rounds of 8 positions without bounds checks (numerators past the block are 0,
+                        // their V row is the block's last); two accumulator sets, even and odd positions
+                        lds_order();
+                        if constexpr (!kMC) {
 #pragma unroll
-                        for (int u = 0; u < 8; ++u) {
-                            const double vlo = bf16_bits_to_f32(vw[u] & 0xffffu), vhi = __uint_as_float(vw[u] & 0xffff0000u);
-                            double (&A)[2][2] = pa[u & 1];
-                            A[0][0] = fma(pp[u].x, vlo, A[0][0]);
-                            A[0][1] = fma(pp[u].x, vhi, A[0][1]);
-                            A[1][0] = fma(pp[u].y, vlo, A[1][0]);
-                            A[1][1] = fma(pp[u].y, vhi, A[1][1]);
+                            for (int u = 0; u < 8; ++u) (&pa[0][0][0])[u] = 0.0;
                         }
+                        if (np > 0) {
+                            const uint32_t* const vrow = reinterpret_cast<const uint32_t*>(S.kvv[jb]) + lane;
+                            const int rounds = (np + 7) >> 3;               // <= 2
+                            for (int t0 = 0; t0 < 8 * rounds; t0 += 8) {
+                                double2 pp[8];
+                                uint32_t vw[8];
+#pragma unroll
+                                for (int u = 0; u < 8; ++u) {
+                                    pp[u] = *reinterpret_cast<const double2*>(S.pw[c][t0 + u]);
+                                    vw[u] = vrow[(kAD / 2) * min(t0 + u, np - 1)];
+                                }
+#pragma unroll
+                                for (int u = 0; u < 8; ++u) {
+                                    const double vlo = bf16_bits_to_f32(vw[u] & 0xffffu), vhi = __uint_as_float(vw[u] & 0xffff0000u);
+                                    double (&A)[2][2] = pa[u & 1];
+                                    A[0][0] = fma(pp[u].x, vlo, A[0][0]);
+                                    A[0][1] = fma(pp[u].x, vhi, A[0][1]);
+                                    A[1][0] = fma(pp[u].y, vlo, A[1][0]);
+                                    A[1][1] = fma(pp[u].y, vhi, A[1][1]);
+                                }
+                            }
+                        }
+                        lds_add(&S.sync[kConsumed + SL_B], lane);     // this chunk's slot rows are read
                     }
                 }
 #pragma unroll
@@ -1006,7 +1104,6 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                     S.pml[c][lane >> 3][0] = mh;
                     S.pml[c][lane >> 3][1] = lh;
                 }
-                lds_add(&S.sync[kConsumed + SL_B], lane);
                 // all four waves' partials in LDS
                 lds_add(&S.sync[kArrive + AR_B], lane);
                 lds_wait(&S.sync[kArrive + AR_B], (uint32_t)(kCW * (gl + 1)), lds_limit, &hdr->abort_flag);
@@ -1442,15 +1539,20 @@ int decode_async_split_min(int attn_split_min) {
     return attn_split_min > 0 ? std::min(attn_split_min, kAMaxLen + 1) : kAMaxLen + 1;
 }
 
-template <bool kW4>
+template <bool kW4, bool kDeep>
 static const void* async_kernel_ptr(const KArgs& ka, bool debug) {
-    if (ka.n_steps > 1) return reinterpret_cast<const void*>(&decode_async_kernel<false, true, kW4>);
-    if (debug) return reinterpret_cast<const void*>(&decode_async_kernel<true, false, kW4>);
-    return reinterpret_cast<const void*>(&decode_async_kernel<false, false, kW4>);
+    if (ka.n_steps > 1) return reinterpret_cast<const void*>(&decode_async_kernel<false, true, kW4, kDeep>);
+    if (debug) return reinterpret_cast<const void*>(&decode_async_kernel<true, false, kW4, kDeep>);
+    return reinterpret_cast<const void*>(&decode_async_kernel<false, false, kW4, kDeep>);
 }
 
 int launch_decode_async(const KArgs& ka, bool debug, bool int4, hipStream_t stream, hipEvent_t t0, hipEvent_t t1) {
-    const void* fn = int4 ? async_kernel_ptr<true>(ka, debug) : async_kernel_ptr<false>(ka, debug);
+    // the launch's last step attends over cache_len pos + n_steps; past one chunk per slice
+    // (32 x 64 positions) it needs the chunked instantiation
+    const int steps = ka.n_steps > 1 ? ka.n_steps : 1;
+    const bool deep = ka.pos + steps > kARanks * kAMaxLen;
+    const void* fn = int4 ? (deep ? async_kernel_ptr<true, true>(ka, debug) : async_kernel_ptr<true, false>(ka, debug))
+                          : (deep ? async_kernel_ptr<false, true>(ka, debug) : async_kernel_ptr<false, false>(ka, debug));
     int st = check_residency(fn);
     if (st != MQ_OK) return st;
     KArgs copy = ka;
@@ -1461,5 +1563,12 @@ int launch_decode_async(const KArgs& ka, bool debug, bool int4, hipStream_t stre
 }
 
 int decode_async_max_len() { return kASplitLen; }
+
+// The longest cache_len for which the automatic choice takes this kernel. Past 2048 positions
+// each further 64-position chunk of a rank's slice costs ~2 us per layer (it is loaded while
+// the chunk before it is attended over, and written once all four compute waves are done with
+// that one); measured against the XCD-aware kernel (tok/s, 64 steps from each depth):
+// 2040: 2,082 vs 1,834; 4096: 1,799 vs 1,657; 6144: 1,578 vs 1,532; 8192: 1,408 vs 1,438.
+int decode_async_auto_len() { return kARanks * 224; }
 
 }  // namespace mq

@@ -278,6 +278,7 @@ hipError_t launch_resident(const void* fn, dim3 grid, dim3 block, void** args, h
 // attention past 64).
 size_t decode_async_workspace_bytes(const DecodeShape& s);
 bool decode_async_supports(const DecodeShape& s, bool int8, int cache_len);
+int decode_async_auto_len();
 int launch_decode_async(const KArgs& k, bool debug, bool int4, hipStream_t stream, hipEvent_t t0, hipEvent_t t1);
 
 // XCD-aware kernel (decode_xcd.hip).

@@ -54,6 +54,8 @@ int set_decode_variant(int variant);
 // runtime, about 10 us more per launch); 0 (default): plain launches.
 int set_cooperative_launch(int on);
 int decode_variant_in_use(const DecodeShape& s, bool int8);
+// the kernel a step attending over cache_len positions uses (or minus a refusal's status)
+int decode_variant_for(const DecodeShape& s, bool int8, int cache_len);
 // After an in-kernel placement failure: use the single-level kernel from now on.
 void mark_xcd_unusable();
 // Several decode steps in one launch: step i's input is tokens[i] (device memory) for

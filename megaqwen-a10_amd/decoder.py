@@ -41,7 +41,7 @@ VARIANTS = {"auto": 0, "flat": 1, "xcd": 2, "async": 3}
 def set_decode_variant(name: str) -> None:
     """Select the decode kernel for all following steps in this process:
     ``"auto"`` (default: the async-wave kernel for INT8 Qwen3-0.6B-shape steps
-    up to 2048 cached positions, else the XCD-aware kernel when the workgroups of
+    up to 7168 cached positions (10240 when forced), else the XCD-aware kernel when the workgroups of
     each residue class g mod 8 share one XCD, checked once per device),
     ``"flat"`` (single-level exchanges), ``"xcd"`` or ``"async"``."""
     lib = _lib.load()
@@ -55,11 +55,16 @@ def set_cooperative_launch(enable: bool) -> None:
     _lib.check(_lib.load().mq_decode_set_cooperative(int(bool(enable))), "mq_decode_set_cooperative")
 
 
-def decode_variant(hidden_size: int = 1024, intermediate_size: int = 3072, int8: bool = True) -> str:
-    """The kernel a step with these dims would use now."""
+def decode_variant(hidden_size: int = 1024, intermediate_size: int = 3072, int8: bool = True,
+                   cache_len: int | None = None) -> str:
+    """The kernel a step with these dims would use now (attending over ``cache_len`` cached
+    positions, the first step's 1 when omitted)."""
     lib = _lib.load()
     dims = _lib.ModelDims(hidden_size, intermediate_size, 16, 8, 128, 151936)
-    v = lib.mq_decode_variant(ctypes.byref(dims), int(int8))
+    if cache_len is None:
+        v = lib.mq_decode_variant(ctypes.byref(dims), int(int8))
+    else:
+        v = lib.mq_decode_variant_at(ctypes.byref(dims), int(int8), int(cache_len))
     if v < 0:
         _lib.check(-v, "mq_decode_variant")
     return {1: "flat", 2: "xcd", 3: "async"}[v]
@@ -599,7 +604,7 @@ class A10Int4MegakernelDecoder(_DecoderBase):
     projections given as packed nibbles (uint8 [out, in / 2], from ``quantize_int4``) and
     their fp32 group scales ([out, in / 128]) in the same packing order, and the LM head
     INT8 per row (``quantize_state(..., weight_format="int4")`` + ``pack_int8``). Hidden
-    1024 / intermediate 3072 up to 2048 positions, on the async-wave kernel
+    1024 / intermediate 3072 up to 10240 positions, on the async-wave kernel
     (mq_int4_decode_step; one launch for a whole generation with
     mq_int4_decode_generate). No batched prefill (prompts run as decode steps)."""
 

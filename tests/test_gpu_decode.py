@@ -529,20 +529,20 @@ def test_a10decoder_generate(mq, dev, int8):
 def test_forced_kernel_out_of_range_is_refused(mq, dev, small):
     """A kernel forced by set_decode_variant that cannot run a step refuses it with MQError
     (nothing launched, position unchanged) instead of running another kernel: the
-    async-wave kernel past its 2048 positions."""
+    async-wave kernel past its 10240 positions."""
     dec0, d, prompt, cfg, keep = small
     embed, layers, scales, lm_q, lm_s, fnorm, _, _ = keep
-    S = 2100
+    S = 10250
     cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
     dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
-    dec.prefill_random_kv(2050, seed=1)
+    dec.prefill_random_kv(10240, seed=1)
     mq.set_decode_variant("async")
     try:
         with pytest.raises(mq._lib.MQError, match="async-wave"):
             dec.decode_step(int(prompt[0]))
     finally:
         mq.set_decode_variant("auto")
-    assert dec.position() == 2050
+    assert dec.position() == 10240
     assert 0 <= dec.decode_step(int(prompt[0])) < cfg.vocab_size          # the automatic choice runs it
     del dec
     torch.cuda.empty_cache()

@@ -7,7 +7,7 @@ greedy tokens from one launch; one launch and one launch per step agreeing
 bitwise (tokens and KV caches), greedy and sampled; sampled tokens against the
 float64 oracle's Gumbel-max choice wherever its top-2 margin exceeds fp32
 logit error; a launch past one workgroup's 64-position slot (split attention);
-one launch past the async-wave kernel's 2048 positions (the XCD-aware kernel's
+one launch past the async-wave kernel's 10240 positions (the XCD-aware kernel's
 multi-step form);
 argument validation; a forced in-kernel wait expiry that leaves the decoder
 where it started; a P-token prefill in one launch (P = 8 and 64) whose whole KV
@@ -123,19 +123,53 @@ def test_one_launch_past_one_slot(mq, dev, small):
     torch.cuda.empty_cache()
 
 
-def test_one_launch_beyond_async_range(mq, dev, small):
-    """Past the async-wave kernel's 2048 positions the launch runs on the XCD-aware kernel's
-    multi-step form (split attention): one launch equals one launch per step on that kernel,
-    tokens and caches. (Per-step launches below 2048 positions would take the async-wave
-    kernel, whose split attention rounds differently in the last fp32 bits: same tokens here,
-    a few cache values one bf16 ulp apart.)"""
+def test_one_launch_across_async_chunks(mq, dev, small):
+    """On the async-wave kernel a rank's slice streams through its LDS slot in chunks of 64
+    positions past 2048 cached positions: from a seeded cache of depth 2030, 150 steps in one
+    launch (one chunk per rank, then two from cache_len 2049) equal one launch per step,
+    tokens and KV caches."""
     dec0, d, prompt, cfg, keep = small
     embed, layers, scales, lm_q, lm_s, fnorm, _, _ = keep
-    S = 2048 + 16
+    S, depth, n = 2200, 2030, 150
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
+    dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
+    mq.set_decode_variant("async")
+    try:
+        print(f"2-layer model: depth {depth}, {n} steps in one launch", flush=True)
+        dec.prefill_random_kv(depth, seed=5)
+        got = dec._generate_one_launch([int(prompt[0])], n)
+        assert got is not None
+        assert dec.position() == depth + n
+        k1, v1 = _caches(dec)
+        dec.prefill_random_kv(depth, seed=5)
+        tok, want = int(prompt[0]), []
+        for _ in range(n):
+            tok = dec.decode_step(tok)
+            want.append(tok)
+        k2, v2 = _caches(dec)
+    finally:
+        mq.set_decode_variant("auto")
+    assert got == want
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    del dec
+    torch.cuda.empty_cache()
+
+
+def test_one_launch_beyond_async_range(mq, dev, small):
+    """Past the async-wave kernel's 10240 positions the launch runs on the XCD-aware kernel's
+    multi-step form (split attention): one launch gives the tokens of one launch per step on
+    that kernel, and the same KV cache rows wherever both take the same arithmetic path:
+    positions below 2048, where each workgroup's slice holds at most 64 positions. (Past that,
+    the one-step kernel takes a slice's scores on the bf16 matrix cores with fp32 sums and the
+    multi-step form, which has no registers for those slices, in fp64, so later rows can round
+    differently in their last bits.)"""
+    dec0, d, prompt, cfg, keep = small
+    embed, layers, scales, lm_q, lm_s, fnorm, _, _ = keep
+    S = 10240 + 16
     cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
     dec = mq.A10Int8MegakernelDecoder(embed, layers, scales, lm_q, lm_s, fnorm, cos, sin, cfg.num_layers, S)
     n = S - len(prompt) + 1
-    print(f"2-layer model: {len(prompt)} + {n - 1} steps in one launch past 2048 positions", flush=True)
+    print(f"2-layer model: {len(prompt)} + {n - 1} steps in one launch past 10240 positions", flush=True)
     got = dec._generate_one_launch(prompt, n)
     assert got is not None
     assert dec.position() == S
@@ -146,7 +180,7 @@ def test_one_launch_beyond_async_range(mq, dev, small):
     finally:
         mq.set_decode_variant("auto")
     k2, v2 = _caches(dec)
-    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert torch.equal(k1[:, :, :2048], k2[:, :, :2048]) and torch.equal(v1[:, :, :2048], v2[:, :, :2048])
     del dec
     torch.cuda.empty_cache()
 

@@ -1,7 +1,7 @@
 """One-launch generation on the XCD-aware kernel's multi-step form (run with -m gpu).
 
 The async-wave kernel runs a whole generation in one launch for INT8 weights of the
-Qwen3-0.6B shape up to 2048 positions; everything else (bf16 weights, the reference's own
+Qwen3-0.6B shape up to 10240 positions; everything else (bf16 weights, the reference's own
 A10Decoder.generate path, a10_decode.py:358-393; FP8 weights; the Qwen3-1.7B shape; longer
 contexts) runs on the XCD-aware kernel, whose multi-step instantiation loops over the steps
 inside one launch and hands each token to every workgroup through one tagged word. Gates:

@@ -37,10 +37,9 @@ def test_full_int4_32_tokens(mq, dev):
     torch.cuda.empty_cache()
 
 
-def _small_int4(mq, dev, num_layers):
+def _small_int4(mq, dev, num_layers, S=64):
     cfg = mq.QWEN3_0_6B.with_(num_layers=num_layers, vocab_size=4096)
     state, prompt = mq.random_init_state(cfg, seed=3, norm_jitter=0.1)
-    S = 64
     cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta, device=dev)
     qstate = mq.quantize_state(state, cfg, dev, weight_format="int4")
     embed, layers, scales, lm_q, lm_s, fnorm = mq.pack_int8(qstate, cfg)
@@ -123,4 +122,17 @@ def test_int4_runs_on_the_async_kernel_only(mq, dev):
     assert dec.generate(prompt, 12, device_loop=True) == _greedy(dec, prompt, 12)
     assert not dec.prefill_supported()
     del dec, keep
+    torch.cuda.empty_cache()
+
+
+def test_int4_long_context_matches_oracle(mq, dev):
+    """INT4 weights past 2048 cached positions, where a rank's slice streams through its LDS slot
+    in two 64-position chunks: 6 greedy steps after a seeded N(0,1) KV pre-fill of depth 2100,
+    tokens equal to the live oracle's from the same cache."""
+    from .test_gpu_longctx import _check_long
+    depth = 2100
+    print(f"INT4 2-layer model at depth {depth}", flush=True)
+    dec, ref, prompt, keep = _small_int4(mq, dev, 2, S=depth + 16)
+    _check_long(mq, dev, dec, ref, prompt, depth, 0)
+    del dec, ref, keep
     torch.cuda.empty_cache()

@@ -171,12 +171,20 @@ def test_bf16_long_context_matches_oracle(xcd, mq, dev):
     _check_long(mq, dev, dec, ref, prompt.tolist(), depth, 0)
 
 
-def test_full_model_long_context_matches_oracle(xcd, mq, dev):
+@pytest.fixture(params=["xcd", "async"])
+def kernel_variant(request, mq):
+    mq.set_decode_variant(request.param)
+    yield request.param
+    mq.set_decode_variant("auto")
+
+
+def test_full_model_long_context_matches_oracle(kernel_variant, mq, dev):
     """Qwen3-0.6B shape (28 layers, full vocabulary) at depth 4096: 4 greedy steps
-    against the live float64 oracle from the same pre-filled cache."""
+    against the live float64 oracle from the same pre-filled cache, on the XCD-aware kernel
+    and on the async-wave kernel (slices of 129 positions in three chunks)."""
     depth = 4096
     cfg = mq.QWEN3_0_6B
-    print("building qwen3_0.6b_int8 at depth 4096", flush=True)
+    print(f"building qwen3_0.6b_int8 at depth 4096 ({kernel_variant})", flush=True)
     state, prompt = mq.random_init_state(cfg, seed=0)
     qstate = mq.quantize_state(state, cfg, dev)
     del state
@@ -259,9 +267,30 @@ def test_async_split_attention_matches_unsplit(asyncv, small):
     assert e < 1e-6, e
 
 
-@pytest.mark.parametrize("depth", [100, 1000, 2040])
+@pytest.mark.parametrize("depth", [100, 1000, 2040, 2100, 4100, 8180, 10200])
 def test_async_long_context_matches_oracle(asyncv, mq, dev, depth):
     """Past the 64 positions of one workgroup's slot: 6 greedy steps after a seeded N(0,1) KV
-    pre-fill, against the oracle started from the same cache (the last step at cache_len 2046)."""
+    pre-fill, against the oracle started from the same cache. A rank's slice streams through its
+    slot in chunks of 64: one chunk up to 2048 positions, two at 2100, three at 4100, four at
+    8180, five at 10200 (the last step at cache_len 10206)."""
     print(f"async long context depth {depth}", flush=True)
     _check_long(mq, dev, *_long_case(mq, dev, depth), depth, 0)
+
+
+
+def test_automatic_kernel_by_context_length(mq, dev):
+    """The automatic choice takes the async-wave kernel up to 7168 cached positions and the
+    XCD-aware kernel past them (where it is faster); the async-wave kernel, when forced, covers
+    10240 and refuses longer ones."""
+    mq.set_decode_variant("auto")
+    v = lambda n: mq.decode_variant(1024, 3072, int8=True, cache_len=n)
+    assert v(1) == v(2048) == v(2049) == v(7168) == "async"
+    assert v(7169) == v(10240) == v(20000) == "xcd"
+    mq.set_decode_variant("async")
+    try:
+        assert v(10240) == "async"
+        with pytest.raises(mq._lib.MQError, match="async-wave"):
+            v(10241)
+    finally:
+        mq.set_decode_variant("auto")
+    assert mq.decode_variant(2048, 6144, int8=True, cache_len=100) == "xcd"
