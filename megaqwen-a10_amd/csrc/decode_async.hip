@@ -689,11 +689,23 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                 const int64_t cb = ((int64_t)l * kAX + x) * kv_head_stride;
                 int s0, ns;
                 attn_slice(pos, s0, ns);
-                const uint32_t ci0 = kDeep ? cbase + (uint32_t)(l * nch) : (uint32_t)gl;
-                for (int k = 0; k < nch; ++k) {
+                const uint32_t qn = ld32(static_cast<const uint8_t*>(lw.q_norm_weight) + 4 * opaque(lane));
+                const uint32_t kn = ld32(static_cast<const uint8_t*>(lw.k_norm_weight) + 4 * opaque(lane));
+                // this step's RoPE row rides with layer 0's first chunk (slot B is free once the
+                // previous step's last attention is done)
+                const uint32_t cw = l == 0 ? ld32(a.cos_t + (int64_t)pos * D + 2 * opaque(lane)) : 0u;
+                const uint32_t sw = l == 0 ? ld32(a.sin_t + (int64_t)pos * D + 2 * opaque(lane)) : 0u;
+                auto put_gains = [&](int ls) {
+                    put32(S.qkn[0], ls, qn);
+                    put32(S.qkn[1], ls, kn);
+                    if (l == 0) {
+                        put32(S.rope[0], ls, cw);
+                        put32(S.rope[1], ls, sw);
+                    }
+                };
+                if constexpr (!kDeep) {
                     const int ln = opaque(lane);
-                    const int lim = min(min(ns, pos - s0) - kAMaxLen * k, kAMaxLen);   // rows from the cache
-                    const int64_t kb0 = cb + (int64_t)(s0 + kAMaxLen * k) * D;
+                    const int lim = min(ns, pos - s0);
                     uint4 rk[kAMaxLen / 4], rv[kAMaxLen / 4];
 #pragma unroll
                     for (int i = 0; i < kAMaxLen / 4; ++i) {
@@ -701,18 +713,12 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                         rk[i] = make_uint4(0, 0, 0, 0);
                         rv[i] = make_uint4(0, 0, 0, 0);
                         if (jl < lim) {
-                            rk[i] = ldg16(a.kc + kb0 + (int64_t)jl * D + 8 * (ln % 16));
-                            rv[i] = ldg16(a.vc + kb0 + (int64_t)jl * D + 8 * (ln % 16));
+                            rk[i] = ldg16(a.kc + cb + (int64_t)(s0 + jl) * D + 8 * (ln % 16));
+                            rv[i] = ldg16(a.vc + cb + (int64_t)(s0 + jl) * D + 8 * (ln % 16));
                         }
                     }
-                    const uint32_t qn = k == 0 ? ld32(static_cast<const uint8_t*>(lw.q_norm_weight) + 4 * ln) : 0u;
-                    const uint32_t kn = k == 0 ? ld32(static_cast<const uint8_t*>(lw.k_norm_weight) + 4 * ln) : 0u;
-                    // this step's RoPE row rides with layer 0's first chunk (slot B is free once
-                    // the previous step's last attention is done)
-                    const uint32_t cw = l == 0 && k == 0 ? ld32(a.cos_t + (int64_t)pos * D + 2 * ln) : 0u;
-                    const uint32_t sw = l == 0 && k == 0 ? ld32(a.sin_t + (int64_t)pos * D + 2 * ln) : 0u;
-                    await_free(SL_B, (int)(ci0 + k));
-                    if (l > 0 && k == 0) store_row(l - 1);
+                    await_free(SL_B, gl);
+                    if (l > 0) store_row(l - 1);
                     const int ls = opaque(ln);
 #pragma unroll
                     for (int i = 0; i < kAMaxLen / 4; ++i) {
@@ -722,15 +728,41 @@ __global__ void __launch_bounds__(kThreads, 1) decode_async_kernel(KArgs a) {
                             reinterpret_cast<uint4*>(S.kvv[jl])[ls % 16] = rv[i];
                         }
                     }
-                    if (k == 0) {
-                        put32(S.qkn[0], ls, qn);
-                        put32(S.qkn[1], ls, kn);
-                        if (l == 0) {
-                            put32(S.rope[0], ls, cw);
-                            put32(S.rope[1], ls, sw);
+                    put_gains(ls);
+                    raise(SL_B, gl);
+                } else {
+                    // chunk k's rows, each chunk loaded as soon as the one before it is in the slot
+                    const int lim_all = min(ns, pos - s0);
+                    const uint32_t ci0 = cbase + (uint32_t)(l * nch);
+                    for (int k = 0; k < nch; ++k) {
+                        const int ln = opaque(lane);
+                        const int lim = min(lim_all - kAMaxLen * k, kAMaxLen);   // rows from the cache
+                        const int64_t kb0 = cb + (int64_t)(s0 + kAMaxLen * k) * D;
+                        uint4 rk[kAMaxLen / 4], rv[kAMaxLen / 4];
+#pragma unroll
+                        for (int i = 0; i < kAMaxLen / 4; ++i) {
+                            const int jl = 4 * i + ln / 16;
+                            rk[i] = make_uint4(0, 0, 0, 0);
+                            rv[i] = make_uint4(0, 0, 0, 0);
+                            if (jl < lim) {
+                                rk[i] = ldg16(a.kc + kb0 + (int64_t)jl * D + 8 * (ln % 16));
+                                rv[i] = ldg16(a.vc + kb0 + (int64_t)jl * D + 8 * (ln % 16));
+                            }
                         }
+                        await_free(SL_B, (int)(ci0 + k));
+                        if (l > 0 && k == 0) store_row(l - 1);
+                        const int ls = opaque(ln);
+#pragma unroll
+                        for (int i = 0; i < kAMaxLen / 4; ++i) {
+                            const int jl = 4 * i + ls / 16;
+                            if (jl < lim) {
+                                reinterpret_cast<uint4*>(S.kvk[jl])[(ls % 16) ^ (jl % 16)] = rk[i];
+                                reinterpret_cast<uint4*>(S.kvv[jl])[ls % 16] = rv[i];
+                            }
+                        }
+                        if (k == 0) put_gains(ls);
+                        raise(SL_B, (int)(ci0 + k));
                     }
-                    raise(SL_B, (int)(ci0 + k));
                 }
             }
         }
