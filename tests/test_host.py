@@ -117,6 +117,19 @@ def test_cooperative_switch_is_host_only(mq):
     mq.set_cooperative_launch(False)
 
 
+def test_variant_query_rejects_bad_arguments_without_launching(mq):
+    """mq_decode_variant_at refuses a cache_len below 1 and dims without a kernel before it looks
+    at the device (minus the status, as mq_decode_variant)."""
+    from megaqwen_a10_amd import _lib
+    lib = _lib.load()
+    dims = _lib.ModelDims(1024, 3072, 16, 8, 128, 151936)
+    for n in (0, -5):
+        assert lib.mq_decode_variant_at(ctypes.byref(dims), 1, n) == -_lib.MQ_ERR_INVALID_ARGUMENT
+        assert "cache_len" in _lib.last_error()
+    bad = _lib.ModelDims(1000, 3072, 16, 8, 128, 151936)
+    assert lib.mq_decode_variant_at(ctypes.byref(bad), 1, 10) == -_lib.MQ_ERR_UNSUPPORTED
+
+
 def test_batch_api_rejects_bad_arguments_without_launching(mq):
     from megaqwen_a10_amd import _lib
     lib = _lib.load()
