@@ -13,12 +13,16 @@ library (``lib/libmegaqwen_a10.so``, declared in include/megaqwen_a10.h):
   one persistent-kernel launch per token.
 * ``A10Fp8MegakernelDecoder`` / ``A10Int4MegakernelDecoder`` — the same step with FP8
   E4M3 weights, or INT4 weights per group of 128 (no counterpart in the reference).
+* ``A10Chat`` — the reference's chat front end (a10_chat.py:222-604) over ``A10Decoder``:
+  ChatML prompts, streamed replies, history; ``chat_prompt`` / ``clean_reply`` its host steps.
 * ``A10Int8BatchDecoder`` — up to 16 independent sequences per step on the int8
   matrix cores (Qwen3-1.7B shapes; no counterpart in the reference).
 * ``precompute_rope_freqs`` / ``make_rope`` — RoPE tables.
 * ``random_init_state`` / ``quantize_state`` / ``pack_int8`` / ``pack_bf16`` —
   seeded weights and the reference's tensor packing.
 """
+from . import chat
+from .chat import A10Chat, chat_prompt, clean_reply
 from .config import QWEN3_0_6B, QWEN3_1_7B, ModelConfig
 from .decoder import (A10Decoder, A10Fp8MegakernelDecoder, A10Int4MegakernelDecoder, A10Int8BatchDecoder,
                       A10Int8MegakernelDecoder, A10MegakernelDecoder, config_from_checkpoint, decode_variant, load_checkpoint_state,
@@ -31,6 +35,7 @@ from .weights import pack_bf16, pack_int8, quantize_state, random_init_state, st
 
 __all__ = [
     "ModelConfig", "QWEN3_0_6B", "QWEN3_1_7B",
+    "A10Chat", "chat_prompt", "clean_reply",
     "A10Decoder", "A10Fp8MegakernelDecoder", "A10Int4MegakernelDecoder", "A10Int8BatchDecoder", "A10Int8MegakernelDecoder", "A10MegakernelDecoder", "set_decode_variant",
     "decode_variant", "set_cooperative_launch", "config_from_checkpoint", "load_checkpoint_state", "load_tokenizer",
     "int8_gemv", "int8_gemv_repeat", "quantize_per_channel",

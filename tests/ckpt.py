@@ -4,7 +4,8 @@ A directory holds what ``A10Decoder(model_path)`` reads the way the reference's
 ``_load_model`` reads a Qwen3 checkpoint (a10_decode.py:281-325): safetensors
 shards under HF key names, ``config.json``, and optionally a tokenizer
 (``tokenizer.json`` + ``tokenizer_config.json``, a word-level vocabulary
-``w0 .. w{V-1}`` so that token ids and text map one to one).
+``w0 .. w{V-1}`` so that token ids and text map one to one). ``oracle_tokens`` gives
+the float64 oracle's greedy tokens for the state dict such a directory was written from.
 """
 from __future__ import annotations
 
@@ -77,3 +78,37 @@ def tied_state_with_defaults(state: dict, cfg, drop_qk_norm_layers=()) -> dict:
         for n in ("q_norm", "k_norm"):
             want[f"model.layers.{i}.self_attn.{n}.weight"] = torch.ones(cfg.head_dim, dtype=torch.bfloat16)
     return want
+
+
+def oracle_tokens(mq, cfg, state, prompt, n_new: int, max_seq_len: int, int8: bool, with_margins: bool = False):
+    """Greedy tokens of the float64 oracle for ``prompt`` from a (tied, defaulted) bf16 state
+    dict; with ``int8`` the oracle quantizes every projection and the head with its own CPU
+    restatement (bench_int8.py:19-24). With ``with_margins`` also the top-2 logit margins."""
+    from oracle.quant import quantize_per_channel as ref_quantize
+    from oracle.ref_cpu import Dims, RefDecoder, greedy_generate
+    layers = []
+    scales = [] if int8 else None
+    for i in range(cfg.num_layers):
+        p = f"model.layers.{i}"
+        layers.append(state[f"{p}.input_layernorm.weight"])
+        for n in ("q", "k", "v"):
+            layers.append(state[f"{p}.self_attn.{n}_proj.weight"])
+        layers.append(state[f"{p}.self_attn.q_norm.weight"])
+        layers.append(state[f"{p}.self_attn.k_norm.weight"])
+        layers.append(state[f"{p}.self_attn.o_proj.weight"])
+        layers.append(state[f"{p}.post_attention_layernorm.weight"])
+        for n in ("gate", "up", "down"):
+            layers.append(state[f"{p}.mlp.{n}_proj.weight"])
+    lm, lm_s = state["lm_head.weight"], None
+    if int8:
+        for i in range(cfg.num_layers):
+            for j in (1, 2, 3, 6, 8, 9, 10):             # projections in each layer's 11 tensors
+                q, s = ref_quantize(layers[11 * i + j])
+                layers[11 * i + j] = q
+                scales.append(s)
+        lm, lm_s = ref_quantize(lm)
+    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, max_seq_len, cfg.rope_theta)
+    ref = RefDecoder(Dims(vocab_size=cfg.vocab_size), state["model.embed_tokens.weight"], layers, scales,
+                     state["model.norm.weight"], lm, lm_s, cos, sin, cfg.num_layers, max_seq_len)
+    toks, margins = greedy_generate(ref, prompt, n_new)
+    return (toks, margins) if with_margins else toks

@@ -16,47 +16,12 @@ from __future__ import annotations
 import pytest
 import torch
 
-from oracle.quant import quantize_per_channel as ref_quantize
-from oracle.ref_cpu import Dims, RefDecoder, greedy_generate
-
-from .ckpt import text_of, tied_state_with_defaults, write_checkpoint
+from .ckpt import oracle_tokens, text_of, tied_state_with_defaults, write_checkpoint
 
 pytestmark = pytest.mark.gpu
 
 N_NEW = 16
 S = 64
-
-
-def _oracle_tokens(mq, cfg, state, prompt, int8):
-    """Greedy tokens of the float64 oracle from a (tied, defaulted) bf16 state dict."""
-    layers = []
-    scales = [] if int8 else None
-    for i in range(cfg.num_layers):
-        p = f"model.layers.{i}"
-        layers.append(state[f"{p}.input_layernorm.weight"])
-        for n in ("q", "k", "v"):
-            w = state[f"{p}.self_attn.{n}_proj.weight"]
-            layers.append(w)
-        layers.append(state[f"{p}.self_attn.q_norm.weight"])
-        layers.append(state[f"{p}.self_attn.k_norm.weight"])
-        layers.append(state[f"{p}.self_attn.o_proj.weight"])
-        layers.append(state[f"{p}.post_attention_layernorm.weight"])
-        for n in ("gate", "up", "down"):
-            layers.append(state[f"{p}.mlp.{n}_proj.weight"])
-    lm, lm_s = state["lm_head.weight"], None
-    if int8:
-        qi = [1, 2, 3, 6, 8, 9, 10]                  # projections in each layer's 11 tensors
-        for i in range(cfg.num_layers):
-            for j in qi:
-                q, s = ref_quantize(layers[11 * i + j])
-                layers[11 * i + j] = q
-                scales.append(s)
-        lm, lm_s = ref_quantize(lm)
-    cos, sin = mq.precompute_rope_freqs(cfg.head_dim, S, cfg.rope_theta)
-    ref = RefDecoder(Dims(vocab_size=cfg.vocab_size), state["model.embed_tokens.weight"], layers, scales,
-                     state["model.norm.weight"], lm, lm_s, cos, sin, cfg.num_layers, S)
-    toks, _ = greedy_generate(ref, prompt, N_NEW)
-    return toks
 
 
 @pytest.fixture(scope="module")
@@ -70,7 +35,7 @@ def seeded(mq):
 def test_a10decoder_from_checkpoint_with_tokenizer(mq, dev, seeded, tmp_path, int8):
     cfg, state, prompt = seeded
     want_state = tied_state_with_defaults(state, cfg, drop_qk_norm_layers=(1,))
-    want = _oracle_tokens(mq, cfg, want_state, prompt, int8)
+    want = oracle_tokens(mq, cfg, want_state, prompt, N_NEW, S, int8)
     # EOS: the first token from the eleventh on that does not occur before it (else none)
     k = next((i for i in range(10, N_NEW) if want[i] not in want[:i]), None)
     eos = want[k] if k is not None else None
