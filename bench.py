@@ -465,7 +465,7 @@ def run_formats(args, mq, torch):
                       "(steady state; INT8 and FP8 E4M3 beside it)",
             "value": step["int4"], "unit": "us", "n_gpus": 1, "steps": 1, "warmup": 1,
             "ms_per_step": round(step["int4"] / 1e3, 5), "higher_is_better": False, "scaling": "weak",
-            "vs_baseline": None, "dtype": "int4 / fp8 / int8 weights, fp32 activations and sums", "data": "synthetic",
+            "vs_baseline": None, "dtype": "int4 / fp8 / int8 weights, fp32 activations; fp32 sums (int8, fp8), exact products and fp64 sums (int4)", "data": "synthetic",
             "config": {"workload": "other weight formats: N(0, 0.02) bf16 weights per config-2 shape quantized to INT8 "
                                    "per row, INT4 per group of 128, FP8 E4M3 per row; one launch of the format's "
                                    "steady-state matvec over rotating copies (about 2 GB), time / reps; error = rel. "

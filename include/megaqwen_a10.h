@@ -431,8 +431,10 @@ int mq_int8_gemv_repeat(const float* x, const int8_t* w, int64_t copy_stride, in
  *                s = bf16(amax / 7) (fp32 division rounded to bf16), floored at 1e-12;
  *                q = clamp(round_half_even(fp32(w) / s), -8, 7);
  *     q uint8 [M,K/2], byte i = (q[2i] & 15) | (q[2i+1] & 15) << 4; scale fp32 [M,K/128].
- * Matvecs: y[j] = sum_k dequant(w)[j,k] * x[k], x fp32 [K], y fp32 [M], fp32
- * accumulation; 16-byte aligned x and w; K <= 16384 and K % 16 == 0 (FP8) or
+ * Matvecs: y[j] = sum_k dequant(w)[j,k] * x[k], x fp32 [K] (finite), y fp32 [M];
+ * FP8 accumulates in fp32, INT4 forms exact integer products of x's 55-bit
+ * fixed-point digits on the int8 matrix cores and sums them in fp64; 16-byte
+ * aligned x and w; K <= 16384 and K % 16 == 0 (FP8) or
  * K % 128 == 0 (INT4). The _repeat forms are the steady-state form of
  * mq_int8_gemv_repeat (reps matvecs over n_copies copies copy_stride bytes
  * apart, y [n_copies, M]). */

@@ -26,15 +26,18 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 __device__ __forceinline__ uint32_t exp_field(float v) { return (__float_as_uint(v) >> 23) & 0xffu; }
 
 // X = trunc(v * 2^(181 - emax)) for fp32 v whose biased exponent is at most emax
-// (|X| < 2^55), as its eight digits: X = sum_d dig[d] 2^(49 - 7d), dig[0] in
-// [-64, 63], the others in [0, 127]. Zeros and denormals give X = 0.
-__device__ __forceinline__ void digits55(float v, uint32_t emax, int (&dig)[8]) {
+// (|X| < 2^55; fixed55), and as its eight digits: X = sum_d dig[d] 2^(49 - 7d), dig[0]
+// in [-64, 63], the others in [0, 127] (digits55). Zeros and denormals give X = 0.
+__device__ __forceinline__ int64_t fixed55(float v, uint32_t emax) {
     const uint32_t b = __float_as_uint(v);
     const uint32_t e = (b >> 23) & 0xffu;
     const uint64_t m = (uint64_t)((b & 0x7fffffu) | 0x800000u) << 31;
     const uint32_t sh = emax - e;
-    uint64_t X = (e != 0u && sh < 56u) ? (m >> sh) : 0ull;
-    if (b >> 31) X = (uint64_t)(-(int64_t)X);
+    const uint64_t X = (e != 0u && sh < 56u) ? (m >> sh) : 0ull;
+    return (b >> 31) ? -(int64_t)X : (int64_t)X;
+}
+__device__ __forceinline__ void digits55(float v, uint32_t emax, int (&dig)[8]) {
+    const uint64_t X = (uint64_t)fixed55(v, emax);
     const uint32_t lo = (uint32_t)X, hi = (uint32_t)(X >> 32);
     dig[0] = ((int)(hi << 8)) >> 25;                     // bits 49..55, sign-extended
     dig[1] = (int)((hi >> 10) & 127u);

@@ -103,6 +103,29 @@ def test_int4_gemv_parity(mq, dev, shape):
     assert _rel(y.cpu().double().numpy(), ref) <= 1e-5
 
 
+@pytest.mark.parametrize("shape", [(64, 1024), (40, 384)], ids=str)
+def test_int4_gemv_one_hot_and_scale_layouts(mq, dev, shape):
+    """One-hot activations read single dequantized weights back exactly (s * q is exact in
+    fp32), at unit, tiny and negative magnitudes; and scales not 16-byte aligned (read one
+    group at a time) give the same result as aligned ones (read four groups at a time)."""
+    M, K = shape
+    print(f"int4 gemv one-hot / scale layouts {M}x{K}", flush=True)
+    q, s = of.quantize_int4_groups(_weights(M, K, seed=7 + K))
+    deq = np.asarray(of.dequant_int4(q, s), dtype=np.float64)
+    qd, sd = q.to(dev), s.to(dev)
+    for k, v in ((0, 1.0), (K // 2 + 3, -1.0), (K - 1, 2.0 ** -100), (129 % K, -3.0 * 2.0 ** 90)):
+        e = torch.zeros(K)
+        e[k] = v
+        yk = mq.int4_gemv(e.to(dev), qd, sd).cpu().double().numpy()
+        assert np.array_equal(yk, (deq[:, k] * v).astype(np.float32).astype(np.float64)), (k, v)
+    x = torch.randn(K, generator=torch.Generator().manual_seed(3), dtype=torch.float32).to(dev)
+    buf = torch.zeros(s.numel() + 1, dtype=torch.float32, device=dev)
+    s_off = buf[1:].view(M, K // 128)
+    s_off.copy_(sd)
+    assert s_off.data_ptr() % 16 == 4
+    assert torch.equal(mq.int4_gemv(x, qd, s_off), mq.int4_gemv(x, qd, sd))
+
+
 @pytest.mark.parametrize("fmt", ["fp8", "int4"])
 @pytest.mark.parametrize("shape,n,reps", [((1024, 2048), 3, 7), ((4096, 1024), 2, 5), ((37, 128), 2, 9)], ids=str)
 def test_fmt_gemv_repeat_parity(mq, dev, fmt, shape, n, reps):
