@@ -283,7 +283,10 @@ struct SliceRegs {
 // permuted (chunk g at g ^ (r % 16), see kst_chunk) so that 16 rows read at the
 // same head dims hit 16 different bank groups, issued by NW waves (wave < NW).
 // Asynchronous: wait for the loads (vmcnt) and barrier before reading them.
-template <int NW = kWaves, class AS>
+// kAll: every wave issues all of its instructions (rows past jend repeat row
+// jend - 1, into rows of at.kst past the slice), so that the number of loads in
+// flight is fixed and later waits can count them.
+template <int NW = kWaves, bool kAll = false, class AS>
 __device__ __forceinline__ void attn_slice_k(AS& at, const uint16_t* kh, int j0, int jend, int lane, int wave) {
     constexpr int PW = AS::kNR / (4 * NW);         // instructions per wave
     static_assert(AS::kNR % (4 * NW) == 0, "whole instructions per wave");
@@ -297,8 +300,8 @@ __device__ __forceinline__ void attn_slice_k(AS& at, const uint16_t* kh, int j0,
     for (int i = 0; i < PW; ++i) {
         const int c = wave * PW + i + z;
         const int r = 4 * c + lane / 16;
-        const int j = j0 + r;
-        if (4 * c < jend - j0 && j < jend)
+        const int j = kAll ? min(j0 + r, jend - 1) : j0 + r;
+        if (kAll || (4 * c < jend - j0 && j < jend))
             __builtin_amdgcn_global_load_lds(
                 (const void __attribute__((address_space(1)))*)(kh + (int64_t)j * kHD + kst_chunk(lane % 16, r) * 8),
                 (void __attribute__((address_space(3)))*)(&at.kst[4 * c][0]), 16, 0, 0);

@@ -215,6 +215,22 @@ __device__ __forceinline__ double block_sum64(double v, double* red, int half, i
     return tree_sum<N>(r);
 }
 
+// Workgroup barrier for data in LDS only: this wave's LDS operations complete, then
+// s_barrier. __syncthreads (a workgroup-scope release fence) also waits for every
+// outstanding global load, LDS-direct loads among them; loads issued before this
+// barrier stay in flight across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// block_sum64 with lds_barrier
+template <int N>
+__device__ __forceinline__ double block_sum64_lds(double v, double* red, int half, int wave, int lane) {
+    v = wave_sum64(v);
+    double* r = red + half * N;
+    if (lane == 0) r[wave] = v;
+    lds_barrier();
+    return tree_sum<N>(r);
+}
+
 // 1/sqrt(v) for v > 0 in fp64: the hardware estimate refined by two Newton
 // steps y <- y (3/2 - v/2 y^2). Each step squares the relative error, so the
 // result is within about an ulp of the correctly rounded value (the estimate's

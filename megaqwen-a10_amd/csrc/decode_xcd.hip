@@ -320,13 +320,13 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
         // bf16: stage B's QK-norm gains, at the start of stage A (no exchange poll before
         // their use, so the loads overlap stage A's work)
         if constexpr (kLateInputs) load_gains(lw);
-
+        const int64_t cache_base = ((int64_t)l * kNX + x) * kv_head_stride;
         // ---------------- A: RMSNorm + QKV rows -> XCD-local words ----------------
-        {
+        auto stage_a = [&]() {
             double ss = 0.0;
 #pragma unroll
             for (int i = 0; i < PT; ++i) { const double v = hid[tid + i * kThreads]; ss = fma(v, v, ss); }
-            const double tot = block_sum64<kWaves>(ss, red, 0, wave, lane);
+            const double tot = block_sum64_lds<kWaves>(ss, red, 0, wave, lane);
             trace(l, 0);
             const double rstd = rms_scale(tot, H, kEps);
 #pragma unroll
@@ -334,19 +334,30 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 const int k = tid + i * kThreads;
                 xdf[xd_index<W>(k)] = (double)(float)((double)hid[k] * rstd * (double)after_wait_bf16(wln[i]));
             }
-            __syncthreads();
+            lds_barrier();
             stA.compute(xd, part, wave, lane);
-            __syncthreads();
+            lds_barrier();
             if (tid < ROWS_A) {
                 double v = Stage_<W, ROWS_A, H, 1>::row_sum(part, tid);
                 if (kInt8) v = v * (double)after_wait_f(scA);
                 ll_put_xcd(&qkvx[ROWS_A * r + tid], __float_as_uint((float)v), tag(l, XS_QKV));
             }
             trace(l, 1);
+        };
+        // Split slices of up to kSlice positions: their K rows go straight to LDS, issued
+        // here so that they stream during stage A, whose barriers wait for LDS data only.
+        // The loads stage A consumes (issued a stage ahead) are waited for first, and
+        // stage A is compiled a second time for this path: no wait in it then has to
+        // count the slice's loads, which stay in flight until stage B.
+        if (sdma) {
+            wait_vmem();
+            attn_slice_k<kWaves, true>(at, a.kc + cache_base, opaque(sj0), min(sj1, pos), lane, wave);
+            stage_a();
+        } else {
+            stage_a();
         }
 
         // ---------------- B: attention for head pair x (every rank) ----------------
-        const int64_t cache_base = ((int64_t)l * kNX + x) * kv_head_stride;
         {
             // this stage's step-independent inputs (O weights, K/V rows of earlier
             // positions, QK-norm gains) were loaded during the previous layer
@@ -362,16 +373,11 @@ __global__ void __launch_bounds__(kThreads, 1) decode_xcd_kernel(KArgs a) {
                 const int cc = (spre && side == 0) ? kst_chunk(c, j) : c;
                 if (j < npre) *reinterpret_cast<uint4*>(&at.kv_pre[side][j][cc * 4]) = pre[i];
             }
-            // split slices: the K rows (to LDS) and V words, all loads in flight
-            // at once (opaque offsets keep the addresses from being hoisted out
-            // of the layer loop). A __syncthreads would wait for the LDS-direct
-            // loads, so they are issued after the last barrier before the QKV wait.
+            // split slices: the V words (to registers; the K rows were issued at the
+            // start of stage A), all in flight at once (opaque offsets keep the addresses
+            // from being hoisted out of the layer loop)
             SliceRegs<kSlice> sr;
-            if (sdma) {
-                const int oj0 = opaque(sj0);
-                attn_slice_k(at, a.kc + cache_base, oj0, min(sj1, pos), lane, tid / kWave);
-                attn_slice_v(sr, a.vc + cache_base, oj0, min(sj1, pos), lane, tid / kWave);
-            }
+            if (sdma) attn_slice_v(sr, a.vc + cache_base, opaque(sj0), min(sj1, pos), lane, tid / kWave);
             {
                 float v1[1];
                 wt.get_strided<1>(qkvx + tid, 0, tag(l, XS_QKV), v1);
