@@ -408,7 +408,10 @@ __device__ __forceinline__ void attn_scores_mfma(AS& at, int j0, int j1, int pos
 // tolerance) the numerators are the hardware fp32 2^x of (s - m) log2(e)
 // (relative error about 2^-23) instead of the fp64 exp, and the products and
 // sums are fp32 (fixed order) instead of fp64.
-template <int TV, bool kFastExp = false, class AS, class VWord, class Emit, class Mark>
+// kGroups (fp64 path): the P @ V loop tests its bound once per group of 8 slots, for
+// callers whose vword(t) is a finite V word for every t < TV (slots past the wave's
+// positions carry numerator 0, so they add exact zeros).
+template <int TV, bool kFastExp = false, bool kGroups = false, class AS, class VWord, class Emit, class Mark>
 __device__ __forceinline__ void attn_softmax_pv(AS& at, VWord vword, int j0, int n, int pos, int tid, int lane,
                                                 int wave, Emit emit, Mark mark) {
     static_assert(TV <= kWave, "one P @ V chunk");
@@ -450,16 +453,29 @@ __device__ __forceinline__ void attn_softmax_pv(AS& at, VWord vword, int j0, int
             p1 = exp(at.p[1][jl] - M1);
         }
         double a00 = 0.0, a01 = 0.0, a10 = 0.0, a11 = 0.0;
+        // this position's V word, read once (selected per slot without a branch or an LDS read)
+        const uint32_t vcur = at.kv_cur[1][lane];
+        auto slot = [&](int t) {
+            const uint32_t vw = t * kWaves == tc ? vcur : vword(t);
+            const double r0 = readlane64(p0, t), r1 = readlane64(p1, t);
+            const double v0 = __uint_as_float(vw << 16);
+            const double v1 = __uint_as_float(vw & 0xffff0000u);
+            a00 = fma(r0, v0, a00); a01 = fma(r0, v1, a01);
+            a10 = fma(r1, v0, a10); a11 = fma(r1, v1, a11);
+        };
+        if constexpr (kGroups) {
 #pragma unroll
-        for (int t = 0; t < TV; ++t) {
-            if (t < T) {
-                const uint32_t vw = t * kWaves == tc ? at.kv_cur[1][lane] : vword(t);
-                const double r0 = readlane64(p0, t), r1 = readlane64(p1, t);
-                const double v0 = __uint_as_float(vw << 16);
-                const double v1 = __uint_as_float(vw & 0xffff0000u);
-                a00 = fma(r0, v0, a00); a01 = fma(r0, v1, a01);
-                a10 = fma(r1, v0, a10); a11 = fma(r1, v1, a11);
+            for (int tb = 0; tb < TV; tb += 8) {
+                if (tb < T) {
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        if (tb + u < TV) slot(tb + u);
+                }
             }
+        } else {
+#pragma unroll
+            for (int t = 0; t < TV; ++t)
+                if (t < T) slot(t);
         }
         attn_finish(at, a00, a01, a10, a11, wave_sum64(p0), wave_sum64(p1), M0, M1, tid, lane, wave, emit, mark);
     }
@@ -475,8 +491,8 @@ __device__ __forceinline__ void attn_partial_regs(AS& at, const SliceRegs<NR>& s
     attn_scores_mfma(at, j0, j1, pos, scale, lane, wave);
     __syncthreads();
     mark(0);
-    attn_softmax_pv<NR / kWaves>(at, [&](int t) { return sr.v[t]; }, j0, j1 - j0, pos, tid, lane, wave, emit,
-                                 mark);
+    attn_softmax_pv<NR / kWaves, false, true>(at, [&](int t) { return sr.v[t]; }, j0, j1 - j0, pos, tid, lane, wave,
+                                              emit, mark);
 }
 
 // attn_partial for a range [j0, j1) of at most kKvLds positions whose K rows
