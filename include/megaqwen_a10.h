@@ -282,7 +282,7 @@ int mq_int4_decode_step(const mq_decode_args* args, hipStream_t stream);
 int mq_int8_decode_step_noalloc(const mq_decode_args* args, hipStream_t stream);
 /* Several steps per launch (see mq_generate_args): INT8, bf16 and FP8 weights.
  * The async-wave kernel runs the launch within its range (INT8 Qwen3-0.6B shape,
- * position + steps <= 7168; 10240 when forced), the XCD-aware kernel's multi-step form otherwise
+ * position + steps <= 6144; 10240 when forced), the XCD-aware kernel's multi-step form otherwise
  * (every compiled shape and format, up to 32768 positions with split attention);
  * MQ_ERR_UNSUPPORTED on the single-level kernel. */
 int mq_int8_decode_generate(const mq_decode_args* args, const mq_generate_args* gen, hipStream_t stream);
@@ -333,7 +333,7 @@ int mq_int8_decode_batch_step(const mq_batch_args* args, hipStream_t stream);
 
 /* Kernel variant for all following steps in this process: 0 = automatic
  * (default: the async-wave kernel for INT8 steps of the Qwen3-0.6B shape up to
- * 7168 cached positions, otherwise the XCD-aware kernel, when the workgroups of
+ * 6144 cached positions, otherwise the XCD-aware kernel, when the workgroups of
  * each residue class g mod 8 share one XCD and the 8 classes cover the 8 XCDs,
  * checked once per device), 1 = single-level exchange kernel, 2 = XCD-aware,
  * 3 = async-wave (INT8 Qwen3-0.6B shape, cache_len <= 10240 only). */

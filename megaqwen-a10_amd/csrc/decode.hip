@@ -521,8 +521,8 @@ bool xcd_placement_ok() {
 }
 
 // The kernel a step of these dims with `cache_len` cached positions uses: the async-wave
-// kernel (3) for the INT8 Qwen3-0.6B shape up to 7168 positions (it runs to 10240 when forced;
-// past 7168 the XCD-aware kernel is faster), the XCD-aware kernel (2) otherwise when the
+// kernel (3) for the INT8 Qwen3-0.6B shape up to 6144 positions (it runs to 10240 when forced;
+// past 6144 the XCD-aware kernel is faster), the XCD-aware kernel (2) otherwise when the
 // workgroup placement allows, else the single-level kernel (1).
 // A refusal returns its status negated (MQ_ERR_UNSUPPORTED is 2, the XCD-aware kernel's
 // number, so it must not share the positive range).

@@ -1596,11 +1596,12 @@ int launch_decode_async(const KArgs& ka, bool debug, bool int4, hipStream_t stre
 
 int decode_async_max_len() { return kASplitLen; }
 
-// The longest cache_len for which the automatic choice takes this kernel. Past 2048 positions
-// each further 64-position chunk of a rank's slice costs ~2 us per layer (it is loaded while
-// the chunk before it is attended over, and written once all four compute waves are done with
-// that one); measured against the XCD-aware kernel (tok/s, 64 steps from each depth):
-// 2040: 2,082 vs 1,834; 4096: 1,799 vs 1,657; 6144: 1,578 vs 1,532; 8192: 1,408 vs 1,438.
-int decode_async_auto_len() { return kARanks * 224; }
+// The longest cache_len for which the automatic choice takes this kernel: rank slices of up to
+// three 64-position chunks. Past 2048 positions each further chunk of a rank's slice costs ~2 us
+// per layer (it is loaded while the chunk before it is attended over, and written once all four
+// compute waves are done with that one); measured against the XCD-aware kernel (kernel us per
+// step, 64 steps from each depth): 4608: 560 vs 600; 5120: 565 vs 604; 5632: 574 vs 608; 6144
+// (the steps reach a fourth chunk): 628 vs 618; 7168: 645 vs 631; 8192: 703 vs 649.
+int decode_async_auto_len() { return kARanks * 192; }
 
 }  // namespace mq

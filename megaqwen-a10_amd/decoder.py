@@ -41,7 +41,7 @@ VARIANTS = {"auto": 0, "flat": 1, "xcd": 2, "async": 3}
 def set_decode_variant(name: str) -> None:
     """Select the decode kernel for all following steps in this process:
     ``"auto"`` (default: the async-wave kernel for INT8 Qwen3-0.6B-shape steps
-    up to 7168 cached positions (10240 when forced), else the XCD-aware kernel when the workgroups of
+    up to 6144 cached positions (10240 when forced), else the XCD-aware kernel when the workgroups of
     each residue class g mod 8 share one XCD, checked once per device),
     ``"flat"`` (single-level exchanges), ``"xcd"`` or ``"async"``."""
     lib = _lib.load()

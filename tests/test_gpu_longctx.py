@@ -279,13 +279,13 @@ def test_async_long_context_matches_oracle(asyncv, mq, dev, depth):
 
 
 def test_automatic_kernel_by_context_length(mq, dev):
-    """The automatic choice takes the async-wave kernel up to 7168 cached positions and the
-    XCD-aware kernel past them (where it is faster); the async-wave kernel, when forced, covers
-    10240 and refuses longer ones."""
+    """The automatic choice takes the async-wave kernel up to 6144 cached positions (rank slices
+    of up to three 64-position chunks) and the XCD-aware kernel past them (where it is faster);
+    the async-wave kernel, when forced, covers 10240 and refuses longer ones."""
     mq.set_decode_variant("auto")
     v = lambda n: mq.decode_variant(1024, 3072, int8=True, cache_len=n)
-    assert v(1) == v(2048) == v(2049) == v(7168) == "async"
-    assert v(7169) == v(10240) == v(20000) == "xcd"
+    assert v(1) == v(2048) == v(2049) == v(6144) == "async"
+    assert v(6145) == v(7168) == v(10240) == v(20000) == "xcd"
     mq.set_decode_variant("async")
     try:
         assert v(10240) == "async"
